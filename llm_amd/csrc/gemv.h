@@ -1,0 +1,121 @@
+// Host-side interface of the quantised matrix kernels (gemv.hip) used by the
+// model orchestration (model.cpp).
+#pragma once
+
+#include "common.h"
+
+namespace llmhip {
+
+// How logical rows of a matrix sit in the 16-row tiles.  A fused epilogue
+// needs both rows of a pair in one tile: RoPE pairs and [gate; up] pairs.
+enum RowMap : uint32_t {
+  MAP_IDENT = 0,  // position = row
+  MAP_NEOX = 1,   // inside each head of hd rows, row i and i+hd/2 land 8 lanes apart
+  MAP_GATEUP = 2  // rows [0,ff) gate and [ff,2ff) up: gate i and up i land 8 lanes apart
+};
+
+// A quantised matrix in the tiled layout.
+struct QMat {
+  int device = 0;
+  Geom g;
+  uint8_t* qs = nullptr;  // device
+  uint8_t* sc = nullptr;  // device
+  uint64_t bytes = 0;
+  // row map (RowMap): NEOX pairs rows inside heads of map_hd rows for rows
+  // [map_seg0, map_seg1); GATEUP pairs row i with row ff + i.
+  uint32_t map = MAP_IDENT, map_hd = 0, map_seg0 = 0, map_seg1 = 0, ff = 0;
+};
+
+enum Prologue : int {
+  PRO_PLAIN = 0,  // x[t*ldx + e]
+  PRO_RMS = 1,    // RMSNorm(x[t]) * nw  (cpu.go:81-98), recomputed per workgroup
+  PRO_MERGE = 2   // merge of the attention chunks (flash-decoding), fused.go K3 input hook
+};
+
+enum Epilogue : int {
+  EPI_STORE = 0,   // y[t*ldy + row] = v
+  EPI_ACC = 1,     // y[t*ldy + row] += v           (residual add, K3 / K5)
+  EPI_QKV = 2,     // + bias, RoPE on pairs, q out, K/V appended to the cache (K1)
+  EPI_GATEUP = 3,  // act[t*ff + i] = silu(gate_i) * up_i                   (K4)
+  EPI_ARGMAX = 4   // STORE, and each workgroup's (max, index) of its rows    (head)
+};
+
+struct GemvArgs {
+  // matrix
+  const uint8_t* qs;
+  const uint8_t* sc;
+  uint32_t rows, nb, ng, tail, tiles, k;
+  uint32_t map, map_hd, map_seg0, map_seg1;  // RowMap; NEOX applies to rows [seg0, seg1)
+  uint32_t ntok;                             // tokens in the launch
+  uint32_t split;                            // waves sharing one tile (split-K): 1, 2 or 4
+  // prologue
+  const float* x;
+  uint32_t ldx;
+  uint32_t xrow0;  // token t reads row xrow0 + t of x (head: the last token of a chunk)
+  const float* nw;
+  float eps;
+  const float* pv;
+  const float* ml;
+  uint32_t heads, hd, smax, chunk;  // attention partials [t][h][smax][hd], chunk positions each
+  const uint32_t* state;            // (pos, step) on the device
+  // epilogue
+  float* y;
+  uint32_t ldy;
+  const float* bias;  // QKV biases, logical row order (nullptr: none)
+  const float* cs;    // RoPE table [pos][hd/2][cos, sin]
+  float* kv;          // this layer's cache [2][ctx][kvd]
+  uint32_t nq, nk, kvd, ctx;
+  uint32_t neox;
+  uint32_t ff;
+  float* amax_v;  // EPI_ARGMAX: per-workgroup partials
+  uint32_t* amax_i;
+};
+
+// Bytes of LDS a launch needs, and whether the shape is supported.
+int gemv_launch(const GemvArgs& a, uint32_t qtype, int pro, int epi, hipStream_t s);
+// Workgroups the launch uses along x (EPI_ARGMAX partial count).
+uint32_t gemv_groups(const GemvArgs& a);
+// Picks the split-K factor for a matrix of `tiles` row tiles.
+uint32_t gemv_pick_split(uint32_t tiles, uint32_t ng);
+
+// Fill a GemvArgs with the matrix fields of m.
+void gemv_bind(GemvArgs* a, const QMat& m);
+
+// Allocation and device repack of raw GGUF blocks.
+int qmat_alloc(QMat* m, int device, uint32_t type, uint64_t rows, uint64_t k);
+void qmat_release(QMat* m);
+// Host staging for uploads: pinned + device buffers of one piece.
+struct Stager {
+  int device = -1;
+  uint8_t* host[2] = {nullptr, nullptr};
+  uint8_t* dev[2] = {nullptr, nullptr};
+  hipEvent_t done[2] = {nullptr, nullptr};
+  int cur = 0;
+  uint64_t cap = 0;
+  hipStream_t stream = nullptr;
+};
+int stager_init(Stager* st, int device, uint64_t cap, hipStream_t s);
+void stager_free(Stager* st);
+// Upload raw GGUF bytes [byte_off, byte_off+nbytes) of a tensor whose first
+// row is logical row row_off of m (a fused matrix holds several tensors).
+int qmat_upload(Stager* st, const QMat& m, const void* raw, uint64_t nbytes, uint64_t byte_off, uint64_t row_off);
+// Dequantise rows [0, rows) (logical order) into out_dev[rows][k].
+int qmat_dequant(const QMat& m, float* out_dev, hipStream_t s);
+// Embedding gather: x[t][:] = row tokens[state[1] + t] of m (exact), t < ntok.
+int embed_launch(const QMat& m, const int32_t* tokens, const uint32_t* state, float* x, uint32_t ntok,
+                 hipStream_t s);
+
+// Per-type launchers, instantiated in gemv_q40.hip / gemv_q41.hip / gemv_q80.hip.
+template <uint32_t QT>
+int gemv_launch_qt(const GemvArgs& a, int pro, int epi, hipStream_t s);
+template <uint32_t QT>
+int repack_launch_qt(const QMat& m, const uint8_t* raw_dev, uint64_t n, uint64_t blk0, uint64_t row_off,
+                     uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1, uint32_t ff, hipStream_t s);
+template <uint32_t QT>
+int dequant_launch_qt(const QMat& m, float* out, uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1, uint32_t ff,
+                      hipStream_t s);
+template <uint32_t QT>
+int embed_launch_qt(const QMat& m, const int32_t* tokens, const uint32_t* state, float* x, uint32_t ntok,
+                    hipStream_t s);
+
+}  // namespace llmhip

@@ -1,0 +1,679 @@
+// Device code of the quantised matrix kernels: tiled-layout repack, exact
+// dequantisation and the MFMA dequant-matvec with its fused prologues and
+// epilogues.  Included by one translation unit per weight type.
+//
+// Arithmetic of the matvec.  cpu.go:164-215 computes, per row and per block of
+// 32, s = sum_j (q_j - 8) x_j in f32 and then sum += d * s.  Here the block
+// product runs on the matrix cores: the weights (q - 8, or q, or int8) are
+// exact in f16; each activation is scaled by a power of two per token (so its
+// largest magnitude sits in [2^14, 2^15)) and split exactly into
+// hi = f16(x) and lo = f16(x - hi), two MFMA rows, 22 significant bits in
+// all.  v_mfma_f32_16x16x32_f16 sums the 32 products of a block in f32 for 16
+// rows at once; the block scale d is applied in f32 afterwards, as in the CPU
+// path.  The result differs from the CPU path only by f32 rounding order
+// (about 1e-7 relative), within the 1e-5 tolerance of the kernel sweep.
+#pragma once
+
+#include "gemv.h"
+
+namespace llmhip {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// F16ToF32 of f16.go:6-28 in integer operations: exact for every pattern,
+// NaN payloads included.
+__device__ __forceinline__ float f16_exact(uint32_t h) {
+  uint32_t sign = (h >> 15) << 31, exp = (h >> 10) & 0x1f, man = h & 0x3ff;
+  if (exp == 0) {
+    if (man == 0) return __uint_as_float(sign);
+    uint32_t sh = __clz(man) - 21;  // shifts until bit 10 is set
+    return __uint_as_float(sign | (113u - sh) << 23 | ((man << sh) & 0x3ff) << 13);
+  }
+  if (exp == 31) return __uint_as_float(sign | 0xffu << 23 | man << 13);
+  return __uint_as_float(sign | (exp + 112u) << 23 | man << 13);
+}
+
+// The f16 bits of a scale as f32 through the hardware conversion (exact for
+// every finite value, subnormals included).
+__device__ __forceinline__ float f16_hw(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+__device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+
+// ------------------------------------------------------------ row maps
+
+__host__ __device__ inline uint32_t pos_of_row(uint32_t lr, uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1,
+                                               uint32_t ff) {
+  if (map == MAP_NEOX && lr >= seg0 && lr < seg1) {
+    uint32_t local = lr - seg0, h = local / hd, k = local % hd, hp = hd / 2;
+    uint32_t side = k >= hp, i = side ? k - hp : k;
+    return seg0 + h * hd + 16 * (i / 8) + (i % 8) + 8 * side;
+  }
+  if (map == MAP_GATEUP) {
+    uint32_t side = lr >= ff, i = side ? lr - ff : lr;
+    return 16 * (i / 8) + 8 * side + (i % 8);
+  }
+  return lr;
+}
+
+__host__ __device__ inline uint32_t row_of_pos(uint32_t p, uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1,
+                                               uint32_t ff) {
+  if (map == MAP_NEOX && p >= seg0 && p < seg1) {
+    uint32_t local = p - seg0, h = local / hd, w = local % hd, c = w % 16;
+    return seg0 + h * hd + (c / 8) * (hd / 2) + 8 * (w / 16) + (c % 8);
+  }
+  if (map == MAP_GATEUP) {
+    uint32_t c = p % 16;
+    return (c / 8) * ff + 8 * (p / 16) + (c % 8);
+  }
+  return p;
+}
+
+// ------------------------------------------------------------- layout
+
+template <uint32_t QT>
+struct QT_ {
+  static constexpr uint32_t BB = QT == LLMHIP_Q4_0 ? 18 : QT == LLMHIP_Q4_1 ? 20 : 34;  // GGUF bytes/block
+  static constexpr uint32_t QB = QT == LLMHIP_Q8_0 ? 32 : 16;                          // quant bytes/block
+  static constexpr uint32_t SB = QT == LLMHIP_Q4_1 ? 4 : 2;                            // scale bytes/block
+  static constexpr uint32_t QO = QT == LLMHIP_Q4_1 ? 4 : 2;                            // quants offset in GGUF block
+};
+
+// Byte offset, inside a tile's quants, of the 4 bytes (Q8: 8) that MFMA lane
+// (16*w + r) holds for block b.
+template <uint32_t QT>
+__host__ __device__ inline uint32_t qs_off(uint32_t b, uint32_t lanew, uint32_t ng, uint32_t tail) {
+  uint32_t g4 = b / 4, j = b % 4;
+  if (QT == LLMHIP_Q8_0) {
+    if (g4 < ng) return g4 * 2048 + (j / 2) * 1024 + lanew * 16 + (j % 2) * 8;
+    return ng * 2048 + lanew * tail * 8 + j * 8;
+  }
+  if (g4 < ng) return g4 * 1024 + lanew * 16 + j * 4;
+  return ng * 1024 + lanew * tail * 4 + j * 4;
+}
+
+template <uint32_t QT>
+__host__ __device__ inline uint32_t sc_off(uint32_t b, uint32_t r, uint32_t ng, uint32_t tail) {
+  constexpr uint32_t SB = QT_<QT>::SB;
+  uint32_t g4 = b / 4, j = b % 4;
+  if (g4 < ng) return g4 * 64 * SB + (r * 4 + j) * SB;
+  return ng * 64 * SB + (r * tail + j) * SB;
+}
+
+// One thread per GGUF block: scales verbatim, quants into MFMA lane order.
+// Q8_0 bytes of k-group w are reordered to the element order the
+// dequantiser produces (see dq8): word0 = e(4w), e(16+4w), e(4w+2),
+// e(16+4w+2); word1 = e(4w+1), e(16+4w+1), e(4w+3), e(16+4w+3).
+template <uint32_t QT>
+__global__ void repack_kernel(const uint8_t* __restrict__ raw, uint64_t n, uint64_t blk0, uint64_t row_off,
+                              uint8_t* __restrict__ qs, uint8_t* __restrict__ sc, uint32_t nb, uint32_t ng,
+                              uint32_t tail, uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1, uint32_t ff) {
+  typedef QT_<QT> T;
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  uint64_t gb = blk0 + i;
+  uint32_t lr = (uint32_t)(row_off + gb / nb), b = (uint32_t)(gb % nb);
+  uint32_t p = pos_of_row(lr, map, hd, seg0, seg1, ff), t = p / 16, r = p % 16;
+  const uint8_t* blk = raw + i * T::BB;
+  uint8_t* sct = sc + (uint64_t)t * 16 * nb * T::SB + sc_off<QT>(b, r, ng, tail);
+  for (uint32_t k = 0; k < T::SB; k++) sct[k] = blk[k];
+  uint8_t* qt = qs + (uint64_t)t * 16 * nb * T::QB;
+  const uint8_t* q = blk + T::QO;
+  if (QT == LLMHIP_Q8_0) {
+    for (uint32_t w = 0; w < 4; w++) {
+      uint32_t w0 = q[4 * w] | q[16 + 4 * w] << 8 | q[4 * w + 2] << 16 | (uint32_t)q[16 + 4 * w + 2] << 24;
+      uint32_t w1 = q[4 * w + 1] | q[16 + 4 * w + 1] << 8 | q[4 * w + 3] << 16 | (uint32_t)q[16 + 4 * w + 3] << 24;
+      uint32_t o = qs_off<QT>(b, 16 * w + r, ng, tail);
+      *(uint32_t*)(qt + o) = w0;
+      *(uint32_t*)(qt + o + 4) = w1;
+    }
+  } else {
+    for (uint32_t w = 0; w < 4; w++) {
+      uint32_t word = q[4 * w] | q[4 * w + 1] << 8 | q[4 * w + 2] << 16 | (uint32_t)q[4 * w + 3] << 24;
+      *(uint32_t*)(qt + qs_off<QT>(b, 16 * w + r, ng, tail)) = word;
+    }
+  }
+}
+
+// The 32 f32 weights of block b of the row at tile position p, exactly as
+// cpu.go forms them: d*f32(q-8) (Q4_0), d*f32(q)+m (Q4_1), d*f32(i8) (Q8_0).
+template <uint32_t QT>
+__device__ inline void dequant_block(const uint8_t* qs, const uint8_t* sc, uint32_t nb, uint32_t ng, uint32_t tail,
+                                     uint32_t p, uint32_t b, float* out) {
+  typedef QT_<QT> T;
+  uint32_t t = p / 16, r = p % 16;
+  const uint8_t* qt = qs + (uint64_t)t * 16 * nb * T::QB;
+  const uint8_t* sct = sc + (uint64_t)t * 16 * nb * T::SB + sc_off<QT>(b, r, ng, tail);
+  float d = f16_exact(sct[0] | sct[1] << 8);
+  float m = 0;
+  if (QT == LLMHIP_Q4_1) m = f16_exact(sct[2] | sct[3] << 8);
+  for (uint32_t w = 0; w < 4; w++) {
+    uint32_t o = qs_off<QT>(b, 16 * w + r, ng, tail);
+    if (QT == LLMHIP_Q8_0) {
+      uint32_t w0 = *(const uint32_t*)(qt + o), w1 = *(const uint32_t*)(qt + o + 4);
+      const uint32_t e0[4] = {4 * w, 16 + 4 * w, 4 * w + 2, 16 + 4 * w + 2};
+      const uint32_t e1[4] = {4 * w + 1, 16 + 4 * w + 1, 4 * w + 3, 16 + 4 * w + 3};
+      for (int i = 0; i < 4; i++) {
+        out[e0[i]] = __fmul_rn(d, (float)(int8_t)(w0 >> (8 * i)));
+        out[e1[i]] = __fmul_rn(d, (float)(int8_t)(w1 >> (8 * i)));
+      }
+    } else {
+      uint32_t word = *(const uint32_t*)(qt + o);
+      for (int i = 0; i < 4; i++) {
+        uint32_t byte = (word >> (8 * i)) & 255u;
+        int lo = byte & 15, hi = byte >> 4;
+        if (QT == LLMHIP_Q4_0) {
+          out[4 * w + i] = __fmul_rn(d, (float)(lo - 8));
+          out[16 + 4 * w + i] = __fmul_rn(d, (float)(hi - 8));
+        } else {
+          out[4 * w + i] = __fadd_rn(__fmul_rn(d, (float)lo), m);
+          out[16 + 4 * w + i] = __fadd_rn(__fmul_rn(d, (float)hi), m);
+        }
+      }
+    }
+  }
+}
+
+// out[lr][k] for every logical row; one thread per (row, block).
+template <uint32_t QT>
+__global__ void dequant_kernel(const uint8_t* __restrict__ qs, const uint8_t* __restrict__ sc, uint32_t rows,
+                               uint32_t nb, uint32_t ng, uint32_t tail, uint32_t map, uint32_t hd, uint32_t seg0,
+                               uint32_t seg1, uint32_t ff, float* __restrict__ out) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (uint64_t)rows * nb) return;
+  uint32_t lr = (uint32_t)(i / nb), b = (uint32_t)(i % nb);
+  float v[32];
+  dequant_block<QT>(qs, sc, nb, ng, tail, pos_of_row(lr, map, hd, seg0, seg1, ff), b, v);
+  float* o = out + (uint64_t)lr * nb * 32 + b * 32;
+  for (int j = 0; j < 32; j++) o[j] = v[j];
+}
+
+// Embedding gather (kernels.go:19-73): x[t][:] = row tokens[state[1]+t].
+template <uint32_t QT>
+__global__ void embed_kernel(const uint8_t* __restrict__ qs, const uint8_t* __restrict__ sc, uint32_t nb, uint32_t ng,
+                             uint32_t tail, const int32_t* __restrict__ tokens, const uint32_t* __restrict__ state,
+                             float* __restrict__ x) {
+  uint32_t t = blockIdx.y;
+  uint32_t row = (uint32_t)tokens[state[1] + t];
+  for (uint32_t b = threadIdx.x; b < nb; b += blockDim.x) {
+    float v[32];
+    dequant_block<QT>(qs, sc, nb, ng, tail, row, b, v);
+    float* o = x + (uint64_t)t * nb * 32 + b * 32;
+    for (int j = 0; j < 32; j++) o[j] = v[j];
+  }
+}
+
+// ------------------------------------------------------------ dequantisers
+
+// Word w of a Q4 block (byte i: element 4w+i low nibble, 16+4w+i high) as
+// eight f16 weights in the order 4w, 4w+2, 16+4w, 16+4w+2, 4w+1, 4w+3,
+// 16+4w+1, 16+4w+3.  0x6400|n is the f16 1024+n; a nibble in bits 4-7 gives
+// 1024+16n, scaled back by 1/16.  Every step is exact.
+template <bool Q41>
+__device__ __forceinline__ h8 dq4(uint32_t w) {
+  const h2 lo_off = Q41 ? h2{(_Float16)-1024, (_Float16)-1024} : h2{(_Float16)-1032, (_Float16)-1032};
+  const h2 hi_off = Q41 ? h2{(_Float16)-64, (_Float16)-64} : h2{(_Float16)-72, (_Float16)-72};
+  const h2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+  uint32_t w8 = w >> 8;
+  h2 a = as_h2((w & 0x000F000Fu) | 0x64006400u) + lo_off;
+  h2 b = as_h2((w & 0x00F000F0u) | 0x64006400u) * s16 + hi_off;
+  h2 c = as_h2((w8 & 0x000F000Fu) | 0x64006400u) + lo_off;
+  h2 d = as_h2((w8 & 0x00F000F0u) | 0x64006400u) * s16 + hi_off;
+  return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Two repacked Q8_0 words as eight f16 weights in the same element order:
+// bytes 0 and 2 of a word form one pair, bytes 1 and 3 the other.  With
+// the sign bit flipped a byte is i8+128; 0x64 above it gives 1024+i8+128.
+__device__ __forceinline__ h8 dq8(uint32_t w0, uint32_t w1) {
+  const h2 off = {(_Float16)-1152, (_Float16)-1152};
+  uint32_t a = w0 ^ 0x80808080u, b = w1 ^ 0x80808080u;
+  h2 p = as_h2(__builtin_amdgcn_perm(0x64646464u, a, 0x04020400u)) + off;
+  h2 q = as_h2(__builtin_amdgcn_perm(0x64646464u, a, 0x04030401u)) + off;
+  h2 r = as_h2(__builtin_amdgcn_perm(0x64646464u, b, 0x04020400u)) + off;
+  h2 s = as_h2(__builtin_amdgcn_perm(0x64646464u, b, 0x04030401u)) + off;
+  return h8{p[0], p[1], q[0], q[1], r[0], r[1], s[0], s[1]};
+}
+
+// ------------------------------------------------------------ reductions
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// -------------------------------------------------------------- the kernel
+
+constexpr int GW = 256;  // threads per workgroup: 4 waves
+
+// LDS layout of one launch (bytes).
+struct Lds {
+  uint32_t xs, misc, bsum, part, stage, wts, total;
+};
+
+__host__ __device__ inline Lds lds_layout(int NT, int pro, uint32_t qtype, uint32_t nb, uint32_t k, uint32_t heads,
+                                          uint32_t smax) {
+  Lds L;
+  uint32_t o = 0;
+  L.xs = o;
+  o += nb * 4 * 2 * NT * 16;
+  L.misc = o;
+  o += 64 * 4;
+  L.bsum = o;
+  if (qtype == LLMHIP_Q4_1) o += nb * NT * 4;
+  L.part = o;
+  o += 4 * 64 * 2 * 4;
+  L.stage = o;
+  L.wts = o;
+  if (pro == PRO_MERGE) {
+    o += NT * k * 4;
+    L.wts = o;
+    o += NT * heads * (smax + 1) * 4;
+  }
+  L.total = o;
+  return L;
+}
+
+template <uint32_t QT, int NT, int PRO, int EPI>
+__global__ __launch_bounds__(GW) void gemv_kernel(GemvArgs a) {
+  typedef QT_<QT> T;
+  constexpr int S = 2 * NT;  // MFMA rows used: hi and lo of each token
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t t0 = blockIdx.y * NT;
+  const int nt = min((int)NT, (int)(a.ntok - t0));
+  const uint32_t nb = a.nb, K = a.k;
+  const Lds L = lds_layout(NT, PRO, QT, nb, K, a.heads, a.smax);
+  h8* xs = (h8*)(lds + L.xs);
+  float* misc = (float*)(lds + L.misc);  // [0,16) wave partials, [16,24) s, [24,32) exps, [32,..) argmax
+  float* bsum = (float*)(lds + L.bsum);
+  float* stage = (float*)(lds + L.stage);
+  float* wts = (float*)(lds + L.wts);
+  int* exps = (int*)(misc + 24);
+
+  // ---- prologue: the activations of nt tokens into MFMA operand order
+  float s_rms[NT];
+  if (PRO == PRO_RMS) {
+    // cpu.go:90-94: ss = sum x^2 (f32); s = f32(1/sqrt(f64(ss/n + eps)))
+    for (int t = 0; t < nt; t++) {
+      const float* xr = a.x + (uint64_t)(a.xrow0 + t0 + t) * a.ldx;
+      float ss = 0;
+      for (uint32_t e = tid; e < K; e += GW) ss += xr[e] * xr[e];
+      ss = wave_sum(ss);
+      if (lane == 0) misc[wave * NT + t] = ss;
+    }
+    __syncthreads();
+    if (tid < nt) {
+      float ss = misc[0 * NT + tid] + misc[1 * NT + tid] + misc[2 * NT + tid] + misc[3 * NT + tid];
+      misc[16 + tid] = (float)(1.0 / sqrt((double)(ss / (float)K + a.eps)));
+    }
+    __syncthreads();
+    for (int t = 0; t < NT; t++) s_rms[t] = t < nt ? misc[16 + t] : 0.f;
+  }
+  if (PRO == PRO_MERGE) {
+    // Chunk weights exp(m_c - M) and 1/sum(exp(m_c - M) l_c) per (token, head).
+    const uint32_t H = a.heads, SM = a.smax;
+    for (uint32_t th = tid; th < (uint32_t)nt * H; th += GW) {
+      uint32_t t = th / H, h = th % H;
+      uint32_t pos = a.state[0] + t0 + t;
+      uint32_t nc = (pos + a.chunk) / a.chunk;
+      const float* mlp = a.ml + ((uint64_t)(t0 + t) * H + h) * SM * 2;
+      float M = -INFINITY;
+      for (uint32_t c = 0; c < nc; c++) M = fmaxf(M, mlp[2 * c]);
+      float l = 0;
+      float* w = wts + (t * H + h) * (SM + 1);
+      for (uint32_t c = 0; c < nc; c++) {
+        float e = expf(mlp[2 * c] - M);
+        w[c] = e;
+        l += e * mlp[2 * c + 1];
+      }
+      w[SM] = 1.f / l;
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < (uint32_t)nt * K; i += GW) {
+      uint32_t t = i / K, e = i % K, h = e / a.hd, dd = e % a.hd;
+      uint32_t pos = a.state[0] + t0 + t;
+      uint32_t nc = (pos + a.chunk) / a.chunk;
+      const float* w = wts + (t * H + h) * (SM + 1);
+      const float* pvp = a.pv + (((uint64_t)(t0 + t) * H + h) * SM) * a.hd + dd;
+      float o = 0;
+      for (uint32_t c = 0; c < nc; c++) o += w[c] * pvp[(uint64_t)c * a.hd];
+      stage[t * K + e] = o * w[SM];
+    }
+    __syncthreads();
+  }
+  auto load8 = [&](int t, uint32_t e) -> f4 {  // 4 activations at e (e % 4 == 0)
+    if (PRO == PRO_MERGE) return *(const f4*)(stage + t * K + e);
+    const float* xr = a.x + (uint64_t)(a.xrow0 + t0 + t) * a.ldx + e;
+    f4 v = *(const f4*)xr;
+    if (PRO == PRO_RMS) {
+      f4 w = *(const f4*)(a.nw + e);
+      for (int i = 0; i < 4; i++) v[i] = __fmul_rn(__fmul_rn(v[i], s_rms[t]), w[i]);  // cpu.go:96
+    }
+    return v;
+  };
+  // largest magnitude per token -> power-of-two scale
+  for (int t = 0; t < nt; t++) {
+    float m = 0;
+    for (uint32_t e = tid * 4; e < K; e += GW * 4) {
+      f4 v = load8(t, e);
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    }
+    m = wave_max(m);
+    if (lane == 0) misc[wave * NT + t] = m;
+  }
+  __syncthreads();
+  if (tid < NT) {
+    int e = 0;
+    if (tid < nt) {
+      float m = fmaxf(fmaxf(misc[tid], misc[NT + tid]), fmaxf(misc[2 * NT + tid], misc[3 * NT + tid]));
+      if (m > 0 && m <= 3.0e38f) {
+        int E;
+        frexpf(m, &E);
+        e = 15 - E;
+      }
+    }
+    exps[tid] = e;
+  }
+  __syncthreads();
+  for (uint32_t it = tid; it < (uint32_t)NT * nb * 4; it += GW) {
+    uint32_t t = it / (nb * 4), rem = it % (nb * 4), b = rem / 4, g = rem % 4;
+    h8 hi = {}, lo = {};
+    if ((int)t < nt) {
+      int ex = exps[t];
+      f4 A = load8(t, b * 32 + 4 * g), C = load8(t, b * 32 + 16 + 4 * g);
+      float v[8] = {A[0], A[2], C[0], C[2], A[1], A[3], C[1], C[3]};
+      for (int i = 0; i < 8; i++) {
+        float s = ldexpf(v[i], ex);
+        _Float16 h = (_Float16)s;
+        hi[i] = h;
+        lo[i] = (_Float16)(s - (float)h);
+      }
+    }
+    xs[(b * 4 + g) * S + 2 * t] = hi;
+    xs[(b * 4 + g) * S + 2 * t + 1] = lo;
+  }
+  if (QT == LLMHIP_Q4_1) {
+    for (uint32_t it = tid; it < (uint32_t)NT * nb; it += GW) {
+      uint32_t t = it / nb, b = it % nb;
+      float sx = 0;
+      if ((int)t < nt) {
+        for (int j = 0; j < 32; j += 4) {
+          f4 v = load8(t, b * 32 + j);
+          sx += v[0] + v[1] + v[2] + v[3];
+        }
+        sx = ldexpf(sx, exps[t]);
+      }
+      bsum[t * nb + b] = sx;
+    }
+  }
+  __syncthreads();
+
+  // ---- main loop: each wave one 16-row tile over its share of the blocks
+  const uint32_t split = a.split, tpw = 4 / split;
+  const uint32_t lt = wave / split, sp = wave % split;
+  const uint32_t tile = blockIdx.x * tpw + lt;
+  const int r = lane & 15, q = lane >> 4;  // B/D column (row in tile), k-group / D row group
+  const int slot = lane & 15;              // A row: token slot
+  float acc0 = 0, acc1 = 0;
+  if (tile < a.tiles) {
+    const uint8_t* qt = a.qs + (uint64_t)tile * 16 * nb * T::QB;
+    const uint8_t* st = a.sc + (uint64_t)tile * 16 * nb * T::SB;
+    auto block = [&](uint32_t b, h8 B, uint32_t dbits, uint32_t mbits) {
+      h8 A = {};
+      if (slot < S) A = xs[(b * 4 + q) * S + slot];
+      f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4{0, 0, 0, 0}, 0, 0, 0);
+      float d = f16_hw(dbits);
+      acc0 += d * (D[0] + D[1]);
+      if (NT > 1) acc1 += d * (D[2] + D[3]);
+      if (QT == LLMHIP_Q4_1) {
+        float m = f16_hw(mbits);
+        if (2 * q < NT) acc0 += m * bsum[(2 * q) * nb + b];
+        if (2 * q + 1 < NT) acc1 += m * bsum[(2 * q + 1) * nb + b];
+      }
+    };
+    for (uint32_t g4 = sp; g4 < a.ng; g4 += split) {
+      if (QT == LLMHIP_Q8_0) {
+        uint4 w01 = *(const uint4*)(qt + g4 * 2048 + lane * 16);
+        uint4 w23 = *(const uint4*)(qt + g4 * 2048 + 1024 + lane * 16);
+        uint2 sv = *(const uint2*)(st + g4 * 128 + r * 8);
+        block(4 * g4 + 0, dq8(w01.x, w01.y), sv.x & 0xffff, 0);
+        block(4 * g4 + 1, dq8(w01.z, w01.w), sv.x >> 16, 0);
+        block(4 * g4 + 2, dq8(w23.x, w23.y), sv.y & 0xffff, 0);
+        block(4 * g4 + 3, dq8(w23.z, w23.w), sv.y >> 16, 0);
+      } else if (QT == LLMHIP_Q4_1) {
+        uint4 w = *(const uint4*)(qt + g4 * 1024 + lane * 16);
+        uint4 sv = *(const uint4*)(st + g4 * 256 + r * 16);
+        block(4 * g4 + 0, dq4<true>(w.x), sv.x & 0xffff, sv.x >> 16);
+        block(4 * g4 + 1, dq4<true>(w.y), sv.y & 0xffff, sv.y >> 16);
+        block(4 * g4 + 2, dq4<true>(w.z), sv.z & 0xffff, sv.z >> 16);
+        block(4 * g4 + 3, dq4<true>(w.w), sv.w & 0xffff, sv.w >> 16);
+      } else {
+        uint4 w = *(const uint4*)(qt + g4 * 1024 + lane * 16);
+        uint2 sv = *(const uint2*)(st + g4 * 128 + r * 8);
+        block(4 * g4 + 0, dq4<false>(w.x), sv.x & 0xffff, 0);
+        block(4 * g4 + 1, dq4<false>(w.y), sv.x >> 16, 0);
+        block(4 * g4 + 2, dq4<false>(w.z), sv.y & 0xffff, 0);
+        block(4 * g4 + 3, dq4<false>(w.w), sv.y >> 16, 0);
+      }
+    }
+    if (a.tail && (a.ng % split) == sp) {
+      const uint32_t ng = a.ng, tail = a.tail;
+      for (uint32_t j = 0; j < tail; j++) {
+        uint32_t b = 4 * ng + j;
+        const uint8_t* s = st + sc_off<QT>(b, r, ng, tail);
+        uint32_t dbits = s[0] | s[1] << 8, mbits = 0;
+        if (QT == LLMHIP_Q4_1) mbits = s[2] | s[3] << 8;
+        const uint8_t* qq = qt + qs_off<QT>(b, lane, ng, tail);
+        if (QT == LLMHIP_Q8_0) {
+          block(b, dq8(*(const uint32_t*)qq, *(const uint32_t*)(qq + 4)), dbits, 0);
+        } else {
+          block(b, dq4<QT == LLMHIP_Q4_1>(*(const uint32_t*)qq), dbits, mbits);
+        }
+      }
+    }
+  }
+  // ---- split-K: partial sums of the waves of a tile, added in a fixed order
+  if (split > 1) {
+    float* part = (float*)(lds + L.part);
+    part[(wave * 64 + lane) * 2] = acc0;
+    part[(wave * 64 + lane) * 2 + 1] = acc1;
+    __syncthreads();
+    if (sp == 0) {
+      for (uint32_t s = 1; s < split; s++) {
+        acc0 += part[((wave + s) * 64 + lane) * 2];
+        acc1 += part[((wave + s) * 64 + lane) * 2 + 1];
+      }
+    }
+  }
+  // ---- epilogue: lane holds rows r of the tile for tokens 2q and 2q+1
+  const bool active = sp == 0 && tile < a.tiles;
+  const uint32_t p = tile * 16 + r;
+  const uint32_t lr = row_of_pos(p, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
+  const bool rvalid = active && lr < a.rows;
+  const int tA = 2 * q, tB = 2 * q + 1;
+  float vA = (tA < nt) ? ldexpf(acc0, -exps[tA]) : 0.f;
+  float vB = (NT > 1 && tB < nt) ? ldexpf(acc1, -exps[tB]) : 0.f;
+  if (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_ARGMAX) {
+    if (rvalid) {
+      if (tA < nt) {
+        float* y = a.y + (uint64_t)(t0 + tA) * a.ldy + lr;
+        *y = EPI == EPI_ACC ? *y + vA : vA;
+      }
+      if (NT > 1 && tB < nt) {
+        float* y = a.y + (uint64_t)(t0 + tB) * a.ldy + lr;
+        *y = EPI == EPI_ACC ? *y + vB : vB;
+      }
+    }
+  }
+  if (EPI == EPI_ARGMAX) {
+    // (max, lowest index) of token 0 over this workgroup's rows; NaN never
+    // wins (cpu.go:389-397).  Rows are disjoint across workgroups.
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    if (rvalid && q == 0 && nt > 0 && vA == vA) {
+      bv = vA;
+      bi = lr;
+    }
+    for (int o = 8; o > 0; o >>= 1) {
+      float ov = __shfl_xor(bv, o);
+      uint32_t oi = __shfl_xor(bi, o);
+      if (oi != 0xffffffffu && (bi == 0xffffffffu || ov > bv || (ov == bv && oi < bi))) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    float* av = misc + 32;
+    uint32_t* ai = (uint32_t*)(misc + 40);
+    if (lane == 0) {
+      av[wave] = bv;
+      ai[wave] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < 4; w++) {
+        if (ai[w] != 0xffffffffu && (bi == 0xffffffffu || av[w] > bv || (av[w] == bv && ai[w] < bi))) {
+          bv = av[w];
+          bi = ai[w];
+        }
+      }
+      a.amax_v[blockIdx.x] = bv;
+      a.amax_i[blockIdx.x] = bi;
+    }
+  }
+  if (EPI == EPI_QKV) {
+    // bias (qwen2), then RoPE of (q, k) pairs with the host table, then
+    // K and V into the cache at pos (kernels_fused.go:47-73; cpu.go:284-303)
+    if (a.bias && rvalid) {
+      float bb = a.bias[lr];
+      vA += bb;
+      vB += bb;
+    }
+    const int pm = a.neox ? 8 : 1;
+    float oA = __shfl_xor(vA, pm), oB = __shfl_xor(vB, pm);
+    if (rvalid) {
+      const uint32_t hd = a.hd, hp = hd / 2;
+      for (int u = 0; u < 2; u++) {
+        int t = u ? tB : tA;
+        if (t >= nt || (u && NT == 1)) continue;
+        float v = u ? vB : vA, o = u ? oB : oA;
+        uint32_t pos = a.state[0] + t0 + t;
+        if (lr < a.nq + a.nk) {
+          uint32_t j = lr < a.nq ? lr : lr - a.nq, w = j % hd;
+          uint32_t i = a.neox ? w % hp : w / 2;
+          bool first = a.neox ? w < hp : (w % 2) == 0;
+          float c = a.cs[((uint64_t)pos * hp + i) * 2], sn = a.cs[((uint64_t)pos * hp + i) * 2 + 1];
+          float x = first ? v : o, z = first ? o : v;
+          float res = first ? __fsub_rn(__fmul_rn(x, c), __fmul_rn(z, sn))    // cpu.go:381
+                            : __fadd_rn(__fmul_rn(x, sn), __fmul_rn(z, c));  // cpu.go:382
+          if (lr < a.nq) a.y[(uint64_t)(t0 + t) * a.nq + lr] = res;
+          else a.kv[(uint64_t)pos * a.kvd + j] = res;
+        } else {
+          a.kv[(uint64_t)a.ctx * a.kvd + (uint64_t)pos * a.kvd + (lr - a.nq - a.nk)] = v;
+        }
+      }
+    }
+  }
+  if (EPI == EPI_GATEUP) {
+    // act = g / (1 + exp(-g)) * u (cpu.go:345); gate row i at lane r, up row i at r+8
+    float uA = __shfl_xor(vA, 8), uB = __shfl_xor(vB, 8);
+    if (active && r < 8) {
+      uint32_t i = 8 * tile + r;
+      if (i < a.ff) {
+        if (tA < nt) a.y[(uint64_t)(t0 + tA) * a.ff + i] = vA / (1.f + expf(-vA)) * uA;
+        if (NT > 1 && tB < nt) a.y[(uint64_t)(t0 + tB) * a.ff + i] = vB / (1.f + expf(-vB)) * uB;
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------- dispatch
+
+template <uint32_t QT, int NT, int PRO, int EPI>
+static int launch_one(const GemvArgs& a, dim3 grid, uint32_t lds, hipStream_t s) {
+  auto k = gemv_kernel<QT, NT, PRO, EPI>;
+  static bool big = false;
+  if (lds > 65536 && !big) {
+    LLM_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    big = true;
+  }
+  hipLaunchKernelGGL(k, grid, dim3(GW), lds, s, a);
+  LLM_HIP(hipGetLastError());
+  return 0;
+}
+
+template <uint32_t QT, int NT>
+static int launch_nt(const GemvArgs& a, int pro, int epi, dim3 grid, uint32_t lds, hipStream_t s) {
+  switch (pro * 8 + epi) {
+    case PRO_PLAIN * 8 + EPI_STORE: return launch_one<QT, NT, PRO_PLAIN, EPI_STORE>(a, grid, lds, s);
+    case PRO_PLAIN * 8 + EPI_ACC: return launch_one<QT, NT, PRO_PLAIN, EPI_ACC>(a, grid, lds, s);
+    case PRO_RMS * 8 + EPI_QKV: return launch_one<QT, NT, PRO_RMS, EPI_QKV>(a, grid, lds, s);
+    case PRO_MERGE * 8 + EPI_ACC: return launch_one<QT, NT, PRO_MERGE, EPI_ACC>(a, grid, lds, s);
+    case PRO_RMS * 8 + EPI_GATEUP: return launch_one<QT, NT, PRO_RMS, EPI_GATEUP>(a, grid, lds, s);
+    case PRO_RMS * 8 + EPI_ARGMAX: return launch_one<QT, NT, PRO_RMS, EPI_ARGMAX>(a, grid, lds, s);
+    case PRO_RMS * 8 + EPI_STORE: return launch_one<QT, NT, PRO_RMS, EPI_STORE>(a, grid, lds, s);
+  }
+  return set_error(LLMHIP_ERR_ARG, "llm: gemv: unsupported prologue/epilogue %d/%d", pro, epi);
+}
+
+template <uint32_t QT>
+int gemv_launch_qt(const GemvArgs& a, int pro, int epi, hipStream_t s) {
+  int nt = a.ntok <= 1 ? 1 : a.ntok <= 2 ? 2 : 4;
+  Lds L = lds_layout(nt, pro, QT, a.nb, a.k, a.heads, a.smax);
+  if (L.total > 160 * 1024)
+    return set_error(LLMHIP_ERR_ARG, "llm: gemv: k=%u needs %u bytes of LDS", a.k, L.total);
+  if (epi == EPI_ARGMAX && a.ntok != 1) return set_error(LLMHIP_ERR_ARG, "llm: gemv: argmax epilogue needs one token");
+  dim3 grid(gemv_groups(a), (a.ntok + nt - 1) / nt);
+  switch (nt) {
+    case 1: return launch_nt<QT, 1>(a, pro, epi, grid, L.total, s);
+    case 2: return launch_nt<QT, 2>(a, pro, epi, grid, L.total, s);
+    default: return launch_nt<QT, 4>(a, pro, epi, grid, L.total, s);
+  }
+}
+
+template <uint32_t QT>
+int repack_launch_qt(const QMat& m, const uint8_t* raw_dev, uint64_t n, uint64_t blk0, uint64_t row_off,
+                     uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1, uint32_t ff, hipStream_t s) {
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(repack_kernel<QT>, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, raw_dev, n, blk0,
+                     row_off, m.qs, m.sc, m.g.nb, m.g.ng, m.g.tail, map, hd, seg0, seg1, ff);
+  LLM_HIP(hipGetLastError());
+  return 0;
+}
+
+template <uint32_t QT>
+int dequant_launch_qt(const QMat& m, float* out, uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1, uint32_t ff,
+                      hipStream_t s) {
+  uint64_t n = m.g.rows * m.g.nb;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(dequant_kernel<QT>, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, m.qs, m.sc,
+                     (uint32_t)m.g.rows, m.g.nb, m.g.ng, m.g.tail, map, hd, seg0, seg1, ff, out);
+  LLM_HIP(hipGetLastError());
+  return 0;
+}
+
+template <uint32_t QT>
+int embed_launch_qt(const QMat& m, const int32_t* tokens, const uint32_t* state, float* x, uint32_t ntok,
+                    hipStream_t s) {
+  hipLaunchKernelGGL(embed_kernel<QT>, dim3(1, ntok), dim3(64), 0, s, m.qs, m.sc, m.g.nb, m.g.ng, m.g.tail, tokens,
+                     state, x);
+  LLM_HIP(hipGetLastError());
+  return 0;
+}
+
+#define LLMHIP_INSTANTIATE(QT)                                                                                   \
+  template int gemv_launch_qt<QT>(const GemvArgs&, int, int, hipStream_t);                                     \
+  template int repack_launch_qt<QT>(const QMat&, const uint8_t*, uint64_t, uint64_t, uint64_t, uint32_t,       \
+                                    uint32_t, uint32_t, uint32_t, uint32_t, hipStream_t);                      \
+  template int dequant_launch_qt<QT>(const QMat&, float*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t,    \
+                                     hipStream_t);                                                             \
+  template int embed_launch_qt<QT>(const QMat&, const int32_t*, const uint32_t*, float*, uint32_t, hipStream_t);
+
+}  // namespace llmhip

@@ -1,0 +1,6 @@
+// Kernels of the quantised matrix path for one weight type.
+#include "gemv_impl.h"
+
+namespace llmhip {
+LLMHIP_INSTANTIATE(LLMHIP_Q4_0)
+}  // namespace llmhip

@@ -1,0 +1,331 @@
+// Host side of the quantised matrices: errors, allocation, staged upload with
+// the repack on the device, dispatch of the typed kernels, and the
+// llmhip_qmat_* / llmhip_device_* entry points.
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "gemv.h"
+
+namespace llmhip {
+
+static thread_local std::string g_err;
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+void clear_error() { g_err.clear(); }
+
+const char* last_error() { return g_err.c_str(); }
+
+int qmat_alloc(QMat* m, int device, uint32_t type, uint64_t rows, uint64_t k) {
+  QType q;
+  if (!qtype_of(type, &q))
+    return set_error(LLMHIP_ERR_TYPE, "llm: ggml type %u has no GPU kernel (Q4_0, Q4_1, Q8_0)", type);
+  if (rows == 0 || k == 0 || k % 32 != 0 || rows > (1u << 31) || k > (1u << 20))
+    return set_error(LLMHIP_ERR_ARG, "llm: a [%llu][%llu] quantised matrix is not supported (k a multiple of 32)",
+                     (unsigned long long)rows, (unsigned long long)k);
+  m->device = device;
+  m->g = make_geom(q, rows, k);
+  LLM_HIP(hipSetDevice(device));
+  uint64_t qb = m->g.qs_bytes(), sb = m->g.sc_bytes();
+  LLM_HIP(hipMalloc(&m->qs, qb));
+  if (hipMalloc(&m->sc, sb) != hipSuccess) {
+    (void)hipFree(m->qs);
+    m->qs = nullptr;
+    return set_error(LLMHIP_ERR_DEVICE, "llm: hipMalloc of %llu bytes failed", (unsigned long long)sb);
+  }
+  // padding rows of the last tile must read as zero weights
+  LLM_HIP(hipMemset(m->qs, 0, qb));
+  LLM_HIP(hipMemset(m->sc, 0, sb));
+  m->bytes = qb + sb;
+  return 0;
+}
+
+void qmat_release(QMat* m) {
+  if (m->qs) (void)hipFree(m->qs);
+  if (m->sc) (void)hipFree(m->sc);
+  m->qs = m->sc = nullptr;
+}
+
+void gemv_bind(GemvArgs* a, const QMat& m) {
+  a->qs = m.qs;
+  a->sc = m.sc;
+  a->rows = (uint32_t)m.g.rows;
+  a->nb = m.g.nb;
+  a->ng = m.g.ng;
+  a->tail = m.g.tail;
+  a->tiles = (uint32_t)m.g.tiles;
+  a->k = (uint32_t)m.g.k;
+  a->map = m.map;
+  a->map_hd = m.map_hd;
+  a->map_seg0 = m.map_seg0;
+  a->map_seg1 = m.map_seg1;
+  a->ff = m.ff;
+  a->split = gemv_pick_split(a->tiles, a->ng);
+}
+
+uint32_t gemv_pick_split(uint32_t tiles, uint32_t ng) {
+  // Enough waves to cover 256 CUs several times over: split the blocks of
+  // a tile over 2 or 4 waves when the matrix has few tiles.
+  if (tiles < 512 && ng >= 4) return 4;
+  if (tiles < 1024 && ng >= 2) return 2;
+  return 1;
+}
+
+uint32_t gemv_groups(const GemvArgs& a) {
+  uint32_t tpw = 4 / a.split;
+  return (a.tiles + tpw - 1) / tpw;
+}
+
+int gemv_launch(const GemvArgs& a, uint32_t qtype, int pro, int epi, hipStream_t s) {
+  if (a.ntok == 0) return 0;
+  if (a.split != 1 && a.split != 2 && a.split != 4) return set_error(LLMHIP_ERR_ARG, "llm: gemv: split %u", a.split);
+  switch (qtype) {
+    case LLMHIP_Q4_0: return gemv_launch_qt<LLMHIP_Q4_0>(a, pro, epi, s);
+    case LLMHIP_Q4_1: return gemv_launch_qt<LLMHIP_Q4_1>(a, pro, epi, s);
+    case LLMHIP_Q8_0: return gemv_launch_qt<LLMHIP_Q8_0>(a, pro, epi, s);
+  }
+  return set_error(LLMHIP_ERR_TYPE, "llm: ggml type %u has no GPU kernel", qtype);
+}
+
+int stager_init(Stager* st, int device, uint64_t cap, hipStream_t s) {
+  st->device = device;
+  st->cap = cap;
+  st->stream = s;
+  LLM_HIP(hipSetDevice(device));
+  for (int i = 0; i < 2; i++) {
+    LLM_HIP(hipHostMalloc((void**)&st->host[i], cap, hipHostMallocDefault));
+    LLM_HIP(hipMalloc((void**)&st->dev[i], cap));
+    LLM_HIP(hipEventCreateWithFlags(&st->done[i], hipEventDisableTiming));
+    LLM_HIP(hipEventRecord(st->done[i], s));
+  }
+  return 0;
+}
+
+void stager_free(Stager* st) {
+  for (int i = 0; i < 2; i++) {
+    if (st->done[i]) (void)hipEventSynchronize(st->done[i]);
+    if (st->host[i]) (void)hipHostFree(st->host[i]);
+    if (st->dev[i]) (void)hipFree(st->dev[i]);
+    if (st->done[i]) (void)hipEventDestroy(st->done[i]);
+    st->host[i] = st->dev[i] = nullptr;
+    st->done[i] = nullptr;
+  }
+}
+
+static int repack_dev(const QMat& m, const uint8_t* raw_dev, uint64_t n, uint64_t blk0, uint64_t row_off,
+                      hipStream_t s) {
+  switch (m.g.q.type) {
+    case LLMHIP_Q4_0:
+      return repack_launch_qt<LLMHIP_Q4_0>(m, raw_dev, n, blk0, row_off, m.map, m.map_hd, m.map_seg0, m.map_seg1,
+                                           m.ff, s);
+    case LLMHIP_Q4_1:
+      return repack_launch_qt<LLMHIP_Q4_1>(m, raw_dev, n, blk0, row_off, m.map, m.map_hd, m.map_seg0, m.map_seg1,
+                                           m.ff, s);
+    case LLMHIP_Q8_0:
+      return repack_launch_qt<LLMHIP_Q8_0>(m, raw_dev, n, blk0, row_off, m.map, m.map_hd, m.map_seg0, m.map_seg1,
+                                           m.ff, s);
+  }
+  return set_error(LLMHIP_ERR_TYPE, "llm: ggml type %u has no GPU kernel", m.g.q.type);
+}
+
+// The reference repacks each block on the host (gpu.go:363-389) and uploads
+// the result; here the raw blocks cross PCIe once and the repack runs on the
+// device, double-buffered so the host copy of piece i+1 overlaps piece i.
+int qmat_upload(Stager* st, const QMat& m, const void* raw, uint64_t nbytes, uint64_t byte_off, uint64_t row_off) {
+  const uint32_t bb = m.g.q.block_bytes;
+  if (nbytes % bb != 0 || byte_off % bb != 0)
+    return set_error(LLMHIP_ERR_ARG, "llm: upload of %llu bytes at %llu is not whole %u-byte blocks",
+                     (unsigned long long)nbytes, (unsigned long long)byte_off, bb);
+  uint64_t blk0 = byte_off / bb, nblk = nbytes / bb;
+  if (row_off * m.g.nb + blk0 + nblk > m.g.rows * m.g.nb)
+    return set_error(LLMHIP_ERR_ARG, "llm: upload past the end of a [%llu][%llu] matrix",
+                     (unsigned long long)m.g.rows, (unsigned long long)m.g.k);
+  const uint8_t* src = (const uint8_t*)raw;
+  uint64_t per = st->cap / bb;
+  LLM_HIP(hipSetDevice(st->device));
+  for (uint64_t i = 0; i < nblk; i += per) {
+    uint64_t n = nblk - i < per ? nblk - i : per;
+    int c = st->cur;
+    st->cur ^= 1;
+    LLM_HIP(hipEventSynchronize(st->done[c]));
+    memcpy(st->host[c], src + i * bb, n * bb);
+    LLM_HIP(hipMemcpyAsync(st->dev[c], st->host[c], n * bb, hipMemcpyHostToDevice, st->stream));
+    LLM_TRY(repack_dev(m, st->dev[c], n, blk0 + i, row_off, st->stream));
+    LLM_HIP(hipEventRecord(st->done[c], st->stream));
+  }
+  return 0;
+}
+
+int qmat_dequant(const QMat& m, float* out, hipStream_t s) {
+  switch (m.g.q.type) {
+    case LLMHIP_Q4_0:
+      return dequant_launch_qt<LLMHIP_Q4_0>(m, out, m.map, m.map_hd, m.map_seg0, m.map_seg1, m.ff, s);
+    case LLMHIP_Q4_1:
+      return dequant_launch_qt<LLMHIP_Q4_1>(m, out, m.map, m.map_hd, m.map_seg0, m.map_seg1, m.ff, s);
+    case LLMHIP_Q8_0:
+      return dequant_launch_qt<LLMHIP_Q8_0>(m, out, m.map, m.map_hd, m.map_seg0, m.map_seg1, m.ff, s);
+  }
+  return set_error(LLMHIP_ERR_TYPE, "llm: ggml type %u has no GPU kernel", m.g.q.type);
+}
+
+int embed_launch(const QMat& m, const int32_t* tokens, const uint32_t* state, float* x, uint32_t ntok,
+                 hipStream_t s) {
+  if (ntok == 0) return 0;
+  switch (m.g.q.type) {
+    case LLMHIP_Q4_0: return embed_launch_qt<LLMHIP_Q4_0>(m, tokens, state, x, ntok, s);
+    case LLMHIP_Q8_0: return embed_launch_qt<LLMHIP_Q8_0>(m, tokens, state, x, ntok, s);
+    case LLMHIP_Q4_1: return embed_launch_qt<LLMHIP_Q4_1>(m, tokens, state, x, ntok, s);
+  }
+  return set_error(LLMHIP_ERR_TYPE, "llm: token_embd.weight must be Q8_0 or Q4_0");
+}
+
+}  // namespace llmhip
+
+using namespace llmhip;
+
+// ------------------------------------------------------------------ C-ABI
+
+struct llmhip_qmat {
+  QMat m;
+  Stager st;
+  hipStream_t stream = nullptr;
+};
+
+extern "C" {
+
+const char* llmhip_last_error(void) { return last_error(); }
+
+int llmhip_device_count(int* n) {
+  clear_error();
+  *n = 0;
+  hipError_t e = hipGetDeviceCount(n);
+  if (e == hipErrorNoDevice) {
+    *n = 0;
+    return 0;
+  }
+  if (e != hipSuccess) return set_error(LLMHIP_ERR_DEVICE, "llm: no GPU: %s", hipGetErrorString(e));
+  return 0;
+}
+
+int llmhip_device_limits(int ordinal, llmhip_limits* out) {
+  clear_error();
+  hipDeviceProp_t p;
+  LLM_HIP(hipGetDeviceProperties(&p, ordinal));
+  out->max_invocations_per_workgroup = (uint32_t)p.maxThreadsPerBlock;
+  out->max_workgroup_storage = (uint32_t)p.sharedMemPerBlock;
+  out->max_workgroups_per_dimension = (uint32_t)p.maxGridSize[0];
+  out->max_storage_buffers = 0xffffffffu;  // no binding slots: kernels take raw pointers
+  out->max_binding_size = p.totalGlobalMem;
+  out->max_buffer_size = p.totalGlobalMem;
+  out->memory_budget = p.totalGlobalMem;
+  return 0;
+}
+
+int llmhip_qmat_create(int ordinal, uint32_t ggml_type, uint64_t rows, uint64_t k, llmhip_qmat** out) {
+  clear_error();
+  *out = nullptr;
+  llmhip_qmat* q = new llmhip_qmat();
+  int rc = qmat_alloc(&q->m, ordinal, ggml_type, rows, k);
+  if (rc == 0 && hipStreamCreateWithFlags(&q->stream, hipStreamNonBlocking) != hipSuccess)
+    rc = set_error(LLMHIP_ERR_DEVICE, "llm: hipStreamCreate failed");
+  if (rc == 0) rc = stager_init(&q->st, ordinal, 4ull << 20, q->stream);
+  if (rc != 0) {
+    stager_free(&q->st);
+    if (q->stream) (void)hipStreamDestroy(q->stream);
+    qmat_release(&q->m);
+    delete q;
+    return rc;
+  }
+  *out = q;
+  return 0;
+}
+
+int llmhip_qmat_upload(llmhip_qmat* q, const void* raw, uint64_t nbytes, uint64_t byte_offset) {
+  clear_error();
+  LLM_TRY(qmat_upload(&q->st, q->m, raw, nbytes, byte_offset, 0));
+  LLM_HIP(hipStreamSynchronize(q->stream));
+  return 0;
+}
+
+int llmhip_qmat_dequant(llmhip_qmat* q, float* out_dev, void* hip_stream) {
+  clear_error();
+  LLM_HIP(hipSetDevice(q->m.device));
+  LLM_HIP(hipStreamSynchronize(q->stream));
+  return qmat_dequant(q->m, out_dev, (hipStream_t)hip_stream);
+}
+
+static int qmat_gemv_args(llmhip_qmat* q, const float* x, float* y, int n, GemvArgs* a) {
+  if (n < 1 || n > 64) return set_error(LLMHIP_ERR_ARG, "llm: gemv of %d tokens (1..64)", n);
+  memset(a, 0, sizeof *a);
+  gemv_bind(a, q->m);
+  a->ntok = (uint32_t)n;
+  a->x = x;
+  a->ldx = a->k;
+  a->y = y;
+  a->ldy = a->rows;
+  return 0;
+}
+
+int llmhip_qmat_gemv(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, int accumulate, void* hip_stream) {
+  clear_error();
+  GemvArgs a;
+  LLM_TRY(qmat_gemv_args(q, x_dev, y_dev, n, &a));
+  LLM_HIP(hipSetDevice(q->m.device));
+  LLM_HIP(hipStreamSynchronize(q->stream));
+  return gemv_launch(a, q->m.g.q.type, PRO_PLAIN, accumulate ? EPI_ACC : EPI_STORE, (hipStream_t)hip_stream);
+}
+
+uint64_t llmhip_qmat_bytes(const llmhip_qmat* q) { return q->m.bytes; }
+uint64_t llmhip_qmat_gguf_bytes(const llmhip_qmat* q) { return q->m.g.gguf_bytes(); }
+
+int llmhip_qmat_bench(llmhip_qmat* const* mats, int count, const float* x_dev, float* y_dev, int n, int iters,
+                      int warmup, void* hip_stream, float* avg_us) {
+  clear_error();
+  if (count < 1 || iters < 1) return set_error(LLMHIP_ERR_ARG, "llm: bench of %d matrices, %d iterations", count, iters);
+  hipStream_t s = (hipStream_t)hip_stream;
+  GemvArgs args[64];
+  if (count > 64) return set_error(LLMHIP_ERR_ARG, "llm: bench of more than 64 matrices");
+  for (int i = 0; i < count; i++) {
+    LLM_TRY(qmat_gemv_args(mats[i], x_dev, y_dev, n, &args[i]));
+    if (mats[i]->m.g.q.type != mats[0]->m.g.q.type || mats[i]->m.g.rows != mats[0]->m.g.rows ||
+        mats[i]->m.g.k != mats[0]->m.g.k)
+      return set_error(LLMHIP_ERR_ARG, "llm: bench matrices differ in shape or type");
+    LLM_HIP(hipStreamSynchronize(mats[i]->stream));
+  }
+  LLM_HIP(hipSetDevice(mats[0]->m.device));
+  const uint32_t t = mats[0]->m.g.q.type;
+  for (int i = 0; i < warmup; i++) LLM_TRY(gemv_launch(args[i % count], t, PRO_PLAIN, EPI_STORE, s));
+  hipEvent_t e0, e1;
+  LLM_HIP(hipEventCreate(&e0));
+  LLM_HIP(hipEventCreate(&e1));
+  LLM_HIP(hipEventRecord(e0, s));
+  for (int i = 0; i < iters; i++) LLM_TRY(gemv_launch(args[i % count], t, PRO_PLAIN, EPI_STORE, s));
+  LLM_HIP(hipEventRecord(e1, s));
+  LLM_HIP(hipEventSynchronize(e1));
+  float ms = 0;
+  LLM_HIP(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *avg_us = ms * 1000.f / (float)iters;
+  return 0;
+}
+
+void llmhip_qmat_free(llmhip_qmat* q) {
+  if (!q) return;
+  (void)hipSetDevice(q->m.device);
+  stager_free(&q->st);
+  if (q->stream) (void)hipStreamDestroy(q->stream);
+  qmat_release(&q->m);
+  delete q;
+}
+
+}  // extern "C"

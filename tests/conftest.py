@@ -1,0 +1,30 @@
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs through libllmhip.so on cuda:0)")
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """The GPU tests run only where a GPU exists; there they must not be skipped."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("a gpu-marked test ran without a GPU (run `pytest -m 'not gpu'` on CPU machines)")
+    from llm_amd import _lib
+    _lib.lib()  # raises if libllmhip.so was not built
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="session")
+def oracle():
+    from oracle import cpuref
+    cpuref.lib()
+    return cpuref
