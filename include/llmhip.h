@@ -112,6 +112,133 @@ LLMHIP_API int llmhip_qmat_bench(llmhip_qmat* const* mats, int count, const floa
                       int warmup, void* hip_stream, float* avg_us);
 LLMHIP_API void llmhip_qmat_free(llmhip_qmat* m);
 
+/* -------------------------------------------------------------- models */
+
+/* Config, config.go:11-23 (what ConfigFrom reads from the GGUF metadata). */
+typedef struct llmhip_config {
+  int32_t layers, embd, ff, heads, kv_heads, head_dim, vocab, ctx;
+  float rope_base, eps;
+  int32_t arch; /* 0 llama (rope NORM), 1 qwen2 (rope NEOX, QKV biases) */
+  int32_t rope_neox, bias, tied_output;
+} llmhip_config;
+
+/* Stats, gpu.go:56-60: submits are graph launches / synchronising calls,
+ * dispatches are kernel launches (graph nodes replayed). */
+typedef struct llmhip_stats {
+  int64_t submits, dispatches, tokens;
+} llmhip_stats;
+
+typedef struct llmhip_model llmhip_model;
+
+/* The allocating half of NewGPU (gpu.go:465-541): ctx is clamped to cfg->ctx
+ * when <= 0 or larger (gpu.go:470-472); activations, the f32 KV cache and the
+ * RoPE table (cos and sin of pos * base^(-2i/hd) in double, gpu.go:524-534)
+ * are allocated against lim->memory_budget (lim NULL: the device's limits).
+ * prefill_batch is the prompt chunk (PrefillBatch, gpu.go:165; 0 = 64). */
+LLMHIP_API int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_config* cfg, int ctx,
+                                   int prefill_batch, llmhip_model** out);
+/* Declare a tensor of the GGUF file (name, ggml type, dims with dims[0] the
+ * contiguous one).  Every tensor the model needs must be declared before the
+ * first upload; names the model does not use are accepted and ignored. */
+LLMHIP_API int llmhip_model_tensor(llmhip_model* m, const char* name, uint32_t ggml_type, const uint64_t* dims,
+                                   uint32_t ndims);
+/* Stream raw tensor bytes [byte_offset, byte_offset+nbytes) of a declared
+ * tensor (whole blocks for quantised types): streamMat / loadF32 /
+ * loadGroup of gpu.go:297-407 and fused.go:108-190, with the repack, the
+ * QKV and gate/up concatenation and the NEOX pairing done on the device. */
+LLMHIP_API int llmhip_model_upload(llmhip_model* m, const char* name, const void* raw, uint64_t nbytes,
+                                   uint64_t byte_offset);
+/* Check that every needed tensor arrived in full ("llm: missing tensor"). */
+LLMHIP_API int llmhip_model_finalize(llmhip_model* m);
+/* Run a prompt from position 0 (prefill, gpu.go:853-900) in chunks of
+ * prefill_batch tokens; optionally copy out the last token's logits (vocab
+ * floats, PrefillLogits gpu.go:904-927) and the greedy token it samples.
+ * Requires 1 <= n <= ctx and ids in [0, vocab). */
+LLMHIP_API int llmhip_model_prefill(llmhip_model* m, const int32_t* ids, int n, float* logits, int32_t* first);
+/* cnt greedy decode steps (one hipGraph launch each; gpu.go:987-1009): each
+ * embeds the last sampled token, runs the layers and the head and samples on
+ * the GPU.  out receives the cnt sampled ids.  Requires pos + cnt <= ctx. */
+LLMHIP_API int llmhip_model_decode(llmhip_model* m, int cnt, int32_t* out);
+/* The first n 4-byte words of a named buffer as float32 (Peek, gpu.go:1018-1043):
+ * x, q, gate (the SwiGLU activations), logits, state, tokens, outb, and
+ * kvblk.N. (layer N's cache [2][ctx][kvd]). */
+LLMHIP_API int llmhip_model_peek(llmhip_model* m, const char* name, float* out, uint64_t n);
+LLMHIP_API uint64_t llmhip_model_memory_used(const llmhip_model* m);
+LLMHIP_API int llmhip_model_stats(const llmhip_model* m, llmhip_stats* out);
+LLMHIP_API int llmhip_model_config(const llmhip_model* m, llmhip_config* out, int* ctx);
+/* Run only the first `layers` layers (no head, no sampling; Layers, gpu.go:143-146). 0 = all. */
+LLMHIP_API int llmhip_model_set_layers(llmhip_model* m, int layers);
+/* Leave kernel classes out of every pass, comma-separated (Skip, gpu.go:769-784):
+ * embed, k1, k2, k3, k4, k5, head, argmax, adv, or all.  Output is garbage then. */
+LLMHIP_API int llmhip_model_set_skip(llmhip_model* m, const char* classes);
+/* Average device microseconds of one launch of a kernel of the decode step,
+ * launched `iters` times back-to-back on the model's stream between hipEvents,
+ * with the arguments it has in the graph: "head", or "k1".."k5" of layer 0.
+ * bytes receives its algorithmic bytes (GGUF weight bytes + KV bytes read). */
+LLMHIP_API int llmhip_model_bench_kernel(llmhip_model* m, const char* kernel, int iters, float* avg_us,
+                                         uint64_t* bytes);
+LLMHIP_API void llmhip_model_free(llmhip_model* m);
+
+/* ====================================================================
+ * Layer 2: the reference's host package in C++ (llm_*).
+ * ==================================================================== */
+
+/* Which error a GGUF parse returned (gguf/gguf.go:29-34 plus I/O). */
+enum { LLM_GGUF_OK = 0, LLM_GGUF_MAGIC = 1, LLM_GGUF_VERSION = 2, LLM_GGUF_BOUND = 3, LLM_GGUF_FORMAT = 4,
+       LLM_GGUF_IO = 5 };
+
+typedef struct llm_gguf llm_gguf;
+
+/* gguf.Parse (gguf/gguf.go:292-407) of a file or of bytes in memory; *kind is
+ * one of LLM_GGUF_*.  Reads the header only, with the reference's bounds. */
+LLMHIP_API int llm_gguf_parse_file(const char* path, llm_gguf** out, int* kind);
+LLMHIP_API int llm_gguf_parse_bytes(const void* data, uint64_t size, llm_gguf** out, int* kind);
+LLMHIP_API void llm_gguf_free(llm_gguf* g);
+LLMHIP_API int llm_gguf_info(const llm_gguf* g, uint64_t* ntensors, uint64_t* nkv, uint64_t* data_offset,
+                             uint64_t* alignment, uint32_t* version);
+LLMHIP_API int llm_gguf_tensor_info(const llm_gguf* g, uint64_t i, char* name, uint64_t name_cap, uint32_t* type,
+                                    uint32_t* ndims, uint64_t* dims, uint64_t* offset, uint64_t* size);
+LLMHIP_API int llm_gguf_find_tensor(const llm_gguf* g, const char* name, uint64_t* index);
+/* File.Uint / Float / Str (gguf/gguf.go:410-432): 1 when present with that kind. */
+LLMHIP_API int llm_gguf_meta_uint(const llm_gguf* g, const char* key, uint64_t* v);
+LLMHIP_API int llm_gguf_meta_float(const llm_gguf* g, const char* key, double* v);
+LLMHIP_API int llm_gguf_meta_str(const llm_gguf* g, const char* key, char* buf, uint64_t cap);
+/* ConfigFrom, config.go:29-73. */
+LLMHIP_API int llm_config_from(const llm_gguf* g, llmhip_config* out);
+
+/* Package tunables: DecodeBatch (gpu.go:1052, bounded by MaxBatch 16) and
+ * PrefillBatch (gpu.go:165), read by the next llm_new_gpu / generate. */
+LLMHIP_API int llm_set_decode_batch(int n);
+LLMHIP_API int llm_set_prefill_batch(int n);
+
+/* Timing, gpu.go:930-939 (nanoseconds).  record_ns stays 0: the passes are
+ * recorded once, as hipGraphs, not per submit. */
+typedef struct llm_timing {
+  int64_t prefill_ns, decode_ns;
+  int64_t prompt_tokens, generated, submits, dispatches;
+  int64_t record_ns, submit_ns;
+} llm_timing;
+
+/* emit(tok, user) returns nonzero to continue (the emit func of Generate). */
+typedef int (*llm_emit_fn)(int32_t tok, void* user);
+
+typedef struct llm_gpu llm_gpu;
+
+/* NewGPU (gpu.go:465-764): parse the file at path, ConfigFrom, create the
+ * model and stream every tensor in 4 MiB whole-block pieces. lim NULL: the
+ * device's limits. */
+LLMHIP_API int llm_new_gpu(int ordinal, const llmhip_limits* lim, const char* path, int ctx, llm_gpu** out);
+/* Generate (gpu.go:946-1014). */
+LLMHIP_API int llm_gpu_generate(llm_gpu* g, const int32_t* prompt, int n_prompt, int n, int32_t eos, llm_emit_fn emit,
+                                void* user, llm_timing* tm);
+/* PrefillLogits (gpu.go:904-927): vocab floats of the last prompt token. */
+LLMHIP_API int llm_gpu_prefill_logits(llm_gpu* g, const int32_t* prompt, int n_prompt, float* logits);
+LLMHIP_API int llm_gpu_peek(llm_gpu* g, const char* name, float* out, uint64_t n);
+LLMHIP_API int llm_gpu_config(const llm_gpu* g, llmhip_config* out, int* ctx);
+/* The device-layer model (MemoryUsed, Stats, Layers, Skip, bench). */
+LLMHIP_API llmhip_model* llm_gpu_model(llm_gpu* g);
+LLMHIP_API void llm_gpu_free(llm_gpu* g);
+
 #ifdef __cplusplus
 }
 #endif

@@ -30,9 +30,31 @@ class Limits(ctypes.Structure):
                 ("memory_budget", ctypes.c_uint64)]
 
 
+class Config(ctypes.Structure):
+    """Config, config.go:11-23."""
+    _fields_ = [(n, ctypes.c_int32) for n in
+                ("layers", "embd", "ff", "heads", "kv_heads", "head_dim", "vocab", "ctx")] + \
+               [("rope_base", ctypes.c_float), ("eps", ctypes.c_float)] + \
+               [(n, ctypes.c_int32) for n in ("arch", "rope_neox", "bias", "tied_output")]
+
+
+class Stats(ctypes.Structure):
+    """Stats, gpu.go:56-60."""
+    _fields_ = [("submits", ctypes.c_int64), ("dispatches", ctypes.c_int64), ("tokens", ctypes.c_int64)]
+
+
+class Timing(ctypes.Structure):
+    """Timing, gpu.go:930-939, in nanoseconds."""
+    _fields_ = [(n, ctypes.c_int64) for n in ("prefill_ns", "decode_ns", "prompt_tokens", "generated", "submits",
+                                                "dispatches", "record_ns", "submit_ns")]
+
+
+EMIT = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_int32, ctypes.c_void_p)
+
 _lib = None
 
 P, I, U32, U64, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float
+PU64 = ctypes.POINTER(ctypes.c_uint64)
 
 # (name, restype, argtypes) of every exported function
 SIGNATURES = [
@@ -47,6 +69,40 @@ SIGNATURES = [
     ("llmhip_qmat_gguf_bytes", U64, [P]),
     ("llmhip_qmat_bench", I, [ctypes.POINTER(P), I, P, P, I, I, I, P, ctypes.POINTER(F)]),
     ("llmhip_qmat_free", None, [P]),
+    ("llmhip_model_create", I, [I, ctypes.POINTER(Limits), ctypes.POINTER(Config), I, I, ctypes.POINTER(P)]),
+    ("llmhip_model_tensor", I, [P, ctypes.c_char_p, U32, PU64, U32]),
+    ("llmhip_model_upload", I, [P, ctypes.c_char_p, P, U64, U64]),
+    ("llmhip_model_finalize", I, [P]),
+    ("llmhip_model_prefill", I, [P, P, I, P, P]),
+    ("llmhip_model_decode", I, [P, I, P]),
+    ("llmhip_model_peek", I, [P, ctypes.c_char_p, P, U64]),
+    ("llmhip_model_memory_used", U64, [P]),
+    ("llmhip_model_stats", I, [P, ctypes.POINTER(Stats)]),
+    ("llmhip_model_config", I, [P, ctypes.POINTER(Config), ctypes.POINTER(I)]),
+    ("llmhip_model_set_layers", I, [P, I]),
+    ("llmhip_model_set_skip", I, [P, ctypes.c_char_p]),
+    ("llmhip_model_bench_kernel", I, [P, ctypes.c_char_p, I, ctypes.POINTER(F), PU64]),
+    ("llmhip_model_free", None, [P]),
+    ("llm_gguf_parse_file", I, [ctypes.c_char_p, ctypes.POINTER(P), ctypes.POINTER(I)]),
+    ("llm_gguf_parse_bytes", I, [P, U64, ctypes.POINTER(P), ctypes.POINTER(I)]),
+    ("llm_gguf_free", None, [P]),
+    ("llm_gguf_info", I, [P, PU64, PU64, PU64, PU64, ctypes.POINTER(U32)]),
+    ("llm_gguf_tensor_info", I, [P, U64, ctypes.c_char_p, U64, ctypes.POINTER(U32), ctypes.POINTER(U32), PU64, PU64,
+                                 PU64]),
+    ("llm_gguf_find_tensor", I, [P, ctypes.c_char_p, PU64]),
+    ("llm_gguf_meta_uint", I, [P, ctypes.c_char_p, PU64]),
+    ("llm_gguf_meta_float", I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    ("llm_gguf_meta_str", I, [P, ctypes.c_char_p, ctypes.c_char_p, U64]),
+    ("llm_config_from", I, [P, ctypes.POINTER(Config)]),
+    ("llm_set_decode_batch", I, [I]),
+    ("llm_set_prefill_batch", I, [I]),
+    ("llm_new_gpu", I, [I, ctypes.POINTER(Limits), ctypes.c_char_p, I, ctypes.POINTER(P)]),
+    ("llm_gpu_generate", I, [P, P, I, I, ctypes.c_int32, EMIT, P, ctypes.POINTER(Timing)]),
+    ("llm_gpu_prefill_logits", I, [P, P, I, P]),
+    ("llm_gpu_peek", I, [P, ctypes.c_char_p, P, U64]),
+    ("llm_gpu_config", I, [P, ctypes.POINTER(Config), ctypes.POINTER(I)]),
+    ("llm_gpu_model", P, [P]),
+    ("llm_gpu_free", None, [P]),
 ]
 
 

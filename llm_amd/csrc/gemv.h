@@ -37,7 +37,8 @@ enum Epilogue : int {
   EPI_ACC = 1,     // y[t*ldy + row] += v           (residual add, K3 / K5)
   EPI_QKV = 2,     // + bias, RoPE on pairs, q out, K/V appended to the cache (K1)
   EPI_GATEUP = 3,  // act[t*ff + i] = silu(gate_i) * up_i                   (K4)
-  EPI_ARGMAX = 4   // STORE, and each workgroup's (max, index) of its rows    (head)
+  EPI_ARGMAX = 4,  // STORE, and each workgroup's (max, index) of its rows    (head)
+  EPI_SWIGLU = 5   // y[t*ldy + row] = silu(aux[t*ldy + row]) * v  (up, gate stored apart)
 };
 
 struct GemvArgs {
@@ -46,6 +47,7 @@ struct GemvArgs {
   const uint8_t* sc;
   uint32_t rows, nb, ng, tail, tiles, k;
   uint32_t map, map_hd, map_seg0, map_seg1;  // RowMap; NEOX applies to rows [seg0, seg1)
+  uint32_t row_base;                         // QKV: first row of this matrix in [q; k; v]
   uint32_t ntok;                             // tokens in the launch
   uint32_t split;                            // waves sharing one tile (split-K): 1, 2 or 4
   // prologue
@@ -69,6 +71,7 @@ struct GemvArgs {
   uint32_t ff;
   float* amax_v;  // EPI_ARGMAX: per-workgroup partials
   uint32_t* amax_i;
+  const float* aux;  // EPI_SWIGLU: the gate values
 };
 
 // Bytes of LDS a launch needs, and whether the shape is supported.

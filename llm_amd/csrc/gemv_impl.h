@@ -501,6 +501,21 @@ __global__ __launch_bounds__(GW) void gemv_kernel(GemvArgs a) {
   const int tA = 2 * q, tB = 2 * q + 1;
   float vA = (tA < nt) ? ldexpf(acc0, -exps[tA]) : 0.f;
   float vB = (NT > 1 && tB < nt) ? ldexpf(acc1, -exps[tB]) : 0.f;
+  if (EPI == EPI_SWIGLU) {
+    // act = g / (1 + exp(-g)) * u (cpu.go:345) with g from the gate's own launch
+    if (rvalid) {
+      if (tA < nt) {
+        uint64_t o = (uint64_t)(t0 + tA) * a.ldy + lr;
+        float gg = a.aux[o];
+        a.y[o] = gg / (1.f + expf(-gg)) * vA;
+      }
+      if (NT > 1 && tB < nt) {
+        uint64_t o = (uint64_t)(t0 + tB) * a.ldy + lr;
+        float gg = a.aux[o];
+        a.y[o] = gg / (1.f + expf(-gg)) * vB;
+      }
+    }
+  }
   if (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_ARGMAX) {
     if (rvalid) {
       if (tA < nt) {
@@ -550,9 +565,11 @@ __global__ __launch_bounds__(GW) void gemv_kernel(GemvArgs a) {
   }
   if (EPI == EPI_QKV) {
     // bias (qwen2), then RoPE of (q, k) pairs with the host table, then
-    // K and V into the cache at pos (kernels_fused.go:47-73; cpu.go:284-303)
+    // K and V into the cache at pos (kernels_fused.go:47-73; cpu.go:284-303).
+    // lf is the row in [q; k; v]; a launch may cover one of the three.
+    const uint32_t lf = a.row_base + lr;
     if (a.bias && rvalid) {
-      float bb = a.bias[lr];
+      float bb = a.bias[lf];
       vA += bb;
       vB += bb;
     }
@@ -565,18 +582,18 @@ __global__ __launch_bounds__(GW) void gemv_kernel(GemvArgs a) {
         if (t >= nt || (u && NT == 1)) continue;
         float v = u ? vB : vA, o = u ? oB : oA;
         uint32_t pos = a.state[0] + t0 + t;
-        if (lr < a.nq + a.nk) {
-          uint32_t j = lr < a.nq ? lr : lr - a.nq, w = j % hd;
+        if (lf < a.nq + a.nk) {
+          uint32_t j = lf < a.nq ? lf : lf - a.nq, w = j % hd;
           uint32_t i = a.neox ? w % hp : w / 2;
           bool first = a.neox ? w < hp : (w % 2) == 0;
           float c = a.cs[((uint64_t)pos * hp + i) * 2], sn = a.cs[((uint64_t)pos * hp + i) * 2 + 1];
           float x = first ? v : o, z = first ? o : v;
           float res = first ? __fsub_rn(__fmul_rn(x, c), __fmul_rn(z, sn))    // cpu.go:381
                             : __fadd_rn(__fmul_rn(x, sn), __fmul_rn(z, c));  // cpu.go:382
-          if (lr < a.nq) a.y[(uint64_t)(t0 + t) * a.nq + lr] = res;
+          if (lf < a.nq) a.y[(uint64_t)(t0 + t) * a.nq + lf] = res;
           else a.kv[(uint64_t)pos * a.kvd + j] = res;
         } else {
-          a.kv[(uint64_t)a.ctx * a.kvd + (uint64_t)pos * a.kvd + (lr - a.nq - a.nk)] = v;
+          a.kv[(uint64_t)a.ctx * a.kvd + (uint64_t)pos * a.kvd + (lf - a.nq - a.nk)] = v;
         }
       }
     }
@@ -619,6 +636,7 @@ static int launch_nt(const GemvArgs& a, int pro, int epi, dim3 grid, uint32_t ld
     case PRO_RMS * 8 + EPI_GATEUP: return launch_one<QT, NT, PRO_RMS, EPI_GATEUP>(a, grid, lds, s);
     case PRO_RMS * 8 + EPI_ARGMAX: return launch_one<QT, NT, PRO_RMS, EPI_ARGMAX>(a, grid, lds, s);
     case PRO_RMS * 8 + EPI_STORE: return launch_one<QT, NT, PRO_RMS, EPI_STORE>(a, grid, lds, s);
+    case PRO_RMS * 8 + EPI_SWIGLU: return launch_one<QT, NT, PRO_RMS, EPI_SWIGLU>(a, grid, lds, s);
   }
   return set_error(LLMHIP_ERR_ARG, "llm: gemv: unsupported prologue/epilogue %d/%d", pro, epi);
 }

@@ -1,0 +1,160 @@
+// The non-matrix kernels of the forward pass: attention over the f32 KV cache
+// in chunks of positions (flash-decoding partials, merged by the O-projection
+// prologue), the final argmax reduction, and the state advance.
+#include "layer.h"
+
+namespace llmhip {
+
+// One workgroup per (chunk of CH positions, KV head, token): the GQ query heads
+// that share the KV head read its keys and values once (the reference's K2
+// reads them once per query head, kernels_fused.go:82-146).  Writes the
+// chunk's softmax statistics (max m, sum l of exp(s - m)) and sum_p e_p v_p.
+// A chunk wholly past the causal bound writes nothing: the merge never reads it.
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const uint32_t c = blockIdx.x, g = blockIdx.y, t = blockIdx.z;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t HD = a.hd, GQ = a.heads / a.kv_heads, CH = a.chunk;
+  const uint32_t pos = a.state[0] + t, n = pos + 1;
+  const uint32_t p0 = c * CH;
+  if (p0 >= n) return;
+  const uint32_t L = min(CH, n - p0);
+  const uint32_t KS = HD + 1;  // padded row: lanes reading different rows hit different banks
+  float* qs = sm;               // [GQ][HD]
+  float* ks = qs + GQ * HD;     // [CH][HD+1]
+  float* vs = ks + CH * KS;     // [CH][HD]
+  float* sc = vs + CH * HD;     // [GQ][CH]
+  const float* qg = a.q + (uint64_t)t * a.heads * HD + (uint64_t)g * GQ * HD;
+  for (uint32_t i = tid; i < GQ * HD; i += blockDim.x) qs[i] = qg[i];
+  const float* kb = a.kv + (uint64_t)p0 * a.kvd + g * HD;
+  const float* vb = a.kv + (uint64_t)a.ctx * a.kvd + (uint64_t)p0 * a.kvd + g * HD;
+  for (uint32_t i = tid; i < L * HD; i += blockDim.x) {
+    uint32_t p = i / HD, d = i % HD;
+    ks[p * KS + d] = kb[(uint64_t)p * a.kvd + d];
+    vs[p * HD + d] = vb[(uint64_t)p * a.kvd + d];
+  }
+  __syncthreads();
+  // scores: s = (q . k) * scale, the dot product in index order (cpu.go:312-316)
+  for (uint32_t i = tid; i < GQ * L; i += blockDim.x) {
+    uint32_t h = i / L, p = i % L;
+    const float* qq = qs + h * HD;
+    const float* kk = ks + p * KS;
+    float s = 0;
+    for (uint32_t d = 0; d < HD; d++) s += qq[d] * kk[d];
+    sc[h * CH + p] = s * a.scale;
+  }
+  __syncthreads();
+  // per head: m = max, e = exp(s - m), l = sum e (one wave per head)
+  for (uint32_t h = wave; h < GQ; h += 4) {
+    float m = -INFINITY;
+    for (uint32_t p = lane; p < L; p += 64) m = fmaxf(m, sc[h * CH + p]);
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    float l = 0;
+    for (uint32_t p = lane; p < L; p += 64) {
+      float e = expf(sc[h * CH + p] - m);
+      sc[h * CH + p] = e;
+      l += e;
+    }
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+    if (lane == 0) {
+      float* mlp = a.ml + (((uint64_t)t * a.heads + g * GQ + h) * a.smax + c) * 2;
+      mlp[0] = m;
+      mlp[1] = l;
+    }
+  }
+  __syncthreads();
+  // o = sum_p e_p v_p
+  for (uint32_t i = tid; i < GQ * HD; i += blockDim.x) {
+    uint32_t h = i / HD, d = i % HD;
+    const float* e = sc + h * CH;
+    float o = 0;
+    for (uint32_t p = 0; p < L; p++) o += e[p] * vs[p * HD + d];
+    a.pv[(((uint64_t)t * a.heads + g * GQ + h) * a.smax + c) * HD + d] = o;
+  }
+}
+
+uint32_t attn_lds_bytes(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t chunk) {
+  uint32_t gq = heads / kv_heads;
+  return 4 * (gq * hd + chunk * (hd + 1) + chunk * hd + gq * chunk);
+}
+
+int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s) {
+  if (ntok == 0) return 0;
+  uint32_t lds = attn_lds_bytes(a.heads, a.kv_heads, a.hd, a.chunk);
+  hipLaunchKernelGGL(attn_kernel, dim3(a.smax, a.kv_heads, ntok), dim3(256), lds, s, a);
+  LLM_HIP(hipGetLastError());
+  return 0;
+}
+
+// Greedy sampling (cpu.go:389-397): the lowest index of the largest logit,
+// NaN never wins, and a NaN logit 0 is never displaced.  Combines the
+// per-workgroup partials of the head's matvec, writes the token to
+// tokens[step + adv] and out[0], then advances (pos, step) by adv.
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
+                                                     uint32_t n, const float* __restrict__ logits,
+                                                     int32_t* __restrict__ tokens, int32_t* __restrict__ outb,
+                                                     uint32_t* __restrict__ state, uint32_t adv) {
+  __shared__ float sv[4];
+  __shared__ uint32_t si[4];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float bv = -INFINITY;
+  uint32_t bi = 0xffffffffu;
+  for (uint32_t i = tid; i < n; i += 256) {
+    float v = pv[i];
+    uint32_t ix = pi[i];
+    if (ix != 0xffffffffu && (bi == 0xffffffffu || v > bv || (v == bv && ix < bi))) {
+      bv = v;
+      bi = ix;
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    float ov = __shfl_xor(bv, o);
+    uint32_t oi = __shfl_xor(bi, o);
+    if (oi != 0xffffffffu && (bi == 0xffffffffu || ov > bv || (ov == bv && oi < bi))) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; w++)
+      if (si[w] != 0xffffffffu && (bi == 0xffffffffu || sv[w] > bv || (sv[w] == bv && si[w] < bi))) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    float l0 = logits[0];
+    if (bi == 0xffffffffu || l0 != l0) bi = 0;
+    uint32_t step = state[1];
+    tokens[step + adv] = (int32_t)bi;
+    outb[0] = (int32_t)bi;
+    state[0] += adv;
+    state[1] = step + adv;
+  }
+}
+
+int argmax_launch(const float* pv, const uint32_t* pi, uint32_t n, const float* logits, int32_t* tokens,
+                  int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s) {
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, s, pv, pi, n, logits, tokens, outb, state, adv);
+  LLM_HIP(hipGetLastError());
+  return 0;
+}
+
+// state += n (kernels.go:407-415)
+__global__ void advance_kernel(uint32_t* state, uint32_t n) {
+  if (threadIdx.x == 0) {
+    state[0] += n;
+    state[1] += n;
+  }
+}
+
+int advance_launch(uint32_t* state, uint32_t n, hipStream_t s) {
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, s, state, n);
+  LLM_HIP(hipGetLastError());
+  return 0;
+}
+
+}  // namespace llmhip

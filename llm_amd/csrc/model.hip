@@ -1,0 +1,833 @@
+// The model: device buffers under a memory budget, the weights in fused
+// groups, and the forward pass recorded once into hipGraphs (one decode step,
+// one prefill chunk per chunk length).  Every kernel reads the position from
+// the device-side state, so a graph replays at any position.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "gemv.h"
+#include "layer.h"
+
+namespace llmhip {
+
+struct TensorInfo {
+  uint32_t type = 0;
+  std::vector<uint64_t> dims;
+  uint64_t size = 0, received = 0;
+  bool used = false;
+};
+
+struct Layer {
+  QMat qkv[3];
+  uint32_t qkv_type[3] = {0, 0, 0}, qkv_base[3] = {0, 0, 0};
+  int nqkv = 0;
+  QMat o;
+  QMat gu[2];
+  int ngu = 0;
+  QMat down;
+  float* attn_norm = nullptr;
+  float* ffn_norm = nullptr;
+  float* bias = nullptr;  // [q; k; v] biases (qwen2)
+  float* kv = nullptr;    // [2][ctx][kvd]
+};
+
+struct Model {
+  int device = 0;
+  llmhip_limits lim{};
+  llmhip_config cfg{};
+  uint32_t ctx = 0, pm = 64, chunk = 64, smax = 0, kvd = 0;
+  uint64_t used = 0;
+  std::vector<void*> allocs;
+  hipStream_t stream = nullptr;
+  Stager st;
+  float *x = nullptr, *q = nullptr, *act = nullptr, *gbuf = nullptr, *logits = nullptr, *pv = nullptr,
+        *ml = nullptr, *amax_v = nullptr, *cs = nullptr;
+  uint32_t *amax_i = nullptr, *state = nullptr;
+  int32_t *tokens = nullptr, *outb = nullptr;
+  int32_t* host = nullptr;  // pinned: prompt ids in, sampled ids out
+  uint32_t host_cap = 0;
+  QMat embd, out;
+  bool tied = false;
+  float* out_norm = nullptr;
+  std::vector<Layer> layers;
+  std::map<std::string, TensorInfo> tensors;
+  bool allocated = false, finalized = false;
+  hipGraphExec_t decode_exec = nullptr;
+  std::map<uint32_t, hipGraphExec_t> chunk_exec;  // key: 2*m + last
+  std::map<uint32_t, uint32_t> graph_nodes;       // dispatches per graph key (decode: 1)
+  llmhip_stats stats{};
+  int layers_limit = 0;
+  std::set<std::string> skip;
+  uint32_t pos = 0;  // host mirror of state[0] (== state[1])
+  bool prompted = false;
+  uint32_t dispatches = 0;  // counter while recording
+};
+
+static int dalloc(Model& m, void** p, uint64_t bytes) {
+  bytes = (bytes + 255) & ~255ull;
+  if (m.used + bytes > m.lim.memory_budget)
+    return set_error(LLMHIP_ERR_BUDGET,
+                     "llm: the model needs more GPU memory than the %llu bytes granted (run with a larger budget)",
+                     (unsigned long long)m.lim.memory_budget);
+  LLM_HIP(hipMalloc(p, bytes));
+  LLM_HIP(hipMemset(*p, 0, bytes));
+  m.allocs.push_back(*p);
+  m.used += bytes;
+  return 0;
+}
+
+template <class T>
+static int dalloc_n(Model& m, T** p, uint64_t n) {
+  return dalloc(m, (void**)p, n * sizeof(T));
+}
+
+static int qalloc(Model& m, QMat* q, uint32_t type, uint64_t rows, uint64_t k) {
+  QType qt;
+  if (!qtype_of(type, &qt))
+    return set_error(LLMHIP_ERR_TYPE, "llm: a tensor has ggml type %u, which has no GPU kernel yet (Q4_0, Q4_1, Q8_0)",
+                     type);
+  Geom g = make_geom(qt, rows, k);
+  uint64_t bytes = g.qs_bytes() + g.sc_bytes();
+  if (m.used + bytes > m.lim.memory_budget)
+    return set_error(LLMHIP_ERR_BUDGET,
+                     "llm: the model needs more GPU memory than the %llu bytes granted (run with a larger budget)",
+                     (unsigned long long)m.lim.memory_budget);
+  LLM_TRY(qmat_alloc(q, m.device, type, rows, k));
+  m.used += q->bytes;
+  return 0;
+}
+
+static void destroy_graphs(Model& m) {
+  if (m.decode_exec) (void)hipGraphExecDestroy(m.decode_exec);
+  m.decode_exec = nullptr;
+  for (auto& kv : m.chunk_exec) (void)hipGraphExecDestroy(kv.second);
+  m.chunk_exec.clear();
+  m.graph_nodes.clear();
+}
+
+static void model_destroy(Model* m) {
+  if (!m) return;
+  (void)hipSetDevice(m->device);
+  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  destroy_graphs(*m);
+  stager_free(&m->st);
+  qmat_release(&m->embd);
+  qmat_release(&m->out);
+  for (auto& l : m->layers) {
+    for (auto& q : l.qkv) qmat_release(&q);
+    qmat_release(&l.o);
+    for (auto& q : l.gu) qmat_release(&q);
+    qmat_release(&l.down);
+  }
+  for (void* p : m->allocs) (void)hipFree(p);
+  if (m->host) (void)hipHostFree(m->host);
+  if (m->stream) (void)hipStreamDestroy(m->stream);
+  delete m;
+}
+
+// ------------------------------------------------------------ tensors
+
+static std::string layer_name(int l, const char* suffix) { return "blk." + std::to_string(l) + "." + suffix; }
+
+// Expected shape of every tensor the forward pass reads (cpu.go:225-366).
+static bool expected(const Model& m, const std::string& name, bool* quant, std::vector<uint64_t>* dims) {
+  const llmhip_config& c = m.cfg;
+  uint64_t E = c.embd, F = c.ff, kvd = m.kvd, V = c.vocab;
+  if (name == "token_embd.weight") { *quant = true; *dims = {E, V}; return true; }
+  if (name == "output_norm.weight") { *quant = false; *dims = {E}; return true; }
+  if (name == "output.weight") { *quant = true; *dims = {E, V}; return true; }
+  if (name.rfind("blk.", 0) != 0) return false;
+  size_t dot = name.find('.', 4);
+  if (dot == std::string::npos) return false;
+  int l = atoi(name.c_str() + 4);
+  if (l < 0 || l >= c.layers || std::to_string(l) != name.substr(4, dot - 4)) return false;
+  std::string s = name.substr(dot + 1);
+  if (s == "attn_norm.weight" || s == "ffn_norm.weight") { *quant = false; *dims = {E}; return true; }
+  if (s == "attn_q.weight" || s == "attn_output.weight") { *quant = true; *dims = {E, E}; return true; }
+  if (s == "attn_k.weight" || s == "attn_v.weight") { *quant = true; *dims = {E, kvd}; return true; }
+  if (s == "ffn_gate.weight" || s == "ffn_up.weight") { *quant = true; *dims = {E, F}; return true; }
+  if (s == "ffn_down.weight") { *quant = true; *dims = {F, E}; return true; }
+  if (c.bias) {
+    if (s == "attn_q.bias") { *quant = false; *dims = {E}; return true; }
+    if (s == "attn_k.bias" || s == "attn_v.bias") { *quant = false; *dims = {kvd}; return true; }
+  }
+  return false;
+}
+
+static const TensorInfo* need(Model& m, const std::string& n) {
+  auto it = m.tensors.find(n);
+  if (it == m.tensors.end()) {
+    set_error(LLMHIP_ERR_FORMAT, "llm: missing tensor %s", n.c_str());
+    return nullptr;
+  }
+  return &it->second;
+}
+
+// Allocate every weight once all tensors are declared: the fused groups need
+// the types of all their members (fused.go:108-190 concatenates QKV and
+// gate/up when they share a type; here mixed types get one matrix each).
+static int allocate(Model& m) {
+  const llmhip_config& c = m.cfg;
+  const uint32_t E = c.embd, F = c.ff, kvd = m.kvd, hd = c.head_dim;
+  const TensorInfo* te = need(m, "token_embd.weight");
+  if (!te) return LLMHIP_ERR_FORMAT;
+  if (te->type != LLMHIP_Q8_0 && te->type != LLMHIP_Q4_0)
+    return set_error(LLMHIP_ERR_TYPE, "llm: token_embd.weight must be Q8_0 or Q4_0");
+  LLM_TRY(qalloc(m, &m.embd, te->type, c.vocab, E));
+  if (!need(m, "output_norm.weight")) return LLMHIP_ERR_FORMAT;
+  LLM_TRY(dalloc_n(m, &m.out_norm, E));
+  m.tied = c.tied_output != 0;
+  if (!m.tied) {
+    const TensorInfo* to = need(m, "output.weight");
+    if (!to) return LLMHIP_ERR_FORMAT;
+    LLM_TRY(qalloc(m, &m.out, to->type, c.vocab, E));
+  }
+  m.layers.resize(c.layers);
+  for (int l = 0; l < c.layers; l++) {
+    Layer& L = m.layers[l];
+    const TensorInfo* t[7];
+    const char* names[7] = {"attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight",
+                            "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"};
+    for (int i = 0; i < 7; i++)
+      if (!(t[i] = need(m, layer_name(l, names[i])))) return LLMHIP_ERR_FORMAT;
+    if (!need(m, layer_name(l, "attn_norm.weight")) || !need(m, layer_name(l, "ffn_norm.weight")))
+      return LLMHIP_ERR_FORMAT;
+    LLM_TRY(dalloc_n(m, &L.attn_norm, E));
+    LLM_TRY(dalloc_n(m, &L.ffn_norm, E));
+    if (c.bias) {
+      for (const char* b : {"attn_q.bias", "attn_k.bias", "attn_v.bias"})
+        if (!need(m, layer_name(l, b))) return LLMHIP_ERR_FORMAT;
+      LLM_TRY(dalloc_n(m, &L.bias, E + 2 * kvd));
+    }
+    // Q, K, V: one matrix [q; k; v] when they share a type
+    if (t[0]->type == t[1]->type && t[1]->type == t[2]->type) {
+      L.nqkv = 1;
+      L.qkv_type[0] = t[0]->type;
+      if (c.rope_neox) {
+        L.qkv[0].map = MAP_NEOX;
+        L.qkv[0].map_hd = hd;
+        L.qkv[0].map_seg0 = 0;
+        L.qkv[0].map_seg1 = E + kvd;
+      }
+      LLM_TRY(qalloc(m, &L.qkv[0], t[0]->type, E + 2 * kvd, E));
+    } else {
+      L.nqkv = 3;
+      uint32_t rows[3] = {E, kvd, kvd}, base[3] = {0, E, E + kvd};
+      for (int i = 0; i < 3; i++) {
+        L.qkv_type[i] = t[i]->type;
+        L.qkv_base[i] = base[i];
+        if (c.rope_neox && i < 2) {
+          L.qkv[i].map = MAP_NEOX;
+          L.qkv[i].map_hd = hd;
+          L.qkv[i].map_seg0 = 0;
+          L.qkv[i].map_seg1 = rows[i];
+        }
+        LLM_TRY(qalloc(m, &L.qkv[i], t[i]->type, rows[i], E));
+      }
+    }
+    LLM_TRY(qalloc(m, &L.o, t[3]->type, E, E));
+    if (t[4]->type == t[5]->type && F % 8 == 0) {
+      L.ngu = 1;
+      L.gu[0].map = MAP_GATEUP;
+      L.gu[0].ff = F;
+      LLM_TRY(qalloc(m, &L.gu[0], t[4]->type, 2 * F, E));
+    } else {
+      L.ngu = 2;
+      LLM_TRY(qalloc(m, &L.gu[0], t[4]->type, F, E));
+      LLM_TRY(qalloc(m, &L.gu[1], t[5]->type, F, E));
+    }
+    LLM_TRY(qalloc(m, &L.down, t[6]->type, E, F));
+    LLM_TRY(dalloc_n(m, &L.kv, 2ull * m.ctx * kvd));
+  }
+  m.allocated = true;
+  return 0;
+}
+
+// Where the bytes of a tensor go: a matrix (and its first row there) or a
+// float array (and its float offset).
+static int route(Model& m, const std::string& name, QMat** q, uint64_t* row_off, float** f) {
+  *q = nullptr;
+  *f = nullptr;
+  *row_off = 0;
+  const uint32_t E = m.cfg.embd, kvd = m.kvd, F = m.cfg.ff;
+  if (name == "token_embd.weight") { *q = &m.embd; return 0; }
+  if (name == "output.weight") { *q = &m.out; return 0; }
+  if (name == "output_norm.weight") { *f = m.out_norm; return 0; }
+  int l = atoi(name.c_str() + 4);
+  Layer& L = m.layers[l];
+  std::string s = name.substr(name.find('.', 4) + 1);
+  if (s == "attn_norm.weight") { *f = L.attn_norm; return 0; }
+  if (s == "ffn_norm.weight") { *f = L.ffn_norm; return 0; }
+  if (s == "attn_q.bias") { *f = L.bias; return 0; }
+  if (s == "attn_k.bias") { *f = L.bias + E; return 0; }
+  if (s == "attn_v.bias") { *f = L.bias + E + kvd; return 0; }
+  int i = s == "attn_q.weight" ? 0 : s == "attn_k.weight" ? 1 : s == "attn_v.weight" ? 2 : -1;
+  if (i >= 0) {
+    if (L.nqkv == 1) {
+      *q = &L.qkv[0];
+      *row_off = i == 0 ? 0 : i == 1 ? E : E + kvd;
+    } else {
+      *q = &L.qkv[i];
+    }
+    return 0;
+  }
+  if (s == "attn_output.weight") { *q = &L.o; return 0; }
+  if (s == "ffn_gate.weight" || s == "ffn_up.weight") {
+    bool up = s == "ffn_up.weight";
+    if (L.ngu == 1) {
+      *q = &L.gu[0];
+      *row_off = up ? F : 0;
+    } else {
+      *q = &L.gu[up ? 1 : 0];
+    }
+    return 0;
+  }
+  if (s == "ffn_down.weight") { *q = &L.down; return 0; }
+  return set_error(LLMHIP_ERR_ARG, "llm: no place for tensor %s", name.c_str());
+}
+
+// ------------------------------------------------------------ recording
+
+static bool skipped(const Model& m, const char* cls) { return m.skip.count("all") || m.skip.count(cls); }
+
+static int gemv_rec(Model& m, const char* cls, const GemvArgs& a, uint32_t qtype, int pro, int epi) {
+  if (skipped(m, cls)) return 0;
+  m.dispatches++;
+  return gemv_launch(a, qtype, pro, epi, m.stream);
+}
+
+static GemvArgs base_args(const Model& m, const QMat& q, uint32_t ntok) {
+  GemvArgs a;
+  memset(&a, 0, sizeof a);
+  gemv_bind(&a, q);
+  a.ntok = ntok;
+  a.eps = m.cfg.eps;
+  a.state = m.state;
+  a.heads = m.cfg.heads;
+  a.hd = m.cfg.head_dim;
+  a.smax = m.smax;
+  a.chunk = m.chunk;
+  return a;
+}
+
+static int rec_k1(Model& m, const Layer& L, uint32_t ntok) {
+  const llmhip_config& c = m.cfg;
+  for (int i = 0; i < L.nqkv; i++) {
+    GemvArgs a = base_args(m, L.qkv[i], ntok);
+    a.x = m.x;
+    a.ldx = c.embd;
+    a.nw = L.attn_norm;
+    a.y = m.q;
+    a.bias = L.bias;
+    a.cs = m.cs;
+    a.kv = L.kv;
+    a.nq = c.embd;
+    a.nk = m.kvd;
+    a.kvd = m.kvd;
+    a.ctx = m.ctx;
+    a.neox = c.rope_neox;
+    a.row_base = L.qkv_base[i];
+    LLM_TRY(gemv_rec(m, "k1", a, L.qkv_type[i], PRO_RMS, EPI_QKV));
+  }
+  return 0;
+}
+
+static AttnArgs attn_args(const Model& m, const Layer& L) {
+  AttnArgs a;
+  a.q = m.q;
+  a.kv = L.kv;
+  a.pv = m.pv;
+  a.ml = m.ml;
+  a.state = m.state;
+  a.heads = m.cfg.heads;
+  a.kv_heads = m.cfg.kv_heads;
+  a.hd = m.cfg.head_dim;
+  a.kvd = m.kvd;
+  a.ctx = m.ctx;
+  a.smax = m.smax;
+  a.chunk = m.chunk;
+  a.scale = (float)(1 / std::sqrt((double)m.cfg.head_dim));  // cpu.go:304
+  return a;
+}
+
+static int rec_k2(Model& m, const Layer& L, uint32_t ntok) {
+  if (skipped(m, "k2")) return 0;
+  m.dispatches++;
+  return attn_launch(attn_args(m, L), ntok, m.stream);
+}
+
+static int rec_k3(Model& m, const Layer& L, uint32_t ntok) {
+  GemvArgs a = base_args(m, L.o, ntok);
+  a.pv = m.pv;
+  a.ml = m.ml;
+  a.y = m.x;
+  a.ldy = m.cfg.embd;
+  return gemv_rec(m, "k3", a, L.o.g.q.type, PRO_MERGE, EPI_ACC);
+}
+
+static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
+  const llmhip_config& c = m.cfg;
+  if (L.ngu == 1) {
+    GemvArgs a = base_args(m, L.gu[0], ntok);
+    a.x = m.x;
+    a.ldx = c.embd;
+    a.nw = L.ffn_norm;
+    a.y = m.act;
+    a.ff = c.ff;
+    return gemv_rec(m, "k4", a, L.gu[0].g.q.type, PRO_RMS, EPI_GATEUP);
+  }
+  GemvArgs g = base_args(m, L.gu[0], ntok);
+  g.x = m.x;
+  g.ldx = c.embd;
+  g.nw = L.ffn_norm;
+  g.y = m.gbuf;
+  g.ldy = c.ff;
+  LLM_TRY(gemv_rec(m, "k4", g, L.gu[0].g.q.type, PRO_RMS, EPI_STORE));
+  GemvArgs u = base_args(m, L.gu[1], ntok);
+  u.x = m.x;
+  u.ldx = c.embd;
+  u.nw = L.ffn_norm;
+  u.y = m.act;
+  u.ldy = c.ff;
+  u.aux = m.gbuf;
+  return gemv_rec(m, "k4", u, L.gu[1].g.q.type, PRO_RMS, EPI_SWIGLU);
+}
+
+static int rec_k5(Model& m, const Layer& L, uint32_t ntok) {
+  GemvArgs a = base_args(m, L.down, ntok);
+  a.x = m.act;
+  a.ldx = m.cfg.ff;
+  a.y = m.x;
+  a.ldy = m.cfg.embd;
+  return gemv_rec(m, "k5", a, L.down.g.q.type, PRO_PLAIN, EPI_ACC);
+}
+
+static GemvArgs head_args(const Model& m, uint32_t xrow) {
+  const QMat& w = m.tied ? m.embd : m.out;
+  GemvArgs a = base_args(m, w, 1);
+  a.x = m.x;
+  a.ldx = m.cfg.embd;
+  a.xrow0 = xrow;
+  a.nw = m.out_norm;
+  a.y = m.logits;
+  a.ldy = m.cfg.vocab;
+  a.amax_v = m.amax_v;
+  a.amax_i = m.amax_i;
+  return a;
+}
+
+static int rec_head(Model& m, uint32_t xrow, uint32_t adv) {
+  const QMat& w = m.tied ? m.embd : m.out;
+  GemvArgs a = head_args(m, xrow);
+  LLM_TRY(gemv_rec(m, "head", a, w.g.q.type, PRO_RMS, EPI_ARGMAX));
+  if (skipped(m, "argmax")) return 0;
+  m.dispatches++;
+  return argmax_launch(m.amax_v, m.amax_i, gemv_groups(a), m.logits, m.tokens, m.outb, m.state, adv, m.stream);
+}
+
+static int rec_adv(Model& m, uint32_t n) {
+  if (skipped(m, "adv")) return 0;
+  m.dispatches++;
+  return advance_launch(m.state, n, m.stream);
+}
+
+// One pass of ntok tokens at positions state[0] .. state[0]+ntok-1: the
+// embedding, the layers, and (head) the logits and the sampled token of the
+// last one, which goes to tokens[step + ntok]; state advances by ntok.
+static int record_pass(Model& m, uint32_t ntok, bool head) {
+  if (!skipped(m, "embed")) {
+    m.dispatches++;
+    LLM_TRY(embed_launch(m.embd, m.tokens, m.state, m.x, ntok, m.stream));
+  }
+  int nl = m.cfg.layers;
+  if (m.layers_limit != 0 && m.layers_limit < nl) {
+    nl = std::max(m.layers_limit, 0);
+    head = false;
+  }
+  for (int l = 0; l < nl; l++) {
+    const Layer& L = m.layers[l];
+    LLM_TRY(rec_k1(m, L, ntok));
+    LLM_TRY(rec_k2(m, L, ntok));
+    LLM_TRY(rec_k3(m, L, ntok));
+    LLM_TRY(rec_k4(m, L, ntok));
+    LLM_TRY(rec_k5(m, L, ntok));
+  }
+  if (head) return rec_head(m, ntok - 1, ntok);
+  return rec_adv(m, ntok);
+}
+
+// Capture record_pass into a graph (once per key).
+static int graph_for(Model& m, uint32_t ntok, bool head, hipGraphExec_t* out) {
+  uint32_t key = 2 * ntok + (head ? 1 : 0);
+  auto it = m.chunk_exec.find(key);
+  if (it != m.chunk_exec.end()) {
+    *out = it->second;
+    return 0;
+  }
+  hipGraph_t g = nullptr;
+  m.dispatches = 0;
+  LLM_HIP(hipStreamBeginCapture(m.stream, hipStreamCaptureModeThreadLocal));
+  int rc = record_pass(m, ntok, head);
+  hipError_t e = hipStreamEndCapture(m.stream, &g);
+  if (rc != 0) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return set_error(LLMHIP_ERR_DEVICE, "llm: graph capture failed: %s", hipGetErrorString(e));
+  hipGraphExec_t ex = nullptr;
+  e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return set_error(LLMHIP_ERR_DEVICE, "llm: graph instantiate failed: %s", hipGetErrorString(e));
+  m.chunk_exec[key] = ex;
+  m.graph_nodes[key] = m.dispatches;
+  *out = ex;
+  return 0;
+}
+
+static int launch_graph(Model& m, uint32_t ntok, bool head) {
+  hipGraphExec_t ex;
+  LLM_TRY(graph_for(m, ntok, head, &ex));
+  LLM_HIP(hipGraphLaunch(ex, m.stream));
+  m.stats.dispatches += m.graph_nodes[2 * ntok + (head ? 1 : 0)];
+  return 0;
+}
+
+}  // namespace llmhip
+
+using namespace llmhip;
+
+struct llmhip_model {
+  Model* m;
+};
+
+extern "C" {
+
+int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_config* cfg, int ctx, int prefill_batch,
+                        llmhip_model** out) {
+  clear_error();
+  *out = nullptr;
+  const llmhip_config& c = *cfg;
+  if (c.layers <= 0 || c.embd <= 0 || c.ff <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.vocab <= 0 ||
+      c.embd % c.heads != 0 || c.heads % c.kv_heads != 0 || c.head_dim != c.embd / c.heads)
+    return set_error(LLMHIP_ERR_FORMAT, "llm: implausible hyperparameters");
+  if (c.embd % 32 != 0 || c.ff % 32 != 0)
+    return set_error(LLMHIP_ERR_FORMAT, "llm: embedding %d and feed-forward %d must be multiples of 32", c.embd, c.ff);
+  if (c.head_dim % 2 != 0 || (c.rope_neox && c.head_dim % 16 != 0))
+    return set_error(LLMHIP_ERR_FORMAT, "llm: head size %d is not supported", c.head_dim);
+  Model* m = new Model();
+  m->device = ordinal;
+  m->cfg = c;
+  if (lim) m->lim = *lim;
+  else if (llmhip_device_limits(ordinal, &m->lim) != 0) {
+    delete m;
+    return LLMHIP_ERR_DEVICE;
+  }
+  int cx = ctx;
+  if (cx <= 0 || cx > c.ctx) cx = c.ctx;  // gpu.go:470-472
+  if (cx <= 0) {
+    delete m;
+    return set_error(LLMHIP_ERR_FORMAT, "llm: context length %d", cx);
+  }
+  m->ctx = (uint32_t)cx;
+  m->pm = prefill_batch > 0 ? (uint32_t)std::min(prefill_batch, 64) : 64;
+  m->kvd = (uint32_t)(c.kv_heads * c.head_dim);
+  m->smax = (m->ctx + m->chunk - 1) / m->chunk;
+  auto fail = [&](int rc) {
+    model_destroy(m);
+    return rc;
+  };
+  if (hipSetDevice(ordinal) != hipSuccess) return fail(set_error(LLMHIP_ERR_DEVICE, "llm: no GPU %d", ordinal));
+  if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess)
+    return fail(set_error(LLMHIP_ERR_DEVICE, "llm: hipStreamCreate failed"));
+  int rc;
+  const uint64_t E = c.embd, F = c.ff, V = c.vocab, pm = m->pm, H = c.heads;
+  if ((rc = dalloc_n(*m, &m->x, pm * E)) || (rc = dalloc_n(*m, &m->q, pm * E)) ||
+      (rc = dalloc_n(*m, &m->act, pm * F)) || (rc = dalloc_n(*m, &m->gbuf, pm * F)) ||
+      (rc = dalloc_n(*m, &m->logits, V)) || (rc = dalloc_n(*m, &m->amax_v, V / 16 + 64)) ||
+      (rc = dalloc_n(*m, &m->amax_i, V / 16 + 64)) || (rc = dalloc_n(*m, &m->pv, pm * H * m->smax * c.head_dim)) ||
+      (rc = dalloc_n(*m, &m->ml, pm * H * m->smax * 2)) || (rc = dalloc_n(*m, &m->state, 2)) ||
+      (rc = dalloc_n(*m, &m->tokens, (uint64_t)m->ctx + 1)) || (rc = dalloc_n(*m, &m->outb, 1)) ||
+      (rc = dalloc_n(*m, &m->cs, (uint64_t)m->ctx * c.head_dim)))
+    return fail(rc);
+  // RoPE table in double precision, gpu.go:524-534 (and cpu.go:374-375)
+  std::vector<float> cs((size_t)m->ctx * c.head_dim);
+  const int hp = c.head_dim / 2;
+  for (uint32_t p = 0; p < m->ctx; p++)
+    for (int i = 0; i < hp; i++) {
+      double theta = (double)p * std::pow((double)c.rope_base, -(double)(2 * i) / (double)c.head_dim);
+      double sn, co;
+      sincos(theta, &sn, &co);
+      cs[((size_t)p * hp + i) * 2] = (float)co;
+      cs[((size_t)p * hp + i) * 2 + 1] = (float)sn;
+    }
+  if (hipMemcpy(m->cs, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+    return fail(set_error(LLMHIP_ERR_DEVICE, "llm: RoPE table upload failed"));
+  m->host_cap = std::max<uint32_t>(m->ctx + 1, 64);
+  if (hipHostMalloc((void**)&m->host, (size_t)m->host_cap * 4, hipHostMallocDefault) != hipSuccess)
+    return fail(set_error(LLMHIP_ERR_DEVICE, "llm: hipHostMalloc failed"));
+  if ((rc = stager_init(&m->st, ordinal, 4ull << 20, m->stream))) return fail(rc);
+  *out = new llmhip_model{m};
+  return 0;
+}
+
+int llmhip_model_tensor(llmhip_model* h, const char* name, uint32_t type, const uint64_t* dims, uint32_t ndims) {
+  clear_error();
+  Model& m = *h->m;
+  if (m.allocated) return set_error(LLMHIP_ERR_STATE, "llm: tensor %s declared after the first upload", name);
+  bool quant;
+  std::vector<uint64_t> want;
+  TensorInfo t;
+  t.type = type;
+  t.dims.assign(dims, dims + ndims);
+  if (!expected(m, name, &quant, &want)) {
+    t.used = false;
+    m.tensors[name] = t;
+    return 0;
+  }
+  t.used = true;
+  if (t.dims != want) {
+    std::string got, exp;
+    for (auto d : t.dims) got += std::to_string(d) + " ";
+    for (auto d : want) exp += std::to_string(d) + " ";
+    return set_error(LLMHIP_ERR_FORMAT, "llm: tensor %s has dims [%s], want [%s]", name, got.c_str(), exp.c_str());
+  }
+  uint64_t elems = 1;
+  for (auto d : t.dims) elems *= d;
+  if (quant) {
+    QType q;
+    if (!qtype_of(type, &q))
+      return set_error(LLMHIP_ERR_TYPE, "llm: tensor %s has ggml type %u, which has no GPU kernel yet (Q4_0, Q4_1, Q8_0)",
+                       name, type);
+    t.size = elems / 32 * q.block_bytes;
+  } else {
+    if (type != LLMHIP_F32) return set_error(LLMHIP_ERR_FORMAT, "llm: tensor %s missing or not F32", name);
+    t.size = elems * 4;
+  }
+  m.tensors[name] = t;
+  return 0;
+}
+
+int llmhip_model_upload(llmhip_model* h, const char* name, const void* raw, uint64_t nbytes, uint64_t off) {
+  clear_error();
+  Model& m = *h->m;
+  auto it = m.tensors.find(name);
+  if (it == m.tensors.end()) return set_error(LLMHIP_ERR_ARG, "llm: tensor %s was not declared", name);
+  TensorInfo& t = it->second;
+  if (!t.used) return 0;
+  if (!m.allocated) LLM_TRY(allocate(m));
+  if (off + nbytes > t.size)
+    return set_error(LLMHIP_ERR_ARG, "llm: upload of %s runs past its %llu bytes", name, (unsigned long long)t.size);
+  QMat* q;
+  uint64_t row_off;
+  float* f;
+  LLM_TRY(route(m, name, &q, &row_off, &f));
+  LLM_HIP(hipSetDevice(m.device));
+  if (q) {
+    LLM_TRY(qmat_upload(&m.st, *q, raw, nbytes, off, row_off));
+  } else {
+    if (off % 4 || nbytes % 4) return set_error(LLMHIP_ERR_ARG, "llm: F32 upload of %s not whole floats", name);
+    LLM_HIP(hipStreamSynchronize(m.stream));
+    LLM_HIP(hipMemcpy((char*)f + off, raw, nbytes, hipMemcpyHostToDevice));
+  }
+  t.received += nbytes;
+  return 0;
+}
+
+int llmhip_model_finalize(llmhip_model* h) {
+  clear_error();
+  Model& m = *h->m;
+  if (!m.allocated) LLM_TRY(allocate(m));
+  for (auto& kv : m.tensors)
+    if (kv.second.used && kv.second.received < kv.second.size)
+      return set_error(LLMHIP_ERR_FORMAT, "llm: tensor %s: %llu of %llu bytes uploaded", kv.first.c_str(),
+                       (unsigned long long)kv.second.received, (unsigned long long)kv.second.size);
+  LLM_HIP(hipStreamSynchronize(m.stream));
+  m.stats.submits++;
+  m.finalized = true;
+  return 0;
+}
+
+int llmhip_model_prefill(llmhip_model* h, const int32_t* ids, int n, float* logits, int32_t* first) {
+  clear_error();
+  Model& m = *h->m;
+  if (!m.finalized) return set_error(LLMHIP_ERR_STATE, "llm: model not finalized");
+  if (n <= 0) return set_error(LLMHIP_ERR_ARG, "llm: empty prompt");
+  if ((uint32_t)n > m.ctx) return set_error(LLMHIP_ERR_CONTEXT, "llm: prompt longer than the context");
+  for (int i = 0; i < n; i++)
+    if (ids[i] < 0 || ids[i] >= m.cfg.vocab)
+      return set_error(LLMHIP_ERR_ARG, "llm: token id %d outside the vocabulary of %d", ids[i], m.cfg.vocab);
+  LLM_HIP(hipSetDevice(m.device));
+  // begin (gpu.go:839-847): state = (0, 0), the prompt into tokens[0:]
+  LLM_HIP(hipStreamSynchronize(m.stream));
+  m.host[0] = 0;
+  m.host[1] = 0;
+  LLM_HIP(hipMemcpyAsync(m.state, m.host, 8, hipMemcpyHostToDevice, m.stream));
+  LLM_HIP(hipStreamSynchronize(m.stream));
+  memcpy(m.host, ids, (size_t)n * 4);
+  LLM_HIP(hipMemcpyAsync(m.tokens, m.host, (size_t)n * 4, hipMemcpyHostToDevice, m.stream));
+  bool full = m.layers_limit == 0 || m.layers_limit >= m.cfg.layers;
+  for (int a = 0; a < n; a += (int)m.pm) {
+    int b = std::min(a + (int)m.pm, n);
+    LLM_TRY(launch_graph(m, (uint32_t)(b - a), b == n));
+    m.stats.submits++;
+  }
+  m.pos = (uint32_t)n;
+  m.prompted = full;
+  if (logits) LLM_HIP(hipMemcpyAsync(logits, m.logits, (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.stream));
+  LLM_HIP(hipMemcpyAsync(m.host, m.tokens + n, 4, hipMemcpyDeviceToHost, m.stream));
+  LLM_HIP(hipStreamSynchronize(m.stream));
+  if (first) *first = m.host[0];
+  m.stats.tokens += n;
+  return 0;
+}
+
+int llmhip_model_decode(llmhip_model* h, int cnt, int32_t* out) {
+  clear_error();
+  Model& m = *h->m;
+  if (!m.prompted) return set_error(LLMHIP_ERR_STATE, "llm: decode before a prompt");
+  if (cnt <= 0) return 0;
+  if (m.pos + (uint32_t)cnt > m.ctx)
+    return set_error(LLMHIP_ERR_CONTEXT, "llm: %d more tokens exceed the context of %u at position %u", cnt, m.ctx,
+                     m.pos);
+  LLM_HIP(hipSetDevice(m.device));
+  uint32_t first = m.pos;
+  for (int j = 0; j < cnt; j++) LLM_TRY(launch_graph(m, 1, true));
+  LLM_HIP(hipMemcpyAsync(m.host, m.tokens + first + 1, (size_t)cnt * 4, hipMemcpyDeviceToHost, m.stream));
+  LLM_HIP(hipStreamSynchronize(m.stream));
+  memcpy(out, m.host, (size_t)cnt * 4);
+  m.pos += (uint32_t)cnt;
+  m.stats.submits++;
+  m.stats.tokens += cnt;
+  return 0;
+}
+
+int llmhip_model_peek(llmhip_model* h, const char* name, float* out, uint64_t n) {
+  clear_error();
+  Model& m = *h->m;
+  const void* src = nullptr;
+  uint64_t cap = 0;
+  std::string s = name;
+  const uint64_t E = m.cfg.embd, F = m.cfg.ff;
+  if (s == "x") { src = m.x; cap = m.pm * E; }
+  else if (s == "q") { src = m.q; cap = m.pm * E; }
+  else if (s == "gate" || s == "act") { src = m.act; cap = m.pm * F; }
+  else if (s == "logits") { src = m.logits; cap = m.cfg.vocab; }
+  else if (s == "state") { src = m.state; cap = 2; }
+  else if (s == "tokens") { src = m.tokens; cap = m.ctx + 1; }
+  else if (s == "outb") { src = m.outb; cap = 1; }
+  else if (s.rfind("kvblk.", 0) == 0) {
+    int l = atoi(s.c_str() + 6);
+    if (l >= 0 && l < m.cfg.layers && m.allocated) {
+      src = m.layers[l].kv;
+      cap = 2ull * m.ctx * m.kvd;
+    }
+  }
+  if (!src) return set_error(LLMHIP_ERR_ARG, "llm: no buffer \"%s\"", name);
+  if (n > cap) return set_error(LLMHIP_ERR_ARG, "llm: buffer \"%s\" holds %llu words", name, (unsigned long long)cap);
+  LLM_HIP(hipSetDevice(m.device));
+  LLM_HIP(hipStreamSynchronize(m.stream));
+  LLM_HIP(hipMemcpy(out, src, n * 4, hipMemcpyDeviceToHost));
+  m.stats.submits++;
+  return 0;
+}
+
+uint64_t llmhip_model_memory_used(const llmhip_model* h) { return h->m->used; }
+
+int llmhip_model_stats(const llmhip_model* h, llmhip_stats* out) {
+  *out = h->m->stats;
+  return 0;
+}
+
+int llmhip_model_config(const llmhip_model* h, llmhip_config* out, int* ctx) {
+  *out = h->m->cfg;
+  if (ctx) *ctx = (int)h->m->ctx;
+  return 0;
+}
+
+int llmhip_model_set_layers(llmhip_model* h, int layers) {
+  clear_error();
+  Model& m = *h->m;
+  (void)hipStreamSynchronize(m.stream);
+  if (m.layers_limit != layers) destroy_graphs(m);
+  m.layers_limit = layers;
+  return 0;
+}
+
+int llmhip_model_set_skip(llmhip_model* h, const char* classes) {
+  clear_error();
+  Model& m = *h->m;
+  (void)hipStreamSynchronize(m.stream);
+  std::set<std::string> s;
+  std::string c = classes ? classes : "";
+  size_t a = 0;
+  while (a <= c.size()) {
+    size_t b = c.find(',', a);
+    if (b == std::string::npos) b = c.size();
+    if (b > a) s.insert(c.substr(a, b - a));
+    a = b + 1;
+  }
+  if (s != m.skip) destroy_graphs(m);
+  m.skip = s;
+  return 0;
+}
+
+int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, float* avg_us, uint64_t* bytes) {
+  clear_error();
+  Model& m = *h->m;
+  if (!m.finalized) return set_error(LLMHIP_ERR_STATE, "llm: model not finalized");
+  if (iters < 1) return set_error(LLMHIP_ERR_ARG, "llm: iters %d", iters);
+  LLM_HIP(hipSetDevice(m.device));
+  std::string k = kernel;
+  const Layer& L = m.layers[0];
+  std::set<std::string> saved = m.skip;
+  m.skip.clear();
+  auto one = [&]() -> int {
+    if (k == "head") {
+      const QMat& w = m.tied ? m.embd : m.out;
+      return gemv_launch(head_args(m, 0), w.g.q.type, PRO_RMS, EPI_ARGMAX, m.stream);
+    }
+    if (k == "k1") return rec_k1(m, L, 1);
+    if (k == "k2") return rec_k2(m, L, 1);
+    if (k == "k3") return rec_k3(m, L, 1);
+    if (k == "k4") return rec_k4(m, L, 1);
+    if (k == "k5") return rec_k5(m, L, 1);
+    return set_error(LLMHIP_ERR_ARG, "llm: no kernel \"%s\" (head, k1..k5)", kernel);
+  };
+  uint64_t b = 0;
+  auto wb = [](const QMat& q) { return q.g.gguf_bytes(); };
+  if (k == "head") b = wb(m.tied ? m.embd : m.out);
+  else if (k == "k1") b = wb(L.qkv[0]) + (L.nqkv == 3 ? wb(L.qkv[1]) + wb(L.qkv[2]) : 0);
+  else if (k == "k3") b = wb(L.o);
+  else if (k == "k4") b = wb(L.gu[0]) + (L.ngu == 2 ? wb(L.gu[1]) : 0);
+  else if (k == "k5") b = wb(L.down);
+  int rc = 0;
+  for (int i = 0; i < 3 && rc == 0; i++) rc = one();
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (rc == 0 && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
+    rc = set_error(LLMHIP_ERR_DEVICE, "llm: hipEventCreate failed");
+  if (rc == 0 && hipEventRecord(e0, m.stream) != hipSuccess) rc = set_error(LLMHIP_ERR_DEVICE, "llm: event record");
+  for (int i = 0; i < iters && rc == 0; i++) rc = one();
+  if (rc == 0 && hipEventRecord(e1, m.stream) != hipSuccess) rc = set_error(LLMHIP_ERR_DEVICE, "llm: event record");
+  float ms = 0;
+  if (rc == 0 && hipEventSynchronize(e1) == hipSuccess) (void)hipEventElapsedTime(&ms, e0, e1);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  m.skip = saved;
+  if (rc) return rc;
+  *avg_us = ms * 1000.f / (float)iters;
+  if (bytes) *bytes = b;
+  return 0;
+}
+
+void llmhip_model_free(llmhip_model* h) {
+  if (!h) return;
+  model_destroy(h->m);
+  delete h;
+}
+
+}  // extern "C"

@@ -1,0 +1,159 @@
+"""GPU forward pass against the CPU oracle, through the C-ABI (llm_* / llmhip_*).
+
+Tiny random-init llama and qwen2 models exercise every path (tied Q4_0 head,
+Q8_0 head, NEOX, biases, mixed Q4_0/Q4_1/Q8_0 types, multi-chunk prompts,
+decode batches, the Layers trace, refusals); the BASELINE shapes (SmolLM2 and
+Qwen2.5-0.5B) are checked end to end: step-1 logits within 1e-4 relative and
+greedy tokens identical except at a top-2 logit gap below that tolerance.
+"""
+import numpy as np
+import pytest
+
+from llm_amd import synth
+from tests.parity import LOGIT_TOL, cpu_greedy, gpu_generate, greedy_parity, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _open(spec, ctx):
+    from llm_amd import llm
+    from oracle import cpuref
+    path = synth.cached(spec)
+    print(f"model {spec.arch} L{spec.layers} E{spec.embd} V{spec.vocab} ctx {ctx} at {path}", flush=True)
+    g = llm.NewGPU(0, None, path, ctx)
+    cpu = cpuref.CPU(path, ctx, threads=16)
+    return g, cpu
+
+
+def _check(g, cpu, prompt, n):
+    logits = g.PrefillLogits(prompt)
+    toks, lgs = cpu_greedy(cpu, prompt, n)
+    rel = rel_err(logits, lgs[0])
+    print(f"step-1 logits relative error {rel:.3e}", flush=True)
+    assert rel <= LOGIT_TOL
+    ties = greedy_parity(g, prompt, toks, lgs)
+    print(f"{n} greedy tokens equal ({ties} accepted near-ties)", flush=True)
+    return rel, ties
+
+
+TINY = {
+    "llama": lambda: synth.tiny_llama(),
+    "qwen2": lambda: synth.tiny_qwen(),
+    "qwen2-mixed": lambda: synth.tiny_qwen(seed=3, types={
+        "attn_q": synth.Q8_0, "attn_k": synth.Q4_1, "attn_v": synth.Q4_0, "attn_output": synth.Q4_1,
+        "ffn_gate": synth.Q8_0, "ffn_up": synth.Q4_0, "ffn_down": lambda l: synth.Q4_1 if l % 2 else synth.Q8_0}),
+    "llama-q8embd": lambda: synth.tiny_llama(seed=4, embd_type=synth.Q8_0,
+                                             types={"ffn_down": synth.Q4_1, "attn_output": synth.Q8_0}),
+    "llama-untied-q41": lambda: synth.tiny_llama(seed=5, tied=False, out_type=synth.Q4_1, layers=3),
+}
+
+
+@pytest.mark.parametrize("name", list(TINY))
+def test_tiny_parity(gpu, name):
+    spec = TINY[name]()
+    g, cpu = _open(spec, 512)
+    prompt = synth.prompt(1, 150, spec.vocab)  # three prefill chunks of 64, 64, 22
+    _check(g, cpu, prompt, 40)
+
+
+def test_decode_batches_and_stops(gpu):
+    from llm_amd import llm
+    spec = synth.tiny_qwen()
+    g, cpu = _open(spec, 512)
+    prompt = synth.prompt(2, 37, spec.vocab)
+    ref = gpu_generate(g, prompt, 30)
+    old = llm.DecodeBatch
+    try:
+        for b in (1, 3, 8, 16, 40):
+            llm.DecodeBatch = b
+            assert gpu_generate(g, prompt, 30) == ref, f"decode batch {b}"
+    finally:
+        llm.DecodeBatch = old
+    # eos is not emitted and ends the generation (gpu.go:971-976)
+    out = []
+    tm = g.Generate(list(prompt), 30, ref[5], lambda t: out.append(t) or True)
+    assert out == ref[:ref.index(ref[5])] and tm.Generated == len(out)
+    # emit returning false stops after that token (gpu.go:979-982)
+    out = []
+    g.Generate(list(prompt), 30, -1, lambda t: out.append(t) or len(out) < 4)
+    assert out == ref[:4]
+    # n = 0 generates nothing; n = 1 is the prefill's token
+    assert gpu_generate(g, prompt, 0) == []
+    assert gpu_generate(g, prompt, 1) == ref[:1]
+
+
+def test_trace_layers(gpu):
+    """The residual stream after k layers (trace mode, examples/generate/main.go:212-240)."""
+    spec = synth.tiny_llama(layers=3)
+    g, cpu = _open(spec, 128)
+    prompt = synth.prompt(3, 5, spec.vocab)
+    for k in (-1, 1, 2, 3):
+        g.Layers = k
+        cpu.set_max_layers(k)
+        cpu.reset()
+        for t in prompt:
+            cpu.forward(t)
+        want = cpu.last_x()
+        g.PrefillLogits(prompt)
+        pm = 64
+        got = g.Peek("x", spec.embd * len(prompt)).reshape(len(prompt), spec.embd)[-1]
+        rel = rel_err(got, want)
+        print(f"layers {k}: x relative error {rel:.3e}", flush=True)
+        assert rel <= 1e-5 if k != -1 else np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    g.Layers = 0
+    st = g.Peek("state", 2).view(np.uint32)
+    assert list(st) == [len(prompt), len(prompt)]
+
+
+def test_state_and_tokens(gpu):
+    spec = synth.tiny_llama()
+    g, cpu = _open(spec, 256)
+    prompt = synth.prompt(4, 70, spec.vocab)
+    out = gpu_generate(g, prompt, 12)
+    toks = g.Peek("tokens", 70 + 12).view(np.int32)
+    assert list(toks[:70]) == list(prompt) and list(toks[70:]) == out
+    st = g.Peek("state", 2).view(np.uint32)
+    assert list(st) == [70 + 11, 70 + 11]
+    assert g.Peek("outb", 1).view(np.int32)[0] == out[-1]
+    s = g.Stats
+    assert s.dispatches > 0 and s.submits > 0
+
+
+def test_refusals(gpu):
+    from llm_amd import llm
+    from llm_amd._lib import LLMError
+    spec = synth.tiny_llama()
+    path = synth.cached(spec)
+    g = llm.NewGPU(0, None, path, 64)
+    with pytest.raises(LLMError) as e:
+        g.Generate([1] * 60, 10)  # gpu.go:948-950
+    assert e.value.kind == "CONTEXT"
+    with pytest.raises(LLMError) as e:
+        g.PrefillLogits([1] * 64)  # gpu.go:905-907
+    assert e.value.kind == "CONTEXT"
+    with pytest.raises(LLMError) as e:
+        g.Generate([], 3)  # gpu.go:854-856
+    assert "empty prompt" in str(e.value)
+    with pytest.raises(LLMError) as e:
+        g.Generate([spec.vocab], 3)
+    assert e.value.kind == "ARG"
+    with pytest.raises(LLMError) as e:
+        g.Peek("nothing", 1)
+    lim = llm.DefaultLimits()
+    lim.memory_budget = 4096
+    with pytest.raises(LLMError) as e:
+        llm.NewGPU(0, lim, path, 64)  # gpu.go:175-177
+    assert e.value.kind == "BUDGET"
+    # the budget is what MemoryUsed reports
+    lim.memory_budget = g.MemoryUsed()
+    g2 = llm.NewGPU(0, lim, path, 64)
+    assert g2.MemoryUsed() <= lim.memory_budget
+
+
+@pytest.mark.parametrize("config", ["smollm2", "qwen25"])
+def test_baseline_shapes(gpu, config):
+    """BASELINE configs 2 and 3: 128-token prompt in 64-token chunks, 128 greedy tokens, ctx 512."""
+    spec = synth.smollm2() if config == "smollm2" else synth.qwen25()
+    g, cpu = _open(spec, 512)
+    prompt = synth.prompt(0, 128, spec.vocab)
+    _check(g, cpu, prompt, 128)
