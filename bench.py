@@ -1,0 +1,203 @@
+#!/usr/bin/env python3
+"""Benchmark of the GPU forward pass on one MI355X.
+
+Workload: a seeded random-init Qwen2.5-0.5B-shaped qwen2
+model (24 layers, hidden 896, 14/2 heads, FFN 4864, vocab 151936, Q4_0 layers
+and embedding, Q8_0 output matrix), a 128-token prompt in 64-token prefill
+chunks, 128 greedy tokens at 8 tokens per submit, context 512, f32 KV cache.
+One step is one `bench` round of the reference (examples/generate/main.go:183-207):
+Generate(prompt, 128) with eos -1; `value` is decode tok/s over the K timed
+rounds (prefill tok/s reported beside it).  Inputs are resident in HBM before
+the timed region (the model is loaded once).
+
+Also measured: per-kernel device times of a decode step (HIP events on the
+model's stream, in the decode loop's cache state) for the roofline of the
+dominant kernel; the isolated GEMV sweep with weights read
+from HBM (rotated copies > 512 MB) and warm; and the CPU oracle (a C
+restatement of the reference's cpu.go) timed on this host's cores.
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "decode & prefill tok/s at Qwen2.5-0.5B shape; Q4_0 GEMV HBM GB/s vs peak"
+SWEEP = [(576, 576), (1536, 576), (576, 1536), (896, 896), (4864, 896), (896, 4864), (151936, 896)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def generation(args):
+    import torch
+    from llm_amd import llm, synth
+    spec = synth.qwen25(seed=0)
+    t0 = time.time()
+    path = synth.cached(spec)
+    log(f"model file {path} ready in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    g = llm.NewGPU(0, None, path, args.ctx)
+    log(f"load: {time.time() - t0:.2f}s, GPU memory {g.MemoryUsed()} bytes")
+    prompt = list(synth.prompt(0, args.prompt, spec.vocab))
+    for i in range(args.warmup):
+        tm = g.Generate(prompt, args.gen, -1)
+        log(f"warmup {i}: prefill {tm.PromptTokens / tm.Prefill:.1f} tok/s, decode {tm.Generated / tm.Decode:.1f} tok/s")
+    torch.cuda.synchronize()
+    rounds = []
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        tm = g.Generate(prompt, args.gen, -1)
+        rounds.append(tm)
+        log(f"round {i}: prefill {tm.PromptTokens / tm.Prefill:.1f} tok/s, decode {tm.Generated / tm.Decode:.1f} "
+            f"tok/s ({tm.Dispatches} dispatches)")
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dec = sum(r.Generated for r in rounds) / sum(r.Decode for r in rounds)
+    pre = sum(r.PromptTokens for r in rounds) / sum(r.Prefill for r in rounds)
+    per_round = {
+        "prefill_tok_s": {"median": statistics.median(r.PromptTokens / r.Prefill for r in rounds),
+                          "min": min(r.PromptTokens / r.Prefill for r in rounds),
+                          "max": max(r.PromptTokens / r.Prefill for r in rounds)},
+        "decode_tok_s": {"median": statistics.median(r.Generated / r.Decode for r in rounds),
+                         "min": min(r.Generated / r.Decode for r in rounds),
+                         "max": max(r.Generated / r.Decode for r in rounds)},
+    }
+    # per-kernel device times of one decode step, in the decode loop's cache state
+    g.Generate(prompt, 1, -1)
+    prof = g.profile(tokens=4)
+    classes = {}
+    for cls, layer, nbytes, us in prof:
+        c = classes.setdefault(cls, {"launches": 0, "us": 0.0, "bytes": 0})
+        c["launches"] += 1
+        c["us"] += us
+        c["bytes"] += nbytes
+    for c in classes.values():
+        c["avg_us"] = c["us"] / c["launches"]
+        c["gbps"] = c["bytes"] / c["us"] * 1e-3 if c["us"] > 0 and c["bytes"] else None
+    step_kernel_us = sum(c["us"] for c in classes.values())
+    weights = {k: v for k, v in classes.items() if k in ("k1", "k3", "k4", "k5", "head")}
+    dom = max(weights, key=lambda k: weights[k]["us"])
+    d = classes[dom]
+    achieved = d["bytes"] / d["us"] * 1e-3
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                "bytes_per_launch": d["bytes"] // d["launches"], "avg_us": round(d["avg_us"], 3)}
+    gemv_all = sum(weights[k]["bytes"] for k in weights) / sum(weights[k]["us"] for k in weights) * 1e-3
+    return g, {
+        "value": dec, "prefill": pre, "wall": wall, "rounds": per_round, "ms_per_step": wall / args.steps * 1e3,
+        "classes": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in classes.items()},
+        "step_kernel_us": step_kernel_us, "roofline": roofline, "gemv_aggregate_gbps": gemv_all,
+        "dispatches_per_token": len(prof),
+    }
+
+
+def sweep(args):
+    import numpy as np
+    import torch
+    from llm_amd import kernels, synth
+    out = []
+    for qtype, tname in ((kernels.Q4_0, "q4_0"), (kernels.Q8_0, "q8_0")):
+        for rows, k in SWEEP:
+            rng = np.random.default_rng([1, rows, k, qtype])
+            m = kernels.QMat(qtype, rows, k, synth.quant_blocks(qtype, rows, k, rng, q8_div=8.0))
+            x = torch.randn((1, k), device="cuda:0")
+            y = torch.empty((1, rows), device="cuda:0")
+            nbytes = m.gguf_bytes
+            warm = kernels.bench([m], x, y, iters=200, warmup=20)
+            copies = [m] + [m.clone() for _ in range(min(4095, max(0, -(-args.hbm_bytes // nbytes) - 1)))]
+            iters = max(len(copies), 200)
+            hbm = kernels.bench(copies, x, y, iters=iters, warmup=len(copies))
+            out.append({"type": tname, "rows": rows, "k": k, "n": 1, "bytes": nbytes,
+                        "hbm_us": round(hbm, 3), "hbm_gbps": round(nbytes / hbm * 1e-3, 1),
+                        "hbm_frac": round(nbytes / hbm * 1e-3 / PEAK_HBM_GBS, 4), "copies": len(copies),
+                        "warm_us": round(warm, 3), "warm_gbps": round(nbytes / warm * 1e-3, 1)})
+            log(f"gemv {tname} {rows}x{k}: HBM {out[-1]['hbm_gbps']} GB/s ({out[-1]['hbm_frac']:.1%}) over "
+                f"{len(copies)} copies, warm {out[-1]['warm_gbps']} GB/s")
+            for c in copies:
+                c.close()
+            torch.cuda.synchronize()
+    return out
+
+
+def cpu_baseline(args):
+    """The CPU oracle (C restatement of cpu.go, row-parallel, bit-identical to
+    single-threaded) on a bounded sample of the same workload."""
+    from llm_amd import synth
+    from oracle import cpuref
+    spec = synth.qwen25(seed=0)
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
+    cpu = cpuref.CPU(synth.cached(spec), args.ctx, threads=threads)
+    prompt = list(synth.prompt(0, 8, spec.vocab))
+    t0 = time.perf_counter()
+    for t in prompt:
+        logits = cpu.forward(t)
+    pre = len(prompt) / (time.perf_counter() - t0)
+    n = 0
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0 < args.cpu_seconds or n < 4) and len(prompt) + n < args.ctx:
+        logits = cpu.forward(cpuref.argmax(logits))
+        n += 1
+    dec = n / (time.perf_counter() - t0)
+    log(f"cpu oracle ({threads} threads): prefill {pre:.2f} tok/s, decode {dec:.2f} tok/s over {n} tokens")
+    return {"value": round(dec, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"qwen2.5-0.5b shape (same seeded model), 8 prompt tokens then {n} greedy decode tokens "
+                      f"(~{args.cpu_seconds:.0f}s), decode tok/s of the row-parallel oracle",
+            "prefill_tok_s": round(pre, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--prompt", type=int, default=128)
+    ap.add_argument("--gen", type=int, default=128)
+    ap.add_argument("--ctx", type=int, default=512)
+    ap.add_argument("--hbm-bytes", type=int, default=640 << 20, help="rotated copies per sweep shape")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        log("bench.py: this build measures one GPU; the path shards by independent sequences per GPU "
+            "(see DESIGN.md), and no multi-GPU figure is taken")
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        log("bench.py: no GPU")
+        sys.exit(2)
+    g, r = generation(args)
+    g.close()
+    res = {
+        "metric": METRIC, "value": round(r["value"], 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(r["ms_per_step"], 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: seeded random-init Qwen2.5-0.5B-shaped GGUF (Q4_0 layers/embedding, Q8_0 output)",
+        "config": {"workload": "BASELINE config 3: qwen2 24L/896/14:2 heads/FFN 4864/vocab 151936, 128-token "
+                               "prompt (64-token chunks), 128 greedy tokens (8 per submit), ctx 512, f32 KV",
+                   "prompt": args.prompt, "generate": args.gen, "ctx": args.ctx, "prefill_chunk": 64,
+                   "decode_batch": 8},
+        "prefill_tok_s": round(r["prefill"], 2),
+        "rounds": r["rounds"],
+        "roofline": r["roofline"],
+        "decode_step": {"kernel_us": round(r["step_kernel_us"], 2), "wall_us": round(1e6 / r["value"], 2),
+                        "dispatches": r["dispatches_per_token"],
+                        "gemv_aggregate_gbps": round(r["gemv_aggregate_gbps"], 1), "classes": r["classes"]},
+    }
+    if not args.no_sweep:
+        res["gemv_sweep"] = sweep(args)
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(args)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

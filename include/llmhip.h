@@ -110,6 +110,9 @@ LLMHIP_API uint64_t llmhip_qmat_gguf_bytes(const llmhip_qmat* m);
  * the weights come from HBM. */
 LLMHIP_API int llmhip_qmat_bench(llmhip_qmat* const* mats, int count, const float* x_dev, float* y_dev, int n, int iters,
                       int warmup, void* hip_stream, float* avg_us);
+/* A copy of m on the same device (device-to-device): rotating copies whose
+ * total exceeds the Infinity Cache makes a benchmark read HBM. */
+LLMHIP_API int llmhip_qmat_clone(const llmhip_qmat* m, llmhip_qmat** out);
 LLMHIP_API void llmhip_qmat_free(llmhip_qmat* m);
 
 /* -------------------------------------------------------------- models */
@@ -177,6 +180,19 @@ LLMHIP_API int llmhip_model_set_skip(llmhip_model* m, const char* classes);
  * bytes receives its algorithmic bytes (GGUF weight bytes + KV bytes read). */
 LLMHIP_API int llmhip_model_bench_kernel(llmhip_model* m, const char* kernel, int iters, float* avg_us,
                                          uint64_t* bytes);
+/* One kernel launch timed by llmhip_model_profile. */
+typedef struct llmhip_kernel_time {
+  char cls[8];    /* embed, k1..k5, head, argmax */
+  int32_t layer;  /* -1 outside the layers */
+  uint64_t bytes; /* algorithmic bytes: GGUF weight bytes, or KV bytes read (k2) */
+  float us;       /* device time between HIP events around the launch */
+} llmhip_kernel_time;
+/* Run `tokens` decode steps (>= 1) launching each kernel directly, with HIP
+ * events recorded on the model's stream around every launch, and return the
+ * launches of the last step (at most cap; *n their count).  Advances the
+ * model like llmhip_model_decode(tokens), so the per-kernel times are taken
+ * with the caches as the decode loop leaves them. */
+LLMHIP_API int llmhip_model_profile(llmhip_model* m, int tokens, llmhip_kernel_time* out, int cap, int* n);
 LLMHIP_API void llmhip_model_free(llmhip_model* m);
 
 /* ====================================================================

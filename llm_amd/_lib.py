@@ -49,6 +49,12 @@ class Timing(ctypes.Structure):
                                                 "dispatches", "record_ns", "submit_ns")]
 
 
+class KernelTime(ctypes.Structure):
+    """llmhip_kernel_time: one profiled launch."""
+    _fields_ = [("cls", ctypes.c_char * 8), ("layer", ctypes.c_int32), ("bytes", ctypes.c_uint64),
+                ("us", ctypes.c_float)]
+
+
 EMIT = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_int32, ctypes.c_void_p)
 
 _lib = None
@@ -68,6 +74,7 @@ SIGNATURES = [
     ("llmhip_qmat_bytes", U64, [P]),
     ("llmhip_qmat_gguf_bytes", U64, [P]),
     ("llmhip_qmat_bench", I, [ctypes.POINTER(P), I, P, P, I, I, I, P, ctypes.POINTER(F)]),
+    ("llmhip_qmat_clone", I, [P, ctypes.POINTER(P)]),
     ("llmhip_qmat_free", None, [P]),
     ("llmhip_model_create", I, [I, ctypes.POINTER(Limits), ctypes.POINTER(Config), I, I, ctypes.POINTER(P)]),
     ("llmhip_model_tensor", I, [P, ctypes.c_char_p, U32, PU64, U32]),
@@ -82,6 +89,7 @@ SIGNATURES = [
     ("llmhip_model_set_layers", I, [P, I]),
     ("llmhip_model_set_skip", I, [P, ctypes.c_char_p]),
     ("llmhip_model_bench_kernel", I, [P, ctypes.c_char_p, I, ctypes.POINTER(F), PU64]),
+    ("llmhip_model_profile", I, [P, I, P, I, ctypes.POINTER(I)]),
     ("llmhip_model_free", None, [P]),
     ("llm_gguf_parse_file", I, [ctypes.c_char_p, ctypes.POINTER(P), ctypes.POINTER(I)]),
     ("llm_gguf_parse_bytes", I, [P, U64, ctypes.POINTER(P), ctypes.POINTER(I)]),

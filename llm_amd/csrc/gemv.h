@@ -49,7 +49,8 @@ struct GemvArgs {
   uint32_t map, map_hd, map_seg0, map_seg1;  // RowMap; NEOX applies to rows [seg0, seg1)
   uint32_t row_base;                         // QKV: first row of this matrix in [q; k; v]
   uint32_t ntok;                             // tokens in the launch
-  uint32_t split;                            // waves sharing one tile (split-K): 1, 2 or 4
+  uint32_t split;                            // waves sharing one tile (split-K): 1..16
+  uint32_t waves;                            // waves per workgroup: 4, 8 or 16 (a multiple of split)
   // prologue
   const float* x;
   uint32_t ldx;
@@ -78,8 +79,8 @@ struct GemvArgs {
 int gemv_launch(const GemvArgs& a, uint32_t qtype, int pro, int epi, hipStream_t s);
 // Workgroups the launch uses along x (EPI_ARGMAX partial count).
 uint32_t gemv_groups(const GemvArgs& a);
-// Picks the split-K factor for a matrix of `tiles` row tiles.
-uint32_t gemv_pick_split(uint32_t tiles, uint32_t ng);
+// Picks the split-K factor (waves per tile) and the waves per workgroup.
+void gemv_pick(uint32_t tiles, uint32_t ng, uint32_t tail, uint32_t nb, uint32_t* split, uint32_t* waves);
 
 // Fill a GemvArgs with the matrix fields of m.
 void gemv_bind(GemvArgs* a, const QMat& m);

@@ -43,6 +43,14 @@ __device__ __forceinline__ float f16_hw(uint32_t h) {
 
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16 bytes of streamed weights: a non-temporal load (read once per pass).
+__device__ __forceinline__ uint4 ld_stream16(const uint8_t* p) {
+  u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+
 // ------------------------------------------------------------ row maps
 
 __host__ __device__ inline uint32_t pos_of_row(uint32_t lr, uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1,
@@ -251,79 +259,66 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // -------------------------------------------------------------- the kernel
 
-constexpr int GW = 256;  // threads per workgroup: 4 waves
+constexpr int MAXI = 2;  // 8-element activation items staged per thread and token
 
 // LDS layout of one launch (bytes).
 struct Lds {
-  uint32_t xs, misc, bsum, part, stage, wts, total;
+  uint32_t xs, misc, bsum, part, wts, total;
 };
 
-__host__ __device__ inline Lds lds_layout(int NT, int pro, uint32_t qtype, uint32_t nb, uint32_t k, uint32_t heads,
-                                          uint32_t smax) {
+__host__ __device__ inline Lds lds_layout(int NT, int pro, uint32_t qtype, uint32_t nb, uint32_t waves,
+                                          uint32_t heads, uint32_t smax) {
   Lds L;
   uint32_t o = 0;
   L.xs = o;
   o += nb * 4 * 2 * NT * 16;
   L.misc = o;
-  o += 64 * 4;
+  o += 128 * 4;
   L.bsum = o;
   if (qtype == LLMHIP_Q4_1) o += nb * NT * 4;
   L.part = o;
-  o += 4 * 64 * 2 * 4;
-  L.stage = o;
+  o += waves * 64 * 2 * 4;
   L.wts = o;
-  if (pro == PRO_MERGE) {
-    o += NT * k * 4;
-    L.wts = o;
-    o += NT * heads * (smax + 1) * 4;
-  }
+  if (pro == PRO_MERGE) o += NT * heads * (smax + 1) * 4;
   L.total = o;
   return L;
 }
 
+// (value, index) order of greedy sampling: larger value, then lower index;
+// an empty slot (index ~0u) always loses.
+__device__ __forceinline__ bool amax_better(float v, uint32_t i, float bv, uint32_t bi) {
+  return i != 0xffffffffu && (bi == 0xffffffffu || v > bv || (v == bv && i < bi));
+}
+
 template <uint32_t QT, int NT, int PRO, int EPI>
-__global__ __launch_bounds__(GW) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   typedef QT_<QT> T;
   constexpr int S = 2 * NT;  // MFMA rows used: hi and lo of each token
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const uint32_t bd = blockDim.x, nwv = bd >> 6;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t t0 = blockIdx.y * NT;
   const int nt = min((int)NT, (int)(a.ntok - t0));
-  const uint32_t nb = a.nb, K = a.k;
-  const Lds L = lds_layout(NT, PRO, QT, nb, K, a.heads, a.smax);
+  const uint32_t nb = a.nb, K = a.k, NI = nb * 4;
+  const Lds L = lds_layout(NT, PRO, QT, nb, nwv, a.heads, a.smax);
   h8* xs = (h8*)(lds + L.xs);
-  float* misc = (float*)(lds + L.misc);  // [0,16) wave partials, [16,24) s, [24,32) exps, [32,..) argmax
+  float* misc = (float*)(lds + L.misc);  // [0,64) wave partials, [64,72) rms s, [72,80) exps, [80,128) argmax
   float* bsum = (float*)(lds + L.bsum);
-  float* stage = (float*)(lds + L.stage);
   float* wts = (float*)(lds + L.wts);
-  int* exps = (int*)(misc + 24);
+  int* exps = (int*)(misc + 72);
 
-  // ---- prologue: the activations of nt tokens into MFMA operand order
-  float s_rms[NT];
-  if (PRO == PRO_RMS) {
-    // cpu.go:90-94: ss = sum x^2 (f32); s = f32(1/sqrt(f64(ss/n + eps)))
-    for (int t = 0; t < nt; t++) {
-      const float* xr = a.x + (uint64_t)(a.xrow0 + t0 + t) * a.ldx;
-      float ss = 0;
-      for (uint32_t e = tid; e < K; e += GW) ss += xr[e] * xr[e];
-      ss = wave_sum(ss);
-      if (lane == 0) misc[wave * NT + t] = ss;
-    }
-    __syncthreads();
-    if (tid < nt) {
-      float ss = misc[0 * NT + tid] + misc[1 * NT + tid] + misc[2 * NT + tid] + misc[3 * NT + tid];
-      misc[16 + tid] = (float)(1.0 / sqrt((double)(ss / (float)K + a.eps)));
-    }
-    __syncthreads();
-    for (int t = 0; t < NT; t++) s_rms[t] = t < nt ? misc[16 + t] : 0.f;
-  }
+  // ---- prologue: one round of global loads, the activations of nt tokens
+  // staged in registers as items (block b, k-group g) of 8 elements
+  // (4g..4g+3 and 16+4g..16+4g+3), then scaled, split and stored in MFMA
+  // operand order.
+  f4 va[NT][MAXI], vc[NT][MAXI];
   if (PRO == PRO_MERGE) {
-    // Chunk weights exp(m_c - M) and 1/sum(exp(m_c - M) l_c) per (token, head).
-    const uint32_t H = a.heads, SM = a.smax;
-    for (uint32_t th = tid; th < (uint32_t)nt * H; th += GW) {
+    // flash-decoding merge (fused.go K3 hook, kernels_fused.go:150-170):
+    // att = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c per (token, head)
+    const uint32_t H = a.heads, SM = a.smax, pos0 = a.state[0];
+    for (uint32_t th = tid; th < (uint32_t)nt * H; th += bd) {
       uint32_t t = th / H, h = th % H;
-      uint32_t pos = a.state[0] + t0 + t;
-      uint32_t nc = (pos + a.chunk) / a.chunk;
+      uint32_t nc = (pos0 + t0 + t + a.chunk) / a.chunk;
       const float* mlp = a.ml + ((uint64_t)(t0 + t) * H + h) * SM * 2;
       float M = -INFINITY;
       for (uint32_t c = 0; c < nc; c++) M = fmaxf(M, mlp[2 * c]);
@@ -337,35 +332,93 @@ __global__ __launch_bounds__(GW) void gemv_kernel(GemvArgs a) {
       w[SM] = 1.f / l;
     }
     __syncthreads();
-    for (uint32_t i = tid; i < (uint32_t)nt * K; i += GW) {
-      uint32_t t = i / K, e = i % K, h = e / a.hd, dd = e % a.hd;
-      uint32_t pos = a.state[0] + t0 + t;
-      uint32_t nc = (pos + a.chunk) / a.chunk;
-      const float* w = wts + (t * H + h) * (SM + 1);
-      const float* pvp = a.pv + (((uint64_t)(t0 + t) * H + h) * SM) * a.hd + dd;
-      float o = 0;
-      for (uint32_t c = 0; c < nc; c++) o += w[c] * pvp[(uint64_t)c * a.hd];
-      stage[t * K + e] = o * w[SM];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int k = 0; k < MAXI; k++) {
+        uint32_t it = tid + k * bd;
+        f4 A = {0, 0, 0, 0}, C = {0, 0, 0, 0};
+        if (t < nt && it < NI) {
+          uint32_t b = it / 4, g = it % 4, e = b * 32 + 4 * g, h = e / a.hd, dd = e % a.hd;
+          uint32_t nc = (pos0 + t0 + t + a.chunk) / a.chunk;
+          const float* w = wts + (t * H + h) * (SM + 1);
+          const float* pvp = a.pv + (((uint64_t)(t0 + t) * H + h) * SM) * a.hd + dd;
+#pragma unroll 4
+          for (uint32_t c = 0; c < nc; c++) {
+            f4 p0 = *(const f4*)(pvp + (uint64_t)c * a.hd), p1 = *(const f4*)(pvp + (uint64_t)c * a.hd + 16);
+            A += w[c] * p0;
+            C += w[c] * p1;
+          }
+          A *= w[SM];
+          C *= w[SM];
+        }
+        va[t][k] = A;
+        vc[t][k] = C;
+      }
+  } else {
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int k = 0; k < MAXI; k++) {
+        uint32_t it = tid + k * bd;
+        f4 A = {0, 0, 0, 0}, C = {0, 0, 0, 0};
+        if (t < nt && it < NI) {
+          const float* xr = a.x + (uint64_t)(a.xrow0 + t0 + t) * a.ldx + (it / 4) * 32 + 4 * (it % 4);
+          A = *(const f4*)xr;
+          C = *(const f4*)(xr + 16);
+        }
+        va[t][k] = A;
+        vc[t][k] = C;
+      }
+  }
+  if (PRO == PRO_RMS) {
+    // cpu.go:90-96: ss = sum x^2 (f32); s = f32(1/sqrt(f64(ss/n + eps))); h = x*s*w
+    f4 wa[MAXI], wc[MAXI];
+#pragma unroll
+    for (int k = 0; k < MAXI; k++) {
+      uint32_t it = tid + k * bd;
+      wa[k] = wc[k] = f4{0, 0, 0, 0};
+      if (it < NI) {
+        const float* wr = a.nw + (it / 4) * 32 + 4 * (it % 4);
+        wa[k] = *(const f4*)wr;
+        wc[k] = *(const f4*)(wr + 16);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      float ss = 0;
+#pragma unroll
+      for (int k = 0; k < MAXI; k++)
+        for (int i = 0; i < 4; i++) ss += va[t][k][i] * va[t][k][i] + vc[t][k][i] * vc[t][k][i];
+      ss = wave_sum(ss);
+      if (lane == 0) misc[wave * NT + t] = ss;
     }
     __syncthreads();
+    if (tid < nt) {
+      float ss = 0;
+      for (uint32_t w = 0; w < nwv; w++) ss += misc[w * NT + tid];
+      misc[64 + tid] = (float)(1.0 / sqrt((double)(ss / (float)K + a.eps)));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      float s = t < nt ? misc[64 + t] : 0.f;
+#pragma unroll
+      for (int k = 0; k < MAXI; k++)
+        for (int i = 0; i < 4; i++) {
+          va[t][k][i] = __fmul_rn(__fmul_rn(va[t][k][i], s), wa[k][i]);  // cpu.go:96
+          vc[t][k][i] = __fmul_rn(__fmul_rn(vc[t][k][i], s), wc[k][i]);
+        }
+    }
+    __syncthreads();  // misc partials are reused below
   }
-  auto load8 = [&](int t, uint32_t e) -> f4 {  // 4 activations at e (e % 4 == 0)
-    if (PRO == PRO_MERGE) return *(const f4*)(stage + t * K + e);
-    const float* xr = a.x + (uint64_t)(a.xrow0 + t0 + t) * a.ldx + e;
-    f4 v = *(const f4*)xr;
-    if (PRO == PRO_RMS) {
-      f4 w = *(const f4*)(a.nw + e);
-      for (int i = 0; i < 4; i++) v[i] = __fmul_rn(__fmul_rn(v[i], s_rms[t]), w[i]);  // cpu.go:96
-    }
-    return v;
-  };
   // largest magnitude per token -> power-of-two scale
-  for (int t = 0; t < nt; t++) {
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
     float m = 0;
-    for (uint32_t e = tid * 4; e < K; e += GW * 4) {
-      f4 v = load8(t, e);
-      m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-    }
+#pragma unroll
+    for (int k = 0; k < MAXI; k++)
+      for (int i = 0; i < 4; i++) m = fmaxf(m, fmaxf(fabsf(va[t][k][i]), fabsf(vc[t][k][i])));
     m = wave_max(m);
     if (lane == 0) misc[wave * NT + t] = m;
   }
@@ -373,7 +426,8 @@ __global__ __launch_bounds__(GW) void gemv_kernel(GemvArgs a) {
   if (tid < NT) {
     int e = 0;
     if (tid < nt) {
-      float m = fmaxf(fmaxf(misc[tid], misc[NT + tid]), fmaxf(misc[2 * NT + tid], misc[3 * NT + tid]));
+      float m = 0;
+      for (uint32_t w = 0; w < nwv; w++) m = fmaxf(m, misc[w * NT + tid]);
       if (m > 0 && m <= 3.0e38f) {
         int E;
         frexpf(m, &E);
@@ -383,41 +437,38 @@ __global__ __launch_bounds__(GW) void gemv_kernel(GemvArgs a) {
     exps[tid] = e;
   }
   __syncthreads();
-  for (uint32_t it = tid; it < (uint32_t)NT * nb * 4; it += GW) {
-    uint32_t t = it / (nb * 4), rem = it % (nb * 4), b = rem / 4, g = rem % 4;
-    h8 hi = {}, lo = {};
-    if ((int)t < nt) {
-      int ex = exps[t];
-      f4 A = load8(t, b * 32 + 4 * g), C = load8(t, b * 32 + 16 + 4 * g);
-      float v[8] = {A[0], A[2], C[0], C[2], A[1], A[3], C[1], C[3]};
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int ex = exps[t];
+#pragma unroll
+    for (int k = 0; k < MAXI; k++) {
+      uint32_t it = tid + k * bd;
+      if (it >= NI) continue;
+      const f4 A = va[t][k], C = vc[t][k];
+      const float v[8] = {A[0], A[2], C[0], C[2], A[1], A[3], C[1], C[3]};
+      h8 hi, lo;
       for (int i = 0; i < 8; i++) {
         float s = ldexpf(v[i], ex);
         _Float16 h = (_Float16)s;
         hi[i] = h;
         lo[i] = (_Float16)(s - (float)h);
       }
-    }
-    xs[(b * 4 + g) * S + 2 * t] = hi;
-    xs[(b * 4 + g) * S + 2 * t + 1] = lo;
-  }
-  if (QT == LLMHIP_Q4_1) {
-    for (uint32_t it = tid; it < (uint32_t)NT * nb; it += GW) {
-      uint32_t t = it / nb, b = it % nb;
-      float sx = 0;
-      if ((int)t < nt) {
-        for (int j = 0; j < 32; j += 4) {
-          f4 v = load8(t, b * 32 + j);
-          sx += v[0] + v[1] + v[2] + v[3];
-        }
-        sx = ldexpf(sx, exps[t]);
+      xs[it * S + 2 * t] = hi;
+      xs[it * S + 2 * t + 1] = lo;
+      if (QT == LLMHIP_Q4_1) {
+        // block sums sum_j x_j (cpu.go:196-198), scaled like the operand
+        float sx = (A[0] + A[1] + A[2] + A[3]) + (C[0] + C[1] + C[2] + C[3]);
+        sx += __shfl_xor(sx, 1);
+        sx += __shfl_xor(sx, 2);
+        if ((it & 3) == 0) bsum[t * nb + it / 4] = ldexpf(sx, ex);
       }
-      bsum[t * nb + b] = sx;
     }
   }
   __syncthreads();
 
-  // ---- main loop: each wave one 16-row tile over its share of the blocks
-  const uint32_t split = a.split, tpw = 4 / split;
+  // ---- main loop: each wave one 16-row tile over its share of the block
+  // groups; the weights of up to four groups are in flight at once
+  const uint32_t split = a.split, tpw = nwv / split;
   const uint32_t lt = wave / split, sp = wave % split;
   const uint32_t tile = blockIdx.x * tpw + lt;
   const int r = lane & 15, q = lane >> 4;  // B/D column (row in tile), k-group / D row group
@@ -439,44 +490,67 @@ __global__ __launch_bounds__(GW) void gemv_kernel(GemvArgs a) {
         if (2 * q + 1 < NT) acc1 += m * bsum[(2 * q + 1) * nb + b];
       }
     };
-    for (uint32_t g4 = sp; g4 < a.ng; g4 += split) {
-      if (QT == LLMHIP_Q8_0) {
-        uint4 w01 = *(const uint4*)(qt + g4 * 2048 + lane * 16);
-        uint4 w23 = *(const uint4*)(qt + g4 * 2048 + 1024 + lane * 16);
-        uint2 sv = *(const uint2*)(st + g4 * 128 + r * 8);
-        block(4 * g4 + 0, dq8(w01.x, w01.y), sv.x & 0xffff, 0);
-        block(4 * g4 + 1, dq8(w01.z, w01.w), sv.x >> 16, 0);
-        block(4 * g4 + 2, dq8(w23.x, w23.y), sv.y & 0xffff, 0);
-        block(4 * g4 + 3, dq8(w23.z, w23.w), sv.y >> 16, 0);
-      } else if (QT == LLMHIP_Q4_1) {
-        uint4 w = *(const uint4*)(qt + g4 * 1024 + lane * 16);
-        uint4 sv = *(const uint4*)(st + g4 * 256 + r * 16);
-        block(4 * g4 + 0, dq4<true>(w.x), sv.x & 0xffff, sv.x >> 16);
-        block(4 * g4 + 1, dq4<true>(w.y), sv.y & 0xffff, sv.y >> 16);
-        block(4 * g4 + 2, dq4<true>(w.z), sv.z & 0xffff, sv.z >> 16);
-        block(4 * g4 + 3, dq4<true>(w.w), sv.w & 0xffff, sv.w >> 16);
-      } else {
-        uint4 w = *(const uint4*)(qt + g4 * 1024 + lane * 16);
-        uint2 sv = *(const uint2*)(st + g4 * 128 + r * 8);
-        block(4 * g4 + 0, dq4<false>(w.x), sv.x & 0xffff, 0);
-        block(4 * g4 + 1, dq4<false>(w.y), sv.x >> 16, 0);
-        block(4 * g4 + 2, dq4<false>(w.z), sv.y & 0xffff, 0);
-        block(4 * g4 + 3, dq4<false>(w.w), sv.y >> 16, 0);
+    const uint32_t cnt = a.ng > sp ? (a.ng - sp + split - 1) / split : 0;
+    for (uint32_t i0 = 0; i0 < cnt; i0 += 4) {
+      uint4 w0[4], w1[4], sv[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        if (i0 + u >= cnt) continue;
+        const uint32_t g4 = sp + (i0 + u) * split;
+        if (QT == LLMHIP_Q8_0) {
+          w0[u] = ld_stream16(qt + g4 * 2048 + lane * 16);
+          w1[u] = ld_stream16(qt + g4 * 2048 + 1024 + lane * 16);
+        } else {
+          w0[u] = ld_stream16(qt + g4 * 1024 + lane * 16);
+        }
+        if (QT == LLMHIP_Q4_1) {
+          sv[u] = *(const uint4*)(st + g4 * 256 + r * 16);
+        } else {
+          uint2 x2 = *(const uint2*)(st + g4 * 128 + r * 8);
+          sv[u] = uint4{x2.x, x2.y, 0, 0};
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        if (i0 + u >= cnt) continue;
+        const uint32_t b0 = 4 * (sp + (i0 + u) * split);
+        if (QT == LLMHIP_Q8_0) {
+          block(b0 + 0, dq8(w0[u].x, w0[u].y), sv[u].x & 0xffff, 0);
+          block(b0 + 1, dq8(w0[u].z, w0[u].w), sv[u].x >> 16, 0);
+          block(b0 + 2, dq8(w1[u].x, w1[u].y), sv[u].y & 0xffff, 0);
+          block(b0 + 3, dq8(w1[u].z, w1[u].w), sv[u].y >> 16, 0);
+        } else if (QT == LLMHIP_Q4_1) {
+          block(b0 + 0, dq4<true>(w0[u].x), sv[u].x & 0xffff, sv[u].x >> 16);
+          block(b0 + 1, dq4<true>(w0[u].y), sv[u].y & 0xffff, sv[u].y >> 16);
+          block(b0 + 2, dq4<true>(w0[u].z), sv[u].z & 0xffff, sv[u].z >> 16);
+          block(b0 + 3, dq4<true>(w0[u].w), sv[u].w & 0xffff, sv[u].w >> 16);
+        } else {
+          block(b0 + 0, dq4<false>(w0[u].x), sv[u].x & 0xffff, 0);
+          block(b0 + 1, dq4<false>(w0[u].y), sv[u].x >> 16, 0);
+          block(b0 + 2, dq4<false>(w0[u].z), sv[u].y & 0xffff, 0);
+          block(b0 + 3, dq4<false>(w0[u].w), sv[u].y >> 16, 0);
+        }
       }
     }
     if (a.tail && (a.ng % split) == sp) {
       const uint32_t ng = a.ng, tail = a.tail;
-      for (uint32_t j = 0; j < tail; j++) {
-        uint32_t b = 4 * ng + j;
-        const uint8_t* s = st + sc_off<QT>(b, r, ng, tail);
-        uint32_t dbits = s[0] | s[1] << 8, mbits = 0;
-        if (QT == LLMHIP_Q4_1) mbits = s[2] | s[3] << 8;
+      uint32_t qw[3][2], sb[3];
+#pragma unroll
+      for (uint32_t j = 0; j < 3; j++) {
+        if (j >= tail) continue;
+        const uint32_t b = 4 * ng + j;
         const uint8_t* qq = qt + qs_off<QT>(b, lane, ng, tail);
-        if (QT == LLMHIP_Q8_0) {
-          block(b, dq8(*(const uint32_t*)qq, *(const uint32_t*)(qq + 4)), dbits, 0);
-        } else {
-          block(b, dq4<QT == LLMHIP_Q4_1>(*(const uint32_t*)qq), dbits, mbits);
-        }
+        qw[j][0] = *(const uint32_t*)qq;
+        if (QT == LLMHIP_Q8_0) qw[j][1] = *(const uint32_t*)(qq + 4);
+        const uint8_t* s = st + sc_off<QT>(b, r, ng, tail);
+        sb[j] = QT == LLMHIP_Q4_1 ? *(const uint32_t*)s : (uint32_t)*(const uint16_t*)s;
+      }
+#pragma unroll
+      for (uint32_t j = 0; j < 3; j++) {
+        if (j >= tail) continue;
+        const uint32_t b = 4 * ng + j;
+        if (QT == LLMHIP_Q8_0) block(b, dq8(qw[j][0], qw[j][1]), sb[j] & 0xffff, 0);
+        else block(b, dq4<QT == LLMHIP_Q4_1>(qw[j][0]), sb[j] & 0xffff, sb[j] >> 16);
       }
     }
   }
@@ -529,8 +603,10 @@ __global__ __launch_bounds__(GW) void gemv_kernel(GemvArgs a) {
     }
   }
   if (EPI == EPI_ARGMAX) {
-    // (max, lowest index) of token 0 over this workgroup's rows; NaN never
-    // wins (cpu.go:389-397).  Rows are disjoint across workgroups.
+    // (max, lowest index) of token 0 over this workgroup's rows, NaN never
+    // wins (cpu.go:389-397); argmax_kernel combines the workgroups' partials.
+    float* av = misc + 80;
+    uint32_t* ai = (uint32_t*)(misc + 96);
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
     if (rvalid && q == 0 && nt > 0 && vA == vA) {
@@ -540,25 +616,22 @@ __global__ __launch_bounds__(GW) void gemv_kernel(GemvArgs a) {
     for (int o = 8; o > 0; o >>= 1) {
       float ov = __shfl_xor(bv, o);
       uint32_t oi = __shfl_xor(bi, o);
-      if (oi != 0xffffffffu && (bi == 0xffffffffu || ov > bv || (ov == bv && oi < bi))) {
+      if (amax_better(ov, oi, bv, bi)) {
         bv = ov;
         bi = oi;
       }
     }
-    float* av = misc + 32;
-    uint32_t* ai = (uint32_t*)(misc + 40);
     if (lane == 0) {
       av[wave] = bv;
       ai[wave] = bi;
     }
     __syncthreads();
     if (tid == 0) {
-      for (int w = 1; w < 4; w++) {
-        if (ai[w] != 0xffffffffu && (bi == 0xffffffffu || av[w] > bv || (av[w] == bv && ai[w] < bi))) {
+      for (uint32_t w = 1; w < nwv; w++)
+        if (amax_better(av[w], ai[w], bv, bi)) {
           bv = av[w];
           bi = ai[w];
         }
-      }
       a.amax_v[blockIdx.x] = bv;
       a.amax_i[blockIdx.x] = bi;
     }
@@ -621,7 +694,7 @@ static int launch_one(const GemvArgs& a, dim3 grid, uint32_t lds, hipStream_t s)
     LLM_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     big = true;
   }
-  hipLaunchKernelGGL(k, grid, dim3(GW), lds, s, a);
+  hipLaunchKernelGGL(k, grid, dim3(64 * a.waves), lds, s, a);
   LLM_HIP(hipGetLastError());
   return 0;
 }
@@ -634,17 +707,17 @@ static int launch_nt(const GemvArgs& a, int pro, int epi, dim3 grid, uint32_t ld
     case PRO_RMS * 8 + EPI_QKV: return launch_one<QT, NT, PRO_RMS, EPI_QKV>(a, grid, lds, s);
     case PRO_MERGE * 8 + EPI_ACC: return launch_one<QT, NT, PRO_MERGE, EPI_ACC>(a, grid, lds, s);
     case PRO_RMS * 8 + EPI_GATEUP: return launch_one<QT, NT, PRO_RMS, EPI_GATEUP>(a, grid, lds, s);
-    case PRO_RMS * 8 + EPI_ARGMAX: return launch_one<QT, NT, PRO_RMS, EPI_ARGMAX>(a, grid, lds, s);
     case PRO_RMS * 8 + EPI_STORE: return launch_one<QT, NT, PRO_RMS, EPI_STORE>(a, grid, lds, s);
     case PRO_RMS * 8 + EPI_SWIGLU: return launch_one<QT, NT, PRO_RMS, EPI_SWIGLU>(a, grid, lds, s);
   }
+  if (pro == PRO_RMS && epi == EPI_ARGMAX && NT == 1) return launch_one<QT, 1, PRO_RMS, EPI_ARGMAX>(a, grid, lds, s);
   return set_error(LLMHIP_ERR_ARG, "llm: gemv: unsupported prologue/epilogue %d/%d", pro, epi);
 }
 
 template <uint32_t QT>
 int gemv_launch_qt(const GemvArgs& a, int pro, int epi, hipStream_t s) {
   int nt = a.ntok <= 1 ? 1 : a.ntok <= 2 ? 2 : 4;
-  Lds L = lds_layout(nt, pro, QT, a.nb, a.k, a.heads, a.smax);
+  Lds L = lds_layout(nt, pro, QT, a.nb, a.waves, a.heads, a.smax);
   if (L.total > 160 * 1024)
     return set_error(LLMHIP_ERR_ARG, "llm: gemv: k=%u needs %u bytes of LDS", a.k, L.total);
   if (epi == EPI_ARGMAX && a.ntok != 1) return set_error(LLMHIP_ERR_ARG, "llm: gemv: argmax epilogue needs one token");

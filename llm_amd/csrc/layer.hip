@@ -1,6 +1,6 @@
 // The non-matrix kernels of the forward pass: attention over the f32 KV cache
 // in chunks of positions (flash-decoding partials, merged by the O-projection
-// prologue), the final argmax reduction, and the state advance.
+// prologue), greedy sampling and the state advance.
 #include "layer.h"
 
 namespace llmhip {
@@ -25,13 +25,40 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   float* vs = ks + CH * KS;     // [CH][HD]
   float* sc = vs + CH * HD;     // [GQ][CH]
   const float* qg = a.q + (uint64_t)t * a.heads * HD + (uint64_t)g * GQ * HD;
-  for (uint32_t i = tid; i < GQ * HD; i += blockDim.x) qs[i] = qg[i];
   const float* kb = a.kv + (uint64_t)p0 * a.kvd + g * HD;
   const float* vb = a.kv + (uint64_t)a.ctx * a.kvd + (uint64_t)p0 * a.kvd + g * HD;
-  for (uint32_t i = tid; i < L * HD; i += blockDim.x) {
-    uint32_t p = i / HD, d = i % HD;
-    ks[p * KS + d] = kb[(uint64_t)p * a.kvd + d];
-    vs[p * HD + d] = vb[(uint64_t)p * a.kvd + d];
+  // every load of the workgroup in flight at once: q rows, then K and V rows as float4
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const uint32_t HD4 = HD / 4, NQ4 = GQ * HD4, NK4 = L * HD4;
+  constexpr int U = 8;  // float4 of K (and of V) per thread: CH*HD/4 <= 8*256
+  f4 qr[2], kr[U], vr[U];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    uint32_t i = tid + u * blockDim.x;
+    if (i < NQ4) qr[u] = ((const f4*)qg)[i];
+  }
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    uint32_t i = tid + u * blockDim.x;
+    if (i < NK4) {
+      uint32_t p = i / HD4, d = i % HD4;
+      kr[u] = *(const f4*)(kb + (uint64_t)p * a.kvd + 4 * d);
+      vr[u] = *(const f4*)(vb + (uint64_t)p * a.kvd + 4 * d);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    uint32_t i = tid + u * blockDim.x;
+    if (i < NQ4) ((f4*)qs)[i] = qr[u];
+  }
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    uint32_t i = tid + u * blockDim.x;
+    if (i < NK4) {
+      uint32_t p = i / HD4, d = i % HD4;
+      for (int j = 0; j < 4; j++) ks[p * KS + 4 * d + j] = kr[u][j];
+      ((f4*)vs)[p * HD4 + d] = vr[u];
+    }
   }
   __syncthreads();
   // scores: s = (q . k) * scale, the dot product in index order (cpu.go:312-316)
@@ -80,6 +107,10 @@ uint32_t attn_lds_bytes(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t
 
 int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s) {
   if (ntok == 0) return 0;
+  const uint32_t gq = a.heads / a.kv_heads;
+  if (a.hd % 4 || gq * a.hd / 4 > 2 * 256 || a.chunk * a.hd / 4 > 8 * 256)
+    return set_error(LLMHIP_ERR_ARG, "llm: attention: %u heads per KV head of %u, chunk %u not supported", gq, a.hd,
+                     a.chunk);
   uint32_t lds = attn_lds_bytes(a.heads, a.kv_heads, a.hd, a.chunk);
   hipLaunchKernelGGL(attn_kernel, dim3(a.smax, a.kv_heads, ntok), dim3(256), lds, s, a);
   LLM_HIP(hipGetLastError());
@@ -88,29 +119,50 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s) {
 
 // Greedy sampling (cpu.go:389-397): the lowest index of the largest logit,
 // NaN never wins, and a NaN logit 0 is never displaced.  Combines the
-// per-workgroup partials of the head's matvec, writes the token to
-// tokens[step + adv] and out[0], then advances (pos, step) by adv.
-__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
-                                                     uint32_t n, const float* __restrict__ logits,
-                                                     int32_t* __restrict__ tokens, int32_t* __restrict__ outb,
-                                                     uint32_t* __restrict__ state, uint32_t adv) {
-  __shared__ float sv[4];
-  __shared__ uint32_t si[4];
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float bv = -INFINITY;
-  uint32_t bi = 0xffffffffu;
-  for (uint32_t i = tid; i < n; i += 256) {
-    float v = pv[i];
-    uint32_t ix = pi[i];
-    if (ix != 0xffffffffu && (bi == 0xffffffffu || v > bv || (v == bv && ix < bi))) {
-      bv = v;
-      bi = ix;
+// per-workgroup partials of the head's matvec (all loads in flight at once),
+// writes the token to tokens[step + adv] and out[0] (kernels.go:389-392),
+// then advances (pos, step) by adv (kernels.go:397-415).
+__device__ __forceinline__ bool amax_better(float v, uint32_t i, float bv, uint32_t bi) {
+  return i != 0xffffffffu && (bi == 0xffffffffu || v > bv || (v == bv && i < bi));
+}
+
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
+                                                      uint32_t n, const float* __restrict__ logits,
+                                                      int32_t* __restrict__ tokens, int32_t* __restrict__ outb,
+                                                      uint32_t* __restrict__ state, uint32_t adv) {
+  __shared__ float sv[16];
+  __shared__ uint32_t si[16];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  constexpr int U = 8;
+  float v[U];
+  uint32_t ix[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    uint32_t i = tid + u * blockDim.x;
+    v[u] = -INFINITY;
+    ix[u] = 0xffffffffu;
+    if (i < n) {
+      v[u] = pv[i];
+      ix[u] = pi[i];
     }
   }
+  float bv = -INFINITY;
+  uint32_t bi = 0xffffffffu;
+#pragma unroll
+  for (int u = 0; u < U; u++)
+    if (amax_better(v[u], ix[u], bv, bi)) {
+      bv = v[u];
+      bi = ix[u];
+    }
+  for (uint32_t i = tid + U * blockDim.x; i < n; i += blockDim.x)
+    if (amax_better(pv[i], pi[i], bv, bi)) {
+      bv = pv[i];
+      bi = pi[i];
+    }
   for (int o = 32; o > 0; o >>= 1) {
     float ov = __shfl_xor(bv, o);
     uint32_t oi = __shfl_xor(bi, o);
-    if (oi != 0xffffffffu && (bi == 0xffffffffu || ov > bv || (ov == bv && oi < bi))) {
+    if (amax_better(ov, oi, bv, bi)) {
       bv = ov;
       bi = oi;
     }
@@ -121,8 +173,8 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ p
   }
   __syncthreads();
   if (tid == 0) {
-    for (int w = 1; w < 4; w++)
-      if (si[w] != 0xffffffffu && (bi == 0xffffffffu || sv[w] > bv || (sv[w] == bv && si[w] < bi))) {
+    for (uint32_t w = 1; w < nw; w++)
+      if (amax_better(sv[w], si[w], bv, bi)) {
         bv = sv[w];
         bi = si[w];
       }
@@ -138,7 +190,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ p
 
 int argmax_launch(const float* pv, const uint32_t* pi, uint32_t n, const float* logits, int32_t* tokens,
                   int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s) {
-  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, s, pv, pi, n, logits, tokens, outb, state, adv);
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, pv, pi, n, logits, tokens, outb, state, adv);
   LLM_HIP(hipGetLastError());
   return 0;
 }

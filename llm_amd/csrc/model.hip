@@ -36,6 +36,13 @@ struct Layer {
   float* kv = nullptr;    // [2][ctx][kvd]
 };
 
+struct ProfRec {
+  const char* cls;
+  int layer;
+  uint64_t bytes;
+  hipEvent_t a, b;
+};
+
 struct Model {
   int device = 0;
   llmhip_limits lim{};
@@ -66,7 +73,24 @@ struct Model {
   uint32_t pos = 0;  // host mirror of state[0] (== state[1])
   bool prompted = false;
   uint32_t dispatches = 0;  // counter while recording
+  std::vector<ProfRec>* prof = nullptr;  // eager profiling: events around every launch
+  int cur_layer = -1;
 };
+
+// Brackets one launch with HIP events on the model's stream when profiling.
+template <class F>
+static int launch_rec(Model& m, const char* cls, uint64_t bytes, F&& launch) {
+  m.dispatches++;
+  if (!m.prof) return launch();
+  ProfRec r{cls, m.cur_layer, bytes, nullptr, nullptr};
+  LLM_HIP(hipEventCreate(&r.a));
+  LLM_HIP(hipEventCreate(&r.b));
+  m.prof->push_back(r);
+  LLM_HIP(hipEventRecord(r.a, m.stream));
+  LLM_TRY(launch());
+  LLM_HIP(hipEventRecord(r.b, m.stream));
+  return 0;
+}
 
 static int dalloc(Model& m, void** p, uint64_t bytes) {
   bytes = (bytes + 255) & ~255ull;
@@ -295,10 +319,9 @@ static int route(Model& m, const std::string& name, QMat** q, uint64_t* row_off,
 
 static bool skipped(const Model& m, const char* cls) { return m.skip.count("all") || m.skip.count(cls); }
 
-static int gemv_rec(Model& m, const char* cls, const GemvArgs& a, uint32_t qtype, int pro, int epi) {
+static int gemv_rec(Model& m, const char* cls, const GemvArgs& a, uint32_t qtype, int pro, int epi, uint64_t bytes) {
   if (skipped(m, cls)) return 0;
-  m.dispatches++;
-  return gemv_launch(a, qtype, pro, epi, m.stream);
+  return launch_rec(m, cls, bytes, [&]() { return gemv_launch(a, qtype, pro, epi, m.stream); });
 }
 
 static GemvArgs base_args(const Model& m, const QMat& q, uint32_t ntok) {
@@ -332,7 +355,7 @@ static int rec_k1(Model& m, const Layer& L, uint32_t ntok) {
     a.ctx = m.ctx;
     a.neox = c.rope_neox;
     a.row_base = L.qkv_base[i];
-    LLM_TRY(gemv_rec(m, "k1", a, L.qkv_type[i], PRO_RMS, EPI_QKV));
+    LLM_TRY(gemv_rec(m, "k1", a, L.qkv_type[i], PRO_RMS, EPI_QKV, L.qkv[i].g.gguf_bytes()));
   }
   return 0;
 }
@@ -357,8 +380,9 @@ static AttnArgs attn_args(const Model& m, const Layer& L) {
 
 static int rec_k2(Model& m, const Layer& L, uint32_t ntok) {
   if (skipped(m, "k2")) return 0;
-  m.dispatches++;
-  return attn_launch(attn_args(m, L), ntok, m.stream);
+  // KV bytes read for the last token of the pass (the decode step's one token)
+  uint64_t bytes = 2ull * (m.pos + 1) * m.kvd * 4;
+  return launch_rec(m, "k2", bytes, [&]() { return attn_launch(attn_args(m, L), ntok, m.stream); });
 }
 
 static int rec_k3(Model& m, const Layer& L, uint32_t ntok) {
@@ -367,7 +391,7 @@ static int rec_k3(Model& m, const Layer& L, uint32_t ntok) {
   a.ml = m.ml;
   a.y = m.x;
   a.ldy = m.cfg.embd;
-  return gemv_rec(m, "k3", a, L.o.g.q.type, PRO_MERGE, EPI_ACC);
+  return gemv_rec(m, "k3", a, L.o.g.q.type, PRO_MERGE, EPI_ACC, L.o.g.gguf_bytes());
 }
 
 static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
@@ -379,7 +403,7 @@ static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
     a.nw = L.ffn_norm;
     a.y = m.act;
     a.ff = c.ff;
-    return gemv_rec(m, "k4", a, L.gu[0].g.q.type, PRO_RMS, EPI_GATEUP);
+    return gemv_rec(m, "k4", a, L.gu[0].g.q.type, PRO_RMS, EPI_GATEUP, L.gu[0].g.gguf_bytes());
   }
   GemvArgs g = base_args(m, L.gu[0], ntok);
   g.x = m.x;
@@ -387,7 +411,7 @@ static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
   g.nw = L.ffn_norm;
   g.y = m.gbuf;
   g.ldy = c.ff;
-  LLM_TRY(gemv_rec(m, "k4", g, L.gu[0].g.q.type, PRO_RMS, EPI_STORE));
+  LLM_TRY(gemv_rec(m, "k4", g, L.gu[0].g.q.type, PRO_RMS, EPI_STORE, L.gu[0].g.gguf_bytes()));
   GemvArgs u = base_args(m, L.gu[1], ntok);
   u.x = m.x;
   u.ldx = c.embd;
@@ -395,7 +419,7 @@ static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
   u.y = m.act;
   u.ldy = c.ff;
   u.aux = m.gbuf;
-  return gemv_rec(m, "k4", u, L.gu[1].g.q.type, PRO_RMS, EPI_SWIGLU);
+  return gemv_rec(m, "k4", u, L.gu[1].g.q.type, PRO_RMS, EPI_SWIGLU, L.gu[1].g.gguf_bytes());
 }
 
 static int rec_k5(Model& m, const Layer& L, uint32_t ntok) {
@@ -404,10 +428,16 @@ static int rec_k5(Model& m, const Layer& L, uint32_t ntok) {
   a.ldx = m.cfg.ff;
   a.y = m.x;
   a.ldy = m.cfg.embd;
-  return gemv_rec(m, "k5", a, L.down.g.q.type, PRO_PLAIN, EPI_ACC);
+  return gemv_rec(m, "k5", a, L.down.g.q.type, PRO_PLAIN, EPI_ACC, L.down.g.gguf_bytes());
 }
 
-static GemvArgs head_args(const Model& m, uint32_t xrow) {
+static int rec_adv(Model& m, uint32_t n) {
+  if (skipped(m, "adv")) return 0;
+  m.cur_layer = -1;
+  return launch_rec(m, "adv", 0, [&]() { return advance_launch(m.state, n, m.stream); });
+}
+
+static GemvArgs head_args(const Model& m, uint32_t xrow, uint32_t adv) {
   const QMat& w = m.tied ? m.embd : m.out;
   GemvArgs a = base_args(m, w, 1);
   a.x = m.x;
@@ -418,31 +448,36 @@ static GemvArgs head_args(const Model& m, uint32_t xrow) {
   a.ldy = m.cfg.vocab;
   a.amax_v = m.amax_v;
   a.amax_i = m.amax_i;
+  (void)adv;
   return a;
 }
 
+// The final RMSNorm, the logits and per-workgroup argmax partials of the last
+// token of the pass (recordHead, fused.go:269-289), then the sampling kernel,
+// which writes tokens[step + adv] and advances the state.  With "argmax"
+// skipped the state still advances.
 static int rec_head(Model& m, uint32_t xrow, uint32_t adv) {
   const QMat& w = m.tied ? m.embd : m.out;
-  GemvArgs a = head_args(m, xrow);
-  LLM_TRY(gemv_rec(m, "head", a, w.g.q.type, PRO_RMS, EPI_ARGMAX));
-  if (skipped(m, "argmax")) return 0;
-  m.dispatches++;
-  return argmax_launch(m.amax_v, m.amax_i, gemv_groups(a), m.logits, m.tokens, m.outb, m.state, adv, m.stream);
+  GemvArgs a = head_args(m, xrow, adv);
+  m.cur_layer = -1;
+  LLM_TRY(gemv_rec(m, "head", a, w.g.q.type, PRO_RMS, EPI_ARGMAX, w.g.gguf_bytes()));
+  if (skipped(m, "argmax")) return rec_adv(m, adv);
+  uint32_t groups = gemv_groups(a);
+  return launch_rec(m, "argmax", 8ull * groups, [&]() {
+    return argmax_launch(m.amax_v, m.amax_i, groups, m.logits, m.tokens, m.outb, m.state, adv, m.stream);
+  });
 }
 
-static int rec_adv(Model& m, uint32_t n) {
-  if (skipped(m, "adv")) return 0;
-  m.dispatches++;
-  return advance_launch(m.state, n, m.stream);
-}
 
 // One pass of ntok tokens at positions state[0] .. state[0]+ntok-1: the
 // embedding, the layers, and (head) the logits and the sampled token of the
 // last one, which goes to tokens[step + ntok]; state advances by ntok.
 static int record_pass(Model& m, uint32_t ntok, bool head) {
   if (!skipped(m, "embed")) {
-    m.dispatches++;
-    LLM_TRY(embed_launch(m.embd, m.tokens, m.state, m.x, ntok, m.stream));
+    m.cur_layer = -1;
+    uint64_t row = (uint64_t)m.embd.g.nb * m.embd.g.q.block_bytes;
+    LLM_TRY(launch_rec(m, "embed", row * ntok,
+                       [&]() { return embed_launch(m.embd, m.tokens, m.state, m.x, ntok, m.stream); }));
   }
   int nl = m.cfg.layers;
   if (m.layers_limit != 0 && m.layers_limit < nl) {
@@ -451,6 +486,7 @@ static int record_pass(Model& m, uint32_t ntok, bool head) {
   }
   for (int l = 0; l < nl; l++) {
     const Layer& L = m.layers[l];
+    m.cur_layer = l;
     LLM_TRY(rec_k1(m, L, ntok));
     LLM_TRY(rec_k2(m, L, ntok));
     LLM_TRY(rec_k3(m, L, ntok));
@@ -787,9 +823,9 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
   std::set<std::string> saved = m.skip;
   m.skip.clear();
   auto one = [&]() -> int {
-    if (k == "head") {
+    if (k == "head") {  // without the sampling: repeated launches must not advance the state
       const QMat& w = m.tied ? m.embd : m.out;
-      return gemv_launch(head_args(m, 0), w.g.q.type, PRO_RMS, EPI_ARGMAX, m.stream);
+      return gemv_launch(head_args(m, 0, 0), w.g.q.type, PRO_RMS, EPI_STORE, m.stream);
     }
     if (k == "k1") return rec_k1(m, L, 1);
     if (k == "k2") return rec_k2(m, L, 1);
@@ -822,6 +858,52 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
   *avg_us = ms * 1000.f / (float)iters;
   if (bytes) *bytes = b;
   return 0;
+}
+
+int llmhip_model_profile(llmhip_model* h, int tokens, llmhip_kernel_time* out, int cap, int* n) {
+  clear_error();
+  Model& m = *h->m;
+  *n = 0;
+  if (!m.prompted) return set_error(LLMHIP_ERR_STATE, "llm: profile before a prompt");
+  if (tokens < 1 || m.pos + (uint32_t)tokens > m.ctx)
+    return set_error(LLMHIP_ERR_CONTEXT, "llm: %d profiled tokens exceed the context", tokens);
+  LLM_HIP(hipSetDevice(m.device));
+  LLM_HIP(hipStreamSynchronize(m.stream));
+  int rc = 0;
+  for (int t = 0; t < tokens && rc == 0; t++) {
+    std::vector<ProfRec> recs;
+    m.prof = &recs;
+    rc = record_pass(m, 1, true);
+    m.prof = nullptr;
+    if (hipStreamSynchronize(m.stream) != hipSuccess && rc == 0)
+      rc = set_error(LLMHIP_ERR_DEVICE, "llm: profile step failed");
+    if (rc == 0) {
+      m.pos++;
+      m.stats.tokens++;
+      m.stats.dispatches += (int64_t)recs.size();
+      m.stats.submits++;
+    }
+    if (rc == 0 && t == tokens - 1) {
+      int k = 0;
+      for (auto& r : recs) {
+        if (k >= cap) break;
+        llmhip_kernel_time& o = out[k++];
+        memset(o.cls, 0, sizeof o.cls);
+        strncpy(o.cls, r.cls, sizeof o.cls - 1);
+        o.layer = r.layer;
+        o.bytes = r.bytes;
+        float ms = 0;
+        (void)hipEventElapsedTime(&ms, r.a, r.b);
+        o.us = ms * 1000.f;
+      }
+      *n = k;
+    }
+    for (auto& r : recs) {
+      if (r.a) (void)hipEventDestroy(r.a);
+      if (r.b) (void)hipEventDestroy(r.b);
+    }
+  }
+  return rc;
 }
 
 void llmhip_model_free(llmhip_model* h) {

@@ -4,6 +4,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "gemv.h"
 
@@ -69,25 +70,33 @@ void gemv_bind(GemvArgs* a, const QMat& m) {
   a->map_seg0 = m.map_seg0;
   a->map_seg1 = m.map_seg1;
   a->ff = m.ff;
-  a->split = gemv_pick_split(a->tiles, a->ng);
+  gemv_pick(a->tiles, a->ng, a->tail, a->nb, &a->split, &a->waves);
 }
 
-uint32_t gemv_pick_split(uint32_t tiles, uint32_t ng) {
-  // Enough waves to cover 256 CUs several times over: split the blocks of
-  // a tile over 2 or 4 waves when the matrix has few tiles.
-  if (tiles < 512 && ng >= 4) return 4;
-  if (tiles < 1024 && ng >= 2) return 2;
-  return 1;
+void gemv_pick(uint32_t tiles, uint32_t ng, uint32_t tail, uint32_t nb, uint32_t* split, uint32_t* waves) {
+  // Aim for >= 2048 waves (8 per CU) so the loads of small matrices are all
+  // in flight at once: split a tile's block groups over up to 16 waves, each
+  // keeping at least one group.
+  uint32_t groups = ng + (tail ? 1 : 0), s = 1;
+  while (s < 16 && tiles * s < 2048 && 2 * s <= groups) s *= 2;
+  // the prologue stages at most two 8-element items per thread
+  uint32_t w = 4;
+  while (w < 16 && (w < s || nb * 4 > 2 * 64 * w)) w *= 2;
+  *split = s;
+  *waves = w;
 }
 
 uint32_t gemv_groups(const GemvArgs& a) {
-  uint32_t tpw = 4 / a.split;
+  uint32_t tpw = a.waves / a.split;
   return (a.tiles + tpw - 1) / tpw;
 }
 
 int gemv_launch(const GemvArgs& a, uint32_t qtype, int pro, int epi, hipStream_t s) {
   if (a.ntok == 0) return 0;
-  if (a.split != 1 && a.split != 2 && a.split != 4) return set_error(LLMHIP_ERR_ARG, "llm: gemv: split %u", a.split);
+  if (a.split == 0 || a.split > 16 || (a.split & (a.split - 1)) || a.waves % a.split || a.waves > 16)
+    return set_error(LLMHIP_ERR_ARG, "llm: gemv: split %u over %u waves", a.split, a.waves);
+  if ((uint64_t)a.nb * 4 > 2ull * 64 * a.waves)
+    return set_error(LLMHIP_ERR_ARG, "llm: gemv: k=%u is too long for %u waves", a.k, a.waves);
   switch (qtype) {
     case LLMHIP_Q4_0: return gemv_launch_qt<LLMHIP_Q4_0>(a, pro, epi, s);
     case LLMHIP_Q4_1: return gemv_launch_qt<LLMHIP_Q4_1>(a, pro, epi, s);
@@ -292,8 +301,7 @@ int llmhip_qmat_bench(llmhip_qmat* const* mats, int count, const float* x_dev, f
   clear_error();
   if (count < 1 || iters < 1) return set_error(LLMHIP_ERR_ARG, "llm: bench of %d matrices, %d iterations", count, iters);
   hipStream_t s = (hipStream_t)hip_stream;
-  GemvArgs args[64];
-  if (count > 64) return set_error(LLMHIP_ERR_ARG, "llm: bench of more than 64 matrices");
+  std::vector<GemvArgs> args((size_t)count);
   for (int i = 0; i < count; i++) {
     LLM_TRY(qmat_gemv_args(mats[i], x_dev, y_dev, n, &args[i]));
     if (mats[i]->m.g.q.type != mats[0]->m.g.q.type || mats[i]->m.g.rows != mats[0]->m.g.rows ||
@@ -316,6 +324,25 @@ int llmhip_qmat_bench(llmhip_qmat* const* mats, int count, const float* x_dev, f
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
   *avg_us = ms * 1000.f / (float)iters;
+  return 0;
+}
+
+int llmhip_qmat_clone(const llmhip_qmat* q, llmhip_qmat** out) {
+  clear_error();
+  *out = nullptr;
+  llmhip_qmat* c = nullptr;
+  LLM_TRY(llmhip_qmat_create(q->m.device, q->m.g.q.type, q->m.g.rows, q->m.g.k, &c));
+  c->m.map = q->m.map;
+  c->m.map_hd = q->m.map_hd;
+  c->m.map_seg0 = q->m.map_seg0;
+  c->m.map_seg1 = q->m.map_seg1;
+  c->m.ff = q->m.ff;
+  if (hipMemcpy(c->m.qs, q->m.qs, q->m.g.qs_bytes(), hipMemcpyDeviceToDevice) != hipSuccess ||
+      hipMemcpy(c->m.sc, q->m.sc, q->m.g.sc_bytes(), hipMemcpyDeviceToDevice) != hipSuccess) {
+    llmhip_qmat_free(c);
+    return set_error(LLMHIP_ERR_DEVICE, "llm: clone copy failed");
+  }
+  *out = c;
   return 0;
 }
 

@@ -54,6 +54,15 @@ class QMat:
                                      int(accumulate), _stream(stream)))
         return y
 
+    def clone(self):
+        """A device-to-device copy (for rotating benchmark copies)."""
+        c = QMat.__new__(QMat)
+        c.qtype, c.rows, c.k, c.device = self.qtype, self.rows, self.k, self.device
+        h = ctypes.c_void_p()
+        check(lib().llmhip_qmat_clone(self._h, ctypes.byref(h)))
+        c._h = h
+        return c
+
     @property
     def nbytes(self):
         return lib().llmhip_qmat_bytes(self._h)

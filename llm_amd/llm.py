@@ -218,6 +218,15 @@ class GPU:
         check(lib().llmhip_model_bench_kernel(self._m, kernel.encode(), iters, ctypes.byref(us), ctypes.byref(b)))
         return us.value, b.value
 
+    def profile(self, tokens=3, cap=4096):
+        """Per-launch device times of one decode step, taken with HIP events on
+        the model's stream after `tokens - 1` warm steps: [(cls, layer, bytes, us)].
+        Advances the generation like `tokens` decode steps."""
+        arr = (_lib.KernelTime * cap)()
+        n = ctypes.c_int()
+        check(lib().llmhip_model_profile(self._m, tokens, arr, cap, ctypes.byref(n)))
+        return [(r.cls.decode(), r.layer, r.bytes, r.us) for r in arr[:n.value]]
+
     def close(self):
         if getattr(self, "_h", None):
             lib().llm_gpu_free(self._h)
