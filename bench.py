@@ -69,34 +69,52 @@ def generation(args):
                          "min": min(r.Generated / r.Decode for r in rounds),
                          "max": max(r.Generated / r.Decode for r in rounds)},
     }
-    # per-kernel device times of one decode step, in the decode loop's cache state
+    # per-kernel device times: each decode kernel class launched back to back
+    # across the 24 layers between HIP events on the model's stream
     g.Generate(prompt, 1, -1)
-    prof = g.profile(tokens=4)
+    per_tok = {"k1": spec.layers, "k2": spec.layers, "k3": spec.layers, "k4": spec.layers, "k5": spec.layers,
+               "head": 1}
     classes = {}
-    for cls, layer, nbytes, us in prof:
-        c = classes.setdefault(cls, {"launches": 0, "us": 0.0, "bytes": 0})
-        c["launches"] += 1
-        c["us"] += us
-        c["bytes"] += nbytes
-    for c in classes.values():
-        c["avg_us"] = c["us"] / c["launches"]
-        c["gbps"] = c["bytes"] / c["us"] * 1e-3 if c["us"] > 0 and c["bytes"] else None
-    step_kernel_us = sum(c["us"] for c in classes.values())
-    weights = {k: v for k, v in classes.items() if k in ("k1", "k3", "k4", "k5", "head")}
-    dom = max(weights, key=lambda k: weights[k]["us"])
+    for cls, n in per_tok.items():
+        us, nbytes = g.bench_kernel(cls, 240 if cls != "head" else 50)
+        classes[cls] = {"launches_per_token": n, "avg_us": round(us, 3), "bytes": nbytes,
+                        "us_per_token": round(us * n, 2),
+                        "gbps": round(nbytes / us * 1e-3, 1) if nbytes else None}
+    step_kernel_us = sum(c["us_per_token"] for c in classes.values())
+    dom = max(classes, key=lambda k: classes[k]["us_per_token"])
     d = classes[dom]
-    achieved = d["bytes"] / d["us"] * 1e-3
+    achieved = d["bytes"] / d["avg_us"] * 1e-3
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                "bytes_per_launch": d["bytes"] // d["launches"], "avg_us": round(d["avg_us"], 3)}
-    gemv_all = sum(weights[k]["bytes"] for k in weights) / sum(weights[k]["us"] for k in weights) * 1e-3
+                "bytes_per_launch": d["bytes"], "avg_us": d["avg_us"]}
+    w = [k for k in classes if k != "k2"]
+    gemv_all = sum(classes[k]["bytes"] * classes[k]["launches_per_token"] for k in w) / \
+        sum(classes[k]["us_per_token"] for k in w) * 1e-3
+    dispatches = round(sum(r.Dispatches for r in rounds) / max(1, sum(r.Generated for r in rounds)), 1)
     return g, {
         "value": dec, "prefill": pre, "wall": wall, "rounds": per_round, "ms_per_step": wall / args.steps * 1e3,
-        "classes": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                    for k, v in classes.items()},
-        "step_kernel_us": step_kernel_us, "roofline": roofline, "gemv_aggregate_gbps": gemv_all,
-        "dispatches_per_token": len(prof),
+        "classes": classes, "step_kernel_us": step_kernel_us, "roofline": roofline,
+        "gemv_aggregate_gbps": gemv_all, "dispatches_per_token": dispatches,
     }
+
+
+def long_context(args):
+    """2048-token prompt (32 chunks), 512 greedy tokens, ctx 4096, mixed types."""
+    from llm_amd import llm, synth
+    spec = synth.qwen25_mixed(seed=0)
+    g = llm.NewGPU(0, None, synth.cached(spec), 4096)
+    prompt = list(synth.prompt(0, 2048, spec.vocab))
+    g.Generate(prompt, 8, -1)
+    tm = g.Generate(prompt, 512, -1)
+    us, nbytes = g.bench_kernel("k2", 96)
+    g.close()
+    res = {"workload": "BASELINE config 4: qwen2.5-0.5b shape, Q4_1 ffn_down on odd layers, Q8_0 head, 2048-token "
+                       "prompt, 512 greedy tokens, ctx 4096",
+           "prefill_tok_s": round(tm.PromptTokens / tm.Prefill, 1), "decode_tok_s": round(tm.Generated / tm.Decode, 1),
+           "attention_at_end": {"avg_us": round(us, 2), "kv_bytes": nbytes, "gbps": round(nbytes / us * 1e-3, 1)}}
+    log(f"long context: prefill {res['prefill_tok_s']} tok/s, decode {res['decode_tok_s']} tok/s, "
+        f"attention {us:.1f} us for {nbytes} KV bytes")
+    return res
 
 
 def sweep(args):
@@ -163,6 +181,7 @@ def main():
     ap.add_argument("--ctx", type=int, default=512)
     ap.add_argument("--hbm-bytes", type=int, default=640 << 20, help="rotated copies per sweep shape")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-long", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     args = ap.parse_args()
@@ -189,9 +208,11 @@ def main():
         "rounds": r["rounds"],
         "roofline": r["roofline"],
         "decode_step": {"kernel_us": round(r["step_kernel_us"], 2), "wall_us": round(1e6 / r["value"], 2),
-                        "dispatches": r["dispatches_per_token"],
+                        "dispatches_per_token": r["dispatches_per_token"],
                         "gemv_aggregate_gbps": round(r["gemv_aggregate_gbps"], 1), "classes": r["classes"]},
     }
+    if not args.no_long:
+        res["long_context"] = long_context(args)
     if not args.no_sweep:
         res["gemv_sweep"] = sweep(args)
     if not args.no_cpu:

@@ -175,9 +175,12 @@ LLMHIP_API int llmhip_model_set_layers(llmhip_model* m, int layers);
  * embed, k1, k2, k3, k4, k5, head, argmax, adv, or all.  Output is garbage then. */
 LLMHIP_API int llmhip_model_set_skip(llmhip_model* m, const char* classes);
 /* Average device microseconds of one launch of a kernel of the decode step,
- * launched `iters` times back-to-back on the model's stream between hipEvents,
- * with the arguments it has in the graph: "head", or "k1".."k5" of layer 0.
- * bytes receives its algorithmic bytes (GGUF weight bytes + KV bytes read). */
+ * launched `iters` times back-to-back on the model's stream between hipEvents
+ * with the arguments it has in the decode graph: "head", or "k1".."k5", launch
+ * i using layer i % layers (so consecutive launches read different weights).
+ * bytes receives its algorithmic bytes per launch (GGUF weight bytes; k2: the
+ * KV bytes read at the current position).  It overwrites the activations and
+ * the cache row at the current position: run it between generations. */
 LLMHIP_API int llmhip_model_bench_kernel(llmhip_model* m, const char* kernel, int iters, float* avg_us,
                                          uint64_t* bytes);
 /* One kernel launch timed by llmhip_model_profile. */
@@ -190,8 +193,9 @@ typedef struct llmhip_kernel_time {
 /* Run `tokens` decode steps (>= 1) launching each kernel directly, with HIP
  * events recorded on the model's stream around every launch, and return the
  * launches of the last step (at most cap; *n their count).  Advances the
- * model like llmhip_model_decode(tokens), so the per-kernel times are taken
- * with the caches as the decode loop leaves them. */
+ * model like llmhip_model_decode(tokens).  The times include each launch's
+ * dispatch latency (~2-3 us), so they rank kernels; llmhip_model_bench_kernel
+ * measures durations. */
 LLMHIP_API int llmhip_model_profile(llmhip_model* m, int tokens, llmhip_kernel_time* out, int cap, int* n);
 LLMHIP_API void llmhip_model_free(llmhip_model* m);
 

@@ -73,7 +73,35 @@ struct GemvArgs {
   float* amax_v;  // EPI_ARGMAX: per-workgroup partials
   uint32_t* amax_i;
   const float* aux;  // EPI_SWIGLU: the gate values
+  // prefill (gemm_kernel): activations prepared once per launch by prep_kernel
+  void* xp;        // [tg][nb][64 lanes] 16-byte MFMA operands (hi/lo f16 of 8 tokens)
+  int32_t* xexp;   // [tg*8] power-of-two scale per token
+  float* xbsum;    // [tg*8][nb] scaled block sums (Q4_1)
+  uint32_t tg;     // token groups of 8
 };
+
+// Bytes of the prepared-activation buffers for ntok tokens of k inputs.
+inline uint64_t xprep_bytes(uint32_t ntok, uint32_t k) {
+  uint64_t tg = (ntok + 7) / 8, nb = k / 32;
+  return tg * nb * 64 * 16 + tg * 8 * 4 + tg * 8 * nb * 4 + 3 * 256;
+}
+// Point a.xp / a.xexp / a.xbsum into one buffer of xprep_bytes.
+inline void xprep_bind(GemvArgs* a, void* buf) {
+  uint64_t tg = (a->ntok + 7) / 8, nb = a->nb;
+  char* p = (char*)buf;
+  a->xp = p;
+  p += (tg * nb * 64 * 16 + 255) & ~255ull;
+  a->xexp = (int32_t*)p;
+  p += (tg * 8 * 4 + 255) & ~255ull;
+  a->xbsum = (float*)p;
+  a->tg = (uint32_t)tg;
+}
+// Tokens at or above which the prefill kernel pair (prep + gemm) runs.
+constexpr uint32_t GEMM_MIN_TOKENS = 5;
+// The prefill kernel pair: prep_kernel stages the activations (prologue `pro`)
+// once for the launch, gemm_kernel runs every weight tile over all tokens.
+int prep_launch(const GemvArgs& a, int pro, hipStream_t s);
+int gemm_launch(const GemvArgs& a, uint32_t qtype, int epi, hipStream_t s);
 
 // Bytes of LDS a launch needs, and whether the shape is supported.
 int gemv_launch(const GemvArgs& a, uint32_t qtype, int pro, int epi, hipStream_t s);
@@ -118,6 +146,8 @@ int repack_launch_qt(const QMat& m, const uint8_t* raw_dev, uint64_t n, uint64_t
 template <uint32_t QT>
 int dequant_launch_qt(const QMat& m, float* out, uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1, uint32_t ff,
                       hipStream_t s);
+template <uint32_t QT>
+int gemm_launch_qt(const GemvArgs& a, int epi, hipStream_t s);
 template <uint32_t QT>
 int embed_launch_qt(const QMat& m, const int32_t* tokens, const uint32_t* state, float* x, uint32_t ntok,
                     hipStream_t s);

@@ -290,6 +290,90 @@ __device__ __forceinline__ bool amax_better(float v, uint32_t i, float bv, uint3
   return i != 0xffffffffu && (bi == 0xffffffffu || v > bv || (v == bv && i < bi));
 }
 
+// The per-row epilogue of both matrix kernels.  The lane holds row r of tile
+// `tile` for two tokens of the launch (tokA, tokB; okA/okB say whether they
+// exist), already unscaled.  Every lane of the wave must call it: the RoPE and
+// SwiGLU epilogues exchange values between lanes.
+template <int EPI>
+__device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, int r, bool active, uint32_t tokA,
+                                             bool okA, float vA, uint32_t tokB, bool okB, float vB) {
+  const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
+  const bool rvalid = active && lr < a.rows;
+  if (EPI == EPI_SWIGLU) {
+    // act = g / (1 + exp(-g)) * u (cpu.go:345) with g from the gate's own launch
+    if (rvalid) {
+      if (okA) {
+        uint64_t o = (uint64_t)tokA * a.ldy + lr;
+        float gg = a.aux[o];
+        a.y[o] = gg / (1.f + expf(-gg)) * vA;
+      }
+      if (okB) {
+        uint64_t o = (uint64_t)tokB * a.ldy + lr;
+        float gg = a.aux[o];
+        a.y[o] = gg / (1.f + expf(-gg)) * vB;
+      }
+    }
+  }
+  if (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_ARGMAX) {
+    if (rvalid) {
+      if (okA) {
+        float* y = a.y + (uint64_t)tokA * a.ldy + lr;
+        *y = EPI == EPI_ACC ? *y + vA : vA;
+      }
+      if (okB) {
+        float* y = a.y + (uint64_t)tokB * a.ldy + lr;
+        *y = EPI == EPI_ACC ? *y + vB : vB;
+      }
+    }
+  }
+  if (EPI == EPI_QKV) {
+    // bias (qwen2), then RoPE of (q, k) pairs with the host table, then
+    // K and V into the cache at pos (kernels_fused.go:47-73; cpu.go:284-303).
+    // lf is the row in [q; k; v]; a launch may cover one of the three.
+    const uint32_t lf = a.row_base + lr;
+    if (a.bias && rvalid) {
+      float bb = a.bias[lf];
+      vA += bb;
+      vB += bb;
+    }
+    const int pm = a.neox ? 8 : 1;
+    float oA = __shfl_xor(vA, pm), oB = __shfl_xor(vB, pm);
+    if (rvalid) {
+      const uint32_t hd = a.hd, hp = hd / 2;
+      for (int u = 0; u < 2; u++) {
+        if (!(u ? okB : okA)) continue;
+        uint32_t tok = u ? tokB : tokA;
+        float v = u ? vB : vA, o = u ? oB : oA;
+        uint32_t pos = a.state[0] + tok;
+        if (lf < a.nq + a.nk) {
+          uint32_t j = lf < a.nq ? lf : lf - a.nq, w = j % hd;
+          uint32_t i = a.neox ? w % hp : w / 2;
+          bool first = a.neox ? w < hp : (w % 2) == 0;
+          float c = a.cs[((uint64_t)pos * hp + i) * 2], sn = a.cs[((uint64_t)pos * hp + i) * 2 + 1];
+          float x = first ? v : o, z = first ? o : v;
+          float res = first ? __fsub_rn(__fmul_rn(x, c), __fmul_rn(z, sn))    // cpu.go:381
+                            : __fadd_rn(__fmul_rn(x, sn), __fmul_rn(z, c));  // cpu.go:382
+          if (lf < a.nq) a.y[(uint64_t)tok * a.nq + lf] = res;
+          else a.kv[(uint64_t)pos * a.kvd + j] = res;
+        } else {
+          a.kv[(uint64_t)a.ctx * a.kvd + (uint64_t)pos * a.kvd + (lf - a.nq - a.nk)] = v;
+        }
+      }
+    }
+  }
+  if (EPI == EPI_GATEUP) {
+    // act = g / (1 + exp(-g)) * u (cpu.go:345); gate row i at lane r, up row i at r+8
+    float uA = __shfl_xor(vA, 8), uB = __shfl_xor(vB, 8);
+    if (active && r < 8) {
+      uint32_t i = 8 * tile + r;
+      if (i < a.ff) {
+        if (okA) a.y[(uint64_t)tokA * a.ff + i] = vA / (1.f + expf(-vA)) * uA;
+        if (okB) a.y[(uint64_t)tokB * a.ff + i] = vB / (1.f + expf(-vB)) * uB;
+      }
+    }
+  }
+}
+
 template <uint32_t QT, int NT, int PRO, int EPI>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   typedef QT_<QT> T;
@@ -569,47 +653,20 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   }
   // ---- epilogue: lane holds rows r of the tile for tokens 2q and 2q+1
   const bool active = sp == 0 && tile < a.tiles;
-  const uint32_t p = tile * 16 + r;
-  const uint32_t lr = row_of_pos(p, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
-  const bool rvalid = active && lr < a.rows;
   const int tA = 2 * q, tB = 2 * q + 1;
-  float vA = (tA < nt) ? ldexpf(acc0, -exps[tA]) : 0.f;
-  float vB = (NT > 1 && tB < nt) ? ldexpf(acc1, -exps[tB]) : 0.f;
-  if (EPI == EPI_SWIGLU) {
-    // act = g / (1 + exp(-g)) * u (cpu.go:345) with g from the gate's own launch
-    if (rvalid) {
-      if (tA < nt) {
-        uint64_t o = (uint64_t)(t0 + tA) * a.ldy + lr;
-        float gg = a.aux[o];
-        a.y[o] = gg / (1.f + expf(-gg)) * vA;
-      }
-      if (NT > 1 && tB < nt) {
-        uint64_t o = (uint64_t)(t0 + tB) * a.ldy + lr;
-        float gg = a.aux[o];
-        a.y[o] = gg / (1.f + expf(-gg)) * vB;
-      }
-    }
-  }
-  if (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_ARGMAX) {
-    if (rvalid) {
-      if (tA < nt) {
-        float* y = a.y + (uint64_t)(t0 + tA) * a.ldy + lr;
-        *y = EPI == EPI_ACC ? *y + vA : vA;
-      }
-      if (NT > 1 && tB < nt) {
-        float* y = a.y + (uint64_t)(t0 + tB) * a.ldy + lr;
-        *y = EPI == EPI_ACC ? *y + vB : vB;
-      }
-    }
-  }
+  const bool okA = tA < nt, okB = NT > 1 && tB < nt;
+  const float vA = okA ? ldexpf(acc0, -exps[tA]) : 0.f;
+  const float vB = okB ? ldexpf(acc1, -exps[tB]) : 0.f;
+  row_epilogue<EPI>(a, tile, r, active, t0 + tA, okA, vA, t0 + tB, okB, vB);
   if (EPI == EPI_ARGMAX) {
     // (max, lowest index) of token 0 over this workgroup's rows, NaN never
     // wins (cpu.go:389-397); argmax_kernel combines the workgroups' partials.
+    const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
     float* av = misc + 80;
     uint32_t* ai = (uint32_t*)(misc + 96);
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
-    if (rvalid && q == 0 && nt > 0 && vA == vA) {
+    if (active && lr < a.rows && q == 0 && okA && vA == vA) {
       bv = vA;
       bi = lr;
     }
@@ -636,52 +693,300 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       a.amax_i[blockIdx.x] = bi;
     }
   }
-  if (EPI == EPI_QKV) {
-    // bias (qwen2), then RoPE of (q, k) pairs with the host table, then
-    // K and V into the cache at pos (kernels_fused.go:47-73; cpu.go:284-303).
-    // lf is the row in [q; k; v]; a launch may cover one of the three.
-    const uint32_t lf = a.row_base + lr;
-    if (a.bias && rvalid) {
-      float bb = a.bias[lf];
-      vA += bb;
-      vB += bb;
+}
+
+
+// ------------------------------------------------ prefill: prep + gemm
+
+constexpr int PMAXI = 4;  // items per thread in prep_kernel: k <= 32 * 4 * 256
+
+// One workgroup per token slot: the prologue of the decode kernel for one
+// token (plain, RMSNorm, or the attention merge), written once to global
+// memory in MFMA operand order for every workgroup of gemm_kernel.  Slots
+// past ntok (up to a whole group of 8) are zero.
+template <int PRO>
+__global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float pl[];
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t nb = a.nb, K = a.k, NI = nb * 4;
+  h8* xp = (h8*)a.xp;
+  const uint32_t tg = t / 8, s2 = 2 * (t % 8);
+  float* red = pl;        // [4] partials, [8] s, [9] exp
+  float* wts = pl + 16;   // MERGE: [H][SM+1]
+  if (t >= a.ntok) {
+    for (uint32_t it = tid; it < NI; it += 256) {
+      xp[((uint64_t)tg * nb + it / 4) * 64 + (it % 4) * 16 + s2] = h8{};
+      xp[((uint64_t)tg * nb + it / 4) * 64 + (it % 4) * 16 + s2 + 1] = h8{};
     }
-    const int pm = a.neox ? 8 : 1;
-    float oA = __shfl_xor(vA, pm), oB = __shfl_xor(vB, pm);
-    if (rvalid) {
-      const uint32_t hd = a.hd, hp = hd / 2;
-      for (int u = 0; u < 2; u++) {
-        int t = u ? tB : tA;
-        if (t >= nt || (u && NT == 1)) continue;
-        float v = u ? vB : vA, o = u ? oB : oA;
-        uint32_t pos = a.state[0] + t0 + t;
-        if (lf < a.nq + a.nk) {
-          uint32_t j = lf < a.nq ? lf : lf - a.nq, w = j % hd;
-          uint32_t i = a.neox ? w % hp : w / 2;
-          bool first = a.neox ? w < hp : (w % 2) == 0;
-          float c = a.cs[((uint64_t)pos * hp + i) * 2], sn = a.cs[((uint64_t)pos * hp + i) * 2 + 1];
-          float x = first ? v : o, z = first ? o : v;
-          float res = first ? __fsub_rn(__fmul_rn(x, c), __fmul_rn(z, sn))    // cpu.go:381
-                            : __fadd_rn(__fmul_rn(x, sn), __fmul_rn(z, c));  // cpu.go:382
-          if (lf < a.nq) a.y[(uint64_t)(t0 + t) * a.nq + lf] = res;
-          else a.kv[(uint64_t)pos * a.kvd + j] = res;
-        } else {
-          a.kv[(uint64_t)a.ctx * a.kvd + (uint64_t)pos * a.kvd + (lf - a.nq - a.nk)] = v;
+    for (uint32_t b = tid; b < nb; b += 256) a.xbsum[(uint64_t)t * nb + b] = 0.f;
+    if (tid == 0) a.xexp[t] = 0;
+    return;
+  }
+  f4 va[PMAXI], vc[PMAXI];
+  if (PRO == PRO_MERGE) {
+    const uint32_t H = a.heads, SM = a.smax;
+    const uint32_t nc = (a.state[0] + t + a.chunk) / a.chunk;
+    for (uint32_t h = tid; h < H; h += 256) {
+      const float* mlp = a.ml + ((uint64_t)t * H + h) * SM * 2;
+      float M = -INFINITY;
+      for (uint32_t c = 0; c < nc; c++) M = fmaxf(M, mlp[2 * c]);
+      float l = 0;
+      float* w = wts + h * (SM + 1);
+      for (uint32_t c = 0; c < nc; c++) {
+        float e = expf(mlp[2 * c] - M);
+        w[c] = e;
+        l += e * mlp[2 * c + 1];
+      }
+      w[SM] = 1.f / l;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < PMAXI; k++) {
+      uint32_t it = tid + k * 256;
+      f4 A = {0, 0, 0, 0}, C = {0, 0, 0, 0};
+      if (it < NI) {
+        uint32_t e = (it / 4) * 32 + 4 * (it % 4), h = e / a.hd, dd = e % a.hd;
+        const float* w = wts + h * (SM + 1);
+        const float* pvp = a.pv + (((uint64_t)t * H + h) * SM) * a.hd + dd;
+#pragma unroll 4
+        for (uint32_t c = 0; c < nc; c++) {
+          f4 p0 = *(const f4*)(pvp + (uint64_t)c * a.hd), p1 = *(const f4*)(pvp + (uint64_t)c * a.hd + 16);
+          A += w[c] * p0;
+          C += w[c] * p1;
+        }
+        A *= w[SM];
+        C *= w[SM];
+      }
+      va[k] = A;
+      vc[k] = C;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < PMAXI; k++) {
+      uint32_t it = tid + k * 256;
+      f4 A = {0, 0, 0, 0}, C = {0, 0, 0, 0};
+      if (it < NI) {
+        const float* xr = a.x + (uint64_t)(a.xrow0 + t) * a.ldx + (it / 4) * 32 + 4 * (it % 4);
+        A = *(const f4*)xr;
+        C = *(const f4*)(xr + 16);
+      }
+      va[k] = A;
+      vc[k] = C;
+    }
+  }
+  if (PRO == PRO_RMS) {
+    // cpu.go:90-96
+    float ss = 0;
+#pragma unroll
+    for (int k = 0; k < PMAXI; k++)
+      for (int i = 0; i < 4; i++) ss += va[k][i] * va[k][i] + vc[k][i] * vc[k][i];
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    if (tid == 0) red[8] = (float)(1.0 / sqrt((double)((red[0] + red[1] + red[2] + red[3]) / (float)K + a.eps)));
+    __syncthreads();
+    const float sc = red[8];
+#pragma unroll
+    for (int k = 0; k < PMAXI; k++) {
+      uint32_t it = tid + k * 256;
+      if (it >= NI) continue;
+      const float* wr = a.nw + (it / 4) * 32 + 4 * (it % 4);
+      f4 wa = *(const f4*)wr, wc = *(const f4*)(wr + 16);
+      for (int i = 0; i < 4; i++) {
+        va[k][i] = __fmul_rn(__fmul_rn(va[k][i], sc), wa[i]);
+        vc[k][i] = __fmul_rn(__fmul_rn(vc[k][i], sc), wc[i]);
+      }
+    }
+    __syncthreads();
+  }
+  float m = 0;
+#pragma unroll
+  for (int k = 0; k < PMAXI; k++)
+    for (int i = 0; i < 4; i++) m = fmaxf(m, fmaxf(fabsf(va[k][i]), fabsf(vc[k][i])));
+  m = wave_max(m);
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  if (tid == 0) {
+    float mm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (mm > 0 && mm <= 3.0e38f) {
+      int E;
+      frexpf(mm, &E);
+      e = 15 - E;
+    }
+    ((int*)red)[9] = e;
+    a.xexp[t] = e;
+  }
+  __syncthreads();
+  const int ex = ((int*)red)[9];
+#pragma unroll
+  for (int k = 0; k < PMAXI; k++) {
+    uint32_t it = tid + k * 256;
+    if (it >= NI) continue;
+    const f4 A = va[k], C = vc[k];
+    const float v[8] = {A[0], A[2], C[0], C[2], A[1], A[3], C[1], C[3]};
+    h8 hi, lo;
+    for (int i = 0; i < 8; i++) {
+      float sv = ldexpf(v[i], ex);
+      _Float16 h = (_Float16)sv;
+      hi[i] = h;
+      lo[i] = (_Float16)(sv - (float)h);
+    }
+    h8* dst = xp + ((uint64_t)tg * nb + it / 4) * 64 + (it % 4) * 16 + s2;
+    dst[0] = hi;
+    dst[1] = lo;
+    float sx = (A[0] + A[1] + A[2] + A[3]) + (C[0] + C[1] + C[2] + C[3]);
+    sx += __shfl_xor(sx, 1);
+    sx += __shfl_xor(sx, 2);
+    if ((it & 3) == 0) a.xbsum[(uint64_t)t * nb + it / 4] = ldexpf(sx, ex);
+  }
+}
+
+// Prefill matrix product.  A workgroup owns two 16-row tiles and a range of
+// token groups (grid.y); its four waves split the blocks of k (split-K) and
+// add their partials in LDS in a fixed order.  A weight word is dequantised
+// once and feeds one MFMA per token group and tile; the activation operands
+// come from prep_kernel's buffer (shared by all workgroups through L2).
+constexpr int GT = 2;  // tiles per workgroup
+
+template <uint32_t QT, int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(GemvArgs a) {
+  typedef QT_<QT> T;
+  __shared__ float red[3][64][GT * 8 * 2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const uint32_t nb = a.nb, TG = a.tg;
+  const uint32_t tgpw = (TG + gridDim.y - 1) / gridDim.y, g0 = blockIdx.y * tgpw;
+  const uint32_t ngr = min(tgpw, TG - min(TG, g0));  // token groups of this workgroup
+  const uint32_t tile0 = blockIdx.x * GT;
+  const h8* xp = (const h8*)a.xp;
+  float acc[GT][8][2];
+#pragma unroll
+  for (int u = 0; u < GT; u++)
+#pragma unroll
+    for (int g = 0; g < 8; g++) acc[u][g][0] = acc[u][g][1] = 0.f;
+  bool tv[GT];
+  const uint8_t* qt[GT];
+  const uint8_t* st[GT];
+#pragma unroll
+  for (int u = 0; u < GT; u++) {
+    tv[u] = tile0 + u < a.tiles;
+    uint32_t tt = tv[u] ? tile0 + u : tile0;
+    qt[u] = a.qs + (uint64_t)tt * 16 * nb * T::QB;
+    st[u] = a.sc + (uint64_t)tt * 16 * nb * T::SB;
+  }
+  // one block b for both tiles: B[u] weights, d[u] / m[u] scales
+  auto block = [&](uint32_t b, const h8* B, const float* d, const float* mm) {
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+      if (g >= (int)ngr) break;
+      const h8 A = xp[((uint64_t)(g0 + g) * nb + b) * 64 + lane];
+#pragma unroll
+      for (int u = 0; u < GT; u++) {
+        f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[u], f4{0, 0, 0, 0}, 0, 0, 0);
+        acc[u][g][0] += d[u] * (D[0] + D[1]);
+        acc[u][g][1] += d[u] * (D[2] + D[3]);
+        if (QT == LLMHIP_Q4_1) {
+          acc[u][g][0] += mm[u] * a.xbsum[(uint64_t)((g0 + g) * 8 + 2 * q) * nb + b];
+          acc[u][g][1] += mm[u] * a.xbsum[(uint64_t)((g0 + g) * 8 + 2 * q + 1) * nb + b];
         }
       }
     }
-  }
-  if (EPI == EPI_GATEUP) {
-    // act = g / (1 + exp(-g)) * u (cpu.go:345); gate row i at lane r, up row i at r+8
-    float uA = __shfl_xor(vA, 8), uB = __shfl_xor(vB, 8);
-    if (active && r < 8) {
-      uint32_t i = 8 * tile + r;
-      if (i < a.ff) {
-        if (tA < nt) a.y[(uint64_t)(t0 + tA) * a.ff + i] = vA / (1.f + expf(-vA)) * uA;
-        if (NT > 1 && tB < nt) a.y[(uint64_t)(t0 + tB) * a.ff + i] = vB / (1.f + expf(-vB)) * uB;
+  };
+  for (uint32_t g4 = wave; g4 < a.ng; g4 += 4) {
+    uint4 w0[GT], w1[GT], sv[GT];
+#pragma unroll
+    for (int u = 0; u < GT; u++) {
+      if (QT == LLMHIP_Q8_0) {
+        w0[u] = ld_stream16(qt[u] + g4 * 2048 + lane * 16);
+        w1[u] = ld_stream16(qt[u] + g4 * 2048 + 1024 + lane * 16);
+      } else {
+        w0[u] = ld_stream16(qt[u] + g4 * 1024 + lane * 16);
+      }
+      if (QT == LLMHIP_Q4_1) {
+        sv[u] = *(const uint4*)(st[u] + g4 * 256 + r * 16);
+      } else {
+        uint2 x2 = *(const uint2*)(st[u] + g4 * 128 + r * 8);
+        sv[u] = uint4{x2.x, x2.y, 0, 0};
       }
     }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      h8 B[GT];
+      float d[GT], mm[GT];
+#pragma unroll
+      for (int u = 0; u < GT; u++) {
+        const uint32_t wj = j == 0 ? w0[u].x : j == 1 ? w0[u].y : j == 2 ? w0[u].z : w0[u].w;
+        if (QT == LLMHIP_Q8_0) {
+          const uint4 ww = j < 2 ? w0[u] : w1[u];
+          B[u] = (j % 2 == 0) ? dq8(ww.x, ww.y) : dq8(ww.z, ww.w);
+          const uint32_t sw = j < 2 ? sv[u].x : sv[u].y;
+          d[u] = f16_hw(j % 2 == 0 ? sw & 0xffff : sw >> 16);
+          mm[u] = 0;
+        } else if (QT == LLMHIP_Q4_1) {
+          B[u] = dq4<true>(wj);
+          const uint32_t sw = j == 0 ? sv[u].x : j == 1 ? sv[u].y : j == 2 ? sv[u].z : sv[u].w;
+          d[u] = f16_hw(sw & 0xffff);
+          mm[u] = f16_hw(sw >> 16);
+        } else {
+          B[u] = dq4<false>(wj);
+          const uint32_t sw = j < 2 ? sv[u].x : sv[u].y;
+          d[u] = f16_hw(j % 2 == 0 ? sw & 0xffff : sw >> 16);
+          mm[u] = 0;
+        }
+      }
+      block(4 * g4 + j, B, d, mm);
+    }
   }
+  if (a.tail && (a.ng % 4) == (uint32_t)wave) {
+    for (uint32_t j = 0; j < a.tail; j++) {
+      const uint32_t b = 4 * a.ng + j;
+      h8 B[GT];
+      float d[GT], mm[GT];
+#pragma unroll
+      for (int u = 0; u < GT; u++) {
+        const uint8_t* qq = qt[u] + qs_off<QT>(b, lane, a.ng, a.tail);
+        const uint8_t* s = st[u] + sc_off<QT>(b, r, a.ng, a.tail);
+        if (QT == LLMHIP_Q8_0) B[u] = dq8(*(const uint32_t*)qq, *(const uint32_t*)(qq + 4));
+        else B[u] = dq4<QT == LLMHIP_Q4_1>(*(const uint32_t*)qq);
+        d[u] = f16_hw(s[0] | s[1] << 8);
+        mm[u] = QT == LLMHIP_Q4_1 ? f16_hw(s[2] | s[3] << 8) : 0.f;
+      }
+      block(b, B, d, mm);
+    }
+  }
+  // split-K: waves 1..3 hand their partials to wave 0, which adds them in order
+  if (wave > 0) {
+#pragma unroll
+    for (int u = 0; u < GT; u++)
+#pragma unroll
+      for (int g = 0; g < 8; g++) {
+        red[wave - 1][lane][(u * 8 + g) * 2] = acc[u][g][0];
+        red[wave - 1][lane][(u * 8 + g) * 2 + 1] = acc[u][g][1];
+      }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; w++)
+#pragma unroll
+    for (int u = 0; u < GT; u++)
+#pragma unroll
+      for (int g = 0; g < 8; g++) {
+        acc[u][g][0] += red[w][lane][(u * 8 + g) * 2];
+        acc[u][g][1] += red[w][lane][(u * 8 + g) * 2 + 1];
+      }
+#pragma unroll
+  for (int u = 0; u < GT; u++)
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+      if (g >= (int)ngr) break;
+      const uint32_t tokA = (g0 + g) * 8 + 2 * q, tokB = tokA + 1;
+      const bool okA = tokA < a.ntok, okB = tokB < a.ntok;
+      const float vA = okA ? ldexpf(acc[u][g][0], -a.xexp[tokA]) : 0.f;
+      const float vB = okB ? ldexpf(acc[u][g][1], -a.xexp[tokB]) : 0.f;
+      row_epilogue<EPI>(a, tile0 + u, r, tv[u], tokA, okA, vA, tokB, okB, vB);
+    }
 }
 
 // ----------------------------------------------------------- dispatch
@@ -759,12 +1064,31 @@ int embed_launch_qt(const QMat& m, const int32_t* tokens, const uint32_t* state,
   return 0;
 }
 
+template <uint32_t QT>
+int gemm_launch_qt(const GemvArgs& a, int epi, hipStream_t s) {
+  // token-group splits so that a launch has >= ~512 waves
+  uint32_t wgs = (a.tiles + GT - 1) / GT, ts = 1;
+  while (ts < a.tg && wgs * ts * 4 < 2048) ts *= 2;
+  dim3 grid(wgs, std::min(ts, a.tg));
+  switch (epi) {
+    case EPI_STORE: hipLaunchKernelGGL((gemm_kernel<QT, EPI_STORE>), grid, dim3(256), 0, s, a); break;
+    case EPI_ACC: hipLaunchKernelGGL((gemm_kernel<QT, EPI_ACC>), grid, dim3(256), 0, s, a); break;
+    case EPI_QKV: hipLaunchKernelGGL((gemm_kernel<QT, EPI_QKV>), grid, dim3(256), 0, s, a); break;
+    case EPI_GATEUP: hipLaunchKernelGGL((gemm_kernel<QT, EPI_GATEUP>), grid, dim3(256), 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((gemm_kernel<QT, EPI_SWIGLU>), grid, dim3(256), 0, s, a); break;
+    default: return set_error(LLMHIP_ERR_ARG, "llm: gemm: unsupported epilogue %d", epi);
+  }
+  LLM_HIP(hipGetLastError());
+  return 0;
+}
+
 #define LLMHIP_INSTANTIATE(QT)                                                                                   \
   template int gemv_launch_qt<QT>(const GemvArgs&, int, int, hipStream_t);                                     \
   template int repack_launch_qt<QT>(const QMat&, const uint8_t*, uint64_t, uint64_t, uint64_t, uint32_t,       \
                                     uint32_t, uint32_t, uint32_t, uint32_t, hipStream_t);                      \
   template int dequant_launch_qt<QT>(const QMat&, float*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t,    \
                                      hipStream_t);                                                             \
-  template int embed_launch_qt<QT>(const QMat&, const int32_t*, const uint32_t*, float*, uint32_t, hipStream_t);
+  template int embed_launch_qt<QT>(const QMat&, const int32_t*, const uint32_t*, float*, uint32_t, hipStream_t); \
+  template int gemm_launch_qt<QT>(const GemvArgs&, int, hipStream_t);
 
 }  // namespace llmhip

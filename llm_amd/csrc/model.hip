@@ -54,6 +54,7 @@ struct Model {
   Stager st;
   float *x = nullptr, *q = nullptr, *act = nullptr, *gbuf = nullptr, *logits = nullptr, *pv = nullptr,
         *ml = nullptr, *amax_v = nullptr, *cs = nullptr;
+  void* xprep = nullptr;  // prepared activations of a prefill chunk
   uint32_t *amax_i = nullptr, *state = nullptr;
   int32_t *tokens = nullptr, *outb = nullptr;
   int32_t* host = nullptr;  // pinned: prompt ids in, sampled ids out
@@ -324,6 +325,20 @@ static int gemv_rec(Model& m, const char* cls, const GemvArgs& a, uint32_t qtype
   return launch_rec(m, cls, bytes, [&]() { return gemv_launch(a, qtype, pro, epi, m.stream); });
 }
 
+// A prefill chunk (ntok >= GEMM_MIN_TOKENS) stages its activations once
+// (prep_kernel) and runs gemm_kernel; decode runs gemv_kernel with the
+// prologue fused.  `prep` false reuses the staging of the previous call (the
+// matrices of one mixed-type group share an input).
+static int mat_rec(Model& m, const char* cls, const char* pcls, GemvArgs a, uint32_t qtype, int pro, int epi,
+                   uint64_t bytes, bool prep = true) {
+  if (a.ntok < GEMM_MIN_TOKENS) return gemv_rec(m, cls, a, qtype, pro, epi, bytes);
+  xprep_bind(&a, m.xprep);
+  if (prep && !skipped(m, cls))
+    LLM_TRY(launch_rec(m, pcls, 0, [&]() { return prep_launch(a, pro, m.stream); }));
+  if (skipped(m, cls)) return 0;
+  return launch_rec(m, cls, bytes, [&]() { return gemm_launch(a, qtype, epi, m.stream); });
+}
+
 static GemvArgs base_args(const Model& m, const QMat& q, uint32_t ntok) {
   GemvArgs a;
   memset(&a, 0, sizeof a);
@@ -355,7 +370,7 @@ static int rec_k1(Model& m, const Layer& L, uint32_t ntok) {
     a.ctx = m.ctx;
     a.neox = c.rope_neox;
     a.row_base = L.qkv_base[i];
-    LLM_TRY(gemv_rec(m, "k1", a, L.qkv_type[i], PRO_RMS, EPI_QKV, L.qkv[i].g.gguf_bytes()));
+    LLM_TRY(mat_rec(m, "k1", "p1", a, L.qkv_type[i], PRO_RMS, EPI_QKV, L.qkv[i].g.gguf_bytes(), i == 0));
   }
   return 0;
 }
@@ -391,7 +406,7 @@ static int rec_k3(Model& m, const Layer& L, uint32_t ntok) {
   a.ml = m.ml;
   a.y = m.x;
   a.ldy = m.cfg.embd;
-  return gemv_rec(m, "k3", a, L.o.g.q.type, PRO_MERGE, EPI_ACC, L.o.g.gguf_bytes());
+  return mat_rec(m, "k3", "p3", a, L.o.g.q.type, PRO_MERGE, EPI_ACC, L.o.g.gguf_bytes());
 }
 
 static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
@@ -403,7 +418,7 @@ static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
     a.nw = L.ffn_norm;
     a.y = m.act;
     a.ff = c.ff;
-    return gemv_rec(m, "k4", a, L.gu[0].g.q.type, PRO_RMS, EPI_GATEUP, L.gu[0].g.gguf_bytes());
+    return mat_rec(m, "k4", "p4", a, L.gu[0].g.q.type, PRO_RMS, EPI_GATEUP, L.gu[0].g.gguf_bytes());
   }
   GemvArgs g = base_args(m, L.gu[0], ntok);
   g.x = m.x;
@@ -411,7 +426,7 @@ static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
   g.nw = L.ffn_norm;
   g.y = m.gbuf;
   g.ldy = c.ff;
-  LLM_TRY(gemv_rec(m, "k4", g, L.gu[0].g.q.type, PRO_RMS, EPI_STORE, L.gu[0].g.gguf_bytes()));
+  LLM_TRY(mat_rec(m, "k4", "p4", g, L.gu[0].g.q.type, PRO_RMS, EPI_STORE, L.gu[0].g.gguf_bytes()));
   GemvArgs u = base_args(m, L.gu[1], ntok);
   u.x = m.x;
   u.ldx = c.embd;
@@ -419,7 +434,7 @@ static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
   u.y = m.act;
   u.ldy = c.ff;
   u.aux = m.gbuf;
-  return gemv_rec(m, "k4", u, L.gu[1].g.q.type, PRO_RMS, EPI_SWIGLU, L.gu[1].g.gguf_bytes());
+  return mat_rec(m, "k4", "p4", u, L.gu[1].g.q.type, PRO_RMS, EPI_SWIGLU, L.gu[1].g.gguf_bytes(), false);
 }
 
 static int rec_k5(Model& m, const Layer& L, uint32_t ntok) {
@@ -428,7 +443,7 @@ static int rec_k5(Model& m, const Layer& L, uint32_t ntok) {
   a.ldx = m.cfg.ff;
   a.y = m.x;
   a.ldy = m.cfg.embd;
-  return gemv_rec(m, "k5", a, L.down.g.q.type, PRO_PLAIN, EPI_ACC, L.down.g.gguf_bytes());
+  return mat_rec(m, "k5", "p5", a, L.down.g.q.type, PRO_PLAIN, EPI_ACC, L.down.g.gguf_bytes());
 }
 
 static int rec_adv(Model& m, uint32_t n) {
@@ -588,6 +603,7 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
       (rc = dalloc_n(*m, &m->amax_i, V / 16 + 64)) || (rc = dalloc_n(*m, &m->pv, pm * H * m->smax * c.head_dim)) ||
       (rc = dalloc_n(*m, &m->ml, pm * H * m->smax * 2)) || (rc = dalloc_n(*m, &m->state, 2)) ||
       (rc = dalloc_n(*m, &m->tokens, (uint64_t)m->ctx + 1)) || (rc = dalloc_n(*m, &m->outb, 1)) ||
+      (rc = dalloc(*m, &m->xprep, xprep_bytes(m->pm, (uint32_t)std::max(c.embd, c.ff)))) ||
       (rc = dalloc_n(*m, &m->cs, (uint64_t)m->ctx * c.head_dim)))
     return fail(rc);
   // RoPE table in double precision, gpu.go:524-534 (and cpu.go:374-375)
@@ -818,36 +834,42 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
   if (!m.finalized) return set_error(LLMHIP_ERR_STATE, "llm: model not finalized");
   if (iters < 1) return set_error(LLMHIP_ERR_ARG, "llm: iters %d", iters);
   LLM_HIP(hipSetDevice(m.device));
-  std::string k = kernel;
-  const Layer& L = m.layers[0];
+  const std::string k = kernel;
+  if (k != "head" && k != "k1" && k != "k2" && k != "k3" && k != "k4" && k != "k5")
+    return set_error(LLMHIP_ERR_ARG, "llm: no kernel \"%s\" (head, k1..k5)", kernel);
   std::set<std::string> saved = m.skip;
   m.skip.clear();
-  auto one = [&]() -> int {
+  const int L = m.cfg.layers;
+  auto wb = [](const QMat& q) { return q.g.gguf_bytes(); };
+  // launch i runs layer i % L: consecutive launches read different weights,
+  // as in the decode pass
+  auto one = [&](int i) -> int {
+    const Layer& ly = m.layers[i % L];
     if (k == "head") {  // without the sampling: repeated launches must not advance the state
       const QMat& w = m.tied ? m.embd : m.out;
       return gemv_launch(head_args(m, 0, 0), w.g.q.type, PRO_RMS, EPI_STORE, m.stream);
     }
-    if (k == "k1") return rec_k1(m, L, 1);
-    if (k == "k2") return rec_k2(m, L, 1);
-    if (k == "k3") return rec_k3(m, L, 1);
-    if (k == "k4") return rec_k4(m, L, 1);
-    if (k == "k5") return rec_k5(m, L, 1);
-    return set_error(LLMHIP_ERR_ARG, "llm: no kernel \"%s\" (head, k1..k5)", kernel);
+    if (k == "k1") return rec_k1(m, ly, 1);
+    if (k == "k2") return rec_k2(m, ly, 1);
+    if (k == "k3") return rec_k3(m, ly, 1);
+    if (k == "k4") return rec_k4(m, ly, 1);
+    return rec_k5(m, ly, 1);
   };
   uint64_t b = 0;
-  auto wb = [](const QMat& q) { return q.g.gguf_bytes(); };
+  const Layer& L0 = m.layers[0];
   if (k == "head") b = wb(m.tied ? m.embd : m.out);
-  else if (k == "k1") b = wb(L.qkv[0]) + (L.nqkv == 3 ? wb(L.qkv[1]) + wb(L.qkv[2]) : 0);
-  else if (k == "k3") b = wb(L.o);
-  else if (k == "k4") b = wb(L.gu[0]) + (L.ngu == 2 ? wb(L.gu[1]) : 0);
-  else if (k == "k5") b = wb(L.down);
+  else if (k == "k1") b = wb(L0.qkv[0]) + (L0.nqkv == 3 ? wb(L0.qkv[1]) + wb(L0.qkv[2]) : 0);
+  else if (k == "k2") b = 2ull * (m.pos + 1) * m.kvd * 4;
+  else if (k == "k3") b = wb(L0.o);
+  else if (k == "k4") b = wb(L0.gu[0]) + (L0.ngu == 2 ? wb(L0.gu[1]) : 0);
+  else b = wb(L0.down);
   int rc = 0;
-  for (int i = 0; i < 3 && rc == 0; i++) rc = one();
+  for (int i = 0; i < L && rc == 0; i++) rc = one(i);
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (rc == 0 && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
     rc = set_error(LLMHIP_ERR_DEVICE, "llm: hipEventCreate failed");
   if (rc == 0 && hipEventRecord(e0, m.stream) != hipSuccess) rc = set_error(LLMHIP_ERR_DEVICE, "llm: event record");
-  for (int i = 0; i < iters && rc == 0; i++) rc = one();
+  for (int i = 0; i < iters && rc == 0; i++) rc = one(i);
   if (rc == 0 && hipEventRecord(e1, m.stream) != hipSuccess) rc = set_error(LLMHIP_ERR_DEVICE, "llm: event record");
   float ms = 0;
   if (rc == 0 && hipEventSynchronize(e1) == hipSuccess) (void)hipEventElapsedTime(&ms, e0, e1);

@@ -105,6 +105,17 @@ int gemv_launch(const GemvArgs& a, uint32_t qtype, int pro, int epi, hipStream_t
   return set_error(LLMHIP_ERR_TYPE, "llm: ggml type %u has no GPU kernel", qtype);
 }
 
+int gemm_launch(const GemvArgs& a, uint32_t qtype, int epi, hipStream_t s) {
+  if (a.ntok == 0) return 0;
+  if (a.ntok > a.tg * 8 || a.tg > 8) return set_error(LLMHIP_ERR_ARG, "llm: gemm: %u tokens in %u groups", a.ntok, a.tg);
+  switch (qtype) {
+    case LLMHIP_Q4_0: return gemm_launch_qt<LLMHIP_Q4_0>(a, epi, s);
+    case LLMHIP_Q4_1: return gemm_launch_qt<LLMHIP_Q4_1>(a, epi, s);
+    case LLMHIP_Q8_0: return gemm_launch_qt<LLMHIP_Q8_0>(a, epi, s);
+  }
+  return set_error(LLMHIP_ERR_TYPE, "llm: ggml type %u has no GPU kernel", qtype);
+}
+
 int stager_init(Stager* st, int device, uint64_t cap, hipStream_t s) {
   st->device = device;
   st->cap = cap;
@@ -207,6 +218,7 @@ struct llmhip_qmat {
   QMat m;
   Stager st;
   hipStream_t stream = nullptr;
+  void* xprep = nullptr;  // prepared activations of up to 64 tokens (allocated on first use)
 };
 
 extern "C" {
@@ -284,13 +296,21 @@ static int qmat_gemv_args(llmhip_qmat* q, const float* x, float* y, int n, GemvA
   return 0;
 }
 
+static int qmat_launch(llmhip_qmat* q, GemvArgs& a, int epi, hipStream_t s) {
+  if (a.ntok < GEMM_MIN_TOKENS) return gemv_launch(a, q->m.g.q.type, PRO_PLAIN, epi, s);
+  if (!q->xprep) LLM_HIP(hipMalloc(&q->xprep, xprep_bytes(64, (uint32_t)q->m.g.k)));
+  xprep_bind(&a, q->xprep);
+  LLM_TRY(prep_launch(a, PRO_PLAIN, s));
+  return gemm_launch(a, q->m.g.q.type, epi, s);
+}
+
 int llmhip_qmat_gemv(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, int accumulate, void* hip_stream) {
   clear_error();
   GemvArgs a;
   LLM_TRY(qmat_gemv_args(q, x_dev, y_dev, n, &a));
   LLM_HIP(hipSetDevice(q->m.device));
   LLM_HIP(hipStreamSynchronize(q->stream));
-  return gemv_launch(a, q->m.g.q.type, PRO_PLAIN, accumulate ? EPI_ACC : EPI_STORE, (hipStream_t)hip_stream);
+  return qmat_launch(q, a, accumulate ? EPI_ACC : EPI_STORE, (hipStream_t)hip_stream);
 }
 
 uint64_t llmhip_qmat_bytes(const llmhip_qmat* q) { return q->m.bytes; }
@@ -311,12 +331,13 @@ int llmhip_qmat_bench(llmhip_qmat* const* mats, int count, const float* x_dev, f
   }
   LLM_HIP(hipSetDevice(mats[0]->m.device));
   const uint32_t t = mats[0]->m.g.q.type;
-  for (int i = 0; i < warmup; i++) LLM_TRY(gemv_launch(args[i % count], t, PRO_PLAIN, EPI_STORE, s));
+  (void)t;
+  for (int i = 0; i < warmup; i++) LLM_TRY(qmat_launch(mats[i % count], args[i % count], EPI_STORE, s));
   hipEvent_t e0, e1;
   LLM_HIP(hipEventCreate(&e0));
   LLM_HIP(hipEventCreate(&e1));
   LLM_HIP(hipEventRecord(e0, s));
-  for (int i = 0; i < iters; i++) LLM_TRY(gemv_launch(args[i % count], t, PRO_PLAIN, EPI_STORE, s));
+  for (int i = 0; i < iters; i++) LLM_TRY(qmat_launch(mats[i % count], args[i % count], EPI_STORE, s));
   LLM_HIP(hipEventRecord(e1, s));
   LLM_HIP(hipEventSynchronize(e1));
   float ms = 0;
@@ -351,6 +372,7 @@ void llmhip_qmat_free(llmhip_qmat* q) {
   (void)hipSetDevice(q->m.device);
   stager_free(&q->st);
   if (q->stream) (void)hipStreamDestroy(q->stream);
+  if (q->xprep) (void)hipFree(q->xprep);
   qmat_release(&q->m);
   delete q;
 }

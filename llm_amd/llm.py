@@ -46,7 +46,8 @@ class File:
             o, sz = ctypes.c_uint64(), ctypes.c_uint64()
             check(lib().llm_gguf_tensor_info(handle, i, name, 1024, ctypes.byref(t), ctypes.byref(nd), dims,
                                              ctypes.byref(o), ctypes.byref(sz)))
-            self.Tensors.append(Tensor(name.value.decode(), list(dims[:nd.value]), t.value, o.value, sz.value))
+            self.Tensors.append(Tensor(name.value.decode(errors="surrogateescape"), list(dims[:nd.value]), t.value,
+                                       o.value, sz.value))
         self._by_name = {t.Name: t for t in self.Tensors}
 
     def Tensor(self, name):

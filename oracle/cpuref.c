@@ -750,7 +750,9 @@ EXPORT int cpuref_forward(cpuref_model* m, int32_t tok, float* logits) {
   float* g = (float*)calloc((size_t)c.ff, 4);
   float* u = (float*)calloc((size_t)c.ff, 4);
   float* dn = (float*)calloc((size_t)c.embd, 4);
-  float* scores = (float*)calloc((size_t)m->pos + 1, 4);
+  /* one score row per head, so heads may run on separate threads; each keeps
+   * cpu.go's order, so threaded runs are bit-identical */
+  float* scores = (float*)calloc((size_t)(m->pos + 1) * c.heads, 4);
   int nmax = c.embd > c.ff ? c.embd : c.ff;
   if (c.heads * c.head_dim > nmax) nmax = c.heads * c.head_dim;
   q8act qa = {(float*)calloc((size_t)nmax / 32 + 1, 4), (float*)calloc((size_t)nmax / 32 + 1, 4),
@@ -795,27 +797,32 @@ EXPORT int cpuref_forward(cpuref_model* m, int32_t tok, float* logits) {
     }
     float scale = (float)(1 / sqrt((double)c.head_dim));
     int grp = c.heads / c.kv_heads;
+    const float* kl = m->k[l];
+    const float* vl = m->v[l];
+    int pos = m->pos;
+#pragma omp parallel for num_threads(m->nthreads) if (m->nthreads > 1 && pos >= 64) schedule(static)
     for (int hd = 0; hd < c.heads; hd++) {
       int kvh = hd / grp;
+      float* sc = scores + (size_t)hd * (pos + 1);
       const float* qv = q + hd * c.head_dim;
       float mx = -INFINITY;
-      for (int t = 0; t <= m->pos; t++) {
-        const float* kr = m->k[l] + (size_t)t * kvd + kvh * c.head_dim;
+      for (int t = 0; t <= pos; t++) {
+        const float* kr = kl + (size_t)t * kvd + kvh * c.head_dim;
         float s = 0;
         for (int i = 0; i < c.head_dim; i++) s += qv[i] * kr[i];
-        scores[t] = s * scale;
-        mx = go_maxf(mx, scores[t]);
+        sc[t] = s * scale;
+        mx = go_maxf(mx, sc[t]);
       }
       float sum = 0;
-      for (int t = 0; t <= m->pos; t++) {
-        scores[t] = (float)exp((double)(scores[t] - mx));
-        sum += scores[t];
+      for (int t = 0; t <= pos; t++) {
+        sc[t] = (float)exp((double)(sc[t] - mx));
+        sum += sc[t];
       }
       float* outv = att + hd * c.head_dim;
       for (int i = 0; i < c.head_dim; i++) outv[i] = 0;
-      for (int t = 0; t <= m->pos; t++) {
-        const float* vr = m->v[l] + (size_t)t * kvd + kvh * c.head_dim;
-        float w = scores[t] / sum;
+      for (int t = 0; t <= pos; t++) {
+        const float* vr = vl + (size_t)t * kvd + kvh * c.head_dim;
+        float w = sc[t] / sum;
         for (int i = 0; i < c.head_dim; i++) outv[i] += w * vr[i];
       }
     }
