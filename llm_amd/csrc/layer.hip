@@ -2,6 +2,7 @@
 // in chunks of positions (flash-decoding partials, merged by the O-projection
 // prologue), greedy sampling and the state advance.
 #include "layer.h"
+#include "wave.h"
 
 namespace llmhip {
 
@@ -98,6 +99,110 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     for (uint32_t p = 0; p < L; p++) o += e[p] * vs[p * HD + d];
     a.pv[(((uint64_t)t * a.heads + g * GQ + h) * a.smax + c) * HD + d] = o;
   }
+}
+
+// Short-context attention (every position of the pass below ATTN_FULL_MAX =
+// 256), one 512-thread workgroup per (query head, token) and no split, so the
+// softmax uses the exact maximum over all positions (cpu.go:306-334) and the
+// head's output goes straight to att[t][h*64 + d] for a plain O-projection
+// prologue.  Lane (r, c) of a wave's four 16-lane rows holds float4 c of key
+// and value rows slot + 32j (slot = 4*wave + r, j < 8): loads are coalesced
+// 256-byte rows, q is one float4 per lane, a score is a 16-lane DPP sum that
+// lands in the lanes holding the matching value row, and the weighted value
+// sums are reduced over rows by two shuffles and over waves through LDS.  All
+// global loads are issued before anything waits; a.rows (host-chosen, >= every
+// position count of the pass) bounds the rows read, the rest are masked.
+__global__ __launch_bounds__(512) void attn_full_kernel(AttnArgs a) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  constexpr uint32_t HD = 64, J = ATTN_FULL_MAX / 32;
+  __shared__ float red_m[8], red_l[8];
+  __shared__ __attribute__((aligned(16))) float red_o[8 * HD];
+  const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t g = h / (a.heads / a.kv_heads);
+  const uint32_t c = lane & 15, slot = tid >> 4;
+  const float* kb = a.kv + g * HD + 4 * c;
+  const float* vb = a.kv + (uint64_t)a.ctx * a.kvd + g * HD + 4 * c;
+  const f4 q = *(const f4*)(a.q + (uint64_t)t * a.heads * HD + h * HD + 4 * c);
+  f4 kr[J], vr[J];
+#pragma unroll
+  for (uint32_t j = 0; j < J; j++) {
+    const uint32_t p = slot + 32 * j;
+    if (p < a.rows) {
+      kr[j] = *(const f4*)(kb + (uint64_t)p * a.kvd);
+      vr[j] = *(const f4*)(vb + (uint64_t)p * a.kvd);
+    }
+  }
+  const uint32_t n = a.state[0] + t + 1;
+  // scores s = (q . k) * scale (cpu.go:312-316), masked past the causal bound
+  float sj[J], m = -INFINITY;
+#pragma unroll
+  for (uint32_t j = 0; j < J; j++) {
+    const uint32_t p = slot + 32 * j;
+    float d = 0;
+    if (p < a.rows) d = q[0] * kr[j][0] + q[1] * kr[j][1] + q[2] * kr[j][2] + q[3] * kr[j][3];
+    d = row_sum16(d);
+    sj[j] = p < n ? d * a.scale : -INFINITY;
+    m = fmaxf(m, sj[j]);
+  }
+  m = rows_max4(m);
+  if (lane == 0) red_m[wave] = m;
+  __syncthreads();
+  float M = red_m[0];
+#pragma unroll
+  for (uint32_t w = 1; w < 8; w++) M = fmaxf(M, red_m[w]);
+  // e = exp(s - max); l = sum e; o = sum e v
+  f4 acc = f4{0, 0, 0, 0};
+  float l = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < J; j++) {
+    const uint32_t p = slot + 32 * j;
+    if (p < n) {
+      const float e = expf(sj[j] - M);
+      l += e;
+      acc += e * vr[j];
+    }
+  }
+  l = rows_sum4(l);
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    acc[k] += __shfl_xor(acc[k], 16);
+    acc[k] += __shfl_xor(acc[k], 32);
+  }
+  if (lane < 16) ((f4*)red_o)[wave * 16 + c] = acc;
+  if (lane == 0) red_l[wave] = l;
+  __syncthreads();
+  if (tid < HD) {
+    float L = 0, o = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < 8; w++) {
+      L += red_l[w];
+      o += red_o[w * HD + tid];
+    }
+    a.att[(uint64_t)t * a.heads * HD + h * HD + tid] = o / L;
+  }
+}
+
+bool attn_full_ok(uint32_t heads, uint32_t kv_heads, uint32_t hd) {
+  (void)heads;
+  (void)kv_heads;
+  return hd == 64;
+}
+
+// Rows the short-context kernel reads for a pass whose last position is last_pos.
+uint32_t attn_full_rows(uint32_t last_pos) {
+  uint32_t r = 64;
+  while (r <= last_pos) r *= 2;
+  return r;
+}
+
+int attn_full_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s) {
+  if (ntok == 0) return 0;
+  if (!attn_full_ok(a.heads, a.kv_heads, a.hd) || !a.att || a.rows > ATTN_FULL_MAX || a.rows > a.ctx)
+    return set_error(LLMHIP_ERR_ARG, "llm: attention: head size %u or %u rows not supported by the short-context kernel",
+                     a.hd, a.rows);
+  hipLaunchKernelGGL(attn_full_kernel, dim3(a.heads, ntok), dim3(512), 0, s, a);
+  LLM_HIP(hipGetLastError());
+  return 0;
 }
 
 uint32_t attn_lds_bytes(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t chunk) {

@@ -53,7 +53,7 @@ struct Model {
   hipStream_t stream = nullptr;
   Stager st;
   float *x = nullptr, *q = nullptr, *act = nullptr, *gbuf = nullptr, *logits = nullptr, *pv = nullptr,
-        *ml = nullptr, *amax_v = nullptr, *cs = nullptr;
+        *ml = nullptr, *amax_v = nullptr, *cs = nullptr, *att = nullptr;
   void* xprep = nullptr;  // prepared activations of a prefill chunk
   uint32_t *amax_i = nullptr, *state = nullptr;
   int32_t *tokens = nullptr, *outb = nullptr;
@@ -66,12 +66,13 @@ struct Model {
   std::map<std::string, TensorInfo> tensors;
   bool allocated = false, finalized = false;
   hipGraphExec_t decode_exec = nullptr;
-  std::map<uint32_t, hipGraphExec_t> chunk_exec;  // key: 2*m + last
-  std::map<uint32_t, uint32_t> graph_nodes;       // dispatches per graph key (decode: 1)
+  std::map<uint64_t, hipGraphExec_t> chunk_exec;  // key: graph_key(ntok, attn_rows, head)
+  std::map<uint64_t, uint32_t> graph_nodes;       // dispatches per graph key
   llmhip_stats stats{};
   int layers_limit = 0;
   std::set<std::string> skip;
   uint32_t pos = 0;  // host mirror of state[0] (== state[1])
+  uint32_t attn_rows = 0;  // pass being recorded: cache rows of attn_full_kernel, 0 = chunked attention
   bool prompted = false;
   uint32_t dispatches = 0;  // counter while recording
   std::vector<ProfRec>* prof = nullptr;  // eager profiling: events around every launch
@@ -389,6 +390,8 @@ static AttnArgs attn_args(const Model& m, const Layer& L) {
   a.ctx = m.ctx;
   a.smax = m.smax;
   a.chunk = m.chunk;
+  a.att = m.att;
+  a.rows = m.attn_rows;
   a.scale = (float)(1 / std::sqrt((double)m.cfg.head_dim));  // cpu.go:304
   return a;
 }
@@ -397,15 +400,22 @@ static int rec_k2(Model& m, const Layer& L, uint32_t ntok) {
   if (skipped(m, "k2")) return 0;
   // KV bytes read for the last token of the pass (the decode step's one token)
   uint64_t bytes = 2ull * (m.pos + 1) * m.kvd * 4;
+  if (m.attn_rows)
+    return launch_rec(m, "k2", bytes, [&]() { return attn_full_launch(attn_args(m, L), ntok, m.stream); });
   return launch_rec(m, "k2", bytes, [&]() { return attn_launch(attn_args(m, L), ntok, m.stream); });
 }
 
 static int rec_k3(Model& m, const Layer& L, uint32_t ntok) {
   GemvArgs a = base_args(m, L.o, ntok);
-  a.pv = m.pv;
-  a.ml = m.ml;
   a.y = m.x;
   a.ldy = m.cfg.embd;
+  if (m.attn_rows) {  // the heads' outputs are already merged
+    a.x = m.att;
+    a.ldx = m.cfg.embd;
+    return mat_rec(m, "k3", "p3", a, L.o.g.q.type, PRO_PLAIN, EPI_ACC, L.o.g.gguf_bytes());
+  }
+  a.pv = m.pv;
+  a.ml = m.ml;
   return mat_rec(m, "k3", "p3", a, L.o.g.q.type, PRO_MERGE, EPI_ACC, L.o.g.gguf_bytes());
 }
 
@@ -512,9 +522,21 @@ static int record_pass(Model& m, uint32_t ntok, bool head) {
   return rec_adv(m, ntok);
 }
 
+// The cache rows attn_full_kernel reads for a pass of ntok tokens from
+// position pos, or 0 when the pass needs the chunked kernel.
+static uint32_t full_attn_rows(const Model& m, uint32_t pos, uint32_t ntok) {
+  const uint32_t last = pos + ntok - 1;
+  if (last >= ATTN_FULL_MAX || !attn_full_ok(m.cfg.heads, m.cfg.kv_heads, m.cfg.head_dim)) return 0;
+  return std::min(attn_full_rows(last), m.ctx);
+}
+
+static uint64_t graph_key(uint32_t ntok, uint32_t attn_rows, bool head) {
+  return ((uint64_t)ntok << 32) | ((uint64_t)attn_rows << 1) | (head ? 1 : 0);
+}
+
 // Capture record_pass into a graph (once per key).
 static int graph_for(Model& m, uint32_t ntok, bool head, hipGraphExec_t* out) {
-  uint32_t key = 2 * ntok + (head ? 1 : 0);
+  uint64_t key = graph_key(ntok, m.attn_rows, head);
   auto it = m.chunk_exec.find(key);
   if (it != m.chunk_exec.end()) {
     *out = it->second;
@@ -540,11 +562,13 @@ static int graph_for(Model& m, uint32_t ntok, bool head, hipGraphExec_t* out) {
   return 0;
 }
 
-static int launch_graph(Model& m, uint32_t ntok, bool head) {
+// One pass of ntok tokens whose first position is pos (known on the host).
+static int launch_graph(Model& m, uint32_t pos, uint32_t ntok, bool head) {
   hipGraphExec_t ex;
+  m.attn_rows = full_attn_rows(m, pos, ntok);
   LLM_TRY(graph_for(m, ntok, head, &ex));
   LLM_HIP(hipGraphLaunch(ex, m.stream));
-  m.stats.dispatches += m.graph_nodes[2 * ntok + (head ? 1 : 0)];
+  m.stats.dispatches += m.graph_nodes[graph_key(ntok, m.attn_rows, head)];
   return 0;
 }
 
@@ -597,7 +621,7 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
     return fail(set_error(LLMHIP_ERR_DEVICE, "llm: hipStreamCreate failed"));
   int rc;
   const uint64_t E = c.embd, F = c.ff, V = c.vocab, pm = m->pm, H = c.heads;
-  if ((rc = dalloc_n(*m, &m->x, pm * E)) || (rc = dalloc_n(*m, &m->q, pm * E)) ||
+  if ((rc = dalloc_n(*m, &m->x, pm * E)) || (rc = dalloc_n(*m, &m->q, pm * E)) || (rc = dalloc_n(*m, &m->att, pm * E)) ||
       (rc = dalloc_n(*m, &m->act, pm * F)) || (rc = dalloc_n(*m, &m->gbuf, pm * F)) ||
       (rc = dalloc_n(*m, &m->logits, V)) || (rc = dalloc_n(*m, &m->amax_v, V / 16 + 64)) ||
       (rc = dalloc_n(*m, &m->amax_i, V / 16 + 64)) || (rc = dalloc_n(*m, &m->pv, pm * H * m->smax * c.head_dim)) ||
@@ -725,7 +749,7 @@ int llmhip_model_prefill(llmhip_model* h, const int32_t* ids, int n, float* logi
   bool full = m.layers_limit == 0 || m.layers_limit >= m.cfg.layers;
   for (int a = 0; a < n; a += (int)m.pm) {
     int b = std::min(a + (int)m.pm, n);
-    LLM_TRY(launch_graph(m, (uint32_t)(b - a), b == n));
+    LLM_TRY(launch_graph(m, (uint32_t)a, (uint32_t)(b - a), b == n));
     m.stats.submits++;
   }
   m.pos = (uint32_t)n;
@@ -748,7 +772,7 @@ int llmhip_model_decode(llmhip_model* h, int cnt, int32_t* out) {
                      m.pos);
   LLM_HIP(hipSetDevice(m.device));
   uint32_t first = m.pos;
-  for (int j = 0; j < cnt; j++) LLM_TRY(launch_graph(m, 1, true));
+  for (int j = 0; j < cnt; j++) LLM_TRY(launch_graph(m, first + (uint32_t)j, 1, true));
   LLM_HIP(hipMemcpyAsync(m.host, m.tokens + first + 1, (size_t)cnt * 4, hipMemcpyDeviceToHost, m.stream));
   LLM_HIP(hipStreamSynchronize(m.stream));
   memcpy(out, m.host, (size_t)cnt * 4);
@@ -839,6 +863,7 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
     return set_error(LLMHIP_ERR_ARG, "llm: no kernel \"%s\" (head, k1..k5)", kernel);
   std::set<std::string> saved = m.skip;
   m.skip.clear();
+  m.attn_rows = full_attn_rows(m, m.pos, 1);  // the variant the next decode step runs
   const int L = m.cfg.layers;
   auto wb = [](const QMat& q) { return q.g.gguf_bytes(); };
   // launch i runs layer i % L: consecutive launches read different weights,
@@ -895,6 +920,7 @@ int llmhip_model_profile(llmhip_model* h, int tokens, llmhip_kernel_time* out, i
   for (int t = 0; t < tokens && rc == 0; t++) {
     std::vector<ProfRec> recs;
     m.prof = &recs;
+    m.attn_rows = full_attn_rows(m, m.pos, 1);
     rc = record_pass(m, 1, true);
     m.prof = nullptr;
     if (hipStreamSynchronize(m.stream) != hipSuccess && rc == 0)

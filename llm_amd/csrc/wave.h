@@ -1,0 +1,51 @@
+// Wavefront (64-lane) reductions for CDNA: DPP moves inside each row of 16
+// lanes (a few cycles each, no LDS traffic), then v_readlane of the four row
+// results.  Each step adds a lane's value to its partner's, so every lane of
+// a row ends with the bitwise same result.  Call with the whole wave active.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace llmhip {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141; // lane i <- 7-i within 8
+constexpr int DPP_MIRROR = 0x140;      // lane i <- 15-i within 16
+
+// sum over the 16 lanes of each row, in every lane of the row
+__device__ __forceinline__ float row_sum16(float x) {
+  x += dpp_mov<DPP_XOR1>(x);
+  x += dpp_mov<DPP_XOR2>(x);
+  x += dpp_mov<DPP_HALF_MIRROR>(x);
+  x += dpp_mov<DPP_MIRROR>(x);
+  return x;
+}
+
+__device__ __forceinline__ float row_max16(float x) {
+  x = fmaxf(x, dpp_mov<DPP_XOR1>(x));
+  x = fmaxf(x, dpp_mov<DPP_XOR2>(x));
+  x = fmaxf(x, dpp_mov<DPP_HALF_MIRROR>(x));
+  x = fmaxf(x, dpp_mov<DPP_MIRROR>(x));
+  return x;
+}
+
+__device__ __forceinline__ float lane_value(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+// x equal across each row of 16 lanes -> the sum / max of the four rows (wave-uniform)
+__device__ __forceinline__ float rows_sum4(float x) {
+  return (lane_value(x, 0) + lane_value(x, 16)) + (lane_value(x, 32) + lane_value(x, 48));
+}
+
+__device__ __forceinline__ float rows_max4(float x) {
+  return fmaxf(fmaxf(lane_value(x, 0), lane_value(x, 16)), fmaxf(lane_value(x, 32), lane_value(x, 48)));
+}
+
+}  // namespace llmhip

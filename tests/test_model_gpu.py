@@ -56,6 +56,18 @@ def test_tiny_parity(gpu, name):
     _check(g, cpu, prompt, 40)
 
 
+@pytest.mark.parametrize("prompt_len,heads,kv_heads", [(230, 4, 4), (300, 4, 2), (250, 8, 2), (200, 16, 2)])
+def test_attention_paths(gpu, prompt_len, heads, kv_heads):
+    """Both attention kernels and the switch between them: passes that end
+    below position 256 run the one-workgroup-per-KV-head kernel, later ones the
+    chunked kernel merged in the O-projection; prefill chunks and decode steps
+    on both sides, for 1, 2, 4 and 8 query heads per KV head."""
+    spec = synth.tiny_llama(seed=6 + heads + kv_heads, embd=64 * heads, heads=heads, kv_heads=kv_heads)
+    g, cpu = _open(spec, 512)
+    prompt = synth.prompt(7, prompt_len, spec.vocab)
+    _check(g, cpu, prompt, 320 - prompt_len)
+
+
 def test_decode_batches_and_stops(gpu):
     from llm_amd import llm
     spec = synth.tiny_qwen()
