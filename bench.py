@@ -29,6 +29,43 @@ sys.path.insert(0, ROOT)
 PEAK_HBM_GBS = 8000.0
 METRIC = "decode & prefill tok/s at Qwen2.5-0.5B shape; Q4_0 GEMV HBM GB/s vs peak"
 SWEEP = [(576, 576), (1536, 576), (576, 1536), (896, 896), (4864, 896), (896, 4864), (151936, 896)]
+# HBM bytes per launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+# runs of this script, scaled by the same counters on a copy of known size
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "pmc_decode_qwen25.txt")
+
+
+def kernel_symbols(attn_full):
+    """Device symbol of each decode kernel class of the config-3 model (Q4_0
+    layers, Q8_0 head): gemv_kernel<type, tokens, prologue, epilogue>."""
+    return {"k1": "gemv_kernel<2u, 1, 1, 2>", "k2": "attn_full_kernel" if attn_full else "attn_kernel",
+            "k3": "gemv_kernel<2u, 1, 0, 1>" if attn_full else "gemv_kernel<2u, 1, 2, 1>",
+            "k4": "gemv_kernel<2u, 1, 1, 3>", "k5": "gemv_kernel<2u, 1, 0, 1>", "head": "gemv_kernel<8u, 1, 1, 4>"}
+
+
+def pmc_traffic(cls):
+    """HBM bytes per launch of a decode kernel class from the committed
+    rocprofv3 counter summary (lines `traffic_bytes <class> <bytes>`), or None."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                p = line.split()
+                if len(p) == 3 and p[0] == "traffic_bytes" and p[1] == cls:
+                    return int(p[2])
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration():
+    """A plain 256 MiB device-to-device copy (one elementwise kernel): the
+    known-size reference for the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    x = torch.ones(64 << 20, device="cuda:0")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    y.copy_(x)
+    torch.cuda.synchronize()
+    log(f"copy calibration: {x.numel() * 4} bytes read, {y.numel() * 4} bytes written")
 
 
 def log(*a):
@@ -81,12 +118,16 @@ def generation(args):
                         "us_per_token": round(us * n, 2),
                         "gbps": round(nbytes / us * 1e-3, 1) if nbytes else None}
     step_kernel_us = sum(c["us_per_token"] for c in classes.values())
+    syms = kernel_symbols(args.prompt + 1 < 256)
+    for cls in classes:
+        classes[cls]["symbol"] = syms[cls]
+    # the dominant kernel: the class with the most device time per decode token
     dom = max(classes, key=lambda k: classes[k]["us_per_token"])
     d = classes[dom]
     achieved = d["bytes"] / d["avg_us"] * 1e-3
-    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                "bytes_per_launch": d["bytes"], "avg_us": d["avg_us"]}
+    roofline = {"bound": "hbm", "kernel": dom, "symbol": syms[dom], "achieved": round(achieved, 1),
+                "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                "traffic": pmc_traffic(dom), "bytes_per_launch": d["bytes"], "avg_us": d["avg_us"]}
     w = [k for k in classes if k != "k2"]
     gemv_all = sum(classes[k]["bytes"] * classes[k]["launches_per_token"] for k in w) / \
         sum(classes[k]["us_per_token"] for k in w) * 1e-3
@@ -107,11 +148,16 @@ def long_context(args):
     g.Generate(prompt, 8, -1)
     tm = g.Generate(prompt, 512, -1)
     us, nbytes = g.bench_kernel("k2", 96)
+    classes = {}
+    for cls in ("k1", "k3", "k4", "k5", "head"):
+        cu, cb = g.bench_kernel(cls, 96 if cls != "head" else 20)
+        classes[cls] = {"avg_us": round(cu, 3), "bytes": cb, "gbps": round(cb / cu * 1e-3, 1)}
     g.close()
     res = {"workload": "BASELINE config 4: qwen2.5-0.5b shape, Q4_1 ffn_down on odd layers, Q8_0 head, 2048-token "
                        "prompt, 512 greedy tokens, ctx 4096",
            "prefill_tok_s": round(tm.PromptTokens / tm.Prefill, 1), "decode_tok_s": round(tm.Generated / tm.Decode, 1),
-           "attention_at_end": {"avg_us": round(us, 2), "kv_bytes": nbytes, "gbps": round(nbytes / us * 1e-3, 1)}}
+           "attention_at_end": {"avg_us": round(us, 2), "kv_bytes": nbytes, "gbps": round(nbytes / us * 1e-3, 1)},
+           "classes_at_end": classes}
     log(f"long context: prefill {res['prefill_tok_s']} tok/s, decode {res['decode_tok_s']} tok/s, "
         f"attention {us:.1f} us for {nbytes} KV bytes")
     return res
@@ -184,6 +230,7 @@ def main():
     ap.add_argument("--no-long", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-calibration", action="store_true", help="only run the counter calibration copy")
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py: this build measures one GPU; the path shards by independent sequences per GPU "
@@ -193,6 +240,9 @@ def main():
     if not torch.cuda.is_available():
         log("bench.py: no GPU")
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     g, r = generation(args)
     g.close()
     res = {

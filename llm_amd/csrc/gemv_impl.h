@@ -15,6 +15,7 @@
 #pragma once
 
 #include "gemv.h"
+#include "wave.h"
 
 namespace llmhip {
 
@@ -256,6 +257,9 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
   return v;
 }
+// wave-uniform sum / max through DPP (whole wave active)
+__device__ __forceinline__ float wave_sum_dpp(float v) { return rows_sum4(row_sum16(v)); }
+__device__ __forceinline__ float wave_max_dpp(float v) { return rows_max4(row_max16(v)); }
 
 // -------------------------------------------------------------- the kernel
 
@@ -386,15 +390,66 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   const uint32_t nb = a.nb, K = a.k, NI = nb * 4;
   const Lds L = lds_layout(NT, PRO, QT, nb, nwv, a.heads, a.smax);
   h8* xs = (h8*)(lds + L.xs);
-  float* misc = (float*)(lds + L.misc);  // [0,64) wave partials, [64,72) rms s, [72,80) exps, [80,128) argmax
+  float* misc = (float*)(lds + L.misc);  // [0,64) sum-of-squares partials, [64,128) max partials, then argmax
   float* bsum = (float*)(lds + L.bsum);
   float* wts = (float*)(lds + L.wts);
-  int* exps = (int*)(misc + 72);
+
+  // ---- the weights first: this wave's tile, the first batch of up to four of
+  // its block groups (and the tail blocks) are in flight while the prologue
+  // loads and reduces the activations (up to two tokens: with four, the
+  // registers held across the prologue would spill)
+  constexpr bool HOIST = NT <= 2;
+  const uint32_t split = a.split, tpw = nwv / split;
+  const uint32_t lt = wave / split, sp = wave % split;
+  const uint32_t tile = blockIdx.x * tpw + lt;
+  const bool has_tile = tile < a.tiles;
+  const int r = lane & 15, q = lane >> 4;  // B/D column (row in tile), k-group / D row group
+  const int slot = lane & 15;              // A row: token slot
+  const uint8_t* qt = a.qs + (uint64_t)tile * 16 * nb * T::QB;
+  const uint8_t* st = a.sc + (uint64_t)tile * 16 * nb * T::SB;
+  const uint32_t cnt = has_tile && a.ng > sp ? (a.ng - sp + split - 1) / split : 0;
+  uint4 w0[4], w1[4], sv[4];
+  auto load_batch = [&](uint32_t i0) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      if (i0 + u >= cnt) continue;
+      const uint32_t g4 = sp + (i0 + u) * split;
+      if (QT == LLMHIP_Q8_0) {
+        w0[u] = ld_stream16(qt + g4 * 2048 + lane * 16);
+        w1[u] = ld_stream16(qt + g4 * 2048 + 1024 + lane * 16);
+      } else {
+        w0[u] = ld_stream16(qt + g4 * 1024 + lane * 16);
+      }
+      if (QT == LLMHIP_Q4_1) {
+        sv[u] = *(const uint4*)(st + g4 * 256 + r * 16);
+      } else {
+        uint2 x2 = *(const uint2*)(st + g4 * 128 + r * 8);
+        sv[u] = uint4{x2.x, x2.y, 0, 0};
+      }
+    }
+  };
+  if (HOIST) load_batch(0);
+  const bool has_tail = has_tile && a.tail && (a.ng % split) == sp;
+  uint32_t qw[3][2], sb[3];
+  auto load_tail = [&]() {
+#pragma unroll
+    for (uint32_t j = 0; j < 3; j++) {
+      if (j >= a.tail) continue;
+      const uint32_t b = 4 * a.ng + j;
+      const uint8_t* qq = qt + qs_off<QT>(b, lane, a.ng, a.tail);
+      qw[j][0] = *(const uint32_t*)qq;
+      if (QT == LLMHIP_Q8_0) qw[j][1] = *(const uint32_t*)(qq + 4);
+      const uint8_t* sp8 = st + sc_off<QT>(b, r, a.ng, a.tail);
+      sb[j] = QT == LLMHIP_Q4_1 ? *(const uint32_t*)sp8 : (uint32_t)*(const uint16_t*)sp8;
+    }
+  };
+  if (HOIST && has_tail) load_tail();
 
   // ---- prologue: one round of global loads, the activations of nt tokens
   // staged in registers as items (block b, k-group g) of 8 elements
   // (4g..4g+3 and 16+4g..16+4g+3), then scaled, split and stored in MFMA
-  // operand order.
+  // operand order.  Per-wave partials go through LDS; every thread then
+  // finishes the reduction itself (the same sums in the same order).
   f4 va[NT][MAXI], vc[NT][MAXI];
   if (PRO == PRO_MERGE) {
     // flash-decoding merge (fused.go K3 hook, kernels_fused.go:150-170):
@@ -474,19 +529,15 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int k = 0; k < MAXI; k++)
         for (int i = 0; i < 4; i++) ss += va[t][k][i] * va[t][k][i] + vc[t][k][i] * vc[t][k][i];
-      ss = wave_sum(ss);
+      ss = wave_sum_dpp(ss);
       if (lane == 0) misc[wave * NT + t] = ss;
-    }
-    __syncthreads();
-    if (tid < nt) {
-      float ss = 0;
-      for (uint32_t w = 0; w < nwv; w++) ss += misc[w * NT + tid];
-      misc[64 + tid] = (float)(1.0 / sqrt((double)(ss / (float)K + a.eps)));
     }
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-      float s = t < nt ? misc[64 + t] : 0.f;
+      float ss = 0;
+      for (uint32_t w = 0; w < nwv; w++) ss += misc[w * NT + t];
+      const float s = t < nt ? (float)(1.0 / sqrt((double)(ss / (float)K + a.eps))) : 0.f;
 #pragma unroll
       for (int k = 0; k < MAXI; k++)
         for (int i = 0; i < 4; i++) {
@@ -494,36 +545,34 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
           vc[t][k][i] = __fmul_rn(__fmul_rn(vc[t][k][i], s), wc[k][i]);
         }
     }
-    __syncthreads();  // misc partials are reused below
   }
-  // largest magnitude per token -> power-of-two scale
+  // largest magnitude per token -> power-of-two scale 2^ex[t]
+  float* mpart = misc + 64;
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     float m = 0;
 #pragma unroll
     for (int k = 0; k < MAXI; k++)
       for (int i = 0; i < 4; i++) m = fmaxf(m, fmaxf(fabsf(va[t][k][i]), fabsf(vc[t][k][i])));
-    m = wave_max(m);
-    if (lane == 0) misc[wave * NT + t] = m;
+    m = wave_max_dpp(m);
+    if (lane == 0) mpart[wave * NT + t] = m;
   }
   __syncthreads();
-  if (tid < NT) {
-    int e = 0;
-    if (tid < nt) {
-      float m = 0;
-      for (uint32_t w = 0; w < nwv; w++) m = fmaxf(m, misc[w * NT + tid]);
-      if (m > 0 && m <= 3.0e38f) {
-        int E;
-        frexpf(m, &E);
-        e = 15 - E;
-      }
-    }
-    exps[tid] = e;
-  }
-  __syncthreads();
+  int ex[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
-    const int ex = exps[t];
+    float m = 0;
+    for (uint32_t w = 0; w < nwv; w++) m = fmaxf(m, mpart[w * NT + t]);
+    int e = 0;
+    if (t < nt && m > 0 && m <= 3.0e38f) {
+      int E;
+      frexpf(m, &E);
+      e = 15 - E;
+    }
+    ex[t] = e;
+  }
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
 #pragma unroll
     for (int k = 0; k < MAXI; k++) {
       uint32_t it = tid + k * bd;
@@ -532,7 +581,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       const float v[8] = {A[0], A[2], C[0], C[2], A[1], A[3], C[1], C[3]};
       h8 hi, lo;
       for (int i = 0; i < 8; i++) {
-        float s = ldexpf(v[i], ex);
+        float s = ldexpf(v[i], ex[t]);
         _Float16 h = (_Float16)s;
         hi[i] = h;
         lo[i] = (_Float16)(s - (float)h);
@@ -544,7 +593,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
         float sx = (A[0] + A[1] + A[2] + A[3]) + (C[0] + C[1] + C[2] + C[3]);
         sx += __shfl_xor(sx, 1);
         sx += __shfl_xor(sx, 2);
-        if ((it & 3) == 0) bsum[t * nb + it / 4] = ldexpf(sx, ex);
+        if ((it & 3) == 0) bsum[t * nb + it / 4] = ldexpf(sx, ex[t]);
       }
     }
   }
@@ -552,15 +601,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
 
   // ---- main loop: each wave one 16-row tile over its share of the block
   // groups; the weights of up to four groups are in flight at once
-  const uint32_t split = a.split, tpw = nwv / split;
-  const uint32_t lt = wave / split, sp = wave % split;
-  const uint32_t tile = blockIdx.x * tpw + lt;
-  const int r = lane & 15, q = lane >> 4;  // B/D column (row in tile), k-group / D row group
-  const int slot = lane & 15;              // A row: token slot
   float acc0 = 0, acc1 = 0;
-  if (tile < a.tiles) {
-    const uint8_t* qt = a.qs + (uint64_t)tile * 16 * nb * T::QB;
-    const uint8_t* st = a.sc + (uint64_t)tile * 16 * nb * T::SB;
+  if (has_tile) {
     auto block = [&](uint32_t b, h8 B, uint32_t dbits, uint32_t mbits) {
       h8 A = {};
       if (slot < S) A = xs[(b * 4 + q) * S + slot];
@@ -574,26 +616,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
         if (2 * q + 1 < NT) acc1 += m * bsum[(2 * q + 1) * nb + b];
       }
     };
-    const uint32_t cnt = a.ng > sp ? (a.ng - sp + split - 1) / split : 0;
     for (uint32_t i0 = 0; i0 < cnt; i0 += 4) {
-      uint4 w0[4], w1[4], sv[4];
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        if (i0 + u >= cnt) continue;
-        const uint32_t g4 = sp + (i0 + u) * split;
-        if (QT == LLMHIP_Q8_0) {
-          w0[u] = ld_stream16(qt + g4 * 2048 + lane * 16);
-          w1[u] = ld_stream16(qt + g4 * 2048 + 1024 + lane * 16);
-        } else {
-          w0[u] = ld_stream16(qt + g4 * 1024 + lane * 16);
-        }
-        if (QT == LLMHIP_Q4_1) {
-          sv[u] = *(const uint4*)(st + g4 * 256 + r * 16);
-        } else {
-          uint2 x2 = *(const uint2*)(st + g4 * 128 + r * 8);
-          sv[u] = uint4{x2.x, x2.y, 0, 0};
-        }
-      }
+      if (i0 > 0 || !HOIST) load_batch(i0);
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         if (i0 + u >= cnt) continue;
@@ -616,23 +640,12 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
         }
       }
     }
-    if (a.tail && (a.ng % split) == sp) {
-      const uint32_t ng = a.ng, tail = a.tail;
-      uint32_t qw[3][2], sb[3];
+    if (has_tail) {
+      if (!HOIST) load_tail();
 #pragma unroll
       for (uint32_t j = 0; j < 3; j++) {
-        if (j >= tail) continue;
-        const uint32_t b = 4 * ng + j;
-        const uint8_t* qq = qt + qs_off<QT>(b, lane, ng, tail);
-        qw[j][0] = *(const uint32_t*)qq;
-        if (QT == LLMHIP_Q8_0) qw[j][1] = *(const uint32_t*)(qq + 4);
-        const uint8_t* s = st + sc_off<QT>(b, r, ng, tail);
-        sb[j] = QT == LLMHIP_Q4_1 ? *(const uint32_t*)s : (uint32_t)*(const uint16_t*)s;
-      }
-#pragma unroll
-      for (uint32_t j = 0; j < 3; j++) {
-        if (j >= tail) continue;
-        const uint32_t b = 4 * ng + j;
+        if (j >= a.tail) continue;
+        const uint32_t b = 4 * a.ng + j;
         if (QT == LLMHIP_Q8_0) block(b, dq8(qw[j][0], qw[j][1]), sb[j] & 0xffff, 0);
         else block(b, dq4<QT == LLMHIP_Q4_1>(qw[j][0]), sb[j] & 0xffff, sb[j] >> 16);
       }
@@ -655,8 +668,14 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   const bool active = sp == 0 && tile < a.tiles;
   const int tA = 2 * q, tB = 2 * q + 1;
   const bool okA = tA < nt, okB = NT > 1 && tB < nt;
-  const float vA = okA ? ldexpf(acc0, -exps[tA]) : 0.f;
-  const float vB = okB ? ldexpf(acc1, -exps[tB]) : 0.f;
+  int eA = 0, eB = 0;
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    if (t == tA) eA = ex[t];
+    if (t == tB) eB = ex[t];
+  }
+  const float vA = okA ? ldexpf(acc0, -eA) : 0.f;
+  const float vB = okB ? ldexpf(acc1, -eB) : 0.f;
   row_epilogue<EPI>(a, tile, r, active, t0 + tA, okA, vA, t0 + tB, okB, vB);
   if (EPI == EPI_ARGMAX) {
     // (max, lowest index) of token 0 over this workgroup's rows, NaN never

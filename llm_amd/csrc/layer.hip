@@ -112,13 +112,21 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 // sums are reduced over rows by two shuffles and over waves through LDS.  All
 // global loads are issued before anything waits; a.rows (host-chosen, >= every
 // position count of the pass) bounds the rows read, the rest are masked.
-__global__ __launch_bounds__(512) void attn_full_kernel(AttnArgs a) {
+// Workgroups go to the 8 XCDs round-robin (block b on XCD b % 8), so the query
+// heads of one (token, KV head) instance get blocks on one XCD and read its
+// rows through one L2, and the instances spread over the XCDs: block b serves
+// instance 8*(s / GQ) + b % 8 (= t * kv_heads + g), query head s % GQ of it,
+// with s = b / 8; blocks past the last instance exit at once.
+__global__ __launch_bounds__(512) void attn_full_kernel(AttnArgs a, uint32_t ntok) {
   typedef float f4 __attribute__((ext_vector_type(4)));
   constexpr uint32_t HD = 64, J = ATTN_FULL_MAX / 32;
   __shared__ float red_m[8], red_l[8];
   __shared__ __attribute__((aligned(16))) float red_o[8 * HD];
-  const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t g = h / (a.heads / a.kv_heads);
+  const uint32_t GQ = a.heads / a.kv_heads, sb = blockIdx.x / 8;
+  const uint32_t inst = 8 * (sb / GQ) + blockIdx.x % 8;
+  if (inst >= ntok * a.kv_heads) return;
+  const uint32_t t = inst / a.kv_heads, g = inst % a.kv_heads;
+  const uint32_t h = g * GQ + sb % GQ, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t c = lane & 15, slot = tid >> 4;
   const float* kb = a.kv + g * HD + 4 * c;
   const float* vb = a.kv + (uint64_t)a.ctx * a.kvd + g * HD + 4 * c;
@@ -188,19 +196,17 @@ bool attn_full_ok(uint32_t heads, uint32_t kv_heads, uint32_t hd) {
   return hd == 64;
 }
 
-// Rows the short-context kernel reads for a pass whose last position is last_pos.
-uint32_t attn_full_rows(uint32_t last_pos) {
-  uint32_t r = 64;
-  while (r <= last_pos) r *= 2;
-  return r;
-}
+// Rows the short-context kernel reads for a pass whose last position is
+// last_pos: the next multiple of 64 (one of four graph variants).
+uint32_t attn_full_rows(uint32_t last_pos) { return (last_pos / 64 + 1) * 64; }
 
 int attn_full_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s) {
   if (ntok == 0) return 0;
   if (!attn_full_ok(a.heads, a.kv_heads, a.hd) || !a.att || a.rows > ATTN_FULL_MAX || a.rows > a.ctx)
     return set_error(LLMHIP_ERR_ARG, "llm: attention: head size %u or %u rows not supported by the short-context kernel",
                      a.hd, a.rows);
-  hipLaunchKernelGGL(attn_full_kernel, dim3(a.heads, ntok), dim3(512), 0, s, a);
+  const uint32_t gq = a.heads / a.kv_heads, blocks = 8 * gq * ((ntok * a.kv_heads + 7) / 8);
+  hipLaunchKernelGGL(attn_full_kernel, dim3(blocks), dim3(512), 0, s, a, ntok);
   LLM_HIP(hipGetLastError());
   return 0;
 }

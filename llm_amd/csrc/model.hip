@@ -870,9 +870,9 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
   // as in the decode pass
   auto one = [&](int i) -> int {
     const Layer& ly = m.layers[i % L];
-    if (k == "head") {  // without the sampling: repeated launches must not advance the state
+    if (k == "head") {  // the decode head kernel without the sampling kernel, which advances the state
       const QMat& w = m.tied ? m.embd : m.out;
-      return gemv_launch(head_args(m, 0, 0), w.g.q.type, PRO_RMS, EPI_STORE, m.stream);
+      return gemv_launch(head_args(m, 0, 0), w.g.q.type, PRO_RMS, EPI_ARGMAX, m.stream);
     }
     if (k == "k1") return rec_k1(m, ly, 1);
     if (k == "k2") return rec_k2(m, ly, 1);
