@@ -29,7 +29,6 @@ struct QMat {
 enum Prologue : int {
   PRO_PLAIN = 0,  // x[t*ldx + e]
   PRO_RMS = 1,    // RMSNorm(x[t]) * nw  (cpu.go:81-98), recomputed per workgroup
-  PRO_MERGE = 2   // merge of the attention chunks (flash-decoding), fused.go K3 input hook
 };
 
 enum Epilogue : int {
@@ -57,9 +56,7 @@ struct GemvArgs {
   uint32_t xrow0;  // token t reads row xrow0 + t of x (head: the last token of a chunk)
   const float* nw;
   float eps;
-  const float* pv;
-  const float* ml;
-  uint32_t heads, hd, smax, chunk;  // attention partials [t][h][smax][hd], chunk positions each
+  uint32_t heads, hd;  // QKV epilogue: RoPE per head
   const uint32_t* state;            // (pos, step) on the device
   // epilogue
   float* y;

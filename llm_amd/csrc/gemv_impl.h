@@ -267,11 +267,10 @@ constexpr int MAXI = 2;  // 8-element activation items staged per thread and tok
 
 // LDS layout of one launch (bytes).
 struct Lds {
-  uint32_t xs, misc, bsum, part, wts, total;
+  uint32_t xs, misc, bsum, part, total;
 };
 
-__host__ __device__ inline Lds lds_layout(int NT, int pro, uint32_t qtype, uint32_t nb, uint32_t waves,
-                                          uint32_t heads, uint32_t smax) {
+__host__ __device__ inline Lds lds_layout(int NT, uint32_t qtype, uint32_t nb, uint32_t waves) {
   Lds L;
   uint32_t o = 0;
   L.xs = o;
@@ -282,8 +281,6 @@ __host__ __device__ inline Lds lds_layout(int NT, int pro, uint32_t qtype, uint3
   if (qtype == LLMHIP_Q4_1) o += nb * NT * 4;
   L.part = o;
   o += waves * 64 * 2 * 4;
-  L.wts = o;
-  if (pro == PRO_MERGE) o += NT * heads * (smax + 1) * 4;
   L.total = o;
   return L;
 }
@@ -388,11 +385,10 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   const uint32_t t0 = blockIdx.y * NT;
   const int nt = min((int)NT, (int)(a.ntok - t0));
   const uint32_t nb = a.nb, K = a.k, NI = nb * 4;
-  const Lds L = lds_layout(NT, PRO, QT, nb, nwv, a.heads, a.smax);
+  const Lds L = lds_layout(NT, QT, nb, nwv);
   h8* xs = (h8*)(lds + L.xs);
   float* misc = (float*)(lds + L.misc);  // [0,64) sum-of-squares partials, [64,128) max partials, then argmax
   float* bsum = (float*)(lds + L.bsum);
-  float* wts = (float*)(lds + L.wts);
 
   // ---- the weights first: this wave's tile, the first batch of up to four of
   // its block groups (and the tail blocks) are in flight while the prologue
@@ -451,50 +447,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   // operand order.  Per-wave partials go through LDS; every thread then
   // finishes the reduction itself (the same sums in the same order).
   f4 va[NT][MAXI], vc[NT][MAXI];
-  if (PRO == PRO_MERGE) {
-    // flash-decoding merge (fused.go K3 hook, kernels_fused.go:150-170):
-    // att = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c per (token, head)
-    const uint32_t H = a.heads, SM = a.smax, pos0 = a.state[0];
-    for (uint32_t th = tid; th < (uint32_t)nt * H; th += bd) {
-      uint32_t t = th / H, h = th % H;
-      uint32_t nc = (pos0 + t0 + t + a.chunk) / a.chunk;
-      const float* mlp = a.ml + ((uint64_t)(t0 + t) * H + h) * SM * 2;
-      float M = -INFINITY;
-      for (uint32_t c = 0; c < nc; c++) M = fmaxf(M, mlp[2 * c]);
-      float l = 0;
-      float* w = wts + (t * H + h) * (SM + 1);
-      for (uint32_t c = 0; c < nc; c++) {
-        float e = expf(mlp[2 * c] - M);
-        w[c] = e;
-        l += e * mlp[2 * c + 1];
-      }
-      w[SM] = 1.f / l;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-      for (int k = 0; k < MAXI; k++) {
-        uint32_t it = tid + k * bd;
-        f4 A = {0, 0, 0, 0}, C = {0, 0, 0, 0};
-        if (t < nt && it < NI) {
-          uint32_t b = it / 4, g = it % 4, e = b * 32 + 4 * g, h = e / a.hd, dd = e % a.hd;
-          uint32_t nc = (pos0 + t0 + t + a.chunk) / a.chunk;
-          const float* w = wts + (t * H + h) * (SM + 1);
-          const float* pvp = a.pv + (((uint64_t)(t0 + t) * H + h) * SM) * a.hd + dd;
-#pragma unroll 4
-          for (uint32_t c = 0; c < nc; c++) {
-            f4 p0 = *(const f4*)(pvp + (uint64_t)c * a.hd), p1 = *(const f4*)(pvp + (uint64_t)c * a.hd + 16);
-            A += w[c] * p0;
-            C += w[c] * p1;
-          }
-          A *= w[SM];
-          C *= w[SM];
-        }
-        va[t][k] = A;
-        vc[t][k] = C;
-      }
-  } else {
+  {
 #pragma unroll
     for (int t = 0; t < NT; t++)
 #pragma unroll
@@ -731,7 +684,6 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
   h8* xp = (h8*)a.xp;
   const uint32_t tg = t / 8, s2 = 2 * (t % 8);
   float* red = pl;        // [4] partials, [8] s, [9] exp
-  float* wts = pl + 16;   // MERGE: [H][SM+1]
   if (t >= a.ntok) {
     for (uint32_t it = tid; it < NI; it += 256) {
       xp[((uint64_t)tg * nb + it / 4) * 64 + (it % 4) * 16 + s2] = h8{};
@@ -742,44 +694,7 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
     return;
   }
   f4 va[PMAXI], vc[PMAXI];
-  if (PRO == PRO_MERGE) {
-    const uint32_t H = a.heads, SM = a.smax;
-    const uint32_t nc = (a.state[0] + t + a.chunk) / a.chunk;
-    for (uint32_t h = tid; h < H; h += 256) {
-      const float* mlp = a.ml + ((uint64_t)t * H + h) * SM * 2;
-      float M = -INFINITY;
-      for (uint32_t c = 0; c < nc; c++) M = fmaxf(M, mlp[2 * c]);
-      float l = 0;
-      float* w = wts + h * (SM + 1);
-      for (uint32_t c = 0; c < nc; c++) {
-        float e = expf(mlp[2 * c] - M);
-        w[c] = e;
-        l += e * mlp[2 * c + 1];
-      }
-      w[SM] = 1.f / l;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < PMAXI; k++) {
-      uint32_t it = tid + k * 256;
-      f4 A = {0, 0, 0, 0}, C = {0, 0, 0, 0};
-      if (it < NI) {
-        uint32_t e = (it / 4) * 32 + 4 * (it % 4), h = e / a.hd, dd = e % a.hd;
-        const float* w = wts + h * (SM + 1);
-        const float* pvp = a.pv + (((uint64_t)t * H + h) * SM) * a.hd + dd;
-#pragma unroll 4
-        for (uint32_t c = 0; c < nc; c++) {
-          f4 p0 = *(const f4*)(pvp + (uint64_t)c * a.hd), p1 = *(const f4*)(pvp + (uint64_t)c * a.hd + 16);
-          A += w[c] * p0;
-          C += w[c] * p1;
-        }
-        A *= w[SM];
-        C *= w[SM];
-      }
-      va[k] = A;
-      vc[k] = C;
-    }
-  } else {
+  {
 #pragma unroll
     for (int k = 0; k < PMAXI; k++) {
       uint32_t it = tid + k * 256;
@@ -1029,7 +944,6 @@ static int launch_nt(const GemvArgs& a, int pro, int epi, dim3 grid, uint32_t ld
     case PRO_PLAIN * 8 + EPI_STORE: return launch_one<QT, NT, PRO_PLAIN, EPI_STORE>(a, grid, lds, s);
     case PRO_PLAIN * 8 + EPI_ACC: return launch_one<QT, NT, PRO_PLAIN, EPI_ACC>(a, grid, lds, s);
     case PRO_RMS * 8 + EPI_QKV: return launch_one<QT, NT, PRO_RMS, EPI_QKV>(a, grid, lds, s);
-    case PRO_MERGE * 8 + EPI_ACC: return launch_one<QT, NT, PRO_MERGE, EPI_ACC>(a, grid, lds, s);
     case PRO_RMS * 8 + EPI_GATEUP: return launch_one<QT, NT, PRO_RMS, EPI_GATEUP>(a, grid, lds, s);
     case PRO_RMS * 8 + EPI_STORE: return launch_one<QT, NT, PRO_RMS, EPI_STORE>(a, grid, lds, s);
     case PRO_RMS * 8 + EPI_SWIGLU: return launch_one<QT, NT, PRO_RMS, EPI_SWIGLU>(a, grid, lds, s);
@@ -1041,7 +955,7 @@ static int launch_nt(const GemvArgs& a, int pro, int epi, dim3 grid, uint32_t ld
 template <uint32_t QT>
 int gemv_launch_qt(const GemvArgs& a, int pro, int epi, hipStream_t s) {
   int nt = a.ntok <= 1 ? 1 : a.ntok <= 2 ? 2 : 4;
-  Lds L = lds_layout(nt, pro, QT, a.nb, a.waves, a.heads, a.smax);
+  Lds L = lds_layout(nt, QT, a.nb, a.waves);
   if (L.total > 160 * 1024)
     return set_error(LLMHIP_ERR_ARG, "llm: gemv: k=%u needs %u bytes of LDS", a.k, L.total);
   if (epi == EPI_ARGMAX && a.ntok != 1) return set_error(LLMHIP_ERR_ARG, "llm: gemv: argmax epilogue needs one token");

@@ -8,24 +8,27 @@ namespace llmhip {
 struct AttnArgs {
   const float* q;   // [ntok][heads*hd], RoPE applied
   const float* kv;  // this layer's cache [2][ctx][kvd]
-  float* pv;        // [ntok][heads][smax][hd]
-  float* ml;        // [ntok][heads][smax][2]
+  float* pv;        // split: [ntok][heads][smax][hd] chunk sums of e*v
+  float* ml;        // split: [ntok][heads][smax][2] chunk max and sum of e
+  float* att;       // [ntok][heads*hd] attention output
   const uint32_t* state;
-  uint32_t heads, kv_heads, hd, kvd, ctx, smax, chunk;
-  float scale;  // f32(1/sqrt(hd)), cpu.go:304
-  float* att;     // attn_full_kernel output [ntok][heads*hd]
-  uint32_t rows;  // attn_full_kernel: cache rows read (> every position of the pass)
+  uint32_t heads, kv_heads, hd, kvd, ctx;
+  uint32_t smax;   // chunk slots of pv/ml per (token, head)
+  uint32_t rows;   // cache rows read: > every position of the pass, <= ctx
+  uint32_t split;  // 0: one chunk (rows <= attn_full_max(hd)); 1: chunks of ATTN_SPLIT_ROWS + merge
+  float scale;     // f32(1/sqrt(hd)), cpu.go:304
 };
 
-// Positions the short-context attention kernel covers.
-constexpr uint32_t ATTN_FULL_MAX = 256;
+// Rows per chunk of the split attention kernel.
+constexpr uint32_t ATTN_SPLIT_ROWS = 128;
 
-uint32_t attn_lds_bytes(uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t chunk);
+// Head sizes with an attention kernel.
+bool attn_ok(uint32_t hd);
+// Positions the one-chunk kernel covers.
+uint32_t attn_full_max(uint32_t hd);
+// One launch (one chunk), or two (chunks, merge).  Every position of the pass
+// (state[0] .. state[0] + ntok - 1) must be below a.rows.
 int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s);
-bool attn_full_ok(uint32_t heads, uint32_t kv_heads, uint32_t hd);
-uint32_t attn_full_rows(uint32_t last_pos);
-// Every position of the pass (state[0] .. state[0] + ntok - 1) must be below a.rows.
-int attn_full_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s);
 int argmax_launch(const float* pv, const uint32_t* pi, uint32_t n, const float* logits, int32_t* tokens,
                   int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s);
 int advance_launch(uint32_t* state, uint32_t n, hipStream_t s);

@@ -47,7 +47,7 @@ struct Model {
   int device = 0;
   llmhip_limits lim{};
   llmhip_config cfg{};
-  uint32_t ctx = 0, pm = 64, chunk = 64, smax = 0, kvd = 0;
+  uint32_t ctx = 0, pm = 64, smax = 0, kvd = 0;
   uint64_t used = 0;
   std::vector<void*> allocs;
   hipStream_t stream = nullptr;
@@ -66,13 +66,14 @@ struct Model {
   std::map<std::string, TensorInfo> tensors;
   bool allocated = false, finalized = false;
   hipGraphExec_t decode_exec = nullptr;
-  std::map<uint64_t, hipGraphExec_t> chunk_exec;  // key: graph_key(ntok, attn_rows, head)
+  std::map<uint64_t, hipGraphExec_t> chunk_exec;  // key: graph_key(ntok, attn_rows, attn_split, head)
   std::map<uint64_t, uint32_t> graph_nodes;       // dispatches per graph key
   llmhip_stats stats{};
   int layers_limit = 0;
   std::set<std::string> skip;
   uint32_t pos = 0;  // host mirror of state[0] (== state[1])
-  uint32_t attn_rows = 0;  // pass being recorded: cache rows of attn_full_kernel, 0 = chunked attention
+  uint32_t attn_rows = 0;    // pass being recorded: cache rows its attention reads
+  bool attn_split = false;   // ... and whether it runs in chunks merged by a second kernel
   bool prompted = false;
   uint32_t dispatches = 0;  // counter while recording
   std::vector<ProfRec>* prof = nullptr;  // eager profiling: events around every launch
@@ -349,8 +350,6 @@ static GemvArgs base_args(const Model& m, const QMat& q, uint32_t ntok) {
   a.state = m.state;
   a.heads = m.cfg.heads;
   a.hd = m.cfg.head_dim;
-  a.smax = m.smax;
-  a.chunk = m.chunk;
   return a;
 }
 
@@ -382,6 +381,7 @@ static AttnArgs attn_args(const Model& m, const Layer& L) {
   a.kv = L.kv;
   a.pv = m.pv;
   a.ml = m.ml;
+  a.att = m.att;
   a.state = m.state;
   a.heads = m.cfg.heads;
   a.kv_heads = m.cfg.kv_heads;
@@ -389,9 +389,8 @@ static AttnArgs attn_args(const Model& m, const Layer& L) {
   a.kvd = m.kvd;
   a.ctx = m.ctx;
   a.smax = m.smax;
-  a.chunk = m.chunk;
-  a.att = m.att;
   a.rows = m.attn_rows;
+  a.split = m.attn_split ? 1 : 0;
   a.scale = (float)(1 / std::sqrt((double)m.cfg.head_dim));  // cpu.go:304
   return a;
 }
@@ -400,23 +399,18 @@ static int rec_k2(Model& m, const Layer& L, uint32_t ntok) {
   if (skipped(m, "k2")) return 0;
   // KV bytes read for the last token of the pass (the decode step's one token)
   uint64_t bytes = 2ull * (m.pos + 1) * m.kvd * 4;
-  if (m.attn_rows)
-    return launch_rec(m, "k2", bytes, [&]() { return attn_full_launch(attn_args(m, L), ntok, m.stream); });
+  if (m.attn_split) m.dispatches++;  // the merge kernel
   return launch_rec(m, "k2", bytes, [&]() { return attn_launch(attn_args(m, L), ntok, m.stream); });
 }
 
+// the heads' merged outputs times W_o, added to the residual
 static int rec_k3(Model& m, const Layer& L, uint32_t ntok) {
   GemvArgs a = base_args(m, L.o, ntok);
+  a.x = m.att;
+  a.ldx = m.cfg.embd;
   a.y = m.x;
   a.ldy = m.cfg.embd;
-  if (m.attn_rows) {  // the heads' outputs are already merged
-    a.x = m.att;
-    a.ldx = m.cfg.embd;
-    return mat_rec(m, "k3", "p3", a, L.o.g.q.type, PRO_PLAIN, EPI_ACC, L.o.g.gguf_bytes());
-  }
-  a.pv = m.pv;
-  a.ml = m.ml;
-  return mat_rec(m, "k3", "p3", a, L.o.g.q.type, PRO_MERGE, EPI_ACC, L.o.g.gguf_bytes());
+  return mat_rec(m, "k3", "p3", a, L.o.g.q.type, PRO_PLAIN, EPI_ACC, L.o.g.gguf_bytes());
 }
 
 static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
@@ -522,21 +516,30 @@ static int record_pass(Model& m, uint32_t ntok, bool head) {
   return rec_adv(m, ntok);
 }
 
-// The cache rows attn_full_kernel reads for a pass of ntok tokens from
-// position pos, or 0 when the pass needs the chunked kernel.
-static uint32_t full_attn_rows(const Model& m, uint32_t pos, uint32_t ntok) {
+// The attention of a pass of ntok tokens from position pos: one chunk while
+// every position is below attn_full_max (rows read: the next multiple of 64),
+// else chunks merged by a second kernel (rows read: the next multiple of a
+// granule of >= 512 rows, at most 16 per context).  Each (rows, split) pair is
+// a graph variant.
+static void attn_plan(Model& m, uint32_t pos, uint32_t ntok) {
   const uint32_t last = pos + ntok - 1;
-  if (last >= ATTN_FULL_MAX || !attn_full_ok(m.cfg.heads, m.cfg.kv_heads, m.cfg.head_dim)) return 0;
-  return std::min(attn_full_rows(last), m.ctx);
+  if (last < attn_full_max(m.cfg.head_dim)) {
+    m.attn_rows = std::min((last / 64 + 1) * 64, m.ctx);
+    m.attn_split = false;
+    return;
+  }
+  const uint32_t gran = std::max(512u, (m.ctx / 16 + 127) / 128 * 128);
+  m.attn_rows = std::min((last / gran + 1) * gran, m.ctx);
+  m.attn_split = true;
 }
 
-static uint64_t graph_key(uint32_t ntok, uint32_t attn_rows, bool head) {
-  return ((uint64_t)ntok << 32) | ((uint64_t)attn_rows << 1) | (head ? 1 : 0);
+static uint64_t graph_key(uint32_t ntok, uint32_t rows, bool split, bool head) {
+  return ((uint64_t)ntok << 32) | ((uint64_t)rows << 2) | (split ? 2 : 0) | (head ? 1 : 0);
 }
 
 // Capture record_pass into a graph (once per key).
 static int graph_for(Model& m, uint32_t ntok, bool head, hipGraphExec_t* out) {
-  uint64_t key = graph_key(ntok, m.attn_rows, head);
+  uint64_t key = graph_key(ntok, m.attn_rows, m.attn_split, head);
   auto it = m.chunk_exec.find(key);
   if (it != m.chunk_exec.end()) {
     *out = it->second;
@@ -565,10 +568,10 @@ static int graph_for(Model& m, uint32_t ntok, bool head, hipGraphExec_t* out) {
 // One pass of ntok tokens whose first position is pos (known on the host).
 static int launch_graph(Model& m, uint32_t pos, uint32_t ntok, bool head) {
   hipGraphExec_t ex;
-  m.attn_rows = full_attn_rows(m, pos, ntok);
+  attn_plan(m, pos, ntok);
   LLM_TRY(graph_for(m, ntok, head, &ex));
   LLM_HIP(hipGraphLaunch(ex, m.stream));
-  m.stats.dispatches += m.graph_nodes[graph_key(ntok, m.attn_rows, head)];
+  m.stats.dispatches += m.graph_nodes[graph_key(ntok, m.attn_rows, m.attn_split, head)];
   return 0;
 }
 
@@ -592,8 +595,8 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
     return set_error(LLMHIP_ERR_FORMAT, "llm: implausible hyperparameters");
   if (c.embd % 32 != 0 || c.ff % 32 != 0)
     return set_error(LLMHIP_ERR_FORMAT, "llm: embedding %d and feed-forward %d must be multiples of 32", c.embd, c.ff);
-  if (c.head_dim % 2 != 0 || (c.rope_neox && c.head_dim % 16 != 0))
-    return set_error(LLMHIP_ERR_FORMAT, "llm: head size %d is not supported", c.head_dim);
+  if (!attn_ok((uint32_t)c.head_dim))
+    return set_error(LLMHIP_ERR_FORMAT, "llm: head size %d is not supported (64 or 128)", c.head_dim);
   Model* m = new Model();
   m->device = ordinal;
   m->cfg = c;
@@ -611,7 +614,7 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
   m->ctx = (uint32_t)cx;
   m->pm = prefill_batch > 0 ? (uint32_t)std::min(prefill_batch, 64) : 64;
   m->kvd = (uint32_t)(c.kv_heads * c.head_dim);
-  m->smax = (m->ctx + m->chunk - 1) / m->chunk;
+  m->smax = (m->ctx + ATTN_SPLIT_ROWS - 1) / ATTN_SPLIT_ROWS;
   auto fail = [&](int rc) {
     model_destroy(m);
     return rc;
@@ -863,7 +866,7 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
     return set_error(LLMHIP_ERR_ARG, "llm: no kernel \"%s\" (head, k1..k5)", kernel);
   std::set<std::string> saved = m.skip;
   m.skip.clear();
-  m.attn_rows = full_attn_rows(m, m.pos, 1);  // the variant the next decode step runs
+  attn_plan(m, m.pos, 1);  // the variant the next decode step runs
   const int L = m.cfg.layers;
   auto wb = [](const QMat& q) { return q.g.gguf_bytes(); };
   // launch i runs layer i % L: consecutive launches read different weights,
@@ -920,7 +923,7 @@ int llmhip_model_profile(llmhip_model* h, int tokens, llmhip_kernel_time* out, i
   for (int t = 0; t < tokens && rc == 0; t++) {
     std::vector<ProfRec> recs;
     m.prof = &recs;
-    m.attn_rows = full_attn_rows(m, m.pos, 1);
+    attn_plan(m, m.pos, 1);
     rc = record_pass(m, 1, true);
     m.prof = nullptr;
     if (hipStreamSynchronize(m.stream) != hipSuccess && rc == 0)

@@ -11,11 +11,6 @@ int prep_launch(const GemvArgs& a, int pro, hipStream_t s) {
   switch (pro) {
     case PRO_PLAIN: hipLaunchKernelGGL(prep_kernel<PRO_PLAIN>, grid, dim3(256), lds, s, a); break;
     case PRO_RMS: hipLaunchKernelGGL(prep_kernel<PRO_RMS>, grid, dim3(256), lds, s, a); break;
-    case PRO_MERGE:
-      lds += a.heads * (a.smax + 1) * 4;
-      if (lds > 64 * 1024) return set_error(LLMHIP_ERR_ARG, "llm: prep: %u heads x %u chunks", a.heads, a.smax);
-      hipLaunchKernelGGL(prep_kernel<PRO_MERGE>, grid, dim3(256), lds, s, a);
-      break;
     default: return set_error(LLMHIP_ERR_ARG, "llm: prep: prologue %d", pro);
   }
   LLM_HIP(hipGetLastError());

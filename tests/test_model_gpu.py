@@ -56,16 +56,18 @@ def test_tiny_parity(gpu, name):
     _check(g, cpu, prompt, 40)
 
 
-@pytest.mark.parametrize("prompt_len,heads,kv_heads", [(230, 4, 4), (300, 4, 2), (250, 8, 2), (200, 16, 2)])
-def test_attention_paths(gpu, prompt_len, heads, kv_heads):
-    """Both attention kernels and the switch between them: passes that end
-    below position 256 run the one-workgroup-per-KV-head kernel, later ones the
-    chunked kernel merged in the O-projection; prefill chunks and decode steps
-    on both sides, for 1, 2, 4 and 8 query heads per KV head."""
-    spec = synth.tiny_llama(seed=6 + heads + kv_heads, embd=64 * heads, heads=heads, kv_heads=kv_heads)
+@pytest.mark.parametrize("prompt_len,heads,kv_heads,hd", [
+    (230, 4, 4, 64), (300, 4, 2, 64), (250, 8, 2, 64), (200, 16, 2, 64), (100, 2, 1, 128), (140, 4, 2, 128)])
+def test_attention_paths(gpu, prompt_len, heads, kv_heads, hd):
+    """Both attention forms and the switch between them: passes whose
+    positions are all below 256 (head size 64) or 128 (head size 128) run one
+    chunk per query head, later ones chunks of 128 rows merged by a second
+    kernel; prefill chunks and decode steps on both sides, for 1, 2, 4 and 8
+    query heads per KV head and head sizes 64 and 128."""
+    spec = synth.tiny_llama(seed=6 + heads + kv_heads + hd, embd=hd * heads, heads=heads, kv_heads=kv_heads)
     g, cpu = _open(spec, 512)
     prompt = synth.prompt(7, prompt_len, spec.vocab)
-    _check(g, cpu, prompt, 320 - prompt_len)
+    _check(g, cpu, prompt, (320 if hd == 64 else 200) - prompt_len)
 
 
 def test_decode_batches_and_stops(gpu):
@@ -160,6 +162,10 @@ def test_refusals(gpu):
     lim.memory_budget = g.MemoryUsed()
     g2 = llm.NewGPU(0, lim, path, 64)
     assert g2.MemoryUsed() <= lim.memory_budget
+    # head sizes without an attention kernel are refused at load
+    with pytest.raises(LLMError) as e:
+        llm.NewGPU(0, None, synth.cached(synth.tiny_llama(seed=9, embd=192, heads=2)), 64)
+    assert e.value.kind == "FORMAT" and "head size 96" in str(e.value)
 
 
 @pytest.mark.parametrize("config", ["smollm2", "qwen25"])
