@@ -51,24 +51,16 @@ inline bool qtype_of(uint32_t t, QType* q) {
   return false;
 }
 
-// The tiled layout of a [rows][k] quantised matrix.  Rows are grouped in
-// tiles of 16 (padded with zero rows), a row's nb = k/32 blocks in groups of
-// four.  For tile t and a full group g4 the quants are one 1 KiB (Q4) or
-// 2 KiB (Q8) chunk in lane order: MFMA lane l = 16*w + r (r the row in the
-// tile, w the k-group) finds word w of each of the group's four blocks of row
-// r at 16*l (Q8: two 1 KiB halves, blocks 0-1 and 2-3, 8 bytes per block).
-// A tail group of nb%4 blocks follows with `tail` words (Q8: 8-byte pairs)
-// per lane.  Scales follow the same tiling: [group][row][block] f16 (Q4_1:
-// d,m pairs).  Device bytes equal GGUF bytes for rows % 16 == 0.
+// Geometry of a [rows][k] quantised matrix on the device: rows in tiles of 16
+// (padded with zero rows), a row's nb = k/32 blocks in ng groups of four and
+// a tail of nb % 4; each tile's quants then its scales (the byte layout is
+// Lay in gemv_impl.h).  Device bytes equal GGUF bytes for rows % 16 == 0.
 struct Geom {
   QType q;
   uint64_t rows, k;
   uint32_t nb, ng, tail;  // blocks per row, full groups, blocks in the tail group
   uint64_t tiles;
-  uint64_t qs_tile_bytes() const { return 16ull * nb * q.qs_bytes; }
-  uint64_t sc_tile_bytes() const { return 16ull * nb * q.sc_bytes; }
-  uint64_t qs_bytes() const { return tiles * qs_tile_bytes(); }
-  uint64_t sc_bytes() const { return tiles * sc_tile_bytes(); }
+  uint64_t dev_bytes() const { return tiles * 16ull * nb * (q.qs_bytes + q.sc_bytes); }
   uint64_t gguf_bytes() const { return rows * nb * (uint64_t)q.block_bytes; }
 };
 

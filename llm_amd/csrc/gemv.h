@@ -18,8 +18,7 @@ enum RowMap : uint32_t {
 struct QMat {
   int device = 0;
   Geom g;
-  uint8_t* qs = nullptr;  // device
-  uint8_t* sc = nullptr;  // device
+  uint8_t* qs = nullptr;  // device: the unit records (quants and scales)
   uint64_t bytes = 0;
   // row map (RowMap): NEOX pairs rows inside heads of map_hd rows for rows
   // [map_seg0, map_seg1); GATEUP pairs row i with row ff + i.
@@ -43,13 +42,14 @@ enum Epilogue : int {
 struct GemvArgs {
   // matrix
   const uint8_t* qs;
-  const uint8_t* sc;
   uint32_t rows, nb, ng, tail, tiles, k;
   uint32_t map, map_hd, map_seg0, map_seg1;  // RowMap; NEOX applies to rows [seg0, seg1)
   uint32_t row_base;                         // QKV: first row of this matrix in [q; k; v]
   uint32_t ntok;                             // tokens in the launch
   uint32_t split;                            // waves sharing one tile (split-K): 1..16
   uint32_t waves;                            // waves per workgroup: 4, 8 or 16 (a multiple of split)
+  uint32_t stream, swaves;                   // one token: workgroups and waves per workgroup of the
+                                             // streaming kernel (large matrices), 0: tile kernel
   // prologue
   const float* x;
   uint32_t ldx;
@@ -106,6 +106,10 @@ int gemv_launch(const GemvArgs& a, uint32_t qtype, int pro, int epi, hipStream_t
 uint32_t gemv_groups(const GemvArgs& a);
 // Picks the split-K factor (waves per tile) and the waves per workgroup.
 void gemv_pick(uint32_t tiles, uint32_t ng, uint32_t tail, uint32_t nb, uint32_t* split, uint32_t* waves);
+// Picks the streaming form for a one-token launch: workgroups (0: none) and waves per workgroup.
+void gemv_pick_stream(uint32_t tiles, uint32_t nb, uint32_t* wgs, uint32_t* waves);
+// Tiles from which one-token launches stream.
+constexpr uint32_t GEMV_STREAM_MIN_TILES = 4096;
 
 // Fill a GemvArgs with the matrix fields of m.
 void gemv_bind(GemvArgs* a, const QMat& m);

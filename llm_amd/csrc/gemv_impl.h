@@ -91,26 +91,33 @@ struct QT_ {
   static constexpr uint32_t QO = QT == LLMHIP_Q4_1 ? 4 : 2;                            // quants offset in GGUF block
 };
 
-// Byte offset, inside a tile's quants, of the 4 bytes (Q8: 8) that MFMA lane
-// (16*w + r) holds for block b.
+// Device layout of a quantised matrix, one buffer: tile t (16 rows of nb
+// blocks, ng groups of 4 and a tail of nb % 4) at t * 16 * nb * (QB + SB),
+// its quants then its scales.  Quants: group g is one QG-byte chunk in MFMA
+// lane order (lane l = 16*w + r finds word w of each block of row r at 16*l;
+// Q8: two 1 KiB halves, blocks 0-1 and 2-3, 8 bytes per block), the tail
+// after the groups with `tail` words (Q8 pairs) per lane.  Scales:
+// [group][row][block] f16 (Q4_1: d, m pairs), the tail's [row][block] last.
+// A tile's bytes are contiguous, and so are its scales.  Device bytes equal
+// GGUF bytes for rows % 16 == 0.
 template <uint32_t QT>
-__host__ __device__ inline uint32_t qs_off(uint32_t b, uint32_t lanew, uint32_t ng, uint32_t tail) {
-  uint32_t g4 = b / 4, j = b % 4;
-  if (QT == LLMHIP_Q8_0) {
-    if (g4 < ng) return g4 * 2048 + (j / 2) * 1024 + lanew * 16 + (j % 2) * 8;
-    return ng * 2048 + lanew * tail * 8 + j * 8;
+struct Lay {
+  static constexpr uint32_t QW = QT == LLMHIP_Q8_0 ? 2 : 1;  // quant words per block and lane
+  static constexpr uint32_t QB = QT_<QT>::QB, SB = QT_<QT>::SB;
+  static constexpr uint32_t QG = 1024 * QW;  // quant bytes of a group
+  __host__ __device__ static uint64_t tile(uint64_t t, uint32_t nb) { return t * 16 * nb * (QB + SB); }
+  // the 4 bytes (Q8: 8) lane word lw holds of block b, from the tile's start
+  __host__ __device__ static uint32_t qoff(uint32_t b, uint32_t lw, uint32_t ng, uint32_t tail) {
+    const uint32_t g = b / 4, j = b % 4;
+    if (g < ng) return g * QG + (QT == LLMHIP_Q8_0 ? (j / 2) * 1024 + lw * 16 + (j % 2) * 8 : lw * 16 + j * 4);
+    return ng * QG + (lw * tail + j) * 4 * QW;
   }
-  if (g4 < ng) return g4 * 1024 + lanew * 16 + j * 4;
-  return ng * 1024 + lanew * tail * 4 + j * 4;
-}
-
-template <uint32_t QT>
-__host__ __device__ inline uint32_t sc_off(uint32_t b, uint32_t r, uint32_t ng, uint32_t tail) {
-  constexpr uint32_t SB = QT_<QT>::SB;
-  uint32_t g4 = b / 4, j = b % 4;
-  if (g4 < ng) return g4 * 64 * SB + (r * 4 + j) * SB;
-  return ng * 64 * SB + (r * tail + j) * SB;
-}
+  // the scale of row r, block b, from the tile's start
+  __host__ __device__ static uint32_t soff(uint32_t b, uint32_t r, uint32_t nb, uint32_t ng, uint32_t tail) {
+    const uint32_t g = b / 4, j = b % 4;
+    return 16 * nb * QB + (g < ng ? g * 64 * SB + (r * 4 + j) * SB : ng * 64 * SB + (r * tail + j) * SB);
+  }
+};
 
 // One thread per GGUF block: scales verbatim, quants into MFMA lane order.
 // Q8_0 bytes of k-group w are reordered to the element order the
@@ -118,8 +125,8 @@ __host__ __device__ inline uint32_t sc_off(uint32_t b, uint32_t r, uint32_t ng, 
 // e(16+4w+2); word1 = e(4w+1), e(16+4w+1), e(4w+3), e(16+4w+3).
 template <uint32_t QT>
 __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint64_t n, uint64_t blk0, uint64_t row_off,
-                              uint8_t* __restrict__ qs, uint8_t* __restrict__ sc, uint32_t nb, uint32_t ng,
-                              uint32_t tail, uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1, uint32_t ff) {
+                              uint8_t* __restrict__ wq, uint64_t tiles, uint32_t nb, uint32_t ng, uint32_t tail,
+                              uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1, uint32_t ff) {
   typedef QT_<QT> T;
   uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
@@ -127,22 +134,23 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint64_t n, uint6
   uint32_t lr = (uint32_t)(row_off + gb / nb), b = (uint32_t)(gb % nb);
   uint32_t p = pos_of_row(lr, map, hd, seg0, seg1, ff), t = p / 16, r = p % 16;
   const uint8_t* blk = raw + i * T::BB;
-  uint8_t* sct = sc + (uint64_t)t * 16 * nb * T::SB + sc_off<QT>(b, r, ng, tail);
+  (void)tiles;
+  uint8_t* tb = wq + Lay<QT>::tile(t, nb);
+  uint8_t* sct = tb + Lay<QT>::soff(b, r, nb, ng, tail);
   for (uint32_t k = 0; k < T::SB; k++) sct[k] = blk[k];
-  uint8_t* qt = qs + (uint64_t)t * 16 * nb * T::QB;
   const uint8_t* q = blk + T::QO;
   if (QT == LLMHIP_Q8_0) {
     for (uint32_t w = 0; w < 4; w++) {
       uint32_t w0 = q[4 * w] | q[16 + 4 * w] << 8 | q[4 * w + 2] << 16 | (uint32_t)q[16 + 4 * w + 2] << 24;
       uint32_t w1 = q[4 * w + 1] | q[16 + 4 * w + 1] << 8 | q[4 * w + 3] << 16 | (uint32_t)q[16 + 4 * w + 3] << 24;
-      uint32_t o = qs_off<QT>(b, 16 * w + r, ng, tail);
-      *(uint32_t*)(qt + o) = w0;
-      *(uint32_t*)(qt + o + 4) = w1;
+      uint8_t* o = tb + Lay<QT>::qoff(b, 16 * w + r, ng, tail);
+      *(uint32_t*)o = w0;
+      *(uint32_t*)(o + 4) = w1;
     }
   } else {
     for (uint32_t w = 0; w < 4; w++) {
       uint32_t word = q[4 * w] | q[4 * w + 1] << 8 | q[4 * w + 2] << 16 | (uint32_t)q[4 * w + 3] << 24;
-      *(uint32_t*)(qt + qs_off<QT>(b, 16 * w + r, ng, tail)) = word;
+      *(uint32_t*)(tb + Lay<QT>::qoff(b, 16 * w + r, ng, tail)) = word;
     }
   }
 }
@@ -150,19 +158,19 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint64_t n, uint6
 // The 32 f32 weights of block b of the row at tile position p, exactly as
 // cpu.go forms them: d*f32(q-8) (Q4_0), d*f32(q)+m (Q4_1), d*f32(i8) (Q8_0).
 template <uint32_t QT>
-__device__ inline void dequant_block(const uint8_t* qs, const uint8_t* sc, uint32_t nb, uint32_t ng, uint32_t tail,
+__device__ inline void dequant_block(const uint8_t* wq, uint64_t tiles, uint32_t nb, uint32_t ng, uint32_t tail,
                                      uint32_t p, uint32_t b, float* out) {
-  typedef QT_<QT> T;
-  uint32_t t = p / 16, r = p % 16;
-  const uint8_t* qt = qs + (uint64_t)t * 16 * nb * T::QB;
-  const uint8_t* sct = sc + (uint64_t)t * 16 * nb * T::SB + sc_off<QT>(b, r, ng, tail);
+  (void)tiles;
+  const uint32_t t = p / 16, r = p % 16;
+  const uint8_t* tb = wq + Lay<QT>::tile(t, nb);
+  const uint8_t* sct = tb + Lay<QT>::soff(b, r, nb, ng, tail);
   float d = f16_exact(sct[0] | sct[1] << 8);
   float m = 0;
   if (QT == LLMHIP_Q4_1) m = f16_exact(sct[2] | sct[3] << 8);
   for (uint32_t w = 0; w < 4; w++) {
-    uint32_t o = qs_off<QT>(b, 16 * w + r, ng, tail);
+    const uint8_t* o = tb + Lay<QT>::qoff(b, 16 * w + r, ng, tail);
     if (QT == LLMHIP_Q8_0) {
-      uint32_t w0 = *(const uint32_t*)(qt + o), w1 = *(const uint32_t*)(qt + o + 4);
+      uint32_t w0 = *(const uint32_t*)o, w1 = *(const uint32_t*)(o + 4);
       const uint32_t e0[4] = {4 * w, 16 + 4 * w, 4 * w + 2, 16 + 4 * w + 2};
       const uint32_t e1[4] = {4 * w + 1, 16 + 4 * w + 1, 4 * w + 3, 16 + 4 * w + 3};
       for (int i = 0; i < 4; i++) {
@@ -170,7 +178,7 @@ __device__ inline void dequant_block(const uint8_t* qs, const uint8_t* sc, uint3
         out[e1[i]] = __fmul_rn(d, (float)(int8_t)(w1 >> (8 * i)));
       }
     } else {
-      uint32_t word = *(const uint32_t*)(qt + o);
+      uint32_t word = *(const uint32_t*)o;
       for (int i = 0; i < 4; i++) {
         uint32_t byte = (word >> (8 * i)) & 255u;
         int lo = byte & 15, hi = byte >> 4;
@@ -188,28 +196,28 @@ __device__ inline void dequant_block(const uint8_t* qs, const uint8_t* sc, uint3
 
 // out[lr][k] for every logical row; one thread per (row, block).
 template <uint32_t QT>
-__global__ void dequant_kernel(const uint8_t* __restrict__ qs, const uint8_t* __restrict__ sc, uint32_t rows,
-                               uint32_t nb, uint32_t ng, uint32_t tail, uint32_t map, uint32_t hd, uint32_t seg0,
-                               uint32_t seg1, uint32_t ff, float* __restrict__ out) {
+__global__ void dequant_kernel(const uint8_t* __restrict__ wq, uint64_t tiles, uint32_t rows, uint32_t nb,
+                               uint32_t ng, uint32_t tail, uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1,
+                               uint32_t ff, float* __restrict__ out) {
   uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (uint64_t)rows * nb) return;
   uint32_t lr = (uint32_t)(i / nb), b = (uint32_t)(i % nb);
   float v[32];
-  dequant_block<QT>(qs, sc, nb, ng, tail, pos_of_row(lr, map, hd, seg0, seg1, ff), b, v);
+  dequant_block<QT>(wq, tiles, nb, ng, tail, pos_of_row(lr, map, hd, seg0, seg1, ff), b, v);
   float* o = out + (uint64_t)lr * nb * 32 + b * 32;
   for (int j = 0; j < 32; j++) o[j] = v[j];
 }
 
 // Embedding gather (kernels.go:19-73): x[t][:] = row tokens[state[1]+t].
 template <uint32_t QT>
-__global__ void embed_kernel(const uint8_t* __restrict__ qs, const uint8_t* __restrict__ sc, uint32_t nb, uint32_t ng,
-                             uint32_t tail, const int32_t* __restrict__ tokens, const uint32_t* __restrict__ state,
+__global__ void embed_kernel(const uint8_t* __restrict__ wq, uint64_t tiles, uint32_t nb, uint32_t ng, uint32_t tail,
+                             const int32_t* __restrict__ tokens, const uint32_t* __restrict__ state,
                              float* __restrict__ x) {
   uint32_t t = blockIdx.y;
   uint32_t row = (uint32_t)tokens[state[1] + t];
   for (uint32_t b = threadIdx.x; b < nb; b += blockDim.x) {
     float v[32];
-    dequant_block<QT>(qs, sc, nb, ng, tail, row, b, v);
+    dequant_block<QT>(wq, tiles, nb, ng, tail, row, b, v);
     float* o = x + (uint64_t)t * nb * 32 + b * 32;
     for (int j = 0; j < 32; j++) o[j] = v[j];
   }
@@ -375,96 +383,38 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
   }
 }
 
-template <uint32_t QT, int NT, int PRO, int EPI>
-__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
-  typedef QT_<QT> T;
-  constexpr int S = 2 * NT;  // MFMA rows used: hi and lo of each token
-  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+// Activations of nt tokens staged once per workgroup (the prologue of both
+// matrix-vector kernels): one round of global loads of items (block b,
+// k-group g) of 8 elements (4g..4g+3 and 16+4g..16+4g+3), RMSNorm for PRO_RMS
+// (cpu.go:90-96), then per token a power-of-two scale 2^ex[t] (largest
+// magnitude in [2^14, 2^15)) and the split into f16 hi + lo, stored in MFMA
+// operand order.  Per-wave partials go through LDS; every thread then
+// finishes each reduction itself (the same sums in the same order).  Ends
+// with a barrier after which xs (and bsum, Q4_1) are complete.
+template <uint32_t QT, int NT, int PRO>
+__device__ __forceinline__ void stage_x(const GemvArgs& a, uint32_t t0, int nt, h8* xs, float* misc, float* bsum,
+                                        int ex[NT]) {
+  constexpr int S = 2 * NT;
   const uint32_t bd = blockDim.x, nwv = bd >> 6;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t t0 = blockIdx.y * NT;
-  const int nt = min((int)NT, (int)(a.ntok - t0));
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const uint32_t nb = a.nb, K = a.k, NI = nb * 4;
-  const Lds L = lds_layout(NT, QT, nb, nwv);
-  h8* xs = (h8*)(lds + L.xs);
-  float* misc = (float*)(lds + L.misc);  // [0,64) sum-of-squares partials, [64,128) max partials, then argmax
-  float* bsum = (float*)(lds + L.bsum);
-
-  // ---- the weights first: this wave's tile, the first batch of up to four of
-  // its block groups (and the tail blocks) are in flight while the prologue
-  // loads and reduces the activations (up to two tokens: with four, the
-  // registers held across the prologue would spill)
-  constexpr bool HOIST = NT <= 2;
-  const uint32_t split = a.split, tpw = nwv / split;
-  const uint32_t lt = wave / split, sp = wave % split;
-  const uint32_t tile = blockIdx.x * tpw + lt;
-  const bool has_tile = tile < a.tiles;
-  const int r = lane & 15, q = lane >> 4;  // B/D column (row in tile), k-group / D row group
-  const int slot = lane & 15;              // A row: token slot
-  const uint8_t* qt = a.qs + (uint64_t)tile * 16 * nb * T::QB;
-  const uint8_t* st = a.sc + (uint64_t)tile * 16 * nb * T::SB;
-  const uint32_t cnt = has_tile && a.ng > sp ? (a.ng - sp + split - 1) / split : 0;
-  uint4 w0[4], w1[4], sv[4];
-  auto load_batch = [&](uint32_t i0) {
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      if (i0 + u >= cnt) continue;
-      const uint32_t g4 = sp + (i0 + u) * split;
-      if (QT == LLMHIP_Q8_0) {
-        w0[u] = ld_stream16(qt + g4 * 2048 + lane * 16);
-        w1[u] = ld_stream16(qt + g4 * 2048 + 1024 + lane * 16);
-      } else {
-        w0[u] = ld_stream16(qt + g4 * 1024 + lane * 16);
-      }
-      if (QT == LLMHIP_Q4_1) {
-        sv[u] = *(const uint4*)(st + g4 * 256 + r * 16);
-      } else {
-        uint2 x2 = *(const uint2*)(st + g4 * 128 + r * 8);
-        sv[u] = uint4{x2.x, x2.y, 0, 0};
-      }
-    }
-  };
-  if (HOIST) load_batch(0);
-  const bool has_tail = has_tile && a.tail && (a.ng % split) == sp;
-  uint32_t qw[3][2], sb[3];
-  auto load_tail = [&]() {
-#pragma unroll
-    for (uint32_t j = 0; j < 3; j++) {
-      if (j >= a.tail) continue;
-      const uint32_t b = 4 * a.ng + j;
-      const uint8_t* qq = qt + qs_off<QT>(b, lane, a.ng, a.tail);
-      qw[j][0] = *(const uint32_t*)qq;
-      if (QT == LLMHIP_Q8_0) qw[j][1] = *(const uint32_t*)(qq + 4);
-      const uint8_t* sp8 = st + sc_off<QT>(b, r, a.ng, a.tail);
-      sb[j] = QT == LLMHIP_Q4_1 ? *(const uint32_t*)sp8 : (uint32_t)*(const uint16_t*)sp8;
-    }
-  };
-  if (HOIST && has_tail) load_tail();
-
-  // ---- prologue: one round of global loads, the activations of nt tokens
-  // staged in registers as items (block b, k-group g) of 8 elements
-  // (4g..4g+3 and 16+4g..16+4g+3), then scaled, split and stored in MFMA
-  // operand order.  Per-wave partials go through LDS; every thread then
-  // finishes the reduction itself (the same sums in the same order).
   f4 va[NT][MAXI], vc[NT][MAXI];
-  {
 #pragma unroll
-    for (int t = 0; t < NT; t++)
+  for (int t = 0; t < NT; t++)
 #pragma unroll
-      for (int k = 0; k < MAXI; k++) {
-        uint32_t it = tid + k * bd;
-        f4 A = {0, 0, 0, 0}, C = {0, 0, 0, 0};
-        if (t < nt && it < NI) {
-          const float* xr = a.x + (uint64_t)(a.xrow0 + t0 + t) * a.ldx + (it / 4) * 32 + 4 * (it % 4);
-          A = *(const f4*)xr;
-          C = *(const f4*)(xr + 16);
-        }
-        va[t][k] = A;
-        vc[t][k] = C;
+    for (int k = 0; k < MAXI; k++) {
+      uint32_t it = tid + k * bd;
+      f4 A = {0, 0, 0, 0}, C = {0, 0, 0, 0};
+      if (t < nt && it < NI) {
+        const float* xr = a.x + (uint64_t)(a.xrow0 + t0 + t) * a.ldx + (it / 4) * 32 + 4 * (it % 4);
+        A = *(const f4*)xr;
+        C = *(const f4*)(xr + 16);
       }
-  }
+      va[t][k] = A;
+      vc[t][k] = C;
+    }
   if (PRO == PRO_RMS) {
-    // cpu.go:90-96: ss = sum x^2 (f32); s = f32(1/sqrt(f64(ss/n + eps))); h = x*s*w
+    // ss = sum x^2 (f32); s = f32(1/sqrt(f64(ss/n + eps))); h = x*s*w
     f4 wa[MAXI], wc[MAXI];
 #pragma unroll
     for (int k = 0; k < MAXI; k++) {
@@ -499,7 +449,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
         }
     }
   }
-  // largest magnitude per token -> power-of-two scale 2^ex[t]
   float* mpart = misc + 64;
 #pragma unroll
   for (int t = 0; t < NT; t++) {
@@ -511,7 +460,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     if (lane == 0) mpart[wave * NT + t] = m;
   }
   __syncthreads();
-  int ex[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     float m = 0;
@@ -551,58 +499,199 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     }
   }
   __syncthreads();
+}
 
-  // ---- main loop: each wave one 16-row tile over its share of the block
-  // groups; the weights of up to four groups are in flight at once
+// One unit of a tile's weights in registers: a group of four blocks (Q4: w0
+// holds the lane's word of each block; Q8: w0, w1 two words of blocks 0,1 and
+// 2,3; sv the scales of row r) or the tail of nb % 4 blocks (component j of
+// w0 / w1 / sv for tail block j).
+struct WUnit {
+  uint4 w0, w1, sv;
+};
+
+// Load group g (< ng) of tile t of the matrix at wq.
+template <uint32_t QT>
+__device__ __forceinline__ void load_group(WUnit& u, const uint8_t* wq, uint32_t nb, uint32_t t, uint32_t g,
+                                           int lane, int r) {
+  typedef Lay<QT> LY;
+  const uint8_t* tb = wq + LY::tile(t, nb);
+  u.w0 = ld_stream16(tb + g * LY::QG + lane * 16);
+  if (QT == LLMHIP_Q8_0) u.w1 = ld_stream16(tb + g * LY::QG + 1024 + lane * 16);
+  const uint8_t* sp = tb + 16 * nb * LY::QB + g * 64 * LY::SB + r * 4 * LY::SB;
+  if (QT == LLMHIP_Q4_1) {
+    u.sv = *(const uint4*)sp;
+  } else {
+    uint2 x2 = *(const uint2*)sp;
+    u.sv = uint4{x2.x, x2.y, 0, 0};
+  }
+}
+
+// Load unit g (< ng: a group, == ng: the tail) of tile t of the matrix at wq.
+template <uint32_t QT>
+__device__ __forceinline__ void load_unit(WUnit& u, const uint8_t* wq, uint32_t nb, uint32_t t, uint32_t g,
+                                          uint32_t ng, uint32_t tail, int lane, int r) {
+  typedef Lay<QT> LY;
+  if (g < ng) {
+    load_group<QT>(u, wq, nb, t, g, lane, r);
+    return;
+  }
+  const uint8_t* tb = wq + LY::tile(t, nb);
+  uint32_t q0[3] = {0, 0, 0}, q1[3] = {0, 0, 0}, s[3] = {0, 0, 0};
+#pragma unroll
+  for (uint32_t j = 0; j < 3; j++) {
+    if (j >= tail) continue;
+    const uint32_t b = 4 * ng + j;
+    const uint8_t* qq = tb + LY::qoff(b, lane, ng, tail);
+    q0[j] = *(const uint32_t*)qq;
+    if (QT == LLMHIP_Q8_0) q1[j] = *(const uint32_t*)(qq + 4);
+    const uint8_t* sp = tb + LY::soff(b, r, nb, ng, tail);
+    s[j] = QT == LLMHIP_Q4_1 ? *(const uint32_t*)sp : (uint32_t)*(const uint16_t*)sp;
+  }
+  u.w0 = uint4{q0[0], q0[1], q0[2], 0};
+  u.w1 = uint4{q1[0], q1[1], q1[2], 0};
+  u.sv = uint4{s[0], s[1], s[2], 0};
+}
+
+// One block through the MFMA: D[token slot][row] = x_slot . w_row over its 32
+// elements, then acc += d * (hi + lo) (and m * sum x for Q4_1).
+template <uint32_t QT, int NT>
+__device__ __forceinline__ void mfma_block(const h8* xs, const float* bsum, uint32_t nb, int q, int slot, uint32_t b,
+                                           h8 B, uint32_t dbits, uint32_t mbits, float& acc0, float& acc1) {
+  constexpr int S = 2 * NT;
+  h8 A = {};
+  if (slot < S) A = xs[(b * 4 + q) * S + slot];
+  f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4{0, 0, 0, 0}, 0, 0, 0);
+  float d = f16_hw(dbits);
+  acc0 += d * (D[0] + D[1]);
+  if (NT > 1) acc1 += d * (D[2] + D[3]);
+  if (QT == LLMHIP_Q4_1) {
+    float m = f16_hw(mbits);
+    if (2 * q < NT) acc0 += m * bsum[(2 * q) * nb + b];
+    if (2 * q + 1 < NT) acc1 += m * bsum[(2 * q + 1) * nb + b];
+  }
+}
+
+// The blocks of unit g of a tile (see WUnit).
+template <uint32_t QT, int NT>
+__device__ __forceinline__ void unit_mfma(const WUnit& u, uint32_t g, uint32_t ng, uint32_t tail, const h8* xs,
+                                          const float* bsum, uint32_t nb, int q, int slot, float& acc0, float& acc1) {
+  if (g < ng) {
+    const uint32_t b0 = 4 * g;
+    if (QT == LLMHIP_Q8_0) {
+      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 0, dq8(u.w0.x, u.w0.y), u.sv.x & 0xffff, 0, acc0, acc1);
+      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 1, dq8(u.w0.z, u.w0.w), u.sv.x >> 16, 0, acc0, acc1);
+      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 2, dq8(u.w1.x, u.w1.y), u.sv.y & 0xffff, 0, acc0, acc1);
+      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 3, dq8(u.w1.z, u.w1.w), u.sv.y >> 16, 0, acc0, acc1);
+    } else if (QT == LLMHIP_Q4_1) {
+      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 0, dq4<true>(u.w0.x), u.sv.x & 0xffff, u.sv.x >> 16, acc0, acc1);
+      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 1, dq4<true>(u.w0.y), u.sv.y & 0xffff, u.sv.y >> 16, acc0, acc1);
+      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 2, dq4<true>(u.w0.z), u.sv.z & 0xffff, u.sv.z >> 16, acc0, acc1);
+      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 3, dq4<true>(u.w0.w), u.sv.w & 0xffff, u.sv.w >> 16, acc0, acc1);
+    } else {
+      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 0, dq4<false>(u.w0.x), u.sv.x & 0xffff, 0, acc0, acc1);
+      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 1, dq4<false>(u.w0.y), u.sv.x >> 16, 0, acc0, acc1);
+      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 2, dq4<false>(u.w0.z), u.sv.y & 0xffff, 0, acc0, acc1);
+      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 3, dq4<false>(u.w0.w), u.sv.y >> 16, 0, acc0, acc1);
+    }
+    return;
+  }
+  const uint32_t q0[3] = {u.w0.x, u.w0.y, u.w0.z}, q1[3] = {u.w1.x, u.w1.y, u.w1.z}, s[3] = {u.sv.x, u.sv.y, u.sv.z};
+#pragma unroll
+  for (uint32_t j = 0; j < 3; j++) {
+    if (j >= tail) continue;
+    const uint32_t b = 4 * ng + j;
+    if (QT == LLMHIP_Q8_0) mfma_block<QT, NT>(xs, bsum, nb, q, slot, b, dq8(q0[j], q1[j]), s[j] & 0xffff, 0, acc0, acc1);
+    else mfma_block<QT, NT>(xs, bsum, nb, q, slot, b, dq4<QT == LLMHIP_Q4_1>(q0[j]), s[j] & 0xffff, s[j] >> 16, acc0,
+                            acc1);
+  }
+}
+
+// Greedy-sampling partials: (max, lowest index) over the rows a workgroup saw
+// (NaN never wins, cpu.go:389-397), written to amax_v/amax_i[blockIdx.x];
+// argmax_kernel combines the workgroups'.  Called by every thread.
+__device__ __forceinline__ void argmax_partial(const GemvArgs& a, float* misc, float bv, uint32_t bi) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const uint32_t nwv = blockDim.x >> 6;
+  float* av = misc + 80;
+  uint32_t* ai = (uint32_t*)(misc + 96);
+  for (int o = 32; o > 0; o >>= 1) {
+    float ov = __shfl_xor(bv, o);
+    uint32_t oi = __shfl_xor(bi, o);
+    if (amax_better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    av[wave] = bv;
+    ai[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (uint32_t w = 1; w < nwv; w++)
+      if (amax_better(av[w], ai[w], bv, bi)) {
+        bv = av[w];
+        bi = ai[w];
+      }
+    a.amax_v[blockIdx.x] = bv;
+    a.amax_i[blockIdx.x] = bi;
+  }
+}
+
+// The decode matrix-vector product (and up to 4 tokens): waves of a
+// workgroup own 16-row tiles, `split` waves share a tile's block groups
+// (split-K, added in a fixed order through LDS).  The first batch of up to
+// four of a wave's units is loaded before the activation prologue, so the
+// weight and activation round trips overlap (up to two tokens: with four, the
+// registers held across the prologue would spill).
+template <uint32_t QT, int NT, int PRO, int EPI>
+__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
+  typedef QT_<QT> T;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const uint32_t bd = blockDim.x, nwv = bd >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const uint32_t t0 = blockIdx.y * NT;
+  const int nt = min((int)NT, (int)(a.ntok - t0));
+  const uint32_t nb = a.nb;
+  const Lds L = lds_layout(NT, QT, nb, nwv);
+  h8* xs = (h8*)(lds + L.xs);
+  float* misc = (float*)(lds + L.misc);  // [0,64) sum-of-squares partials, [64,128) max partials, then argmax
+  float* bsum = (float*)(lds + L.bsum);
+
+  constexpr bool HOIST = NT <= 2;
+  const uint32_t split = a.split, tpw = nwv / split;
+  const uint32_t lt = wave / split, sp = wave % split;
+  const uint32_t tile = blockIdx.x * tpw + lt;
+  const bool has_tile = tile < a.tiles;
+  const int r = lane & 15, q = lane >> 4;  // B/D column (row in tile), k-group / D row group
+  const int slot = lane & 15;              // A row: token slot
+  // this wave's groups: sp, sp + split, ... below ng; the tail goes to wave ng % split
+  const uint32_t cnt = has_tile && a.ng > sp ? (a.ng - sp + split - 1) / split : 0;
+  const bool has_tail = has_tile && a.tail && (a.ng % split) == sp;
+  WUnit w[4], wt;
+  auto load_batch = [&](uint32_t i0) {
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      if (i0 + u < cnt) load_group<QT>(w[u], a.qs, nb, tile, sp + (i0 + u) * split, lane, r);
+  };
+  if (HOIST) {
+    load_batch(0);
+    if (has_tail) load_unit<QT>(wt, a.qs, nb, tile, a.ng, a.ng, a.tail, lane, r);
+  }
+
+  int ex[NT];
+  stage_x<QT, NT, PRO>(a, t0, nt, xs, misc, bsum, ex);
+
   float acc0 = 0, acc1 = 0;
-  if (has_tile) {
-    auto block = [&](uint32_t b, h8 B, uint32_t dbits, uint32_t mbits) {
-      h8 A = {};
-      if (slot < S) A = xs[(b * 4 + q) * S + slot];
-      f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4{0, 0, 0, 0}, 0, 0, 0);
-      float d = f16_hw(dbits);
-      acc0 += d * (D[0] + D[1]);
-      if (NT > 1) acc1 += d * (D[2] + D[3]);
-      if (QT == LLMHIP_Q4_1) {
-        float m = f16_hw(mbits);
-        if (2 * q < NT) acc0 += m * bsum[(2 * q) * nb + b];
-        if (2 * q + 1 < NT) acc1 += m * bsum[(2 * q + 1) * nb + b];
-      }
-    };
-    for (uint32_t i0 = 0; i0 < cnt; i0 += 4) {
-      if (i0 > 0 || !HOIST) load_batch(i0);
+  for (uint32_t i0 = 0; i0 < cnt; i0 += 4) {
+    if (i0 > 0 || !HOIST) load_batch(i0);
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        if (i0 + u >= cnt) continue;
-        const uint32_t b0 = 4 * (sp + (i0 + u) * split);
-        if (QT == LLMHIP_Q8_0) {
-          block(b0 + 0, dq8(w0[u].x, w0[u].y), sv[u].x & 0xffff, 0);
-          block(b0 + 1, dq8(w0[u].z, w0[u].w), sv[u].x >> 16, 0);
-          block(b0 + 2, dq8(w1[u].x, w1[u].y), sv[u].y & 0xffff, 0);
-          block(b0 + 3, dq8(w1[u].z, w1[u].w), sv[u].y >> 16, 0);
-        } else if (QT == LLMHIP_Q4_1) {
-          block(b0 + 0, dq4<true>(w0[u].x), sv[u].x & 0xffff, sv[u].x >> 16);
-          block(b0 + 1, dq4<true>(w0[u].y), sv[u].y & 0xffff, sv[u].y >> 16);
-          block(b0 + 2, dq4<true>(w0[u].z), sv[u].z & 0xffff, sv[u].z >> 16);
-          block(b0 + 3, dq4<true>(w0[u].w), sv[u].w & 0xffff, sv[u].w >> 16);
-        } else {
-          block(b0 + 0, dq4<false>(w0[u].x), sv[u].x & 0xffff, 0);
-          block(b0 + 1, dq4<false>(w0[u].y), sv[u].x >> 16, 0);
-          block(b0 + 2, dq4<false>(w0[u].z), sv[u].y & 0xffff, 0);
-          block(b0 + 3, dq4<false>(w0[u].w), sv[u].y >> 16, 0);
-        }
-      }
-    }
-    if (has_tail) {
-      if (!HOIST) load_tail();
-#pragma unroll
-      for (uint32_t j = 0; j < 3; j++) {
-        if (j >= a.tail) continue;
-        const uint32_t b = 4 * a.ng + j;
-        if (QT == LLMHIP_Q8_0) block(b, dq8(qw[j][0], qw[j][1]), sb[j] & 0xffff, 0);
-        else block(b, dq4<QT == LLMHIP_Q4_1>(qw[j][0]), sb[j] & 0xffff, sb[j] >> 16);
-      }
-    }
+    for (int u = 0; u < 4; u++)
+      if (i0 + u < cnt) unit_mfma<QT, NT>(w[u], sp + (i0 + u) * split, a.ng, a.tail, xs, bsum, nb, q, slot, acc0, acc1);
+  }
+  if (has_tail) {
+    if (!HOIST) load_unit<QT>(wt, a.qs, nb, tile, a.ng, a.ng, a.tail, lane, r);
+    unit_mfma<QT, NT>(wt, a.ng, a.ng, a.tail, xs, bsum, nb, q, slot, acc0, acc1);
   }
   // ---- split-K: partial sums of the waves of a tile, added in a fixed order
   if (split > 1) {
@@ -618,7 +707,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     }
   }
   // ---- epilogue: lane holds rows r of the tile for tokens 2q and 2q+1
-  const bool active = sp == 0 && tile < a.tiles;
+  const bool active = sp == 0 && has_tile;
   const int tA = 2 * q, tB = 2 * q + 1;
   const bool okA = tA < nt, okB = NT > 1 && tB < nt;
   int eA = 0, eB = 0;
@@ -631,40 +720,74 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   const float vB = okB ? ldexpf(acc1, -eB) : 0.f;
   row_epilogue<EPI>(a, tile, r, active, t0 + tA, okA, vA, t0 + tB, okB, vB);
   if (EPI == EPI_ARGMAX) {
-    // (max, lowest index) of token 0 over this workgroup's rows, NaN never
-    // wins (cpu.go:389-397); argmax_kernel combines the workgroups' partials.
     const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
-    float* av = misc + 80;
-    uint32_t* ai = (uint32_t*)(misc + 96);
-    float bv = -INFINITY;
-    uint32_t bi = 0xffffffffu;
-    if (active && lr < a.rows && q == 0 && okA && vA == vA) {
-      bv = vA;
-      bi = lr;
-    }
-    for (int o = 8; o > 0; o >>= 1) {
-      float ov = __shfl_xor(bv, o);
-      uint32_t oi = __shfl_xor(bi, o);
-      if (amax_better(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
+    const bool ok = active && lr < a.rows && q == 0 && okA && vA == vA;
+    argmax_partial(a, misc, ok ? vA : -INFINITY, ok ? lr : 0xffffffffu);
+  }
+}
+
+// Large matrices at one token (the vocabulary head; the 151936-row sweep
+// shape): a grid of a few workgroups per CU, the activations staged once per
+// workgroup, and each of the W waves of the grid streaming its tiles w,
+// w + W, w + 2W, ... as a sequence of units (ng groups, then the tail) with
+// the next R units always in flight: unit i+R is loaded as soon as unit i has
+// gone through the MFMA.  A tile's row epilogue runs after its last unit.
+constexpr int STREAM_RING = 4;
+template <uint32_t QT, int PRO, int EPI>
+__global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
+  constexpr int R = STREAM_RING;
+  typedef QT_<QT> T;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const uint32_t nwv = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const uint32_t nb = a.nb, ng = a.ng, tail = a.tail;
+  const Lds L = lds_layout(1, QT, nb, nwv);
+  h8* xs = (h8*)(lds + L.xs);
+  float* misc = (float*)(lds + L.misc);
+  float* bsum = (float*)(lds + L.bsum);
+  const int r = lane & 15, q = lane >> 4, slot = lane & 15;
+  const uint32_t W = gridDim.x * nwv, gw = blockIdx.x * nwv + wave;
+  const uint32_t upt = ng + (tail ? 1 : 0);
+  const uint32_t ntw = gw < a.tiles ? (a.tiles - 1 - gw) / W + 1 : 0;
+  const uint32_t U = ntw * upt;
+  WUnit w[R];
+  auto fetch = [&](uint32_t i, WUnit& u) {
+    const uint32_t tile = gw + (i / upt) * W;
+    load_unit<QT>(u, a.qs, nb, tile, i % upt, ng, tail, lane, r);
+  };
+#pragma unroll
+  for (int d = 0; d < R; d++)
+    if ((uint32_t)d < U) fetch(d, w[d]);
+
+  int ex[1];
+  stage_x<QT, 1, PRO>(a, 0, 1, xs, misc, bsum, ex);
+
+  float acc0 = 0, acc1 = 0, bv = -INFINITY;
+  uint32_t bi = 0xffffffffu;
+  for (uint32_t i0 = 0; i0 < U; i0 += R) {
+#pragma unroll
+    for (int d = 0; d < R; d++) {
+      const uint32_t i = i0 + d;
+      if (i >= U) break;
+      const uint32_t g = i % upt;
+      unit_mfma<QT, 1>(w[d], g, ng, tail, xs, bsum, nb, q, slot, acc0, acc1);
+      if (i + R < U) fetch(i + R, w[d]);
+      if (g == upt - 1) {  // the tile is complete
+        const uint32_t tile = gw + (i / upt) * W;
+        const float v = q == 0 ? ldexpf(acc0, -ex[0]) : 0.f;
+        row_epilogue<EPI>(a, tile, r, true, 0, q == 0, v, 1, false, 0.f);
+        if (EPI == EPI_ARGMAX) {
+          const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
+          if (q == 0 && lr < a.rows && v == v && amax_better(v, lr, bv, bi)) {
+            bv = v;
+            bi = lr;
+          }
+        }
+        acc0 = acc1 = 0;
       }
     }
-    if (lane == 0) {
-      av[wave] = bv;
-      ai[wave] = bi;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      for (uint32_t w = 1; w < nwv; w++)
-        if (amax_better(av[w], ai[w], bv, bi)) {
-          bv = av[w];
-          bi = ai[w];
-        }
-      a.amax_v[blockIdx.x] = bv;
-      a.amax_i[blockIdx.x] = bi;
-    }
   }
+  if (EPI == EPI_ARGMAX) argmax_partial(a, misc, bv, bi);
 }
 
 
@@ -679,7 +802,7 @@ constexpr int PMAXI = 4;  // items per thread in prep_kernel: k <= 32 * 4 * 256
 template <int PRO>
 __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) float pl[];
-  const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const uint32_t nb = a.nb, K = a.k, NI = nb * 4;
   h8* xp = (h8*)a.xp;
   const uint32_t tg = t / 8, s2 = 2 * (t % 8);
@@ -787,7 +910,7 @@ template <uint32_t QT, int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(GemvArgs a) {
   typedef QT_<QT> T;
   __shared__ float red[3][64][GT * 8 * 2];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int r = lane & 15, q = lane >> 4;
   const uint32_t nb = a.nb, TG = a.tg;
   const uint32_t tgpw = (TG + gridDim.y - 1) / gridDim.y, g0 = blockIdx.y * tgpw;
@@ -800,14 +923,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvArgs a) {
 #pragma unroll
     for (int g = 0; g < 8; g++) acc[u][g][0] = acc[u][g][1] = 0.f;
   bool tv[GT];
-  const uint8_t* qt[GT];
-  const uint8_t* st[GT];
+  uint32_t tt[GT];
 #pragma unroll
   for (int u = 0; u < GT; u++) {
     tv[u] = tile0 + u < a.tiles;
-    uint32_t tt = tv[u] ? tile0 + u : tile0;
-    qt[u] = a.qs + (uint64_t)tt * 16 * nb * T::QB;
-    st[u] = a.sc + (uint64_t)tt * 16 * nb * T::SB;
+    tt[u] = tv[u] ? tile0 + u : tile0;
   }
   // one block b for both tiles: B[u] weights, d[u] / m[u] scales
   auto block = [&](uint32_t b, const h8* B, const float* d, const float* mm) {
@@ -831,18 +951,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvArgs a) {
     uint4 w0[GT], w1[GT], sv[GT];
 #pragma unroll
     for (int u = 0; u < GT; u++) {
-      if (QT == LLMHIP_Q8_0) {
-        w0[u] = ld_stream16(qt[u] + g4 * 2048 + lane * 16);
-        w1[u] = ld_stream16(qt[u] + g4 * 2048 + 1024 + lane * 16);
-      } else {
-        w0[u] = ld_stream16(qt[u] + g4 * 1024 + lane * 16);
-      }
-      if (QT == LLMHIP_Q4_1) {
-        sv[u] = *(const uint4*)(st[u] + g4 * 256 + r * 16);
-      } else {
-        uint2 x2 = *(const uint2*)(st[u] + g4 * 128 + r * 8);
-        sv[u] = uint4{x2.x, x2.y, 0, 0};
-      }
+      WUnit wu;
+      load_unit<QT>(wu, a.qs, nb, tt[u], g4, a.ng, a.tail, lane, r);
+      w0[u] = wu.w0;
+      w1[u] = wu.w1;
+      sv[u] = wu.sv;
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -879,8 +992,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvArgs a) {
       float d[GT], mm[GT];
 #pragma unroll
       for (int u = 0; u < GT; u++) {
-        const uint8_t* qq = qt[u] + qs_off<QT>(b, lane, a.ng, a.tail);
-        const uint8_t* s = st[u] + sc_off<QT>(b, r, a.ng, a.tail);
+        const uint8_t* tb = a.qs + Lay<QT>::tile(tt[u], nb);
+        const uint8_t* qq = tb + Lay<QT>::qoff(b, lane, a.ng, a.tail);
+        const uint8_t* s = tb + Lay<QT>::soff(b, r, nb, a.ng, a.tail);
         if (QT == LLMHIP_Q8_0) B[u] = dq8(*(const uint32_t*)qq, *(const uint32_t*)(qq + 4));
         else B[u] = dq4<QT == LLMHIP_Q4_1>(*(const uint32_t*)qq);
         d[u] = f16_hw(s[0] | s[1] << 8);
@@ -952,8 +1066,25 @@ static int launch_nt(const GemvArgs& a, int pro, int epi, dim3 grid, uint32_t ld
   return set_error(LLMHIP_ERR_ARG, "llm: gemv: unsupported prologue/epilogue %d/%d", pro, epi);
 }
 
+template <uint32_t QT, int PRO, int EPI>
+static int launch_stream(const GemvArgs& a, hipStream_t s) {
+  const Lds L = lds_layout(1, QT, a.nb, a.swaves);
+  hipLaunchKernelGGL((gemv_stream_kernel<QT, PRO, EPI>), dim3(a.stream), dim3(64 * a.swaves), L.total, s, a);
+  LLM_HIP(hipGetLastError());
+  return 0;
+}
+
 template <uint32_t QT>
 int gemv_launch_qt(const GemvArgs& a, int pro, int epi, hipStream_t s) {
+  if (a.stream && a.ntok == 1) {
+    switch (pro * 8 + epi) {
+      case PRO_PLAIN * 8 + EPI_STORE: return launch_stream<QT, PRO_PLAIN, EPI_STORE>(a, s);
+      case PRO_PLAIN * 8 + EPI_ACC: return launch_stream<QT, PRO_PLAIN, EPI_ACC>(a, s);
+      case PRO_RMS * 8 + EPI_STORE: return launch_stream<QT, PRO_RMS, EPI_STORE>(a, s);
+      case PRO_RMS * 8 + EPI_ARGMAX: return launch_stream<QT, PRO_RMS, EPI_ARGMAX>(a, s);
+    }
+    return set_error(LLMHIP_ERR_ARG, "llm: gemv: no streaming form of prologue/epilogue %d/%d", pro, epi);
+  }
   int nt = a.ntok <= 1 ? 1 : a.ntok <= 2 ? 2 : 4;
   Lds L = lds_layout(nt, QT, a.nb, a.waves);
   if (L.total > 160 * 1024)
@@ -972,7 +1103,7 @@ int repack_launch_qt(const QMat& m, const uint8_t* raw_dev, uint64_t n, uint64_t
                      uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1, uint32_t ff, hipStream_t s) {
   if (n == 0) return 0;
   hipLaunchKernelGGL(repack_kernel<QT>, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, raw_dev, n, blk0,
-                     row_off, m.qs, m.sc, m.g.nb, m.g.ng, m.g.tail, map, hd, seg0, seg1, ff);
+                     row_off, m.qs, (uint64_t)m.g.tiles, m.g.nb, m.g.ng, m.g.tail, map, hd, seg0, seg1, ff);
   LLM_HIP(hipGetLastError());
   return 0;
 }
@@ -982,8 +1113,8 @@ int dequant_launch_qt(const QMat& m, float* out, uint32_t map, uint32_t hd, uint
                       hipStream_t s) {
   uint64_t n = m.g.rows * m.g.nb;
   if (n == 0) return 0;
-  hipLaunchKernelGGL(dequant_kernel<QT>, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, m.qs, m.sc,
-                     (uint32_t)m.g.rows, m.g.nb, m.g.ng, m.g.tail, map, hd, seg0, seg1, ff, out);
+  hipLaunchKernelGGL(dequant_kernel<QT>, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, m.qs,
+                     (uint64_t)m.g.tiles, (uint32_t)m.g.rows, m.g.nb, m.g.ng, m.g.tail, map, hd, seg0, seg1, ff, out);
   LLM_HIP(hipGetLastError());
   return 0;
 }
@@ -991,8 +1122,8 @@ int dequant_launch_qt(const QMat& m, float* out, uint32_t map, uint32_t hd, uint
 template <uint32_t QT>
 int embed_launch_qt(const QMat& m, const int32_t* tokens, const uint32_t* state, float* x, uint32_t ntok,
                     hipStream_t s) {
-  hipLaunchKernelGGL(embed_kernel<QT>, dim3(1, ntok), dim3(64), 0, s, m.qs, m.sc, m.g.nb, m.g.ng, m.g.tail, tokens,
-                     state, x);
+  hipLaunchKernelGGL(embed_kernel<QT>, dim3(1, ntok), dim3(64), 0, s, m.qs, (uint64_t)m.g.tiles, m.g.nb, m.g.ng,
+                     m.g.tail, tokens, state, x);
   LLM_HIP(hipGetLastError());
   return 0;
 }

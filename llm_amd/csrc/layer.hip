@@ -38,7 +38,7 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a, uint32_t ntok, ui
   if (u >= units) return;
   const uint32_t NI = ntok * a.kv_heads, inst = u % NI, c = u / NI;
   const uint32_t t = inst / a.kv_heads, g = inst % a.kv_heads, h = g * GQ + sb % GQ;
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, cl = lane & 15, slot = tid >> 4;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id(), cl = lane & 15, slot = tid >> 4;
   const uint32_t row0 = c * C;
   const float* kb = a.kv + g * HD + 4 * cl;
   const float* vb = a.kv + (uint64_t)a.ctx * a.kvd + g * HD + 4 * cl;
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
                                                       uint32_t* __restrict__ state, uint32_t adv) {
   __shared__ float sv[16];
   __shared__ uint32_t si[16];
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id(), nw = blockDim.x >> 6;
   constexpr int U = 8;
   float v[U];
   uint32_t ix[U];

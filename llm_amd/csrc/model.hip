@@ -119,7 +119,7 @@ static int qalloc(Model& m, QMat* q, uint32_t type, uint64_t rows, uint64_t k) {
     return set_error(LLMHIP_ERR_TYPE, "llm: a tensor has ggml type %u, which has no GPU kernel yet (Q4_0, Q4_1, Q8_0)",
                      type);
   Geom g = make_geom(qt, rows, k);
-  uint64_t bytes = g.qs_bytes() + g.sc_bytes();
+  uint64_t bytes = g.dev_bytes();
   if (m.used + bytes > m.lim.memory_budget)
     return set_error(LLMHIP_ERR_BUDGET,
                      "llm: the model needs more GPU memory than the %llu bytes granted (run with a larger budget)",

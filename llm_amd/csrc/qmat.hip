@@ -36,29 +36,21 @@ int qmat_alloc(QMat* m, int device, uint32_t type, uint64_t rows, uint64_t k) {
   m->device = device;
   m->g = make_geom(q, rows, k);
   LLM_HIP(hipSetDevice(device));
-  uint64_t qb = m->g.qs_bytes(), sb = m->g.sc_bytes();
-  LLM_HIP(hipMalloc(&m->qs, qb));
-  if (hipMalloc(&m->sc, sb) != hipSuccess) {
-    (void)hipFree(m->qs);
-    m->qs = nullptr;
-    return set_error(LLMHIP_ERR_DEVICE, "llm: hipMalloc of %llu bytes failed", (unsigned long long)sb);
-  }
+  const uint64_t nbytes = m->g.dev_bytes();
+  LLM_HIP(hipMalloc(&m->qs, nbytes));
   // padding rows of the last tile must read as zero weights
-  LLM_HIP(hipMemset(m->qs, 0, qb));
-  LLM_HIP(hipMemset(m->sc, 0, sb));
-  m->bytes = qb + sb;
+  LLM_HIP(hipMemset(m->qs, 0, nbytes));
+  m->bytes = nbytes;
   return 0;
 }
 
 void qmat_release(QMat* m) {
   if (m->qs) (void)hipFree(m->qs);
-  if (m->sc) (void)hipFree(m->sc);
-  m->qs = m->sc = nullptr;
+  m->qs = nullptr;
 }
 
 void gemv_bind(GemvArgs* a, const QMat& m) {
   a->qs = m.qs;
-  a->sc = m.sc;
   a->rows = (uint32_t)m.g.rows;
   a->nb = m.g.nb;
   a->ng = m.g.ng;
@@ -71,6 +63,19 @@ void gemv_bind(GemvArgs* a, const QMat& m) {
   a->map_seg1 = m.map_seg1;
   a->ff = m.ff;
   gemv_pick(a->tiles, a->ng, a->tail, a->nb, &a->split, &a->waves);
+  gemv_pick_stream(a->tiles, a->nb, &a->stream, &a->swaves);
+}
+
+void gemv_pick_stream(uint32_t tiles, uint32_t nb, uint32_t* wgs, uint32_t* waves) {
+  *wgs = 0;
+  *waves = 4;
+  if (tiles < GEMV_STREAM_MIN_TILES) return;
+  uint32_t w = 4;  // the prologue stages at most two 8-element items per thread
+  while (w < 8 && nb * 4 > 2 * 64 * w) w *= 2;
+  if (nb * 4 > 2 * 64 * w) return;  // k > 8192: the tile kernel
+  // about 16 waves per CU (4 per SIMD), each streaming several tiles
+  *wgs = std::min((tiles + w - 1) / w, 4096u / w);
+  *waves = w;
 }
 
 void gemv_pick(uint32_t tiles, uint32_t ng, uint32_t tail, uint32_t nb, uint32_t* split, uint32_t* waves) {
@@ -87,6 +92,7 @@ void gemv_pick(uint32_t tiles, uint32_t ng, uint32_t tail, uint32_t nb, uint32_t
 }
 
 uint32_t gemv_groups(const GemvArgs& a) {
+  if (a.stream && a.ntok == 1) return a.stream;
   uint32_t tpw = a.waves / a.split;
   return (a.tiles + tpw - 1) / tpw;
 }
@@ -358,8 +364,7 @@ int llmhip_qmat_clone(const llmhip_qmat* q, llmhip_qmat** out) {
   c->m.map_seg0 = q->m.map_seg0;
   c->m.map_seg1 = q->m.map_seg1;
   c->m.ff = q->m.ff;
-  if (hipMemcpy(c->m.qs, q->m.qs, q->m.g.qs_bytes(), hipMemcpyDeviceToDevice) != hipSuccess ||
-      hipMemcpy(c->m.sc, q->m.sc, q->m.g.sc_bytes(), hipMemcpyDeviceToDevice) != hipSuccess) {
+  if (hipMemcpy(c->m.qs, q->m.qs, q->m.g.dev_bytes(), hipMemcpyDeviceToDevice) != hipSuccess) {
     llmhip_qmat_free(c);
     return set_error(LLMHIP_ERR_DEVICE, "llm: clone copy failed");
   }

@@ -8,6 +8,10 @@
 
 namespace llmhip {
 
+// The wave's index in the workgroup, as a wave-uniform (scalar) value, so that
+// per-wave indices and loop bounds derived from it live in SGPRs.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));

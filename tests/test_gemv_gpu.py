@@ -71,6 +71,28 @@ def test_q41_shapes(gpu, oracle, qtype, rows, k, n):
     _check_gemv(gpu, oracle, qtype, rows, k, n)
 
 
+@pytest.mark.parametrize("qtype", [2, 3, 8])
+@pytest.mark.parametrize("rows,k", [(65541, 576), (70000, 224), (65536, 4864)])
+def test_stream_shapes(gpu, oracle, qtype, rows, k):
+    """One-token launches of 4096 tiles or more take the streaming kernel:
+    ragged rows, 1-3 tail blocks, and a k that needs 8 waves per workgroup."""
+    _check_gemv(gpu, oracle, qtype, rows, k, 1)
+
+
+def test_stream_accumulate(gpu, oracle):
+    import torch
+    from llm_amd.kernels import QMat
+    rows, k = 70001, 896
+    raw = _raw(8, rows, k, 4)
+    m = QMat(8, rows, k, raw)
+    x = _x(1, k, 4)
+    y0 = np.random.default_rng(6).standard_normal((1, rows), dtype=np.float32)
+    y = torch.from_numpy(y0).to(gpu)
+    m.gemv(torch.from_numpy(x).to(gpu), y, accumulate=True)
+    want = y0.astype(np.float64) + oracle.matvec(8, raw, rows, k, x[0])[None]
+    assert _rel(y.cpu().numpy(), want) <= TOL
+
+
 def test_accumulate(gpu, oracle):
     import torch
     from llm_amd.kernels import QMat
