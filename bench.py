@@ -36,10 +36,13 @@ PMC_SUMMARY = os.path.join(ROOT, "profiles", "pmc_decode_qwen25.txt")
 
 def kernel_symbols(attn_full):
     """Device symbol of each decode kernel class of the config-3 model (Q4_0
-    layers, Q8_0 head): gemv_kernel<type, tokens, prologue, epilogue>."""
-    return {"k1": "gemv_kernel<2u, 1, 1, 2>", "k2": "attn_full_kernel" if attn_full else "attn_kernel",
-            "k3": "gemv_kernel<2u, 1, 0, 1>" if attn_full else "gemv_kernel<2u, 1, 2, 1>",
-            "k4": "gemv_kernel<2u, 1, 1, 3>", "k5": "gemv_kernel<2u, 1, 0, 1>", "head": "gemv_kernel<8u, 1, 1, 4>"}
+    layers, Q8_0 head): gemv_kernel<type, tokens, prologue, epilogue> (k3 and
+    k5 share one; rocprof tells them apart by grid size), the one-chunk or
+    split attention, the streaming head."""
+    return {"k1": "gemv_kernel<2u, 1, 1, 2>",
+            "k2": "attn_kernel<64u, 8u, false>" if attn_full else "attn_kernel<64u, 4u, true> + attn_merge_kernel<64u>",
+            "k3": "gemv_kernel<2u, 1, 0, 1>", "k4": "gemv_kernel<2u, 1, 1, 3>", "k5": "gemv_kernel<2u, 1, 0, 1>",
+            "head": "gemv_stream_kernel<8u, 1, 4>"}
 
 
 def pmc_traffic(cls):
