@@ -509,14 +509,21 @@ struct WUnit {
   uint4 w0, w1, sv;
 };
 
-// Load group g (< ng) of tile t of the matrix at wq.
-template <uint32_t QT>
+// Load group g (< ng) of tile t of the matrix at wq.  The layer matrices use
+// ordinary (cacheable) loads; the streaming kernel's are non-temporal, so the
+// one-pass read of the vocabulary head does not push the layers out of cache.
+template <uint32_t QT, bool STREAM = false>
 __device__ __forceinline__ void load_group(WUnit& u, const uint8_t* wq, uint32_t nb, uint32_t t, uint32_t g,
                                            int lane, int r) {
   typedef Lay<QT> LY;
   const uint8_t* tb = wq + LY::tile(t, nb);
-  u.w0 = ld_stream16(tb + g * LY::QG + lane * 16);
-  if (QT == LLMHIP_Q8_0) u.w1 = ld_stream16(tb + g * LY::QG + 1024 + lane * 16);
+  if (STREAM) {
+    u.w0 = ld_stream16(tb + g * LY::QG + lane * 16);
+    if (QT == LLMHIP_Q8_0) u.w1 = ld_stream16(tb + g * LY::QG + 1024 + lane * 16);
+  } else {
+    u.w0 = *(const uint4*)(tb + g * LY::QG + lane * 16);
+    if (QT == LLMHIP_Q8_0) u.w1 = *(const uint4*)(tb + g * LY::QG + 1024 + lane * 16);
+  }
   const uint8_t* sp = tb + 16 * nb * LY::QB + g * 64 * LY::SB + r * 4 * LY::SB;
   if (QT == LLMHIP_Q4_1) {
     u.sv = *(const uint4*)sp;
@@ -527,12 +534,12 @@ __device__ __forceinline__ void load_group(WUnit& u, const uint8_t* wq, uint32_t
 }
 
 // Load unit g (< ng: a group, == ng: the tail) of tile t of the matrix at wq.
-template <uint32_t QT>
+template <uint32_t QT, bool STREAM = false>
 __device__ __forceinline__ void load_unit(WUnit& u, const uint8_t* wq, uint32_t nb, uint32_t t, uint32_t g,
                                           uint32_t ng, uint32_t tail, int lane, int r) {
   typedef Lay<QT> LY;
   if (g < ng) {
-    load_group<QT>(u, wq, nb, t, g, lane, r);
+    load_group<QT, STREAM>(u, wq, nb, t, g, lane, r);
     return;
   }
   const uint8_t* tb = wq + LY::tile(t, nb);
@@ -557,17 +564,21 @@ __device__ __forceinline__ void load_unit(WUnit& u, const uint8_t* wq, uint32_t 
 template <uint32_t QT, int NT>
 __device__ __forceinline__ void mfma_block(const h8* xs, const float* bsum, uint32_t nb, int q, int slot, uint32_t b,
                                            h8 B, uint32_t dbits, uint32_t mbits, float& acc0, float& acc1) {
+  // Branch-free (a clamped read, then a select) so that the blocks of a unit
+  // form one basic block and their LDS reads and MFMAs overlap.
   constexpr int S = 2 * NT;
-  h8 A = {};
-  if (slot < S) A = xs[(b * 4 + q) * S + slot];
+  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+  const u4v X = __builtin_bit_cast(u4v, xs[(b * 4 + q) * S + min(slot, S - 1)]);
+  const h8 A = __builtin_bit_cast(h8, X & (slot < S ? ~0u : 0u));
   f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4{0, 0, 0, 0}, 0, 0, 0);
   float d = f16_hw(dbits);
   acc0 += d * (D[0] + D[1]);
   if (NT > 1) acc1 += d * (D[2] + D[3]);
   if (QT == LLMHIP_Q4_1) {
-    float m = f16_hw(mbits);
-    if (2 * q < NT) acc0 += m * bsum[(2 * q) * nb + b];
-    if (2 * q + 1 < NT) acc1 += m * bsum[(2 * q + 1) * nb + b];
+    const float m = f16_hw(mbits);
+    const float s0 = bsum[min(2 * q, NT - 1) * nb + b], s1 = bsum[min(2 * q + 1, NT - 1) * nb + b];
+    acc0 += 2 * q < NT ? m * s0 : 0.f;
+    acc1 += 2 * q + 1 < NT ? m * s1 : 0.f;
   }
 }
 
@@ -753,7 +764,7 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
   WUnit w[R];
   auto fetch = [&](uint32_t i, WUnit& u) {
     const uint32_t tile = gw + (i / upt) * W;
-    load_unit<QT>(u, a.qs, nb, tile, i % upt, ng, tail, lane, r);
+    load_unit<QT, true>(u, a.qs, nb, tile, i % upt, ng, tail, lane, r);
   };
 #pragma unroll
   for (int d = 0; d < R; d++)
