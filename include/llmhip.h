@@ -169,6 +169,11 @@ LLMHIP_API int llmhip_model_peek(llmhip_model* m, const char* name, float* out, 
 LLMHIP_API uint64_t llmhip_model_memory_used(const llmhip_model* m);
 LLMHIP_API int llmhip_model_stats(const llmhip_model* m, llmhip_stats* out);
 LLMHIP_API int llmhip_model_config(const llmhip_model* m, llmhip_config* out, int* ctx);
+/* Store the KV cache in binary16, each K and V element rounded to nearest even
+ * (the F16KV mode of the reference's CPU path, cpu.go:22-24 and 298-299; its
+ * GPU path keeps f32).  Halves the cache and the attention's reads.  Call
+ * before the first llmhip_model_upload / finalize. */
+LLMHIP_API int llmhip_model_set_kv_f16(llmhip_model* m, int on);
 /* Run only the first `layers` layers (no head, no sampling; Layers, gpu.go:143-146). 0 = all. */
 LLMHIP_API int llmhip_model_set_layers(llmhip_model* m, int layers);
 /* Leave kernel classes out of every pass, comma-separated (Skip, gpu.go:769-784):
@@ -230,6 +235,8 @@ LLMHIP_API int llm_config_from(const llm_gguf* g, llmhip_config* out);
  * PrefillBatch (gpu.go:165), read by the next llm_new_gpu / generate. */
 LLMHIP_API int llm_set_decode_batch(int n);
 LLMHIP_API int llm_set_prefill_batch(int n);
+/* F16KV for the next llm_new_gpu (llmhip_model_set_kv_f16; cpu.go:22-24). */
+LLMHIP_API int llm_set_f16kv(int on);
 
 /* Timing, gpu.go:930-939 (nanoseconds).  record_ns stays 0: the passes are
  * recorded once, as hipGraphs, not per submit. */

@@ -87,6 +87,7 @@ SIGNATURES = [
     ("llmhip_model_stats", I, [P, ctypes.POINTER(Stats)]),
     ("llmhip_model_config", I, [P, ctypes.POINTER(Config), ctypes.POINTER(I)]),
     ("llmhip_model_set_layers", I, [P, I]),
+    ("llmhip_model_set_kv_f16", I, [P, I]),
     ("llmhip_model_set_skip", I, [P, ctypes.c_char_p]),
     ("llmhip_model_bench_kernel", I, [P, ctypes.c_char_p, I, ctypes.POINTER(F), PU64]),
     ("llmhip_model_profile", I, [P, I, P, I, ctypes.POINTER(I)]),
@@ -104,6 +105,7 @@ SIGNATURES = [
     ("llm_config_from", I, [P, ctypes.POINTER(Config)]),
     ("llm_set_decode_batch", I, [I]),
     ("llm_set_prefill_batch", I, [I]),
+    ("llm_set_f16kv", I, [I]),
     ("llm_new_gpu", I, [I, ctypes.POINTER(Limits), ctypes.c_char_p, I, ctypes.POINTER(P)]),
     ("llm_gpu_generate", I, [P, P, I, I, ctypes.c_int32, EMIT, P, ctypes.POINTER(Timing)]),
     ("llm_gpu_prefill_logits", I, [P, P, I, P]),

@@ -63,7 +63,8 @@ struct GemvArgs {
   uint32_t ldy;
   const float* bias;  // QKV biases, logical row order (nullptr: none)
   const float* cs;    // RoPE table [pos][hd/2][cos, sin]
-  float* kv;          // this layer's cache [2][ctx][kvd]
+  float* kv;          // this layer's cache [2][ctx][kvd], f32 or (kv16) binary16
+  uint32_t kv16;
   uint32_t nq, nk, kvd, ctx;
   uint32_t neox;
   uint32_t ff;

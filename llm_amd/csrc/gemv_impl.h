@@ -299,6 +299,14 @@ __device__ __forceinline__ bool amax_better(float v, uint32_t i, float bv, uint3
   return i != 0xffffffffu && (bi == 0xffffffffu || v > bv || (v == bv && i < bi));
 }
 
+// One element into the KV cache: f32, or rounded to binary16 (RoundF16 of
+// the F16KV mode, cpu.go:298-299; the hardware conversion rounds to nearest
+// even, subnormals kept, like F32ToF16 in f16.go).
+__device__ __forceinline__ void kv_store(const GemvArgs& a, uint64_t i, float v) {
+  if (a.kv16) ((_Float16*)a.kv)[i] = (_Float16)v;
+  else a.kv[i] = v;
+}
+
 // The per-row epilogue of both matrix kernels.  The lane holds row r of tile
 // `tile` for two tokens of the launch (tokA, tokB; okA/okB say whether they
 // exist), already unscaled.  Every lane of the wave must call it: the RoPE and
@@ -363,9 +371,9 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
           float res = first ? __fsub_rn(__fmul_rn(x, c), __fmul_rn(z, sn))    // cpu.go:381
                             : __fadd_rn(__fmul_rn(x, sn), __fmul_rn(z, c));  // cpu.go:382
           if (lf < a.nq) a.y[(uint64_t)tok * a.nq + lf] = res;
-          else a.kv[(uint64_t)pos * a.kvd + j] = res;
+          else kv_store(a, (uint64_t)pos * a.kvd + j, res);
         } else {
-          a.kv[(uint64_t)a.ctx * a.kvd + (uint64_t)pos * a.kvd + (lf - a.nq - a.nk)] = v;
+          kv_store(a, (uint64_t)a.ctx * a.kvd + (uint64_t)pos * a.kvd + (lf - a.nq - a.nk), v);
         }
       }
     }

@@ -16,6 +16,7 @@ struct AttnArgs {
   uint32_t smax;   // chunk slots of pv/ml per (token, head)
   uint32_t rows;   // cache rows read: > every position of the pass, <= ctx
   uint32_t split;  // 0: one chunk (rows <= attn_full_max(hd)); 1: chunks of ATTN_SPLIT_ROWS + merge
+  uint32_t kv16;   // the cache holds binary16 values (F16KV)
   float scale;     // f32(1/sqrt(hd)), cpu.go:304
 };
 

@@ -27,7 +27,19 @@ namespace llmhip {
 //   SPLIT = true: chunk c covers rows [c*C, c*C + C); writes the partials
 //     (m, l) and o = sum e v for attn_merge_kernel; chunks past the causal
 //     bound write nothing.
-template <uint32_t HD, uint32_t J, bool SPLIT>
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Four consecutive cache elements as f32: an f32 cache, or binary16 (F16KV)
+// widened exactly.
+template <bool KVH>
+__device__ __forceinline__ f4 kv_load4(const float* kv, uint64_t i) {
+  if (!KVH) return *(const f4*)(kv + i);
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const h4 h = *(const h4*)((const _Float16*)kv + i);
+  return f4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+
+template <uint32_t HD, uint32_t J, bool SPLIT, bool KVH>
 __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a, uint32_t ntok, uint32_t units) {
   typedef float f4 __attribute__((ext_vector_type(4)));
   constexpr uint32_t V4 = HD / 64, C = 32 * J;
@@ -40,8 +52,7 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a, uint32_t ntok, ui
   const uint32_t t = inst / a.kv_heads, g = inst % a.kv_heads, h = g * GQ + sb % GQ;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id(), cl = lane & 15, slot = tid >> 4;
   const uint32_t row0 = c * C;
-  const float* kb = a.kv + g * HD + 4 * cl;
-  const float* vb = a.kv + (uint64_t)a.ctx * a.kvd + g * HD + 4 * cl;
+  const uint64_t kb = g * HD + 4 * cl, vb = (uint64_t)a.ctx * a.kvd + g * HD + 4 * cl;  // element offsets
   const float* qp = a.q + (uint64_t)t * a.heads * HD + h * HD + 4 * cl;
   f4 q[V4], kr[J][V4], vr[J][V4];
 #pragma unroll
@@ -52,8 +63,8 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a, uint32_t ntok, ui
     if (p < a.rows) {
 #pragma unroll
       for (uint32_t v = 0; v < V4; v++) {
-        kr[j][v] = *(const f4*)(kb + (uint64_t)p * a.kvd + 64 * v);
-        vr[j][v] = *(const f4*)(vb + (uint64_t)p * a.kvd + 64 * v);
+        kr[j][v] = kv_load4<KVH>(a.kv, kb + (uint64_t)p * a.kvd + 64 * v);
+        vr[j][v] = kv_load4<KVH>(a.kv, vb + (uint64_t)p * a.kvd + 64 * v);
       }
     }
   }
@@ -174,7 +185,8 @@ uint32_t attn_full_max(uint32_t hd) { return hd == 64 ? 256 : 128; }
 template <uint32_t HD, uint32_t J, bool SPLIT>
 static void attn_go(const AttnArgs& a, uint32_t ntok, uint32_t units, hipStream_t s) {
   const uint32_t gq = a.heads / a.kv_heads, blocks = 8 * gq * ((units + 7) / 8);
-  hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT>), dim3(blocks), dim3(512), 0, s, a, ntok, units);
+  if (a.kv16) hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT, true>), dim3(blocks), dim3(512), 0, s, a, ntok, units);
+  else hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT, false>), dim3(blocks), dim3(512), 0, s, a, ntok, units);
 }
 
 int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s) {

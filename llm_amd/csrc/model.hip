@@ -65,6 +65,7 @@ struct Model {
   std::vector<Layer> layers;
   std::map<std::string, TensorInfo> tensors;
   bool allocated = false, finalized = false;
+  bool kv16 = false;  // binary16 KV cache (the F16KV mode of cpu.go:22-24)
   hipGraphExec_t decode_exec = nullptr;
   std::map<uint64_t, hipGraphExec_t> chunk_exec;  // key: graph_key(ntok, attn_rows, attn_split, head)
   std::map<uint64_t, uint32_t> graph_nodes;       // dispatches per graph key
@@ -269,7 +270,7 @@ static int allocate(Model& m) {
       LLM_TRY(qalloc(m, &L.gu[1], t[5]->type, F, E));
     }
     LLM_TRY(qalloc(m, &L.down, t[6]->type, E, F));
-    LLM_TRY(dalloc_n(m, &L.kv, 2ull * m.ctx * kvd));
+    LLM_TRY(dalloc(m, (void**)&L.kv, 2ull * m.ctx * kvd * (m.kv16 ? 2 : 4)));
   }
   m.allocated = true;
   return 0;
@@ -350,6 +351,7 @@ static GemvArgs base_args(const Model& m, const QMat& q, uint32_t ntok) {
   a.state = m.state;
   a.heads = m.cfg.heads;
   a.hd = m.cfg.head_dim;
+  a.kv16 = m.kv16 ? 1 : 0;
   return a;
 }
 
@@ -391,6 +393,7 @@ static AttnArgs attn_args(const Model& m, const Layer& L) {
   a.smax = m.smax;
   a.rows = m.attn_rows;
   a.split = m.attn_split ? 1 : 0;
+  a.kv16 = m.kv16 ? 1 : 0;
   a.scale = (float)(1 / std::sqrt((double)m.cfg.head_dim));  // cpu.go:304
   return a;
 }
@@ -810,7 +813,13 @@ int llmhip_model_peek(llmhip_model* h, const char* name, float* out, uint64_t n)
   if (n > cap) return set_error(LLMHIP_ERR_ARG, "llm: buffer \"%s\" holds %llu words", name, (unsigned long long)cap);
   LLM_HIP(hipSetDevice(m.device));
   LLM_HIP(hipStreamSynchronize(m.stream));
-  LLM_HIP(hipMemcpy(out, src, n * 4, hipMemcpyDeviceToHost));
+  if (m.kv16 && s.rfind("kvblk.", 0) == 0) {  // binary16 cache: widened on the host
+    std::vector<_Float16> h(n);
+    LLM_HIP(hipMemcpy(h.data(), src, n * 2, hipMemcpyDeviceToHost));
+    for (uint64_t i = 0; i < n; i++) out[i] = (float)h[i];
+  } else {
+    LLM_HIP(hipMemcpy(out, src, n * 4, hipMemcpyDeviceToHost));
+  }
   m.stats.submits++;
   return 0;
 }
@@ -825,6 +834,14 @@ int llmhip_model_stats(const llmhip_model* h, llmhip_stats* out) {
 int llmhip_model_config(const llmhip_model* h, llmhip_config* out, int* ctx) {
   *out = h->m->cfg;
   if (ctx) *ctx = (int)h->m->ctx;
+  return 0;
+}
+
+int llmhip_model_set_kv_f16(llmhip_model* h, int on) {
+  clear_error();
+  Model& m = *h->m;
+  if (m.allocated) return set_error(LLMHIP_ERR_STATE, "llm: the KV cache format is fixed once tensors are uploaded");
+  m.kv16 = on != 0;
   return 0;
 }
 

@@ -21,6 +21,8 @@ PieceSize = 4 << 20
 MaxBatch = 16
 PrefillBatch = 64
 DecodeBatch = 8
+# binary16 KV cache for the next NewGPU (the F16KV mode of cpu.go:22-24)
+F16KV = False
 
 
 def DefaultLimits(ordinal=0):
@@ -244,6 +246,7 @@ def NewGPU(dev, lim, path, ctx):
     """NewGPU (gpu.go:465-764): dev is the HIP device ordinal, lim a Limits or
     None for the device's own, path the GGUF file, ctx the KV cache length."""
     lib().llm_set_prefill_batch(int(PrefillBatch))
+    lib().llm_set_f16kv(int(F16KV))
     h = ctypes.c_void_p()
     check(lib().llm_new_gpu(int(dev), ctypes.byref(lim) if lim is not None else None, os.fsencode(path), int(ctx),
                             ctypes.byref(h)))

@@ -25,8 +25,11 @@
  *   cpuref_forward       cpu.go:225-366   pinned: independent vectorised float64 numpy
  *                                         forward on tiny models (attention weights sum
  *                                         to 1, single-position att = v)
- *   quantize_q8 / ExactGGML, F16KV modes  cpu.go:117-140, 298-299: parity unpinned
- *                        beyond closed-form checks of quantize_q8 (not on the graded path)
+ *   F16KV mode           cpu.go:22-24, 298-299  pinned: the float64 forward with a
+ *                                         binary16-rounded cache (numpy RNE), closer to
+ *                                         it than to the exact-cache forward
+ *   quantize_q8 / ExactGGML mode  cpu.go:117-140: parity unpinned beyond closed-form
+ *                        checks of quantize_q8 (not on the graded path)
  *   gguf reader / config_from  gguf/gguf.go:292-407, config.go:29-73: pinned by the
  *                        reference's gguf_test.go cases and refusal cases of config.go
  *

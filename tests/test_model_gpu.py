@@ -15,13 +15,18 @@ from tests.parity import LOGIT_TOL, cpu_greedy, gpu_generate, greedy_parity, rel
 pytestmark = pytest.mark.gpu
 
 
-def _open(spec, ctx):
+def _open(spec, ctx, f16kv=False):
     from llm_amd import llm
     from oracle import cpuref
     path = synth.cached(spec)
-    print(f"model {spec.arch} L{spec.layers} E{spec.embd} V{spec.vocab} ctx {ctx} at {path}", flush=True)
-    g = llm.NewGPU(0, None, path, ctx)
-    cpu = cpuref.CPU(path, ctx, threads=16)
+    print(f"model {spec.arch} L{spec.layers} E{spec.embd} V{spec.vocab} ctx {ctx} f16kv {f16kv} at {path}", flush=True)
+    old = llm.F16KV
+    llm.F16KV = f16kv
+    try:
+        g = llm.NewGPU(0, None, path, ctx)
+    finally:
+        llm.F16KV = old
+    cpu = cpuref.CPU(path, ctx, threads=16, f16kv=f16kv)
     return g, cpu
 
 
@@ -68,6 +73,31 @@ def test_attention_paths(gpu, prompt_len, heads, kv_heads, hd):
     g, cpu = _open(spec, 512)
     prompt = synth.prompt(7, prompt_len, spec.vocab)
     _check(g, cpu, prompt, (320 if hd == 64 else 200) - prompt_len)
+
+
+@pytest.mark.parametrize("name,prompt_len,n", [("llama", 150, 40), ("qwen2", 150, 40), ("qwen2-split", 300, 24),
+                                               ("llama-hd128", 140, 40)])
+def test_f16_kv_cache(gpu, name, prompt_len, n):
+    """The binary16 KV cache (F16KV, cpu.go:22-24, 298-299) against the oracle
+    in the same mode: one-chunk and split attention, head sizes 64 and 128;
+    the cache holds the oracle's rounded values exactly."""
+    spec = {"llama": lambda: synth.tiny_llama(), "qwen2": lambda: synth.tiny_qwen(),
+            "qwen2-split": lambda: synth.tiny_qwen(seed=8), "llama-hd128": lambda: synth.tiny_llama(
+                seed=9, embd=256, heads=2, kv_heads=1)}[name]()
+    g, cpu = _open(spec, 512, f16kv=True)
+    prompt = synth.prompt(12, prompt_len, spec.vocab)
+    _check(g, cpu, prompt, n)
+    kvd = spec.kv_heads * (spec.embd // spec.heads)
+    kv = g.Peek("kvblk.0", 2 * 512 * kvd).reshape(2, 512, kvd)[:, :prompt_len]
+    assert np.array_equal(kv, kv.astype(np.float16).astype(np.float32)), "cache values are not binary16"
+    assert np.all(np.abs(kv[:, 1:]).max(axis=-1) > 0)
+
+
+def test_qwen25_f16_kv_cache(gpu):
+    """BASELINE config 3's shape with the binary16 cache, against the oracle's F16KV mode."""
+    spec = synth.qwen25()
+    g, cpu = _open(spec, 512, f16kv=True)
+    _check(g, cpu, synth.prompt(0, 128, spec.vocab), 64)
 
 
 def test_decode_batches_and_stops(gpu):

@@ -241,10 +241,12 @@ def test_quantize_q8_closed_form():
 
 # ----------------------------------------------- the forward pass, float64
 
-def _forward64(path, tokens):
+def _forward64(path, tokens, f16kv=False):
     """An independent float64 forward pass of the model (cpu.go:225-366 as
     mathematics: dequantised matrices, vectorised attention with the global
-    max), returning the logits of the last token."""
+    max), returning the logits of the last token.  f16kv: K and V rounded
+    through binary16 before they enter the cache (numpy's float16 cast,
+    round to nearest even)."""
     from llm_amd import llm
     f = llm.Parse(path)
     c = llm.ConfigFrom(f)
@@ -293,6 +295,8 @@ def _forward64(path, tokens):
             if c.bias:
                 q, k, v = q + w["attn_q.bias"], k + w["attn_k.bias"], v + w["attn_v.bias"]
             q, k = rope(q, pos, H), rope(k, pos, KVH)
+            if f16kv:
+                k, v = (z.astype(np.float32).astype(np.float16).astype(np.float64) for z in (k, v))
             K[l].append(k)
             V[l].append(v)
             Km, Vm = np.array(K[l]).reshape(pos + 1, KVH, HD), np.array(V[l]).reshape(pos + 1, KVH, HD)
@@ -323,6 +327,24 @@ def test_forward_against_float64(spec):
     rel = np.max(np.abs(got - want)) / np.max(np.abs(want))
     assert rel <= 1e-5, rel
     assert cpu.pos() == len(toks)
+
+
+@pytest.mark.parametrize("spec", [synth.tiny_llama(), synth.tiny_qwen()], ids=["llama", "qwen2"])
+def test_forward_f16kv_against_float64(spec):
+    """The F16KV mode (cpu.go:22-24, 298-299): within 1.5e-5 of a float64
+    forward whose cache holds binary16-rounded K and V, and at least four times
+    closer to it than to the float64 forward with an exact cache.  The f32
+    mode sits 3.5e-5 to 1e-4 from the rounded forward, so a mode that did not
+    round, or rounded something else, fails."""
+    path = synth.cached(spec)
+    toks = list(synth.prompt(11, 60, spec.vocab))
+    cpu = cpuref.CPU(path, 64, f16kv=True)
+    for t in toks:
+        got = cpu.forward(t)
+    want16, want32 = _forward64(path, toks, f16kv=True), _forward64(path, toks)
+    scale = np.max(np.abs(want16))
+    r16, r32 = np.max(np.abs(got - want16)) / scale, np.max(np.abs(got - want32)) / scale
+    assert r16 <= 1.5e-5 and r32 >= 4 * r16, (r16, r32)
 
 
 def test_forward_modes_and_layers():
