@@ -151,6 +151,23 @@ LLMHIP_API int llmhip_model_tensor(llmhip_model* m, const char* name, uint32_t g
  * QKV and gate/up concatenation and the NEOX pairing done on the device. */
 LLMHIP_API int llmhip_model_upload(llmhip_model* m, const char* name, const void* raw, uint64_t nbytes,
                                    uint64_t byte_offset);
+/* The loader's fast path: the same upload, with the nbytes read from the open
+ * file descriptor fd at file_offset (pread, which leaves the descriptor's own
+ * position alone) straight into pinned staging by a pool of host threads,
+ * overlapped with the DMA and repack of the pieces before.  Replaces
+ * streamMat's ReadAt loop (gpu.go:356-389) when the io.ReaderAt is a file;
+ * one call may cover a whole tensor. */
+LLMHIP_API int llmhip_model_upload_file(llmhip_model* m, const char* name, int fd, uint64_t file_offset,
+                                        uint64_t nbytes, uint64_t byte_offset);
+/* The fast path for a whole file: every listed tensor (its declared size, from
+ * file_offsets[i]) in one call.  Consecutive tensors are read in runs of up to
+ * 8 MiB, each with one parallel pread and one DMA, and each tensor's repack
+ * runs on its part of the run; the same result as one llmhip_model_upload per
+ * tensor.  Replaces NewGPU's tensor-by-tensor loadMat / loadMatRows / loadF32 /
+ * loadGroup calls (gpu.go:543-740, fused.go:108-190) when the io.ReaderAt is a
+ * file. */
+LLMHIP_API int llmhip_model_upload_file_tensors(llmhip_model* m, int fd, uint32_t n, const char* const* names,
+                                                const uint64_t* file_offsets);
 /* Check that every needed tensor arrived in full ("llm: missing tensor"). */
 LLMHIP_API int llmhip_model_finalize(llmhip_model* m);
 /* Run a prompt from position 0 (prefill, gpu.go:853-900) in chunks of

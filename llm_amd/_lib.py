@@ -79,6 +79,8 @@ SIGNATURES = [
     ("llmhip_model_create", I, [I, ctypes.POINTER(Limits), ctypes.POINTER(Config), I, I, ctypes.POINTER(P)]),
     ("llmhip_model_tensor", I, [P, ctypes.c_char_p, U32, PU64, U32]),
     ("llmhip_model_upload", I, [P, ctypes.c_char_p, P, U64, U64]),
+    ("llmhip_model_upload_file", I, [P, ctypes.c_char_p, I, U64, U64, U64]),
+    ("llmhip_model_upload_file_tensors", I, [P, I, U32, ctypes.POINTER(ctypes.c_char_p), PU64]),
     ("llmhip_model_finalize", I, [P]),
     ("llmhip_model_prefill", I, [P, P, I, P, P]),
     ("llmhip_model_decode", I, [P, I, P]),

@@ -20,6 +20,7 @@ struct QMat {
   Geom g;
   uint8_t* qs = nullptr;  // device: the unit records (quants and scales)
   uint64_t bytes = 0;
+  bool owned = false;     // qs from qmat_alloc (freed by qmat_release), not placed in a caller's memory
   // row map (RowMap): NEOX pairs rows inside heads of map_hd rows for rows
   // [map_seg0, map_seg1); GATEUP pairs row i with row ff + i.
   uint32_t map = MAP_IDENT, map_hd = 0, map_seg0 = 0, map_seg1 = 0, ff = 0;
@@ -117,22 +118,59 @@ void gemv_bind(GemvArgs* a, const QMat& m);
 
 // Allocation and device repack of raw GGUF blocks.
 int qmat_alloc(QMat* m, int device, uint32_t type, uint64_t rows, uint64_t k);
+// The geometry of a matrix placed at mem (zeroed device memory of at least
+// Geom::dev_bytes(), owned by the caller; nullptr only to size it).
+int qmat_place(QMat* m, int device, uint32_t type, uint64_t rows, uint64_t k, uint8_t* mem);
 void qmat_release(QMat* m);
-// Host staging for uploads: pinned + device buffers of one piece.
+// Host -> device staging for uploads of raw GGUF blocks (stage.cpp):
+// STAGE_BUFS pinned host buffers and as many device buffers of cap bytes.
+constexpr int STAGE_BUFS = 3;
 struct Stager {
   int device = -1;
-  uint8_t* host[2] = {nullptr, nullptr};
-  uint8_t* dev[2] = {nullptr, nullptr};
-  hipEvent_t done[2] = {nullptr, nullptr};
-  int cur = 0;
-  uint64_t cap = 0;
-  hipStream_t stream = nullptr;
+  uint8_t* host[STAGE_BUFS] = {};
+  uint8_t* dev[STAGE_BUFS] = {};
+  hipEvent_t done[STAGE_BUFS] = {};    // the model's stream finished with the buffer
+  hipEvent_t copied[STAGE_BUFS] = {};  // the latest DMA out of the buffer finished
+  hipStream_t copy = nullptr;          // the DMA stream (default priority)
+  int cur = 0;        // the buffer being filled
+  uint64_t used = 0;  // bytes of it handed out
+  uint64_t cap = 0;   // 0: not allocated
+  hipStream_t stream = nullptr;  // the repack and f32 copies run here
 };
 int stager_init(Stager* st, int device, uint64_t cap, hipStream_t s);
 void stager_free(Stager* st);
+// Where upload bytes come from: caller memory, or a file read with pread.
+// Offsets passed with a Source count from mem / file_off.
+struct Source {
+  const uint8_t* mem = nullptr;
+  int fd = -1;
+  uint64_t file_off = 0;
+};
+// Fill dst with bytes [off, off+n) of src, split over the staging threads.
+int stage_read(const Source& src, uint64_t off, void* dst, uint64_t n);
 // Upload raw GGUF bytes [byte_off, byte_off+nbytes) of a tensor whose first
-// row is logical row row_off of m (a fused matrix holds several tensors).
-int qmat_upload(Stager* st, const QMat& m, const void* raw, uint64_t nbytes, uint64_t byte_off, uint64_t row_off);
+// row is logical row row_off of m (a fused matrix holds several tensors);
+// src holds those nbytes.
+int qmat_upload(Stager* st, const QMat& m, const Source& src, uint64_t nbytes, uint64_t byte_off, uint64_t row_off);
+// Bytes [byte_off, byte_off+nbytes) of an f32 tensor at dst (device), staged
+// like the quantised pieces (no synchronisation of the stream).
+int f32_upload(Stager* st, float* dst, const Source& src, uint64_t nbytes, uint64_t byte_off);
+// One piece of a batched file upload: bytes [off, off+bytes) of a tensor
+// (whole blocks of q, or of the f32 array f) found at file offset `file`.
+struct StagePiece {
+  const QMat* q;
+  float* f;
+  uint64_t row_off, off, bytes, file;
+};
+// Upload pieces sorted by file offset, each at most the staging capacity:
+// runs of consecutive pieces are read with one parallel pread and one DMA.
+int stage_file_runs(Stager* st, int fd, const StagePiece* ps, size_t count);
+inline int qmat_upload(Stager* st, const QMat& m, const void* raw, uint64_t nbytes, uint64_t byte_off,
+                       uint64_t row_off) {
+  Source src;
+  src.mem = (const uint8_t*)raw;
+  return qmat_upload(st, m, src, nbytes, byte_off, row_off);
+}
 // Dequantise rows [0, rows) (logical order) into out_dev[rows][k].
 int qmat_dequant(const QMat& m, float* out_dev, hipStream_t s);
 // Embedding gather: x[t][:] = row tokens[state[1] + t] of m (exact), t < ntok.

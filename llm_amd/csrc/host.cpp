@@ -371,7 +371,6 @@ using namespace llm;
 // Tunables of the Go package (gpu.go:20-23,165,1046-1054).
 static int g_decode_batch = 8, g_prefill_batch = 64, g_f16kv = 0;
 static const int kMaxBatch = 16;
-static const uint64_t kPieceSize = 4ull << 20;
 
 struct llm_gguf {
   gguf::File f;
@@ -525,7 +524,6 @@ int llm_new_gpu(int ordinal, const llmhip_limits* lim, const char* path, int ctx
   llm_gguf* gf = nullptr;
   int rc = parse_fd(fd, &gf, nullptr);
   llm_gpu* g = nullptr;
-  std::vector<uint8_t> piece;
   if (rc == 0) {
     g = new llm_gpu();
     rc = config_from(gf->f, &g->cfg);
@@ -537,23 +535,17 @@ int llm_new_gpu(int ordinal, const llmhip_limits* lim, const char* path, int ctx
     const gguf::Tensor& t = gf->f.tensors[i];
     rc = llmhip_model_tensor(g->m, t.name.c_str(), t.type, t.dims.data(), (uint32_t)t.dims.size());
   }
-  for (size_t i = 0; rc == 0 && i < gf->f.tensors.size(); i++) {
-    const gguf::Tensor& t = gf->f.tensors[i];
-    uint64_t be, bb;
-    gguf::block_size(t.type, &be, &bb);
-    uint64_t per = std::max<uint64_t>(1, kPieceSize / bb) * bb;
-    for (uint64_t a = 0; rc == 0 && a < t.size; a += per) {
-      uint64_t n = std::min(per, t.size - a);
-      piece.resize(n);
-      uint64_t got = 0;
-      while (got < n) {
-        ssize_t r = pread(fd, piece.data() + got, n - got, (off_t)(gf->f.data_offset + t.offset + a + got));
-        if (r <= 0) break;
-        got += (uint64_t)r;
-      }
-      if (got < n) rc = set_error(LLMHIP_ERR_IO, "llm: reading %s: short read", t.name.c_str());
-      else rc = llmhip_model_upload(g->m, t.name.c_str(), piece.data(), n, a);
+  // whole tensors straight from the file into pinned staging (the parser
+  // checked that every tensor lies inside the file)
+  if (rc == 0) (void)posix_fadvise(fd, 0, 0, POSIX_FADV_SEQUENTIAL);
+  if (rc == 0) {
+    std::vector<const char*> names;
+    std::vector<uint64_t> offs;
+    for (const gguf::Tensor& t : gf->f.tensors) {
+      names.push_back(t.name.c_str());
+      offs.push_back(gf->f.data_offset + t.offset);
     }
+    rc = llmhip_model_upload_file_tensors(g->m, fd, (uint32_t)names.size(), names.data(), offs.data());
   }
   if (rc == 0) rc = llmhip_model_finalize(g->m);
   close(fd);

@@ -50,6 +50,9 @@ struct Model {
   uint32_t ctx = 0, pm = 64, smax = 0, kvd = 0;
   uint64_t used = 0;
   std::vector<void*> allocs;
+  uint8_t* arena = nullptr;  // weights, norms, biases, KV caches (allocate)
+  uint64_t arena_cap = 0, arena_used = 0;
+  bool sizing = false;
   hipStream_t stream = nullptr;
   Stager st;
   float *x = nullptr, *q = nullptr, *act = nullptr, *gbuf = nullptr, *logits = nullptr, *pv = nullptr,
@@ -96,15 +99,31 @@ static int launch_rec(Model& m, const char* cls, uint64_t bytes, F&& launch) {
   return 0;
 }
 
+static int over_budget(const Model& m) {
+  return set_error(LLMHIP_ERR_BUDGET,
+                   "llm: the model needs more GPU memory than the %llu bytes granted (run with a larger budget)",
+                   (unsigned long long)m.lim.memory_budget);
+}
+
+// Zeroed device memory of `bytes` (rounded up to 256), counted against the
+// budget.  While the weights arena is being sized (m.sizing) only the size is
+// counted; while it is being carved the memory comes from it.
 static int dalloc(Model& m, void** p, uint64_t bytes) {
   bytes = (bytes + 255) & ~255ull;
-  if (m.used + bytes > m.lim.memory_budget)
-    return set_error(LLMHIP_ERR_BUDGET,
-                     "llm: the model needs more GPU memory than the %llu bytes granted (run with a larger budget)",
-                     (unsigned long long)m.lim.memory_budget);
-  LLM_HIP(hipMalloc(p, bytes));
-  LLM_HIP(hipMemset(*p, 0, bytes));
-  m.allocs.push_back(*p);
+  if (m.sizing) {
+    *p = nullptr;
+    m.arena_cap += bytes;
+    return 0;
+  }
+  if (m.used + bytes > m.lim.memory_budget) return over_budget(m);
+  if (m.arena && m.arena_used + bytes <= m.arena_cap) {
+    *p = m.arena + m.arena_used;
+    m.arena_used += bytes;
+  } else {
+    LLM_HIP(hipMalloc(p, bytes));
+    LLM_HIP(hipMemset(*p, 0, bytes));
+    m.allocs.push_back(*p);
+  }
   m.used += bytes;
   return 0;
 }
@@ -119,15 +138,9 @@ static int qalloc(Model& m, QMat* q, uint32_t type, uint64_t rows, uint64_t k) {
   if (!qtype_of(type, &qt))
     return set_error(LLMHIP_ERR_TYPE, "llm: a tensor has ggml type %u, which has no GPU kernel yet (Q4_0, Q4_1, Q8_0)",
                      type);
-  Geom g = make_geom(qt, rows, k);
-  uint64_t bytes = g.dev_bytes();
-  if (m.used + bytes > m.lim.memory_budget)
-    return set_error(LLMHIP_ERR_BUDGET,
-                     "llm: the model needs more GPU memory than the %llu bytes granted (run with a larger budget)",
-                     (unsigned long long)m.lim.memory_budget);
-  LLM_TRY(qmat_alloc(q, m.device, type, rows, k));
-  m.used += q->bytes;
-  return 0;
+  void* mem;
+  LLM_TRY(dalloc(m, &mem, make_geom(qt, rows, k).dev_bytes()));
+  return qmat_place(q, m.device, type, rows, k, (uint8_t*)mem);
 }
 
 static void destroy_graphs(Model& m) {
@@ -199,7 +212,7 @@ static const TensorInfo* need(Model& m, const std::string& n) {
 // Allocate every weight once all tensors are declared: the fused groups need
 // the types of all their members (fused.go:108-190 concatenates QKV and
 // gate/up when they share a type; here mixed types get one matrix each).
-static int allocate(Model& m) {
+static int allocate_pass(Model& m) {
   const llmhip_config& c = m.cfg;
   const uint32_t E = c.embd, F = c.ff, kvd = m.kvd, hd = c.head_dim;
   const TensorInfo* te = need(m, "token_embd.weight");
@@ -272,6 +285,25 @@ static int allocate(Model& m) {
     LLM_TRY(qalloc(m, &L.down, t[6]->type, E, F));
     LLM_TRY(dalloc(m, (void**)&L.kv, 2ull * m.ctx * kvd * (m.kv16 ? 2 : 4)));
   }
+  return 0;
+}
+
+// The weights, norms, biases and KV caches in one zeroed device arena: one
+// pass sizes it, one hipMalloc and one fill, a second pass carves it (about a
+// hundred separate allocations cost milliseconds at load and at free).
+static int allocate(Model& m) {
+  m.sizing = true;
+  m.arena_cap = 0;
+  int rc = allocate_pass(m);
+  m.sizing = false;
+  if (rc) return rc;
+  if (m.used + m.arena_cap > m.lim.memory_budget) return over_budget(m);
+  LLM_HIP(hipSetDevice(m.device));
+  LLM_HIP(hipMalloc((void**)&m.arena, m.arena_cap));
+  m.allocs.push_back(m.arena);
+  LLM_HIP(hipMemsetAsync(m.arena, 0, m.arena_cap, m.stream));
+  m.arena_used = 0;
+  LLM_TRY(allocate_pass(m));
   m.allocated = true;
   return 0;
 }
@@ -652,7 +684,6 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
   m->host_cap = std::max<uint32_t>(m->ctx + 1, 64);
   if (hipHostMalloc((void**)&m->host, (size_t)m->host_cap * 4, hipHostMallocDefault) != hipSuccess)
     return fail(set_error(LLMHIP_ERR_DEVICE, "llm: hipHostMalloc failed"));
-  if ((rc = stager_init(&m->st, ordinal, 4ull << 20, m->stream))) return fail(rc);
   *out = new llmhip_model{m};
   return 0;
 }
@@ -694,9 +725,12 @@ int llmhip_model_tensor(llmhip_model* h, const char* name, uint32_t type, const 
   return 0;
 }
 
-int llmhip_model_upload(llmhip_model* h, const char* name, const void* raw, uint64_t nbytes, uint64_t off) {
-  clear_error();
-  Model& m = *h->m;
+}  // extern "C"
+
+// Staging of one load (a model's uploads, then freed at finalize).
+constexpr uint64_t MODEL_STAGE_BYTES = 8ull << 20;
+
+static int upload_from(Model& m, const char* name, const Source& src, uint64_t nbytes, uint64_t off) {
   auto it = m.tensors.find(name);
   if (it == m.tensors.end()) return set_error(LLMHIP_ERR_ARG, "llm: tensor %s was not declared", name);
   TensorInfo& t = it->second;
@@ -709,15 +743,73 @@ int llmhip_model_upload(llmhip_model* h, const char* name, const void* raw, uint
   float* f;
   LLM_TRY(route(m, name, &q, &row_off, &f));
   LLM_HIP(hipSetDevice(m.device));
-  if (q) {
-    LLM_TRY(qmat_upload(&m.st, *q, raw, nbytes, off, row_off));
-  } else {
-    if (off % 4 || nbytes % 4) return set_error(LLMHIP_ERR_ARG, "llm: F32 upload of %s not whole floats", name);
-    LLM_HIP(hipStreamSynchronize(m.stream));
-    LLM_HIP(hipMemcpy((char*)f + off, raw, nbytes, hipMemcpyHostToDevice));
-  }
+  if (!q && (off % 4 || nbytes % 4))
+    return set_error(LLMHIP_ERR_ARG, "llm: F32 upload of %s not whole floats", name);
+  if (!m.st.cap) LLM_TRY(stager_init(&m.st, m.device, MODEL_STAGE_BYTES, m.stream));
+  if (q)
+    LLM_TRY(qmat_upload(&m.st, *q, src, nbytes, off, row_off));
+  else
+    LLM_TRY(f32_upload(&m.st, f, src, nbytes, off));
   t.received += nbytes;
   return 0;
+}
+
+extern "C" {
+
+int llmhip_model_upload(llmhip_model* h, const char* name, const void* raw, uint64_t nbytes, uint64_t off) {
+  clear_error();
+  Source src;
+  src.mem = (const uint8_t*)raw;
+  return upload_from(*h->m, name, src, nbytes, off);
+}
+
+int llmhip_model_upload_file_tensors(llmhip_model* h, int fd, uint32_t n, const char* const* names,
+                                     const uint64_t* file_offsets) {
+  clear_error();
+  Model& m = *h->m;
+  if (fd < 0) return set_error(LLMHIP_ERR_ARG, "llm: upload from a bad file descriptor");
+  std::vector<StagePiece> ps;
+  std::vector<TensorInfo*> owner;
+  for (uint32_t i = 0; i < n; i++) {
+    auto it = m.tensors.find(names[i]);
+    if (it == m.tensors.end()) return set_error(LLMHIP_ERR_ARG, "llm: tensor %s was not declared", names[i]);
+    TensorInfo& t = it->second;
+    if (!t.used) continue;
+    if (!m.allocated) LLM_TRY(allocate(m));
+    StagePiece p{};
+    QMat* q;
+    LLM_TRY(route(m, names[i], &q, &p.row_off, &p.f));
+    p.q = q;
+    uint64_t per = p.q ? MODEL_STAGE_BYTES / p.q->g.q.block_bytes * p.q->g.q.block_bytes : MODEL_STAGE_BYTES;
+    for (uint64_t a = 0; a < t.size; a += per) {
+      p.off = a;
+      p.bytes = std::min(per, t.size - a);
+      p.file = file_offsets[i] + a;
+      ps.push_back(p);
+      owner.push_back(&t);
+    }
+  }
+  std::vector<size_t> order(ps.size());
+  for (size_t i = 0; i < order.size(); i++) order[i] = i;
+  std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t b) { return ps[a].file < ps[b].file; });
+  std::vector<StagePiece> sorted;
+  for (size_t i : order) sorted.push_back(ps[i]);
+  if (!m.allocated) LLM_TRY(allocate(m));
+  LLM_HIP(hipSetDevice(m.device));
+  if (!m.st.cap) LLM_TRY(stager_init(&m.st, m.device, MODEL_STAGE_BYTES, m.stream));
+  LLM_TRY(stage_file_runs(&m.st, fd, sorted.data(), sorted.size()));
+  for (size_t i = 0; i < ps.size(); i++) owner[i]->received += ps[i].bytes;
+  return 0;
+}
+
+int llmhip_model_upload_file(llmhip_model* h, const char* name, int fd, uint64_t file_offset, uint64_t nbytes,
+                             uint64_t off) {
+  clear_error();
+  if (fd < 0) return set_error(LLMHIP_ERR_ARG, "llm: upload of %s from a bad file descriptor", name);
+  Source src;
+  src.fd = fd;
+  src.file_off = file_offset;
+  return upload_from(*h->m, name, src, nbytes, off);
 }
 
 int llmhip_model_finalize(llmhip_model* h) {
@@ -729,6 +821,7 @@ int llmhip_model_finalize(llmhip_model* h) {
       return set_error(LLMHIP_ERR_FORMAT, "llm: tensor %s: %llu of %llu bytes uploaded", kv.first.c_str(),
                        (unsigned long long)kv.second.received, (unsigned long long)kv.second.size);
   LLM_HIP(hipStreamSynchronize(m.stream));
+  stager_free(&m.st);  // the load is over: release its pinned and device staging
   m.stats.submits++;
   m.finalized = true;
   return 0;

@@ -26,7 +26,7 @@ void clear_error() { g_err.clear(); }
 
 const char* last_error() { return g_err.c_str(); }
 
-int qmat_alloc(QMat* m, int device, uint32_t type, uint64_t rows, uint64_t k) {
+int qmat_place(QMat* m, int device, uint32_t type, uint64_t rows, uint64_t k, uint8_t* mem) {
   QType q;
   if (!qtype_of(type, &q))
     return set_error(LLMHIP_ERR_TYPE, "llm: ggml type %u has no GPU kernel (Q4_0, Q4_1, Q8_0)", type);
@@ -35,18 +35,26 @@ int qmat_alloc(QMat* m, int device, uint32_t type, uint64_t rows, uint64_t k) {
                      (unsigned long long)rows, (unsigned long long)k);
   m->device = device;
   m->g = make_geom(q, rows, k);
+  m->qs = mem;
+  m->owned = false;
+  m->bytes = m->g.dev_bytes();
+  return 0;
+}
+
+int qmat_alloc(QMat* m, int device, uint32_t type, uint64_t rows, uint64_t k) {
+  LLM_TRY(qmat_place(m, device, type, rows, k, nullptr));
   LLM_HIP(hipSetDevice(device));
-  const uint64_t nbytes = m->g.dev_bytes();
-  LLM_HIP(hipMalloc(&m->qs, nbytes));
+  LLM_HIP(hipMalloc(&m->qs, m->bytes));
+  m->owned = true;
   // padding rows of the last tile must read as zero weights
-  LLM_HIP(hipMemset(m->qs, 0, nbytes));
-  m->bytes = nbytes;
+  LLM_HIP(hipMemset(m->qs, 0, m->bytes));
   return 0;
 }
 
 void qmat_release(QMat* m) {
-  if (m->qs) (void)hipFree(m->qs);
+  if (m->qs && m->owned) (void)hipFree(m->qs);
   m->qs = nullptr;
+  m->owned = false;
 }
 
 void gemv_bind(GemvArgs* a, const QMat& m) {
@@ -120,75 +128,6 @@ int gemm_launch(const GemvArgs& a, uint32_t qtype, int epi, hipStream_t s) {
     case LLMHIP_Q8_0: return gemm_launch_qt<LLMHIP_Q8_0>(a, epi, s);
   }
   return set_error(LLMHIP_ERR_TYPE, "llm: ggml type %u has no GPU kernel", qtype);
-}
-
-int stager_init(Stager* st, int device, uint64_t cap, hipStream_t s) {
-  st->device = device;
-  st->cap = cap;
-  st->stream = s;
-  LLM_HIP(hipSetDevice(device));
-  for (int i = 0; i < 2; i++) {
-    LLM_HIP(hipHostMalloc((void**)&st->host[i], cap, hipHostMallocDefault));
-    LLM_HIP(hipMalloc((void**)&st->dev[i], cap));
-    LLM_HIP(hipEventCreateWithFlags(&st->done[i], hipEventDisableTiming));
-    LLM_HIP(hipEventRecord(st->done[i], s));
-  }
-  return 0;
-}
-
-void stager_free(Stager* st) {
-  for (int i = 0; i < 2; i++) {
-    if (st->done[i]) (void)hipEventSynchronize(st->done[i]);
-    if (st->host[i]) (void)hipHostFree(st->host[i]);
-    if (st->dev[i]) (void)hipFree(st->dev[i]);
-    if (st->done[i]) (void)hipEventDestroy(st->done[i]);
-    st->host[i] = st->dev[i] = nullptr;
-    st->done[i] = nullptr;
-  }
-}
-
-static int repack_dev(const QMat& m, const uint8_t* raw_dev, uint64_t n, uint64_t blk0, uint64_t row_off,
-                      hipStream_t s) {
-  switch (m.g.q.type) {
-    case LLMHIP_Q4_0:
-      return repack_launch_qt<LLMHIP_Q4_0>(m, raw_dev, n, blk0, row_off, m.map, m.map_hd, m.map_seg0, m.map_seg1,
-                                           m.ff, s);
-    case LLMHIP_Q4_1:
-      return repack_launch_qt<LLMHIP_Q4_1>(m, raw_dev, n, blk0, row_off, m.map, m.map_hd, m.map_seg0, m.map_seg1,
-                                           m.ff, s);
-    case LLMHIP_Q8_0:
-      return repack_launch_qt<LLMHIP_Q8_0>(m, raw_dev, n, blk0, row_off, m.map, m.map_hd, m.map_seg0, m.map_seg1,
-                                           m.ff, s);
-  }
-  return set_error(LLMHIP_ERR_TYPE, "llm: ggml type %u has no GPU kernel", m.g.q.type);
-}
-
-// The reference repacks each block on the host (gpu.go:363-389) and uploads
-// the result; here the raw blocks cross PCIe once and the repack runs on the
-// device, double-buffered so the host copy of piece i+1 overlaps piece i.
-int qmat_upload(Stager* st, const QMat& m, const void* raw, uint64_t nbytes, uint64_t byte_off, uint64_t row_off) {
-  const uint32_t bb = m.g.q.block_bytes;
-  if (nbytes % bb != 0 || byte_off % bb != 0)
-    return set_error(LLMHIP_ERR_ARG, "llm: upload of %llu bytes at %llu is not whole %u-byte blocks",
-                     (unsigned long long)nbytes, (unsigned long long)byte_off, bb);
-  uint64_t blk0 = byte_off / bb, nblk = nbytes / bb;
-  if (row_off * m.g.nb + blk0 + nblk > m.g.rows * m.g.nb)
-    return set_error(LLMHIP_ERR_ARG, "llm: upload past the end of a [%llu][%llu] matrix",
-                     (unsigned long long)m.g.rows, (unsigned long long)m.g.k);
-  const uint8_t* src = (const uint8_t*)raw;
-  uint64_t per = st->cap / bb;
-  LLM_HIP(hipSetDevice(st->device));
-  for (uint64_t i = 0; i < nblk; i += per) {
-    uint64_t n = nblk - i < per ? nblk - i : per;
-    int c = st->cur;
-    st->cur ^= 1;
-    LLM_HIP(hipEventSynchronize(st->done[c]));
-    memcpy(st->host[c], src + i * bb, n * bb);
-    LLM_HIP(hipMemcpyAsync(st->dev[c], st->host[c], n * bb, hipMemcpyHostToDevice, st->stream));
-    LLM_TRY(repack_dev(m, st->dev[c], n, blk0 + i, row_off, st->stream));
-    LLM_HIP(hipEventRecord(st->done[c], st->stream));
-  }
-  return 0;
 }
 
 int qmat_dequant(const QMat& m, float* out, hipStream_t s) {
