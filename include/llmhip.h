@@ -269,8 +269,8 @@ typedef int (*llm_emit_fn)(int32_t tok, void* user);
 typedef struct llm_gpu llm_gpu;
 
 /* NewGPU (gpu.go:465-764): parse the file at path, ConfigFrom, create the
- * model and stream every tensor in 4 MiB whole-block pieces. lim NULL: the
- * device's limits. */
+ * model and read every tensor straight into pinned staging
+ * (llmhip_model_upload_file_tensors). lim NULL: the device's limits. */
 LLMHIP_API int llm_new_gpu(int ordinal, const llmhip_limits* lim, const char* path, int ctx, llm_gpu** out);
 /* Generate (gpu.go:946-1014). */
 LLMHIP_API int llm_gpu_generate(llm_gpu* g, const int32_t* prompt, int n_prompt, int n, int32_t eos, llm_emit_fn emit,

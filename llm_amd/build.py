@@ -15,6 +15,8 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libllmhip.so")
 ARCH = os.environ.get("LLMHIP_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
+CLI = os.path.join(HERE, "llm-generate")
 
 CFLAGS = ["-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden", f"--offload-arch={ARCH}",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function",
@@ -49,9 +51,23 @@ def build(jobs=None, verbose=True):
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_cli()
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources", file=sys.stderr)
+        print(f"built {LIB} from {len(srcs)} sources and {CLI}", file=sys.stderr)
     return LIB
+
+
+def build_cli():
+    """The llm-generate tool (cli/generate.cpp): host code only, linked against
+    libllmhip.so next to it (rpath $ORIGIN)."""
+    tmp = CLI + ".tmp"
+    r = subprocess.run([CXX, "-O2", "-std=c++17", "-Wall", "-I", os.path.join(os.path.dirname(HERE), "include"),
+                        os.path.join(HERE, "cli", "generate.cpp"), "-L", HERE, "-lllmhip", "-Wl,-rpath,$ORIGIN",
+                        "-o", tmp], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"llm-generate failed to build:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, CLI)
+    return CLI
 
 
 if __name__ == "__main__":
