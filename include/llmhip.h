@@ -99,6 +99,10 @@ LLMHIP_API int llmhip_qmat_dequant(llmhip_qmat* m, float* out_dev, void* hip_str
 /* y_dev[n][rows] (+)= W x_dev[n][k] for n tokens (1 <= n <= 64), in f32:
  * the matvec of cpu.go:143-222 for each token.  accumulate != 0 adds into y. */
 LLMHIP_API int llmhip_qmat_gemv(llmhip_qmat* m, const float* x_dev, float* y_dev, int n, int accumulate, void* hip_stream);
+/* The ExactGGML form (cpu.go:117-140, 166-214): each token's x quantised to
+ * Q8_0 blocks (Q8_1 for Q4_1 weights) as quantizeQ8 does, then ggml's integer
+ * block products scaled by d_w * d_x (+ m_w * s_x); y_dev = the result. */
+LLMHIP_API int llmhip_qmat_gemv_q8(llmhip_qmat* m, const float* x_dev, float* y_dev, int n, void* hip_stream);
 /* Device bytes the matrix holds (equal to its GGUF bytes when rows % 16 == 0). */
 LLMHIP_API uint64_t llmhip_qmat_bytes(const llmhip_qmat* m);
 /* Algorithmic (GGUF-format) bytes of the matrix: rows * k / 32 * block bytes. */
@@ -180,7 +184,8 @@ LLMHIP_API int llmhip_model_prefill(llmhip_model* m, const int32_t* ids, int n, 
  * the GPU.  out receives the cnt sampled ids.  Requires pos + cnt <= ctx. */
 LLMHIP_API int llmhip_model_decode(llmhip_model* m, int cnt, int32_t* out);
 /* The first n 4-byte words of a named buffer as float32 (Peek, gpu.go:1018-1043):
- * x, q, gate (the SwiGLU activations), logits, state, tokens, outb, and
+ * x, q, att (the merged attention output), gate (the SwiGLU activations),
+ * logits, state, tokens, outb, and
  * kvblk.N. (layer N's cache [2][ctx][kvd]). */
 LLMHIP_API int llmhip_model_peek(llmhip_model* m, const char* name, float* out, uint64_t n);
 LLMHIP_API uint64_t llmhip_model_memory_used(const llmhip_model* m);
@@ -191,6 +196,14 @@ LLMHIP_API int llmhip_model_config(const llmhip_model* m, llmhip_config* out, in
  * GPU path keeps f32).  Halves the cache and the attention's reads.  Call
  * before the first llmhip_model_upload / finalize. */
 LLMHIP_API int llmhip_model_set_kv_f16(llmhip_model* m, int on);
+/* The ExactGGML mode of the reference's CPU path (cpu.go:15-21): every matrix
+ * input (the normed residual, the attention output, the SwiGLU activations)
+ * is quantised to Q8_0 blocks (Q8_1 for Q4_1 weights) as quantizeQ8 does
+ * (cpu.go:117-140), each block product is ggml's integer dot product scaled
+ * by d_w * d_x (+ m_w * s_x) (cpu.go:166-214), and the KV cache is binary16.
+ * Results match the CPU path with ExactGGML set, not the f32 path.  Call
+ * before the first upload. */
+LLMHIP_API int llmhip_model_set_exact_ggml(llmhip_model* m, int on);
 /* Run only the first `layers` layers (no head, no sampling; Layers, gpu.go:143-146). 0 = all. */
 LLMHIP_API int llmhip_model_set_layers(llmhip_model* m, int layers);
 /* Leave kernel classes out of every pass, comma-separated (Skip, gpu.go:769-784):
@@ -254,6 +267,8 @@ LLMHIP_API int llm_set_decode_batch(int n);
 LLMHIP_API int llm_set_prefill_batch(int n);
 /* F16KV for the next llm_new_gpu (llmhip_model_set_kv_f16; cpu.go:22-24). */
 LLMHIP_API int llm_set_f16kv(int on);
+/* ExactGGML for the next llm_new_gpu (llmhip_model_set_exact_ggml; cpu.go:15-21). */
+LLMHIP_API int llm_set_exact_ggml(int on);
 
 /* Timing, gpu.go:930-939 (nanoseconds).  record_ns stays 0: the passes are
  * recorded once, as hipGraphs, not per submit. */

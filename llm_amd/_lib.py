@@ -71,6 +71,7 @@ SIGNATURES = [
     ("llmhip_qmat_upload", I, [P, P, U64, U64]),
     ("llmhip_qmat_dequant", I, [P, P, P]),
     ("llmhip_qmat_gemv", I, [P, P, P, I, I, P]),
+    ("llmhip_qmat_gemv_q8", I, [P, P, P, I, P]),
     ("llmhip_qmat_bytes", U64, [P]),
     ("llmhip_qmat_gguf_bytes", U64, [P]),
     ("llmhip_qmat_bench", I, [ctypes.POINTER(P), I, P, P, I, I, I, P, ctypes.POINTER(F)]),
@@ -90,6 +91,7 @@ SIGNATURES = [
     ("llmhip_model_config", I, [P, ctypes.POINTER(Config), ctypes.POINTER(I)]),
     ("llmhip_model_set_layers", I, [P, I]),
     ("llmhip_model_set_kv_f16", I, [P, I]),
+    ("llmhip_model_set_exact_ggml", I, [P, I]),
     ("llmhip_model_set_skip", I, [P, ctypes.c_char_p]),
     ("llmhip_model_bench_kernel", I, [P, ctypes.c_char_p, I, ctypes.POINTER(F), PU64]),
     ("llmhip_model_profile", I, [P, I, P, I, ctypes.POINTER(I)]),
@@ -108,6 +110,7 @@ SIGNATURES = [
     ("llm_set_decode_batch", I, [I]),
     ("llm_set_prefill_batch", I, [I]),
     ("llm_set_f16kv", I, [I]),
+    ("llm_set_exact_ggml", I, [I]),
     ("llm_new_gpu", I, [I, ctypes.POINTER(Limits), ctypes.c_char_p, I, ctypes.POINTER(P)]),
     ("llm_gpu_generate", I, [P, P, I, I, ctypes.c_int32, EMIT, P, ctypes.POINTER(Timing)]),
     ("llm_gpu_prefill_logits", I, [P, P, I, P]),

@@ -18,7 +18,8 @@
 // side of check / trace comes from a reference file (the CPU path is a
 // separate program: any implementation of cpu.go writes the same records)
 // instead of an in-process LoadCPU.  Exit 2 (printing "no GPU") without a
-// GPU; check exits 3 when the logits or tokens fall outside -tol.
+// GPU; check exits 3 when the logits or tokens fall outside -tol.  -f16kv and
+// -exactggml select the CPU path's F16KV and ExactGGML numerics (cpu.go:15-24).
 //
 // Reference file: the 8 bytes "LLMREF01", then records until the end of the
 // file: u32 name length, the name, u32 kind (0 f32, 1 i32), u64 count, count
@@ -57,7 +58,7 @@ double ms_since(std::chrono::steady_clock::time_point t) {
 
 struct Flags {
   int n = 32, ctx = 512, rounds = 5, p = 128, batch = 8, prefillbatch = 64, device = 0;
-  bool f16kv = false;
+  bool f16kv = false, exact = false;
   double tol = 1e-4;
   std::string model = "/models/smollm2-135m-instruct-q4_0.gguf", skip, ids, ref, out, layers = "-1,1,2,5,15,30";
   std::vector<std::string> args;  // positional: token ids
@@ -81,8 +82,8 @@ Flags parse_flags(int argc, char** argv) {
     bool has = false;
     size_t eq = a.find('=');
     if (eq != std::string::npos) v = a.substr(eq + 1), a = a.substr(0, eq), has = true;
-    if (a == "f16kv") {
-      f.f16kv = !has || v == "true" || v == "1";
+    if (a == "f16kv" || a == "exactggml") {
+      (a == "f16kv" ? f.f16kv : f.exact) = !has || v == "true" || v == "1";
       continue;
     }
     if (!has) {
@@ -243,6 +244,7 @@ void open_model(const Flags& f, Model* md) {
   check_rc(llm_set_decode_batch(f.batch));
   check_rc(llm_set_prefill_batch(f.prefillbatch));
   check_rc(llm_set_f16kv(f.f16kv ? 1 : 0));
+  check_rc(llm_set_exact_ggml(f.exact ? 1 : 0));
   t0 = std::chrono::steady_clock::now();
   check_rc(llm_new_gpu(f.device, &lim, f.model.c_str(), f.ctx, &md->g));
   md->m = llm_gpu_model(md->g);

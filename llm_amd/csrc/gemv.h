@@ -29,6 +29,8 @@ struct QMat {
 enum Prologue : int {
   PRO_PLAIN = 0,  // x[t*ldx + e]
   PRO_RMS = 1,    // RMSNorm(x[t]) * nw  (cpu.go:81-98), recomputed per workgroup
+  PRO_Q8 = 2,     // flag: the input then quantised to Q8_0 / Q8_1 blocks and the products formed
+                  // as ggml's CPU backend forms them (the ExactGGML mode, cpu.go:117-140, 166-214)
 };
 
 enum Epilogue : int {
@@ -75,16 +77,18 @@ struct GemvArgs {
   // prefill (gemm_kernel): activations prepared once per launch by prep_kernel
   void* xp;        // [tg][nb][64 lanes] 16-byte MFMA operands (hi/lo f16 of 8 tokens)
   int32_t* xexp;   // [tg*8] power-of-two scale per token
-  float* xbsum;    // [tg*8][nb] scaled block sums (Q4_1)
+  float* xbsum;    // [tg*8][nb] scaled block sums (Q4_1); PRO_Q8: the Q8_1 sums s
+  float* xdx;      // [tg*8][nb] PRO_Q8: the activation block scales d (binary16 values)
   uint32_t tg;     // token groups of 8
+  uint32_t q8;     // the prepared activations are Q8 blocks (PRO_Q8): gemm_kernel's block products
 };
 
 // Bytes of the prepared-activation buffers for ntok tokens of k inputs.
 inline uint64_t xprep_bytes(uint32_t ntok, uint32_t k) {
   uint64_t tg = (ntok + 7) / 8, nb = k / 32;
-  return tg * nb * 64 * 16 + tg * 8 * 4 + tg * 8 * nb * 4 + 3 * 256;
+  return tg * nb * 64 * 16 + tg * 8 * 4 + 2 * tg * 8 * nb * 4 + 4 * 256;
 }
-// Point a.xp / a.xexp / a.xbsum into one buffer of xprep_bytes.
+// Point a.xp / a.xexp / a.xbsum / a.xdx into one buffer of xprep_bytes.
 inline void xprep_bind(GemvArgs* a, void* buf) {
   uint64_t tg = (a->ntok + 7) / 8, nb = a->nb;
   char* p = (char*)buf;
@@ -93,6 +97,8 @@ inline void xprep_bind(GemvArgs* a, void* buf) {
   a->xexp = (int32_t*)p;
   p += (tg * 8 * 4 + 255) & ~255ull;
   a->xbsum = (float*)p;
+  p += (tg * 8 * nb * 4 + 255) & ~255ull;
+  a->xdx = (float*)p;
   a->tg = (uint32_t)tg;
 }
 // Tokens at or above which the prefill kernel pair (prep + gemm) runs.

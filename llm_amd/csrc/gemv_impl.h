@@ -275,10 +275,11 @@ constexpr int MAXI = 2;  // 8-element activation items staged per thread and tok
 
 // LDS layout of one launch (bytes).
 struct Lds {
-  uint32_t xs, misc, bsum, part, total;
+  uint32_t xs, misc, bsum, dx, part, total;
 };
 
-__host__ __device__ inline Lds lds_layout(int NT, uint32_t qtype, uint32_t nb, uint32_t waves) {
+// q8: room for the activation block scales of PRO_Q8.
+__host__ __device__ inline Lds lds_layout(int NT, uint32_t qtype, uint32_t nb, uint32_t waves, bool q8 = false) {
   Lds L;
   uint32_t o = 0;
   L.xs = o;
@@ -287,6 +288,8 @@ __host__ __device__ inline Lds lds_layout(int NT, uint32_t qtype, uint32_t nb, u
   o += 128 * 4;
   L.bsum = o;
   if (qtype == LLMHIP_Q4_1) o += nb * NT * 4;
+  L.dx = o;
+  if (q8) o += nb * NT * 4;
   L.part = o;
   o += waves * 64 * 2 * 4;
   L.total = o;
@@ -299,11 +302,21 @@ __device__ __forceinline__ bool amax_better(float v, uint32_t i, float bv, uint3
   return i != 0xffffffffu && (bi == 0xffffffffu || v > bv || (v == bv && i < bi));
 }
 
+// RoundF16 (f16.go): the binary16 nearest the f32 value v, ties to even,
+// subnormals kept (v_cvt_f16_f32).  The empty asm makes v opaque, so the
+// multiply or add that produced it cannot be fused with the conversion into
+// one mixed-precision instruction (v_fma_mix*_f16), which would round the
+// exact result to binary16 once instead of rounding the f32 value -- a
+// different binary16 wherever the f32 value is a tie.
+__device__ __forceinline__ _Float16 to_f16(float v) {
+  asm volatile("" : "+v"(v));
+  return (_Float16)v;
+}
+
 // One element into the KV cache: f32, or rounded to binary16 (RoundF16 of
-// the F16KV mode, cpu.go:298-299; the hardware conversion rounds to nearest
-// even, subnormals kept, like F32ToF16 in f16.go).
+// the F16KV mode, cpu.go:298-299).
 __device__ __forceinline__ void kv_store(const GemvArgs& a, uint64_t i, float v) {
-  if (a.kv16) ((_Float16*)a.kv)[i] = (_Float16)v;
+  if (a.kv16) ((_Float16*)a.kv)[i] = to_f16(v);
   else a.kv[i] = v;
 }
 
@@ -399,9 +412,14 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
 // operand order.  Per-wave partials go through LDS; every thread then
 // finishes each reduction itself (the same sums in the same order).  Ends
 // with a barrier after which xs (and bsum, Q4_1) are complete.
+//
+// PRO_Q8 (ExactGGML): after the RMSNorm each block of 32 is quantised as
+// quantizeQ8 does (cpu.go:117-140): d = amax / 127, q = round half away from
+// zero of x * (1/d), in f32; hi = q (exact in f16), lo = 0, no scale (ex = 0);
+// dxs[t][b] = RoundF16(d) and, for Q4_1, bsum[t][b] = RoundF16(d * sum q).
 template <uint32_t QT, int NT, int PRO>
 __device__ __forceinline__ void stage_x(const GemvArgs& a, uint32_t t0, int nt, h8* xs, float* misc, float* bsum,
-                                        int ex[NT]) {
+                                        float* dxs, int ex[NT]) {
   constexpr int S = 2 * NT;
   const uint32_t bd = blockDim.x, nwv = bd >> 6;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -421,7 +439,7 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, uint32_t t0, int nt, 
       va[t][k] = A;
       vc[t][k] = C;
     }
-  if (PRO == PRO_RMS) {
+  if (PRO & PRO_RMS) {
     // ss = sum x^2 (f32); s = f32(1/sqrt(f64(ss/n + eps))); h = x*s*w
     f4 wa[MAXI], wc[MAXI];
 #pragma unroll
@@ -456,6 +474,45 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, uint32_t t0, int nt, 
           vc[t][k][i] = __fmul_rn(__fmul_rn(vc[t][k][i], s), wc[k][i]);
         }
     }
+  }
+  if (PRO & PRO_Q8) {
+    // a block's four items sit in four consecutive lanes: its max and its
+    // sum of q are two xor-shuffles
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      ex[t] = 0;
+#pragma unroll
+      for (int k = 0; k < MAXI; k++) {
+        const uint32_t it = tid + k * bd;
+        const f4 A = va[t][k], C = vc[t][k];
+        float am = 0;
+        for (int i = 0; i < 4; i++) am = fmaxf(am, fmaxf(fabsf(A[i]), fabsf(C[i])));
+        am = fmaxf(am, __shfl_xor(am, 1));
+        am = fmaxf(am, __shfl_xor(am, 2));
+        const float d = __fdiv_rn(am, 127.f);
+        const float id = d != 0.f ? __fdiv_rn(1.f, d) : 0.f;
+        const float v[8] = {A[0], A[2], C[0], C[2], A[1], A[3], C[1], C[3]};
+        h8 hi;
+        int qs = 0;
+        for (int i = 0; i < 8; i++) {
+          const float qv = roundf(__fmul_rn(v[i], id));
+          hi[i] = (_Float16)qv;
+          qs += (int)qv;
+        }
+        qs += __shfl_xor(qs, 1);
+        qs += __shfl_xor(qs, 2);
+        if (it < NI) {
+          xs[it * S + 2 * t] = hi;
+          xs[it * S + 2 * t + 1] = h8{};
+          if ((it & 3) == 0) {
+            dxs[t * nb + it / 4] = (float)to_f16(d);
+            if (QT == LLMHIP_Q4_1) bsum[t * nb + it / 4] = (float)to_f16(__fmul_rn(d, (float)qs));
+          }
+        }
+      }
+    }
+    __syncthreads();
+    return;
   }
   float* mpart = misc + 64;
 #pragma unroll
@@ -568,10 +625,14 @@ __device__ __forceinline__ void load_unit(WUnit& u, const uint8_t* wq, uint32_t 
 }
 
 // One block through the MFMA: D[token slot][row] = x_slot . w_row over its 32
-// elements, then acc += d * (hi + lo) (and m * sum x for Q4_1).
-template <uint32_t QT, int NT>
-__device__ __forceinline__ void mfma_block(const h8* xs, const float* bsum, uint32_t nb, int q, int slot, uint32_t b,
-                                           h8 B, uint32_t dbits, uint32_t mbits, float& acc0, float& acc1) {
+// elements, then acc += d * (hi + lo) (and m * sum x for Q4_1).  Q8: the
+// activations are Q8 blocks (hi = q, lo = 0), D is ggml's integer block sum,
+// exact in f32 (at most 32 * 128 * 127 in magnitude), and the block adds
+// d_w * d_x * f32(sum) (+ m_w * s_x), rounded as cpu.go:174-210 rounds it.
+template <uint32_t QT, int NT, bool Q8>
+__device__ __forceinline__ void mfma_block(const h8* xs, const float* bsum, const float* dxs, uint32_t nb, int q,
+                                           int slot, uint32_t b, h8 B, uint32_t dbits, uint32_t mbits, float& acc0,
+                                           float& acc1) {
   // Branch-free (a clamped read, then a select) so that the blocks of a unit
   // form one basic block and their LDS reads and MFMAs overlap.
   constexpr int S = 2 * NT;
@@ -580,6 +641,19 @@ __device__ __forceinline__ void mfma_block(const h8* xs, const float* bsum, uint
   const h8 A = __builtin_bit_cast(h8, X & (slot < S ? ~0u : 0u));
   f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4{0, 0, 0, 0}, 0, 0, 0);
   float d = f16_hw(dbits);
+  if (Q8) {
+    const int tA = min(2 * q, NT - 1), tB = min(2 * q + 1, NT - 1);
+    float pA = __fmul_rn(__fmul_rn(d, dxs[tA * nb + b]), D[0] + D[1]);
+    float pB = __fmul_rn(__fmul_rn(d, dxs[tB * nb + b]), D[2] + D[3]);
+    if (QT == LLMHIP_Q4_1) {
+      const float m = f16_hw(mbits);
+      pA = __fadd_rn(pA, __fmul_rn(m, bsum[tA * nb + b]));
+      pB = __fadd_rn(pB, __fmul_rn(m, bsum[tB * nb + b]));
+    }
+    acc0 += 2 * q < NT ? pA : 0.f;
+    if (NT > 1) acc1 += 2 * q + 1 < NT ? pB : 0.f;
+    return;
+  }
   acc0 += d * (D[0] + D[1]);
   if (NT > 1) acc1 += d * (D[2] + D[3]);
   if (QT == LLMHIP_Q4_1) {
@@ -591,26 +665,31 @@ __device__ __forceinline__ void mfma_block(const h8* xs, const float* bsum, uint
 }
 
 // The blocks of unit g of a tile (see WUnit).
-template <uint32_t QT, int NT>
+template <uint32_t QT, int NT, bool Q8 = false>
 __device__ __forceinline__ void unit_mfma(const WUnit& u, uint32_t g, uint32_t ng, uint32_t tail, const h8* xs,
-                                          const float* bsum, uint32_t nb, int q, int slot, float& acc0, float& acc1) {
+                                          const float* bsum, const float* dxs, uint32_t nb, int q, int slot,
+                                          float& acc0, float& acc1) {
   if (g < ng) {
     const uint32_t b0 = 4 * g;
     if (QT == LLMHIP_Q8_0) {
-      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 0, dq8(u.w0.x, u.w0.y), u.sv.x & 0xffff, 0, acc0, acc1);
-      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 1, dq8(u.w0.z, u.w0.w), u.sv.x >> 16, 0, acc0, acc1);
-      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 2, dq8(u.w1.x, u.w1.y), u.sv.y & 0xffff, 0, acc0, acc1);
-      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 3, dq8(u.w1.z, u.w1.w), u.sv.y >> 16, 0, acc0, acc1);
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 0, dq8(u.w0.x, u.w0.y), u.sv.x & 0xffff, 0, acc0, acc1);
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 1, dq8(u.w0.z, u.w0.w), u.sv.x >> 16, 0, acc0, acc1);
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 2, dq8(u.w1.x, u.w1.y), u.sv.y & 0xffff, 0, acc0, acc1);
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 3, dq8(u.w1.z, u.w1.w), u.sv.y >> 16, 0, acc0, acc1);
     } else if (QT == LLMHIP_Q4_1) {
-      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 0, dq4<true>(u.w0.x), u.sv.x & 0xffff, u.sv.x >> 16, acc0, acc1);
-      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 1, dq4<true>(u.w0.y), u.sv.y & 0xffff, u.sv.y >> 16, acc0, acc1);
-      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 2, dq4<true>(u.w0.z), u.sv.z & 0xffff, u.sv.z >> 16, acc0, acc1);
-      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 3, dq4<true>(u.w0.w), u.sv.w & 0xffff, u.sv.w >> 16, acc0, acc1);
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 0, dq4<true>(u.w0.x), u.sv.x & 0xffff, u.sv.x >> 16,
+                             acc0, acc1);
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 1, dq4<true>(u.w0.y), u.sv.y & 0xffff, u.sv.y >> 16,
+                             acc0, acc1);
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 2, dq4<true>(u.w0.z), u.sv.z & 0xffff, u.sv.z >> 16,
+                             acc0, acc1);
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 3, dq4<true>(u.w0.w), u.sv.w & 0xffff, u.sv.w >> 16,
+                             acc0, acc1);
     } else {
-      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 0, dq4<false>(u.w0.x), u.sv.x & 0xffff, 0, acc0, acc1);
-      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 1, dq4<false>(u.w0.y), u.sv.x >> 16, 0, acc0, acc1);
-      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 2, dq4<false>(u.w0.z), u.sv.y & 0xffff, 0, acc0, acc1);
-      mfma_block<QT, NT>(xs, bsum, nb, q, slot, b0 + 3, dq4<false>(u.w0.w), u.sv.y >> 16, 0, acc0, acc1);
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 0, dq4<false>(u.w0.x), u.sv.x & 0xffff, 0, acc0, acc1);
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 1, dq4<false>(u.w0.y), u.sv.x >> 16, 0, acc0, acc1);
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 2, dq4<false>(u.w0.z), u.sv.y & 0xffff, 0, acc0, acc1);
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 3, dq4<false>(u.w0.w), u.sv.y >> 16, 0, acc0, acc1);
     }
     return;
   }
@@ -619,9 +698,11 @@ __device__ __forceinline__ void unit_mfma(const WUnit& u, uint32_t g, uint32_t n
   for (uint32_t j = 0; j < 3; j++) {
     if (j >= tail) continue;
     const uint32_t b = 4 * ng + j;
-    if (QT == LLMHIP_Q8_0) mfma_block<QT, NT>(xs, bsum, nb, q, slot, b, dq8(q0[j], q1[j]), s[j] & 0xffff, 0, acc0, acc1);
-    else mfma_block<QT, NT>(xs, bsum, nb, q, slot, b, dq4<QT == LLMHIP_Q4_1>(q0[j]), s[j] & 0xffff, s[j] >> 16, acc0,
-                            acc1);
+    if (QT == LLMHIP_Q8_0)
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b, dq8(q0[j], q1[j]), s[j] & 0xffff, 0, acc0, acc1);
+    else
+      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b, dq4<QT == LLMHIP_Q4_1>(q0[j]), s[j] & 0xffff, s[j] >> 16,
+                             acc0, acc1);
   }
 }
 
@@ -672,10 +753,12 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   const uint32_t t0 = blockIdx.y * NT;
   const int nt = min((int)NT, (int)(a.ntok - t0));
   const uint32_t nb = a.nb;
-  const Lds L = lds_layout(NT, QT, nb, nwv);
+  constexpr bool Q8 = (PRO & PRO_Q8) != 0;
+  const Lds L = lds_layout(NT, QT, nb, nwv, Q8);
   h8* xs = (h8*)(lds + L.xs);
   float* misc = (float*)(lds + L.misc);  // [0,64) sum-of-squares partials, [64,128) max partials, then argmax
   float* bsum = (float*)(lds + L.bsum);
+  float* dxs = (float*)(lds + L.dx);
 
   constexpr bool HOIST = NT <= 2;
   const uint32_t split = a.split, tpw = nwv / split;
@@ -699,18 +782,19 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   }
 
   int ex[NT];
-  stage_x<QT, NT, PRO>(a, t0, nt, xs, misc, bsum, ex);
+  stage_x<QT, NT, PRO>(a, t0, nt, xs, misc, bsum, dxs, ex);
 
   float acc0 = 0, acc1 = 0;
   for (uint32_t i0 = 0; i0 < cnt; i0 += 4) {
     if (i0 > 0 || !HOIST) load_batch(i0);
 #pragma unroll
     for (int u = 0; u < 4; u++)
-      if (i0 + u < cnt) unit_mfma<QT, NT>(w[u], sp + (i0 + u) * split, a.ng, a.tail, xs, bsum, nb, q, slot, acc0, acc1);
+      if (i0 + u < cnt)
+        unit_mfma<QT, NT, Q8>(w[u], sp + (i0 + u) * split, a.ng, a.tail, xs, bsum, dxs, nb, q, slot, acc0, acc1);
   }
   if (has_tail) {
     if (!HOIST) load_unit<QT>(wt, a.qs, nb, tile, a.ng, a.ng, a.tail, lane, r);
-    unit_mfma<QT, NT>(wt, a.ng, a.ng, a.tail, xs, bsum, nb, q, slot, acc0, acc1);
+    unit_mfma<QT, NT, Q8>(wt, a.ng, a.ng, a.tail, xs, bsum, dxs, nb, q, slot, acc0, acc1);
   }
   // ---- split-K: partial sums of the waves of a tile, added in a fixed order
   if (split > 1) {
@@ -760,10 +844,12 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
   const uint32_t nwv = blockDim.x >> 6;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const uint32_t nb = a.nb, ng = a.ng, tail = a.tail;
-  const Lds L = lds_layout(1, QT, nb, nwv);
+  constexpr bool Q8 = (PRO & PRO_Q8) != 0;
+  const Lds L = lds_layout(1, QT, nb, nwv, Q8);
   h8* xs = (h8*)(lds + L.xs);
   float* misc = (float*)(lds + L.misc);
   float* bsum = (float*)(lds + L.bsum);
+  float* dxs = (float*)(lds + L.dx);
   const int r = lane & 15, q = lane >> 4, slot = lane & 15;
   const uint32_t W = gridDim.x * nwv, gw = blockIdx.x * nwv + wave;
   const uint32_t upt = ng + (tail ? 1 : 0);
@@ -779,7 +865,7 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
     if ((uint32_t)d < U) fetch(d, w[d]);
 
   int ex[1];
-  stage_x<QT, 1, PRO>(a, 0, 1, xs, misc, bsum, ex);
+  stage_x<QT, 1, PRO>(a, 0, 1, xs, misc, bsum, dxs, ex);
 
   float acc0 = 0, acc1 = 0, bv = -INFINITY;
   uint32_t bi = 0xffffffffu;
@@ -789,7 +875,7 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
       const uint32_t i = i0 + d;
       if (i >= U) break;
       const uint32_t g = i % upt;
-      unit_mfma<QT, 1>(w[d], g, ng, tail, xs, bsum, nb, q, slot, acc0, acc1);
+      unit_mfma<QT, 1, Q8>(w[d], g, ng, tail, xs, bsum, dxs, nb, q, slot, acc0, acc1);
       if (i + R < U) fetch(i + R, w[d]);
       if (g == upt - 1) {  // the tile is complete
         const uint32_t tile = gw + (i / upt) * W;
@@ -831,7 +917,7 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
       xp[((uint64_t)tg * nb + it / 4) * 64 + (it % 4) * 16 + s2] = h8{};
       xp[((uint64_t)tg * nb + it / 4) * 64 + (it % 4) * 16 + s2 + 1] = h8{};
     }
-    for (uint32_t b = tid; b < nb; b += 256) a.xbsum[(uint64_t)t * nb + b] = 0.f;
+    for (uint32_t b = tid; b < nb; b += 256) a.xbsum[(uint64_t)t * nb + b] = a.xdx[(uint64_t)t * nb + b] = 0.f;
     if (tid == 0) a.xexp[t] = 0;
     return;
   }
@@ -850,7 +936,7 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
       vc[k] = C;
     }
   }
-  if (PRO == PRO_RMS) {
+  if (PRO & PRO_RMS) {
     // cpu.go:90-96
     float ss = 0;
 #pragma unroll
@@ -874,6 +960,39 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
       }
     }
     __syncthreads();
+  }
+  if (PRO & PRO_Q8) {  // quantizeQ8 per block, as in stage_x
+    if (tid == 0) a.xexp[t] = 0;
+#pragma unroll
+    for (int k = 0; k < PMAXI; k++) {
+      const uint32_t it = tid + k * 256;
+      const f4 A = va[k], C = vc[k];
+      float am = 0;
+      for (int i = 0; i < 4; i++) am = fmaxf(am, fmaxf(fabsf(A[i]), fabsf(C[i])));
+      am = fmaxf(am, __shfl_xor(am, 1));
+      am = fmaxf(am, __shfl_xor(am, 2));
+      const float d = __fdiv_rn(am, 127.f);
+      const float id = d != 0.f ? __fdiv_rn(1.f, d) : 0.f;
+      const float v[8] = {A[0], A[2], C[0], C[2], A[1], A[3], C[1], C[3]};
+      h8 hi;
+      int qs = 0;
+      for (int i = 0; i < 8; i++) {
+        const float qv = roundf(__fmul_rn(v[i], id));
+        hi[i] = (_Float16)qv;
+        qs += (int)qv;
+      }
+      qs += __shfl_xor(qs, 1);
+      qs += __shfl_xor(qs, 2);
+      if (it >= NI) continue;
+      h8* dst = xp + ((uint64_t)tg * nb + it / 4) * 64 + (it % 4) * 16 + s2;
+      dst[0] = hi;
+      dst[1] = h8{};
+      if ((it & 3) == 0) {
+        a.xdx[(uint64_t)t * nb + it / 4] = (float)to_f16(d);
+        a.xbsum[(uint64_t)t * nb + it / 4] = (float)to_f16(__fmul_rn(d, (float)qs));
+      }
+    }
+    return;
   }
   float m = 0;
 #pragma unroll
@@ -925,7 +1044,7 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
 // come from prep_kernel's buffer (shared by all workgroups through L2).
 constexpr int GT = 2;  // tiles per workgroup
 
-template <uint32_t QT, int EPI>
+template <uint32_t QT, int EPI, bool Q8>
 __global__ __launch_bounds__(256) void gemm_kernel(GemvArgs a) {
   typedef QT_<QT> T;
   __shared__ float red[3][64][GT * 8 * 2];
@@ -957,6 +1076,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvArgs a) {
 #pragma unroll
       for (int u = 0; u < GT; u++) {
         f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[u], f4{0, 0, 0, 0}, 0, 0, 0);
+        if (Q8) {  // ggml's block product, as in mfma_block
+          const uint64_t iA = (uint64_t)((g0 + g) * 8 + 2 * q) * nb + b, iB = iA + nb;
+          float pA = __fmul_rn(__fmul_rn(d[u], a.xdx[iA]), D[0] + D[1]);
+          float pB = __fmul_rn(__fmul_rn(d[u], a.xdx[iB]), D[2] + D[3]);
+          if (QT == LLMHIP_Q4_1) {
+            pA = __fadd_rn(pA, __fmul_rn(mm[u], a.xbsum[iA]));
+            pB = __fadd_rn(pB, __fmul_rn(mm[u], a.xbsum[iB]));
+          }
+          acc[u][g][0] += pA;
+          acc[u][g][1] += pB;
+          continue;
+        }
         acc[u][g][0] += d[u] * (D[0] + D[1]);
         acc[u][g][1] += d[u] * (D[2] + D[3]);
         if (QT == LLMHIP_Q4_1) {
@@ -1071,23 +1202,30 @@ static int launch_one(const GemvArgs& a, dim3 grid, uint32_t lds, hipStream_t s)
   return 0;
 }
 
+template <uint32_t QT, int NT, int Q>
+static int launch_nt_q(const GemvArgs& a, int pro, int epi, dim3 grid, uint32_t lds, hipStream_t s) {
+  constexpr int PP = PRO_PLAIN | Q, PR = PRO_RMS | Q;
+  switch ((pro & PRO_RMS) * 8 + epi) {
+    case PRO_PLAIN * 8 + EPI_STORE: return launch_one<QT, NT, PP, EPI_STORE>(a, grid, lds, s);
+    case PRO_PLAIN * 8 + EPI_ACC: return launch_one<QT, NT, PP, EPI_ACC>(a, grid, lds, s);
+    case PRO_RMS * 8 + EPI_QKV: return launch_one<QT, NT, PR, EPI_QKV>(a, grid, lds, s);
+    case PRO_RMS * 8 + EPI_GATEUP: return launch_one<QT, NT, PR, EPI_GATEUP>(a, grid, lds, s);
+    case PRO_RMS * 8 + EPI_STORE: return launch_one<QT, NT, PR, EPI_STORE>(a, grid, lds, s);
+    case PRO_RMS * 8 + EPI_SWIGLU: return launch_one<QT, NT, PR, EPI_SWIGLU>(a, grid, lds, s);
+  }
+  if ((pro & PRO_RMS) && epi == EPI_ARGMAX && NT == 1) return launch_one<QT, 1, PR, EPI_ARGMAX>(a, grid, lds, s);
+  return set_error(LLMHIP_ERR_ARG, "llm: gemv: unsupported prologue/epilogue %d/%d", pro, epi);
+}
+
 template <uint32_t QT, int NT>
 static int launch_nt(const GemvArgs& a, int pro, int epi, dim3 grid, uint32_t lds, hipStream_t s) {
-  switch (pro * 8 + epi) {
-    case PRO_PLAIN * 8 + EPI_STORE: return launch_one<QT, NT, PRO_PLAIN, EPI_STORE>(a, grid, lds, s);
-    case PRO_PLAIN * 8 + EPI_ACC: return launch_one<QT, NT, PRO_PLAIN, EPI_ACC>(a, grid, lds, s);
-    case PRO_RMS * 8 + EPI_QKV: return launch_one<QT, NT, PRO_RMS, EPI_QKV>(a, grid, lds, s);
-    case PRO_RMS * 8 + EPI_GATEUP: return launch_one<QT, NT, PRO_RMS, EPI_GATEUP>(a, grid, lds, s);
-    case PRO_RMS * 8 + EPI_STORE: return launch_one<QT, NT, PRO_RMS, EPI_STORE>(a, grid, lds, s);
-    case PRO_RMS * 8 + EPI_SWIGLU: return launch_one<QT, NT, PRO_RMS, EPI_SWIGLU>(a, grid, lds, s);
-  }
-  if (pro == PRO_RMS && epi == EPI_ARGMAX && NT == 1) return launch_one<QT, 1, PRO_RMS, EPI_ARGMAX>(a, grid, lds, s);
-  return set_error(LLMHIP_ERR_ARG, "llm: gemv: unsupported prologue/epilogue %d/%d", pro, epi);
+  if (pro & PRO_Q8) return launch_nt_q<QT, NT, PRO_Q8>(a, pro, epi, grid, lds, s);
+  return launch_nt_q<QT, NT, 0>(a, pro, epi, grid, lds, s);
 }
 
 template <uint32_t QT, int PRO, int EPI>
 static int launch_stream(const GemvArgs& a, hipStream_t s) {
-  const Lds L = lds_layout(1, QT, a.nb, a.swaves);
+  const Lds L = lds_layout(1, QT, a.nb, a.swaves, (PRO & PRO_Q8) != 0);
   hipLaunchKernelGGL((gemv_stream_kernel<QT, PRO, EPI>), dim3(a.stream), dim3(64 * a.swaves), L.total, s, a);
   LLM_HIP(hipGetLastError());
   return 0;
@@ -1101,11 +1239,13 @@ int gemv_launch_qt(const GemvArgs& a, int pro, int epi, hipStream_t s) {
       case PRO_PLAIN * 8 + EPI_ACC: return launch_stream<QT, PRO_PLAIN, EPI_ACC>(a, s);
       case PRO_RMS * 8 + EPI_STORE: return launch_stream<QT, PRO_RMS, EPI_STORE>(a, s);
       case PRO_RMS * 8 + EPI_ARGMAX: return launch_stream<QT, PRO_RMS, EPI_ARGMAX>(a, s);
+      case (PRO_RMS | PRO_Q8) * 8 + EPI_ARGMAX: return launch_stream<QT, PRO_RMS | PRO_Q8, EPI_ARGMAX>(a, s);
+      case (PRO_PLAIN | PRO_Q8) * 8 + EPI_STORE: return launch_stream<QT, PRO_PLAIN | PRO_Q8, EPI_STORE>(a, s);
     }
     return set_error(LLMHIP_ERR_ARG, "llm: gemv: no streaming form of prologue/epilogue %d/%d", pro, epi);
   }
   int nt = a.ntok <= 1 ? 1 : a.ntok <= 2 ? 2 : 4;
-  Lds L = lds_layout(nt, QT, a.nb, a.waves);
+  Lds L = lds_layout(nt, QT, a.nb, a.waves, (pro & PRO_Q8) != 0);
   if (L.total > 160 * 1024)
     return set_error(LLMHIP_ERR_ARG, "llm: gemv: k=%u needs %u bytes of LDS", a.k, L.total);
   if (epi == EPI_ARGMAX && a.ntok != 1) return set_error(LLMHIP_ERR_ARG, "llm: gemv: argmax epilogue needs one token");
@@ -1153,12 +1293,16 @@ int gemm_launch_qt(const GemvArgs& a, int epi, hipStream_t s) {
   uint32_t wgs = (a.tiles + GT - 1) / GT, ts = 1;
   while (ts < a.tg && wgs * ts * 4 < 2048) ts *= 2;
   dim3 grid(wgs, std::min(ts, a.tg));
-  switch (epi) {
-    case EPI_STORE: hipLaunchKernelGGL((gemm_kernel<QT, EPI_STORE>), grid, dim3(256), 0, s, a); break;
-    case EPI_ACC: hipLaunchKernelGGL((gemm_kernel<QT, EPI_ACC>), grid, dim3(256), 0, s, a); break;
-    case EPI_QKV: hipLaunchKernelGGL((gemm_kernel<QT, EPI_QKV>), grid, dim3(256), 0, s, a); break;
-    case EPI_GATEUP: hipLaunchKernelGGL((gemm_kernel<QT, EPI_GATEUP>), grid, dim3(256), 0, s, a); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((gemm_kernel<QT, EPI_SWIGLU>), grid, dim3(256), 0, s, a); break;
+  switch (epi * 2 + (a.q8 ? 1 : 0)) {
+#define LLMHIP_GEMM_CASE(E)                                                                                \
+  case E * 2: hipLaunchKernelGGL((gemm_kernel<QT, E, false>), grid, dim3(256), 0, s, a); break; \
+  case E * 2 + 1: hipLaunchKernelGGL((gemm_kernel<QT, E, true>), grid, dim3(256), 0, s, a); break;
+    LLMHIP_GEMM_CASE(EPI_STORE)
+    LLMHIP_GEMM_CASE(EPI_ACC)
+    LLMHIP_GEMM_CASE(EPI_QKV)
+    LLMHIP_GEMM_CASE(EPI_GATEUP)
+    LLMHIP_GEMM_CASE(EPI_SWIGLU)
+#undef LLMHIP_GEMM_CASE
     default: return set_error(LLMHIP_ERR_ARG, "llm: gemm: unsupported epilogue %d", epi);
   }
   LLM_HIP(hipGetLastError());

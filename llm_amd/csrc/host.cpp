@@ -369,7 +369,7 @@ int config_from(const gguf::File& f, llmhip_config* c) {
 using namespace llm;
 
 // Tunables of the Go package (gpu.go:20-23,165,1046-1054).
-static int g_decode_batch = 8, g_prefill_batch = 64, g_f16kv = 0;
+static int g_decode_batch = 8, g_prefill_batch = 64, g_f16kv = 0, g_exact = 0;
 static const int kMaxBatch = 16;
 
 struct llm_gguf {
@@ -509,6 +509,11 @@ int llm_set_f16kv(int on) {
   return 0;
 }
 
+int llm_set_exact_ggml(int on) {
+  g_exact = on != 0;
+  return 0;
+}
+
 int llm_set_prefill_batch(int n) {
   g_prefill_batch = n;
   return 0;
@@ -529,7 +534,8 @@ int llm_new_gpu(int ordinal, const llmhip_limits* lim, const char* path, int ctx
     rc = config_from(gf->f, &g->cfg);
   }
   if (rc == 0) rc = llmhip_model_create(ordinal, lim, &g->cfg, ctx, g_prefill_batch, &g->m);
-  if (rc == 0) rc = llmhip_model_set_kv_f16(g->m, g_f16kv);
+  if (rc == 0) rc = llmhip_model_set_exact_ggml(g->m, g_exact);
+  if (rc == 0 && !g_exact) rc = llmhip_model_set_kv_f16(g->m, g_f16kv);
   if (rc == 0) llmhip_model_config(g->m, &g->cfg, &g->ctx);
   for (size_t i = 0; rc == 0 && i < gf->f.tensors.size(); i++) {
     const gguf::Tensor& t = gf->f.tensors[i];

@@ -69,6 +69,7 @@ struct Model {
   std::map<std::string, TensorInfo> tensors;
   bool allocated = false, finalized = false;
   bool kv16 = false;  // binary16 KV cache (the F16KV mode of cpu.go:22-24)
+  bool q8 = false;    // ExactGGML (cpu.go:15-21): every matrix input quantised to Q8 blocks, binary16 cache
   hipGraphExec_t decode_exec = nullptr;
   std::map<uint64_t, hipGraphExec_t> chunk_exec;  // key: graph_key(ntok, attn_rows, attn_split, head)
   std::map<uint64_t, uint32_t> graph_nodes;       // dispatches per graph key
@@ -357,6 +358,7 @@ static bool skipped(const Model& m, const char* cls) { return m.skip.count("all"
 
 static int gemv_rec(Model& m, const char* cls, const GemvArgs& a, uint32_t qtype, int pro, int epi, uint64_t bytes) {
   if (skipped(m, cls)) return 0;
+  if (m.q8) pro |= PRO_Q8;
   return launch_rec(m, cls, bytes, [&]() { return gemv_launch(a, qtype, pro, epi, m.stream); });
 }
 
@@ -368,6 +370,10 @@ static int mat_rec(Model& m, const char* cls, const char* pcls, GemvArgs a, uint
                    uint64_t bytes, bool prep = true) {
   if (a.ntok < GEMM_MIN_TOKENS) return gemv_rec(m, cls, a, qtype, pro, epi, bytes);
   xprep_bind(&a, m.xprep);
+  if (m.q8) {
+    pro |= PRO_Q8;
+    a.q8 = 1;
+  }
   if (prep && !skipped(m, cls))
     LLM_TRY(launch_rec(m, pcls, 0, [&]() { return prep_launch(a, pro, m.stream); }));
   if (skipped(m, cls)) return 0;
@@ -890,6 +896,7 @@ int llmhip_model_peek(llmhip_model* h, const char* name, float* out, uint64_t n)
   const uint64_t E = m.cfg.embd, F = m.cfg.ff;
   if (s == "x") { src = m.x; cap = m.pm * E; }
   else if (s == "q") { src = m.q; cap = m.pm * E; }
+  else if (s == "att") { src = m.att; cap = m.pm * E; }
   else if (s == "gate" || s == "act") { src = m.act; cap = m.pm * F; }
   else if (s == "logits") { src = m.logits; cap = m.cfg.vocab; }
   else if (s == "state") { src = m.state; cap = 2; }
@@ -934,7 +941,18 @@ int llmhip_model_set_kv_f16(llmhip_model* h, int on) {
   clear_error();
   Model& m = *h->m;
   if (m.allocated) return set_error(LLMHIP_ERR_STATE, "llm: the KV cache format is fixed once tensors are uploaded");
+  if (m.q8 && !on) return set_error(LLMHIP_ERR_STATE, "llm: the ExactGGML mode keeps a binary16 KV cache");
   m.kv16 = on != 0;
+  return 0;
+}
+
+int llmhip_model_set_exact_ggml(llmhip_model* h, int on) {
+  clear_error();
+  Model& m = *h->m;
+  if (m.allocated) return set_error(LLMHIP_ERR_STATE, "llm: the ExactGGML mode is fixed once tensors are uploaded");
+  m.q8 = on != 0;
+  if (m.q8) m.kv16 = true;  // cpu.go:298: ExactGGML stores K and V in binary16
+  destroy_graphs(m);
   return 0;
 }
 
@@ -985,7 +1003,7 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
     const Layer& ly = m.layers[i % L];
     if (k == "head") {  // the decode head kernel without the sampling kernel, which advances the state
       const QMat& w = m.tied ? m.embd : m.out;
-      return gemv_launch(head_args(m, 0, 0), w.g.q.type, PRO_RMS, EPI_ARGMAX, m.stream);
+      return gemv_launch(head_args(m, 0, 0), w.g.q.type, PRO_RMS | (m.q8 ? PRO_Q8 : 0), EPI_ARGMAX, m.stream);
     }
     if (k == "k1") return rec_k1(m, ly, 1);
     if (k == "k2") return rec_k2(m, ly, 1);

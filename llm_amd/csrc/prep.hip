@@ -11,6 +11,8 @@ int prep_launch(const GemvArgs& a, int pro, hipStream_t s) {
   switch (pro) {
     case PRO_PLAIN: hipLaunchKernelGGL(prep_kernel<PRO_PLAIN>, grid, dim3(256), lds, s, a); break;
     case PRO_RMS: hipLaunchKernelGGL(prep_kernel<PRO_RMS>, grid, dim3(256), lds, s, a); break;
+    case PRO_PLAIN | PRO_Q8: hipLaunchKernelGGL(prep_kernel<PRO_PLAIN | PRO_Q8>, grid, dim3(256), lds, s, a); break;
+    case PRO_RMS | PRO_Q8: hipLaunchKernelGGL(prep_kernel<PRO_RMS | PRO_Q8>, grid, dim3(256), lds, s, a); break;
     default: return set_error(LLMHIP_ERR_ARG, "llm: prep: prologue %d", pro);
   }
   LLM_HIP(hipGetLastError());

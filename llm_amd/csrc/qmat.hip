@@ -241,11 +241,12 @@ static int qmat_gemv_args(llmhip_qmat* q, const float* x, float* y, int n, GemvA
   return 0;
 }
 
-static int qmat_launch(llmhip_qmat* q, GemvArgs& a, int epi, hipStream_t s) {
-  if (a.ntok < GEMM_MIN_TOKENS) return gemv_launch(a, q->m.g.q.type, PRO_PLAIN, epi, s);
+static int qmat_launch(llmhip_qmat* q, GemvArgs& a, int epi, hipStream_t s, int pro = PRO_PLAIN) {
+  if (a.ntok < GEMM_MIN_TOKENS) return gemv_launch(a, q->m.g.q.type, pro, epi, s);
   if (!q->xprep) LLM_HIP(hipMalloc(&q->xprep, xprep_bytes(64, (uint32_t)q->m.g.k)));
   xprep_bind(&a, q->xprep);
-  LLM_TRY(prep_launch(a, PRO_PLAIN, s));
+  a.q8 = (pro & PRO_Q8) ? 1 : 0;
+  LLM_TRY(prep_launch(a, pro, s));
   return gemm_launch(a, q->m.g.q.type, epi, s);
 }
 
@@ -256,6 +257,15 @@ int llmhip_qmat_gemv(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, in
   LLM_HIP(hipSetDevice(q->m.device));
   LLM_HIP(hipStreamSynchronize(q->stream));
   return qmat_launch(q, a, accumulate ? EPI_ACC : EPI_STORE, (hipStream_t)hip_stream);
+}
+
+int llmhip_qmat_gemv_q8(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, void* hip_stream) {
+  clear_error();
+  GemvArgs a;
+  LLM_TRY(qmat_gemv_args(q, x_dev, y_dev, n, &a));
+  LLM_HIP(hipSetDevice(q->m.device));
+  LLM_HIP(hipStreamSynchronize(q->stream));
+  return qmat_launch(q, a, EPI_STORE, (hipStream_t)hip_stream, PRO_PLAIN | PRO_Q8);
 }
 
 uint64_t llmhip_qmat_bytes(const llmhip_qmat* q) { return q->m.bytes; }

@@ -54,6 +54,18 @@ class QMat:
                                      int(accumulate), _stream(stream)))
         return y
 
+    def gemv_q8(self, x, stream=None):
+        """The ExactGGML product: each row of x quantised to Q8 blocks, integer block dots."""
+        import torch
+        x = x.contiguous()
+        n = 1 if x.dim() == 1 else x.shape[0]
+        if x.dtype != torch.float32 or x.numel() != n * self.k or not x.is_cuda:
+            raise ValueError("x must be a float32 CUDA tensor of n rows of k")
+        y = torch.empty((n, self.rows), dtype=torch.float32, device=x.device)
+        check(lib().llmhip_qmat_gemv_q8(self._h, ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr()), n,
+                                        _stream(stream)))
+        return y
+
     def clone(self):
         """A device-to-device copy (for rotating benchmark copies)."""
         c = QMat.__new__(QMat)

@@ -23,6 +23,8 @@ PrefillBatch = 64
 DecodeBatch = 8
 # binary16 KV cache for the next NewGPU (the F16KV mode of cpu.go:22-24)
 F16KV = False
+# ggml's CPU-backend products for the next NewGPU: Q8 activation blocks, binary16 cache (cpu.go:15-21)
+ExactGGML = False
 
 
 def DefaultLimits(ordinal=0):
@@ -247,6 +249,7 @@ def NewGPU(dev, lim, path, ctx):
     None for the device's own, path the GGUF file, ctx the KV cache length."""
     lib().llm_set_prefill_batch(int(PrefillBatch))
     lib().llm_set_f16kv(int(F16KV))
+    lib().llm_set_exact_ggml(int(ExactGGML))
     h = ctypes.c_void_p()
     check(lib().llm_new_gpu(int(dev), ctypes.byref(lim) if lim is not None else None, os.fsencode(path), int(ctx),
                             ctypes.byref(h)))

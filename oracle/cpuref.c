@@ -25,11 +25,17 @@
  *   cpuref_forward       cpu.go:225-366   pinned: independent vectorised float64 numpy
  *                                         forward on tiny models (attention weights sum
  *                                         to 1, single-position att = v)
+ *   cpuref_matvec_q8     cpu.go:117-140, 166-214  pinned with ExactGGML below
  *   F16KV mode           cpu.go:22-24, 298-299  pinned: the float64 forward with a
  *                                         binary16-rounded cache (numpy RNE), closer to
  *                                         it than to the exact-cache forward
- *   quantize_q8 / ExactGGML mode  cpu.go:117-140: parity unpinned beyond closed-form
- *                        checks of quantize_q8 (not on the graded path)
+ *   quantize_q8          cpu.go:117-140   pinned: halfway cases (round half away from
+ *                                         zero), the amax element at +-127, the Q8_1 sum
+ *                                         from the unrounded scale, the half-step bound
+ *   ExactGGML mode       cpu.go:15-21     pinned: a float64 forward that quantises every
+ *                                         matrix input the same way (f32 ops), integer
+ *                                         block dots, binary16 cache: within 1e-6, and
+ *                                         1000x closer to it than to the unquantised one
  *   gguf reader / config_from  gguf/gguf.go:292-407, config.go:29-73: pinned by the
  *                        reference's gguf_test.go cases and refusal cases of config.go
  *
@@ -293,6 +299,25 @@ static int matvec(float* dst, const float* x, uint32_t type, const uint8_t* data
 EXPORT int cpuref_matvec(float* dst, const float* x, uint32_t type, const uint8_t* data, int in, int out,
                          int nthreads) {
   return matvec(dst, x, type, data, in, out, NULL, nthreads < 1 ? 1 : nthreads);
+}
+
+/* The ExactGGML form of matvec: x quantised by quantizeQ8, then the integer
+ * block products (the qx != nil branches of cpu.go:166-214). */
+EXPORT int cpuref_matvec_q8(float* dst, const float* x, uint32_t type, const uint8_t* data, int in, int out,
+                            int nthreads) {
+  if (in % 32) {
+    snprintf(g_err, sizeof g_err, "llm: CPU matvec_q8: %d inputs", in);
+    return -1;
+  }
+  int nb = in / 32;
+  float* d = (float*)malloc((size_t)nb * 8);
+  int8_t* qs = (int8_t*)malloc((size_t)in);
+  q8act qx = {d, d + nb, qs};
+  quantize_q8(x, in, &qx);
+  int rc = matvec(dst, x, type, data, in, out, &qx, nthreads < 1 ? 1 : nthreads);
+  free(d);
+  free(qs);
+  return rc;
 }
 
 /* The value of every weight, as the CPU path uses it: the embedding gather

@@ -46,6 +46,7 @@ def lib():
         L.cpuref_f32_to_f16_n.argtypes = [P, P, ctypes.c_size_t]
         L.cpuref_rmsnorm.argtypes = [P, P, P, I, F]
         L.cpuref_matvec.argtypes = [P, P, U32, P, I, I, I]
+        L.cpuref_matvec_q8.argtypes = [P, P, U32, P, I, I, I]
         L.cpuref_dequant.argtypes = [P, U32, P, ctypes.c_uint64]
         L.cpuref_rope.argtypes = [P, I, I, I, F, I]
         L.cpuref_rope_table.argtypes = [P, I, I, F]
@@ -94,13 +95,15 @@ def rmsnorm(x, w, eps):
     return out
 
 
-def matvec(qtype, raw, rows, k, x, threads=1):
-    """y = W x for `rows` rows of `k` weights given as raw GGUF blocks."""
+def matvec(qtype, raw, rows, k, x, threads=1, q8=False):
+    """y = W x for `rows` rows of `k` weights given as raw GGUF blocks; q8:
+    the ExactGGML form (x quantised to Q8 blocks, integer block products)."""
     raw = np.ascontiguousarray(np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray)) else raw,
                                np.uint8)
     x = np.ascontiguousarray(x, np.float32)
     y = np.empty(rows, np.float32)
-    if lib().cpuref_matvec(_p(y), _p(x), qtype, _p(raw), k, rows, threads) != 0:
+    fn = lib().cpuref_matvec_q8 if q8 else lib().cpuref_matvec
+    if fn(_p(y), _p(x), qtype, _p(raw), k, rows, threads) != 0:
         raise RuntimeError(lib().cpuref_error().decode())
     return y
 

@@ -27,11 +27,11 @@ def run(*args):
     return r.returncode, r.stdout, r.stderr
 
 
-def _oracle_ref(spec, prompt, n, path, layers=()):
+def _oracle_ref(spec, prompt, n, path, layers=(), exact=False):
     """The CPU oracle's records for check / trace (what a CPU run of cpu.go writes)."""
     from oracle import cpuref
     model = synth.cached(spec)
-    cpu = cpuref.CPU(model, 512, threads=16)
+    cpu = cpuref.CPU(model, 512, threads=16, exact_ggml=exact)
     toks, lgs = cpu_greedy(cpu, prompt, n)
     recs = {"prompt": np.asarray(prompt, np.int32), "logits": lgs[0], "tokens": np.asarray(toks, np.int32)}
     for k in layers:
@@ -113,3 +113,15 @@ def test_bench(gpu):
     assert len(re.findall(r"^round \d: prefill [\d.]+ tok/s, decode [\d.]+ tok/s$", out, re.M)) == 2
     assert re.search(r"^bench p=64 n=16 rounds=2: prefill median [\d.]+ \(min [\d.]+ max [\d.]+\) tok/s, "
                      r"decode median [\d.]+ \(min [\d.]+ max [\d.]+\) tok/s$", out, re.M)
+
+
+def test_check_exact_ggml(gpu, tmp_path):
+    """-exactggml against the oracle's ExactGGML records (a short prompt: no code on a rounding boundary)."""
+    spec = synth.tiny_qwen()
+    prompt = list(synth.prompt(21, 4, spec.vocab))
+    ref = tmp_path / "cpu_exact.llmref"
+    _oracle_ref(spec, prompt, 8, ref, exact=True)
+    rc, out, err = run("check", "-exactggml", "-model", synth.cached(spec), "-n", 8, "-ref", ref)
+    assert rc == 0 and "equal prefix: 8 of 8" in out
+    rc, out, err = run("check", "-model", synth.cached(spec), "-n", 8, "-ref", ref, "-tol", "1e-4")
+    assert rc == 3, "the f32 numerics must not pass the ExactGGML reference at 1e-4"

@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 
 from llm_amd import synth
+from tests import npblocks
 
 pytestmark = pytest.mark.gpu
 
@@ -55,6 +56,44 @@ def _check_gemv(gpu, oracle, qtype, rows, k, n, seed=7, threads=16):
 @pytest.mark.parametrize("n", [1, 8, 64])
 def test_sweep(gpu, oracle, qtype, rows, k, n):
     _check_gemv(gpu, oracle, qtype, rows, k, n)
+
+
+@pytest.mark.parametrize("qtype", [2, 3, 8])
+@pytest.mark.parametrize("rows,k,n", [(896, 896, 1), (1152, 896, 2), (896, 4864, 3), (4864, 896, 1), (37, 96, 1),
+                                      (130, 224, 2), (33, 576, 4), (896, 896, 8), (9728, 896, 64), (896, 4864, 64),
+                                      (130, 224, 5), (151936, 896, 1), (65541, 576, 1)])
+def test_exact_ggml_gemv(gpu, oracle, qtype, rows, k, n):
+    """The ExactGGML product (cpu.go:117-140, 166-214) against the oracle's,
+    through the decode tile kernel (1-4 tokens), the streaming kernel (one
+    token, >= 4096 tiles) and the prefill pair (>= 5 tokens).  Both sides
+    quantise the same f32 inputs with the same f32 operations, so the codes,
+    the integer block sums and each block's term p_b agree exactly; only the
+    order of the f32 sum over the nb blocks differs, so every output is within
+    2 (nb - 1) u sum_b |p_b| (u = 2^-24) of the oracle's -- for Q4_1, whose
+    m_w s_x terms cancel, that is up to ~1e-5 of max|y|, otherwise ~1e-7.  The
+    f32 product of the same inputs sits 1e-2 to 3e-2 away, so an input left
+    unquantised fails."""
+    import torch
+    from llm_amd.kernels import QMat
+    print(f"gemv_q8 qtype={qtype} rows={rows} k={k} n={n}", flush=True)
+    raw = _raw(qtype, rows, k, 11)
+    m = QMat(qtype, rows, k, raw)
+    x = _x(n, k, 11)
+    x[0, :32] = np.concatenate([[127], np.arange(31) - 14.5])  # scale 1: halfway values round away from zero
+    if k >= 64:
+        x[0, 32:64] = 0  # an all-zero block: d = 0, every code 0
+    y = m.gemv_q8(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    m.close()
+    want = np.stack([oracle.matvec(qtype, raw, rows, k, x[t], threads=16, q8=True) for t in range(n)])
+    plain = np.stack([oracle.matvec(qtype, raw, rows, k, x[t], threads=16) for t in range(min(n, 2))])
+    rel = _rel(y, want)
+    print(f"relative error {rel:.3e}; f32 product {_rel(plain, want[:len(plain)]):.3e} away", flush=True)
+    nb = k // 32
+    for t in range(n):
+        bound = 2 * (nb - 1) * 2.0 ** -24 * np.abs(npblocks.block_terms(qtype, raw, rows, k, x[t])).sum(axis=1)
+        err = np.abs(y[t].astype(np.float64) - want[t])
+        assert np.all(err <= bound + 1e-30), (t, float(np.max(err / (bound + 1e-30))))
+    assert rel <= 2e-5 and _rel(plain, want[:len(plain)]) >= 100 * max(rel, 1e-8)
 
 
 @pytest.mark.parametrize("qtype", [2, 3, 8])

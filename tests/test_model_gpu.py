@@ -15,18 +15,19 @@ from tests.parity import LOGIT_TOL, cpu_greedy, gpu_generate, greedy_parity, rel
 pytestmark = pytest.mark.gpu
 
 
-def _open(spec, ctx, f16kv=False):
+def _open(spec, ctx, f16kv=False, exact=False):
     from llm_amd import llm
     from oracle import cpuref
     path = synth.cached(spec)
-    print(f"model {spec.arch} L{spec.layers} E{spec.embd} V{spec.vocab} ctx {ctx} f16kv {f16kv} at {path}", flush=True)
-    old = llm.F16KV
-    llm.F16KV = f16kv
+    print(f"model {spec.arch} L{spec.layers} E{spec.embd} V{spec.vocab} ctx {ctx} f16kv {f16kv} exact {exact} at "
+          f"{path}", flush=True)
+    old = llm.F16KV, llm.ExactGGML
+    llm.F16KV, llm.ExactGGML = f16kv, exact
     try:
         g = llm.NewGPU(0, None, path, ctx)
     finally:
-        llm.F16KV = old
-    cpu = cpuref.CPU(path, ctx, threads=16, f16kv=f16kv)
+        llm.F16KV, llm.ExactGGML = old
+    cpu = cpuref.CPU(path, ctx, threads=16, f16kv=f16kv, exact_ggml=exact)
     return g, cpu
 
 
@@ -98,6 +99,82 @@ def test_qwen25_f16_kv_cache(gpu):
     spec = synth.qwen25()
     g, cpu = _open(spec, 512, f16kv=True)
     _check(g, cpu, synth.prompt(0, 128, spec.vocab), 64)
+
+
+# ExactGGML end to end.  Every activation code is a discontinuous function
+# of an f32 value: two correct implementations whose f32 sums round in a
+# different order disagree on the codes that sit within that difference of a
+# rounding boundary, and each such flip moves the logits by ~1e-3 (the
+# independent float64 restatement of tests/test_oracle.py shows the same
+# 2.7e-3 / 3.6e-3 steps against the oracle on the same tiny-model inputs).
+# The products themselves are pinned on identical inputs at the summation
+# bound (tests/test_gemv_gpu.py::test_exact_ggml_gemv).  End to end: prompts
+# of 1-4 tokens (few codes, no flip) within 1e-4; longer runs within the flip
+# level -- EXACT_TOL on the tiny models, where one flip moves the logits by
+# 2.7e-3 to 6.6e-3 (measured, GPU and float64 restatement alike), and 5e-3 and
+# closer to the oracle's ExactGGML than to its f32 mode at the Qwen shape --
+# with greedy tokens equal up to near-ties at that level.
+EXACT_TOL = 1e-2
+EXACT_TINY = dict(TINY, **{"qwen2-split": lambda: synth.tiny_qwen(seed=8)})
+
+
+@pytest.mark.parametrize("name", list(TINY))
+def test_exact_ggml_short(gpu, name):
+    """ExactGGML (cpu.go:15-21, 117-140, 166-214) through the decode kernels:
+    prompts of 1 to 4 tokens, logits within 1e-4 of the oracle's."""
+    from oracle import cpuref
+    spec = TINY[name]()
+    g, cpu = _open(spec, 128, exact=True)
+    for plen in (1, 2, 3, 4):
+        prompt = list(synth.prompt(20 + plen, plen, spec.vocab))
+        cpu.reset()
+        for t in prompt:
+            want = cpu.forward(t)
+        rel = rel_err(g.PrefillLogits(prompt), want)
+        print(f"prompt {plen}: logits relative error {rel:.3e}", flush=True)
+        assert rel <= LOGIT_TOL
+
+
+@pytest.mark.parametrize("name,prompt_len,n", [("llama", 150, 40), ("qwen2", 150, 40), ("qwen2-mixed", 150, 40),
+                                               ("llama-untied-q41", 100, 30), ("qwen2-split", 300, 24)])
+def test_exact_ggml(gpu, name, prompt_len, n):
+    """ExactGGML through the prefill pair, both attention forms and decode:
+    Q8_0 / Q8_1 activation blocks for Q4_0, Q4_1 and Q8_0 weights, the
+    binary16 cache; logits and greedy tokens at the flip level."""
+    spec = EXACT_TINY[name]()
+    g, cpu = _open(spec, 512, exact=True)
+    prompt = synth.prompt(13, prompt_len, spec.vocab)
+    logits = g.PrefillLogits(prompt)
+    toks, lgs = cpu_greedy(cpu, prompt, n)
+    rel = rel_err(logits, lgs[0])
+    print(f"step-1 logits relative error {rel:.3e}", flush=True)
+    assert rel <= EXACT_TOL
+    ties = greedy_parity(g, prompt, toks, lgs, tol=EXACT_TOL)
+    print(f"{n} greedy tokens equal ({ties} accepted near-ties)", flush=True)
+    kvd = spec.kv_heads * (spec.embd // spec.heads)
+    kv = g.Peek("kvblk.0", 2 * 512 * kvd).reshape(2, 512, kvd)[:, :prompt_len]
+    assert np.array_equal(kv, kv.astype(np.float16).astype(np.float32)), "cache values are not binary16"
+
+
+def test_qwen25_exact_ggml(gpu):
+    """BASELINE config 3's shape in the ExactGGML mode: ~180k activation codes
+    per token, so flips are certain; measured 0.7e-3 to 1.2e-3 from the
+    oracle's ExactGGML against 2.3e-3 to 3.2e-3 between the oracle's own f32
+    and ExactGGML modes."""
+    from oracle import cpuref
+    spec = synth.qwen25()
+    g, cpu = _open(spec, 512, exact=True)
+    cpu32 = cpuref.CPU(synth.cached(spec), 512, threads=16)
+    prompt = synth.prompt(0, 128, spec.vocab)
+    logits = g.PrefillLogits(prompt)
+    toks, lgs = cpu_greedy(cpu, prompt, 48)
+    for t in prompt:
+        l32 = cpu32.forward(t)
+    rel, rel32 = rel_err(logits, lgs[0]), rel_err(logits, l32)
+    print(f"step-1 logits: {rel:.3e} from the oracle's ExactGGML, {rel32:.3e} from its f32 mode", flush=True)
+    assert rel <= 5e-3 and rel <= 0.6 * rel32
+    ties = greedy_parity(g, prompt, toks, lgs, tol=5e-3)
+    print(f"48 greedy tokens equal ({ties} accepted near-ties)", flush=True)
 
 
 def test_decode_batches_and_stops(gpu):

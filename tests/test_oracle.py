@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 from llm_amd import synth
+from tests import npblocks
 from oracle import cpuref
 
 F16_INF = 0x7C00
@@ -92,32 +93,12 @@ def test_rmsnorm_against_float64():
     assert np.allclose(got, 1.0, rtol=0, atol=1e-7)
 
 
-def _np_dequant(qtype, raw, nblocks):
-    """The GGUF block formats decoded in numpy, vectorised (ggml's layouts:
-    Q4_0 byte j holds element j in the low nibble and j+16 in the high one)."""
-    b = np.frombuffer(raw, np.uint8)
-    if qtype == synth.Q4_0:
-        blk = b.reshape(nblocks, 18)
-        d = blk[:, :2].copy().view(np.float16).astype(np.float64)
-        q = np.concatenate([blk[:, 2:] & 15, blk[:, 2:] >> 4], axis=1).astype(np.float64) - 8
-        return (d * q).reshape(-1)
-    if qtype == synth.Q4_1:
-        blk = b.reshape(nblocks, 20)
-        d = blk[:, :2].copy().view(np.float16).astype(np.float64)
-        m = blk[:, 2:4].copy().view(np.float16).astype(np.float64)
-        q = np.concatenate([blk[:, 4:] & 15, blk[:, 4:] >> 4], axis=1).astype(np.float64)
-        return (d * q + m).reshape(-1)
-    blk = b.reshape(nblocks, 34)
-    d = blk[:, :2].copy().view(np.float16).astype(np.float64)
-    return (d * blk[:, 2:].view(np.int8).astype(np.float64)).reshape(-1)
-
-
 @pytest.mark.parametrize("qtype", [synth.Q4_0, synth.Q4_1, synth.Q8_0])
 def test_dequant_closed_form(qtype):
     rng = np.random.default_rng([2, qtype])
     raw = synth.quant_blocks(qtype, 7, 96, rng)
     got = cpuref.dequant(qtype, raw, 21)
-    want = _np_dequant(qtype, raw, 21)
+    want = npblocks.dequant(qtype, raw, 21)
     # Q4_0 / Q8_0 products are exact in f32; Q4_1 has one rounding (d*q) and one (+m)
     if qtype == synth.Q4_1:
         assert np.max(np.abs(got - want)) <= 2 * np.finfo(np.float32).eps * np.max(np.abs(want))
@@ -132,7 +113,7 @@ def test_matvec_against_float64(qtype, rows, k):
     raw = synth.quant_blocks(qtype, rows, k, rng)
     x = rng.standard_normal(k).astype(np.float32)
     got = cpuref.matvec(qtype, raw, rows, k, x)
-    W = _np_dequant(qtype, raw, rows * k // 32).reshape(rows, k)
+    W = npblocks.dequant(qtype, raw, rows * k // 32).reshape(rows, k)
     want = W @ x.astype(np.float64)
     scale = np.abs(W) @ np.abs(x.astype(np.float64))
     assert np.all(np.abs(got - want) <= 1e-6 * scale + 1e-30)
@@ -239,18 +220,47 @@ def test_quantize_q8_closed_form():
     assert np.all(cpuref.quantize_q8(np.zeros(32, np.float32))[2] == 0)
 
 
+def test_quantize_q8_invariants():
+    """quantizeQ8's rounding and scales pinned by cases the mathematics fixes:
+    with amax = 127 the scale is 1 and halfway values round away from zero
+    (Go's math.Round; half-to-even would give 0, 2, -2); the element of
+    largest magnitude maps to +-127; the Q8_1 sum s uses the unrounded scale;
+    and every element dequantises to within half a step of its value."""
+    x = np.zeros(64, np.float32)
+    x[:8] = [127, 0.5, -0.5, 2.5, -2.5, 1.5, -126.5, 3.4999998]
+    x[32:] = np.float32(1.0) / np.arange(1, 33, dtype=np.float32)  # amax 1: d = 1/127 is not a binary16 value
+    d, s, qs = cpuref.quantize_q8(x)
+    assert d[0] == 1 and list(qs[:8]) == [127, 1, -1, 3, -3, 2, -127, 3]
+    assert s[0] == np.float16(np.sum(qs[:32].astype(np.int64))).astype(np.float32)
+    d1 = np.float32(1) / np.float32(127)
+    assert d[1] == np.float16(d1).astype(np.float32) and d[1] != d1 and qs[32] == 127
+    assert s[1] == np.float16(d1 * np.float32(np.sum(qs[32:].astype(np.int64)))).astype(np.float32)
+    rng = np.random.default_rng(3)
+    y = (rng.standard_normal(32 * 50) * np.exp(rng.uniform(-8, 8, 1600))).astype(np.float32)
+    d, s, qs = cpuref.quantize_q8(y)
+    yb = y.reshape(50, 32).astype(np.float64)
+    step = np.max(np.abs(yb), axis=1) / 127
+    err = np.abs(qs.reshape(50, 32).astype(np.float64) * step[:, None] - yb)
+    assert np.all(err <= step[:, None] * (0.5 + 1e-5))
+    assert np.all(np.abs(qs.reshape(50, 32)).max(axis=1) == 127)
+
+
 # ----------------------------------------------- the forward pass, float64
 
-def _forward64(path, tokens, f16kv=False):
+def _forward64(path, tokens, f16kv=False, exact=False):
     """An independent float64 forward pass of the model (cpu.go:225-366 as
     mathematics: dequantised matrices, vectorised attention with the global
     max), returning the logits of the last token.  f16kv: K and V rounded
     through binary16 before they enter the cache (numpy's float16 cast,
-    round to nearest even)."""
+    round to nearest even).  exact: the products of ggml's CPU backend --
+    each input vector (cast to f32) quantised to Q8 blocks, the integer block
+    dot products exact, sum_b d_w d_x (w . x_q) (+ m_w s_x) in float64 -- and
+    the binary16 cache."""
     from llm_amd import llm
     f = llm.Parse(path)
     c = llm.ConfigFrom(f)
     raw = open(path, "rb").read()
+    f16kv = f16kv or exact
 
     def T(name):
         t, ok = f.Tensor(name)
@@ -259,11 +269,16 @@ def _forward64(path, tokens, f16kv=False):
         if t.Type == synth.F32:
             return np.frombuffer(data, np.float32).astype(np.float64)
         rows, k = t.Dims[1], t.Dims[0]
-        return _np_dequant(t.Type, data, rows * k // 32).reshape(rows, k)
+        wd = npblocks.dequant(t.Type, data, rows * k // 32).reshape(rows, k)
+        if not exact:
+            return wd
+        d, m, q = npblocks.blocks(t.Type, data, rows * k // 32)
+        return _QMat(wd, d.reshape(rows, -1), m.reshape(rows, -1), q.reshape(rows, k // 32, 32))
 
     E, H, KVH, HD, FF = c.embd, c.heads, c.kv_heads, c.head_dim, c.ff
     emb = T("token_embd.weight")
     out = emb if c.tied_output else T("output.weight")
+    emb = emb.wd if exact else emb
 
     def rms(v, w):
         return v / np.sqrt(np.mean(v * v) + c.eps) * w
@@ -314,6 +329,19 @@ def _forward64(path, tokens, f16kv=False):
     return out @ rms(x, T("output_norm.weight"))
 
 
+class _QMat:
+    """A quantised matrix whose product with a vector is ggml's: x quantised by
+    npblocks.quantize_q8, integer block dots, scales applied in float64."""
+
+    def __init__(self, wd, d, m, q):
+        self.wd, self.d, self.m, self.q = wd, d, m, q
+
+    def __matmul__(self, x):
+        dx, sx, qx = npblocks.quantize_q8(x)
+        si = np.einsum("obj,bj->ob", self.q, qx).astype(np.float64)
+        return (self.d * dx[None, :] * si).sum(axis=1) + (self.m * sx[None, :]).sum(axis=1)
+
+
 @pytest.mark.parametrize("spec", [synth.tiny_llama(), synth.tiny_qwen(),
                                   synth.tiny_qwen(seed=7, types={"ffn_down": synth.Q4_1, "attn_v": synth.Q8_0})],
                          ids=["llama", "qwen2", "qwen2-mixed"])
@@ -327,6 +355,25 @@ def test_forward_against_float64(spec):
     rel = np.max(np.abs(got - want)) / np.max(np.abs(want))
     assert rel <= 1e-5, rel
     assert cpu.pos() == len(toks)
+
+
+@pytest.mark.parametrize("spec", [synth.tiny_llama(), synth.tiny_qwen(),
+                                  synth.tiny_qwen(seed=7, types={"ffn_down": synth.Q4_1, "attn_v": synth.Q8_0})],
+                         ids=["llama", "qwen2", "qwen2-mixed"])
+def test_forward_exact_ggml_against_float64(spec):
+    """The ExactGGML mode (cpu.go:15-21, 117-140, 166-214, 298-299): within
+    1e-6 of the float64 forward that quantises every matrix input the same way
+    and keeps a binary16 cache, and at least 1000 times closer to it than to
+    the unquantised float64 forward (measured: 4e-8 to 1.2e-7 against 3e-3 to
+    9e-3), so a wrong rounding, scale or Q4_1 term fails."""
+    path = synth.cached(spec)
+    toks = list(synth.prompt(11, 40, spec.vocab))
+    cpu = cpuref.CPU(path, 64, exact_ggml=True)
+    for t in toks:
+        got = cpu.forward(t)
+    we, wp = _forward64(path, toks, exact=True), _forward64(path, toks)
+    re_, rp = (np.max(np.abs(got - w)) / np.max(np.abs(w)) for w in (we, wp))
+    assert re_ <= 1e-6 and rp >= 1000 * re_, (re_, rp)
 
 
 @pytest.mark.parametrize("spec", [synth.tiny_llama(), synth.tiny_qwen()], ids=["llama", "qwen2"])
