@@ -1,0 +1,126 @@
+// The attention of one query head over one chunk of cache rows, by a
+// workgroup of NW waves (cpu.go:300-334): s = (q . k) * scale, the chunk's
+// max, e = exp(s - max), l = sum e, o = sum e v.  Lane c of a 16-lane row
+// holds float4 c (and c+16 for HD 128) of key and value rows; slot = tid / 16
+// serves rows row0 + slot + S*j (S = 4*NW slots, j < J), so a chunk is
+// C = S*J rows.  Loads are coalesced rows, a score is a 16-lane DPP sum that
+// lands in the lanes holding the matching value row, and the weighted value
+// sums are reduced over rows by two shuffles and over waves through LDS.
+// attn_kernel (layer.hip) runs one chunk per workgroup with it.
+#pragma once
+
+#include "wave.h"
+
+namespace llmhip {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Four consecutive cache elements as f32: an f32 cache, or binary16 (F16KV)
+// widened exactly.
+template <bool KVH>
+__device__ __forceinline__ f4 kv_load4(const float* kv, uint64_t i) {
+  if (!KVH) return *(const f4*)(kv + i);
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const h4 h = *(const h4*)((const _Float16*)kv + i);
+  return f4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+
+template <uint32_t HD, uint32_t NW>
+struct AttnLds {
+  float m[NW], l[NW];
+  f4 o[NW * 16 * (HD / 64)];
+};
+
+template <uint32_t HD, uint32_t J, uint32_t NW, bool KVH>
+struct AttnChunk {
+  static constexpr uint32_t V4 = HD / 64, S = 4 * NW, C = S * J;
+  f4 kr[J][V4], vr[J][V4];
+
+  // Issue the loads of rows row0 + slot + S*j in [from, lim) of KV head g
+  // (the cache is [2][ctx][kvd]); other rows are left as they are.
+  __device__ __forceinline__ void load(const float* kv, uint32_t kvd, uint32_t ctx, uint32_t g, uint32_t row0,
+                                       uint32_t lim, uint32_t from = 0) {
+    const uint32_t cl = threadIdx.x & 15, slot = threadIdx.x >> 4;
+    const uint64_t kb = g * HD + 4 * cl, vb = (uint64_t)ctx * kvd + g * HD + 4 * cl;  // element offsets
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++) {
+      const uint32_t p = row0 + slot + S * j;
+      if (p >= from && p < lim) {
+#pragma unroll
+        for (uint32_t v = 0; v < V4; v++) {
+          kr[j][v] = kv_load4<KVH>(kv, kb + (uint64_t)p * kvd + 64 * v);
+          vr[j][v] = kv_load4<KVH>(kv, vb + (uint64_t)p * kvd + 64 * v);
+        }
+      }
+    }
+  }
+
+  // The rows below n (all of them loaded or set), with q the lane's float4
+  // slice of the query: returns the chunk's max M and sum L in every thread,
+  // and o = sum e v[d] for d = tid < HD.  Two barriers; call with the whole
+  // workgroup.
+  __device__ __forceinline__ void reduce(const f4 (&q)[V4], uint32_t row0, uint32_t n, float scale,
+                                         AttnLds<HD, NW>& sm, float* M_out, float* L_out, float* o_out) const {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id(), cl = lane & 15, slot = tid >> 4;
+    float sj[J], m = -INFINITY;
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++) {
+      const uint32_t p = row0 + slot + S * j;
+      float d = 0;
+      if (p < n)
+#pragma unroll
+        for (uint32_t v = 0; v < V4; v++)
+          d += q[v][0] * kr[j][v][0] + q[v][1] * kr[j][v][1] + q[v][2] * kr[j][v][2] + q[v][3] * kr[j][v][3];
+      d = row_sum16(d);
+      sj[j] = p < n ? d * scale : -INFINITY;
+      m = fmaxf(m, sj[j]);
+    }
+    m = rows_max4(m);
+    if (lane == 0) sm.m[wave] = m;
+    __syncthreads();
+    float M = sm.m[0];
+#pragma unroll
+    for (uint32_t w = 1; w < NW; w++) M = fmaxf(M, sm.m[w]);
+    f4 acc[V4];
+#pragma unroll
+    for (uint32_t v = 0; v < V4; v++) acc[v] = f4{0, 0, 0, 0};
+    float l = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++) {
+      const uint32_t p = row0 + slot + S * j;
+      if (p < n) {
+        const float e = expf(sj[j] - M);
+        l += e;
+#pragma unroll
+        for (uint32_t v = 0; v < V4; v++) acc[v] += e * vr[j][v];
+      }
+    }
+    l = rows_sum4(l);
+#pragma unroll
+    for (uint32_t v = 0; v < V4; v++)
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        acc[v][k] += __shfl_xor(acc[v][k], 16);
+        acc[v][k] += __shfl_xor(acc[v][k], 32);
+      }
+    if (lane < 16)
+#pragma unroll
+      for (uint32_t v = 0; v < V4; v++) sm.o[(wave * 16 + cl) * V4 + v] = acc[v];
+    if (lane == 0) sm.l[wave] = l;
+    __syncthreads();
+    *M_out = M;
+    float L = 0, o = 0;
+    if (tid < HD) {
+      const uint32_t fi = tid / 4, ci = fi % 16, vi = fi / 16, k = tid % 4;
+#pragma unroll
+      for (uint32_t w = 0; w < NW; w++) {
+        L += sm.l[w];
+        o += sm.o[(w * 16 + ci) * V4 + vi][k];
+      }
+    }
+    *L_out = L;
+    *o_out = o;
+  }
+};
+
+}  // namespace llmhip

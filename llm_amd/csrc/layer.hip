@@ -1,21 +1,16 @@
 // The non-matrix kernels of the forward pass: attention over the f32 KV cache
 // (one chunk, or chunks of positions merged by a second kernel), greedy
 // sampling and the state advance.
+#include "attn_core.h"
 #include "layer.h"
 #include "wave.h"
 
 namespace llmhip {
 
-// Attention over the f32 KV cache (cpu.go:300-334): s = (q . k) * scale, the
-// exact softmax max(s), e = exp(s - max), out = sum e v / sum e.  A workgroup
-// of 512 threads serves one query head over C = 32*J cache rows: lane c of a
-// wave's four 16-lane rows holds float4 c (and c+16 for HD 128) of key and
-// value rows slot + 32j (slot = 4*wave + row, j < J).  Loads are coalesced
-// rows, q is HD/64 float4 per lane, a score is a 16-lane DPP sum that lands in
-// the lanes holding the matching value row, and the weighted value sums are
-// reduced over rows by two shuffles and over waves through LDS.  Every global
-// load is issued before anything waits; a.rows (host-chosen, >= every
-// position count of the pass, <= ctx) bounds the rows read, the rest masked.
+// Attention over the KV cache (cpu.go:300-334), one query head per
+// workgroup of 512 threads over C = 32*J cache rows (attn_core.h).  Every
+// global load is issued before anything waits; a.rows (host-chosen, >= every
+// position count of the pass, <= ctx) bounds the rows read.
 //
 // Work units are (token t, KV head g, chunk c) = (u % NI / kv, u % NI % kv,
 // u / NI), NI = ntok * kv_heads.  Workgroups go to the 8 XCDs round-robin
@@ -27,103 +22,28 @@ namespace llmhip {
 //   SPLIT = true: chunk c covers rows [c*C, c*C + C); writes the partials
 //     (m, l) and o = sum e v for attn_merge_kernel; chunks past the causal
 //     bound write nothing.
-typedef float f4 __attribute__((ext_vector_type(4)));
-
-// Four consecutive cache elements as f32: an f32 cache, or binary16 (F16KV)
-// widened exactly.
-template <bool KVH>
-__device__ __forceinline__ f4 kv_load4(const float* kv, uint64_t i) {
-  if (!KVH) return *(const f4*)(kv + i);
-  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-  const h4 h = *(const h4*)((const _Float16*)kv + i);
-  return f4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
-}
-
 template <uint32_t HD, uint32_t J, bool SPLIT, bool KVH>
 __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a, uint32_t ntok, uint32_t units) {
-  typedef float f4 __attribute__((ext_vector_type(4)));
-  constexpr uint32_t V4 = HD / 64, C = 32 * J;
-  __shared__ float red_m[8], red_l[8];
-  __shared__ f4 red_o[8 * 16 * V4];
+  typedef AttnChunk<HD, J, 8, KVH> AC;
+  __shared__ AttnLds<HD, 8> sm;
   const uint32_t GQ = a.heads / a.kv_heads, sb = blockIdx.x / 8;
   const uint32_t u = 8 * (sb / GQ) + blockIdx.x % 8;
   if (u >= units) return;
   const uint32_t NI = ntok * a.kv_heads, inst = u % NI, c = u / NI;
   const uint32_t t = inst / a.kv_heads, g = inst % a.kv_heads, h = g * GQ + sb % GQ;
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id(), cl = lane & 15, slot = tid >> 4;
-  const uint32_t row0 = c * C;
-  const uint64_t kb = g * HD + 4 * cl, vb = (uint64_t)a.ctx * a.kvd + g * HD + 4 * cl;  // element offsets
+  const uint32_t tid = threadIdx.x, cl = tid & 15;
+  const uint32_t row0 = c * AC::C;
   const float* qp = a.q + (uint64_t)t * a.heads * HD + h * HD + 4 * cl;
-  f4 q[V4], kr[J][V4], vr[J][V4];
+  f4 q[AC::V4];
 #pragma unroll
-  for (uint32_t v = 0; v < V4; v++) q[v] = *(const f4*)(qp + 64 * v);
-#pragma unroll
-  for (uint32_t j = 0; j < J; j++) {
-    const uint32_t p = row0 + slot + 32 * j;
-    if (p < a.rows) {
-#pragma unroll
-      for (uint32_t v = 0; v < V4; v++) {
-        kr[j][v] = kv_load4<KVH>(a.kv, kb + (uint64_t)p * a.kvd + 64 * v);
-        vr[j][v] = kv_load4<KVH>(a.kv, vb + (uint64_t)p * a.kvd + 64 * v);
-      }
-    }
-  }
+  for (uint32_t v = 0; v < AC::V4; v++) q[v] = *(const f4*)(qp + 64 * v);
+  AC rows;
+  rows.load(a.kv, a.kvd, a.ctx, g, row0, a.rows);
   const uint32_t n = a.state[0] + t + 1;
   if (SPLIT && row0 >= n) return;  // uniform over the workgroup
-  float sj[J], m = -INFINITY;
-#pragma unroll
-  for (uint32_t j = 0; j < J; j++) {
-    const uint32_t p = row0 + slot + 32 * j;
-    float d = 0;
-    if (p < a.rows)
-#pragma unroll
-      for (uint32_t v = 0; v < V4; v++)
-        d += q[v][0] * kr[j][v][0] + q[v][1] * kr[j][v][1] + q[v][2] * kr[j][v][2] + q[v][3] * kr[j][v][3];
-    d = row_sum16(d);
-    sj[j] = p < n ? d * a.scale : -INFINITY;
-    m = fmaxf(m, sj[j]);
-  }
-  m = rows_max4(m);
-  if (lane == 0) red_m[wave] = m;
-  __syncthreads();
-  float M = red_m[0];
-#pragma unroll
-  for (uint32_t w = 1; w < 8; w++) M = fmaxf(M, red_m[w]);
-  f4 acc[V4];
-#pragma unroll
-  for (uint32_t v = 0; v < V4; v++) acc[v] = f4{0, 0, 0, 0};
-  float l = 0;
-#pragma unroll
-  for (uint32_t j = 0; j < J; j++) {
-    const uint32_t p = row0 + slot + 32 * j;
-    if (p < n) {
-      const float e = expf(sj[j] - M);
-      l += e;
-#pragma unroll
-      for (uint32_t v = 0; v < V4; v++) acc[v] += e * vr[j][v];
-    }
-  }
-  l = rows_sum4(l);
-#pragma unroll
-  for (uint32_t v = 0; v < V4; v++)
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      acc[v][k] += __shfl_xor(acc[v][k], 16);
-      acc[v][k] += __shfl_xor(acc[v][k], 32);
-    }
-  if (lane < 16)
-#pragma unroll
-    for (uint32_t v = 0; v < V4; v++) red_o[(wave * 16 + cl) * V4 + v] = acc[v];
-  if (lane == 0) red_l[wave] = l;
-  __syncthreads();
+  float M, L, o;
+  rows.reduce(q, row0, n, a.scale, sm, &M, &L, &o);
   if (tid < HD) {
-    const uint32_t fi = tid / 4, ci = fi % 16, vi = fi / 16, k = tid % 4;
-    float L = 0, o = 0;
-#pragma unroll
-    for (uint32_t w = 0; w < 8; w++) {
-      L += red_l[w];
-      o += red_o[(w * 16 + ci) * V4 + vi][k];
-    }
     if (SPLIT) {
       const uint64_t th = (uint64_t)t * a.heads + h;
       a.pv[(th * a.smax + c) * HD + tid] = o;

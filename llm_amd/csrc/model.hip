@@ -1015,7 +1015,7 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
   const Layer& L0 = m.layers[0];
   if (k == "head") b = wb(m.tied ? m.embd : m.out);
   else if (k == "k1") b = wb(L0.qkv[0]) + (L0.nqkv == 3 ? wb(L0.qkv[1]) + wb(L0.qkv[2]) : 0);
-  else if (k == "k2") b = 2ull * (m.pos + 1) * m.kvd * 4;
+  else if (k == "k2") b = 2ull * (m.pos + 1) * m.kvd * (m.kv16 ? 2 : 4);
   else if (k == "k3") b = wb(L0.o);
   else if (k == "k4") b = wb(L0.gu[0]) + (L0.ngu == 2 ? wb(L0.gu[1]) : 0);
   else b = wb(L0.down);
