@@ -320,15 +320,60 @@ __device__ __forceinline__ void kv_store(const GemvArgs& a, uint64_t i, float v)
   else a.kv[i] = v;
 }
 
+// The inputs of a row's epilogue that do not depend on the product: the
+// residual rows (EPI_ACC), the bias and the RoPE table entries (EPI_QKV).
+// The decode kernel loads them before its prologue, so that their round trips
+// (state, then the table) overlap the activation staging instead of following
+// the product.
+struct EpiIn {
+  float yA = 0, yB = 0, bias = 0, cA = 0, sA = 0, cB = 0, sB = 0;
+};
+
+template <int EPI>
+__device__ __forceinline__ EpiIn epi_load(const GemvArgs& a, uint32_t tile, int r, bool active, uint32_t tokA,
+                                          bool okA, uint32_t tokB, bool okB) {
+  EpiIn e;
+  const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
+  if (!active || lr >= a.rows) return e;
+  if (EPI == EPI_ACC) {
+    if (okA) e.yA = a.y[(uint64_t)tokA * a.ldy + lr];
+    if (okB) e.yB = a.y[(uint64_t)tokB * a.ldy + lr];
+  }
+  if (EPI == EPI_QKV) {
+    const uint32_t lf = a.row_base + lr;
+    if (a.bias) e.bias = a.bias[lf];
+    if (lf < a.nq + a.nk) {
+      const uint32_t hd = a.hd, hp = hd / 2;
+      const uint32_t j = lf < a.nq ? lf : lf - a.nq, w = j % hd;
+      const uint32_t i = a.neox ? w % hp : w / 2;
+      const uint32_t p0 = a.state[0];
+      if (okA) {
+        const uint64_t o = ((uint64_t)(p0 + tokA) * hp + i) * 2;
+        e.cA = a.cs[o];
+        e.sA = a.cs[o + 1];
+      }
+      if (okB) {
+        const uint64_t o = ((uint64_t)(p0 + tokB) * hp + i) * 2;
+        e.cB = a.cs[o];
+        e.sB = a.cs[o + 1];
+      }
+    }
+  }
+  return e;
+}
+
 // The per-row epilogue of both matrix kernels.  The lane holds row r of tile
 // `tile` for two tokens of the launch (tokA, tokB; okA/okB say whether they
-// exist), already unscaled.  Every lane of the wave must call it: the RoPE and
+// exist), already unscaled; `pre` holds its epi_load inputs, or is null and
+// they are loaded here.  Every lane of the wave must call it: the RoPE and
 // SwiGLU epilogues exchange values between lanes.
 template <int EPI>
 __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, int r, bool active, uint32_t tokA,
-                                             bool okA, float vA, uint32_t tokB, bool okB, float vB) {
+                                             bool okA, float vA, uint32_t tokB, bool okB, float vB,
+                                             const EpiIn* pre = nullptr) {
   const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
   const bool rvalid = active && lr < a.rows;
+  const EpiIn e = pre ? *pre : epi_load<EPI>(a, tile, r, active, tokA, okA, tokB, okB);
   if (EPI == EPI_SWIGLU) {
     // act = g / (1 + exp(-g)) * u (cpu.go:345) with g from the gate's own launch
     if (rvalid) {
@@ -346,14 +391,8 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
   }
   if (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_ARGMAX) {
     if (rvalid) {
-      if (okA) {
-        float* y = a.y + (uint64_t)tokA * a.ldy + lr;
-        *y = EPI == EPI_ACC ? *y + vA : vA;
-      }
-      if (okB) {
-        float* y = a.y + (uint64_t)tokB * a.ldy + lr;
-        *y = EPI == EPI_ACC ? *y + vB : vB;
-      }
+      if (okA) a.y[(uint64_t)tokA * a.ldy + lr] = EPI == EPI_ACC ? e.yA + vA : vA;
+      if (okB) a.y[(uint64_t)tokB * a.ldy + lr] = EPI == EPI_ACC ? e.yB + vB : vB;
     }
   }
   if (EPI == EPI_QKV) {
@@ -362,24 +401,23 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
     // lf is the row in [q; k; v]; a launch may cover one of the three.
     const uint32_t lf = a.row_base + lr;
     if (a.bias && rvalid) {
-      float bb = a.bias[lf];
-      vA += bb;
-      vB += bb;
+      vA += e.bias;
+      vB += e.bias;
     }
     const int pm = a.neox ? 8 : 1;
     float oA = __shfl_xor(vA, pm), oB = __shfl_xor(vB, pm);
     if (rvalid) {
       const uint32_t hd = a.hd, hp = hd / 2;
+      const uint32_t p0 = a.state[0];
       for (int u = 0; u < 2; u++) {
         if (!(u ? okB : okA)) continue;
         uint32_t tok = u ? tokB : tokA;
         float v = u ? vB : vA, o = u ? oB : oA;
-        uint32_t pos = a.state[0] + tok;
+        uint32_t pos = p0 + tok;
         if (lf < a.nq + a.nk) {
           uint32_t j = lf < a.nq ? lf : lf - a.nq, w = j % hd;
-          uint32_t i = a.neox ? w % hp : w / 2;
           bool first = a.neox ? w < hp : (w % 2) == 0;
-          float c = a.cs[((uint64_t)pos * hp + i) * 2], sn = a.cs[((uint64_t)pos * hp + i) * 2 + 1];
+          const float c = u ? e.cB : e.cA, sn = u ? e.sB : e.sA;
           float x = first ? v : o, z = first ? o : v;
           float res = first ? __fsub_rn(__fmul_rn(x, c), __fmul_rn(z, sn))    // cpu.go:381
                             : __fadd_rn(__fmul_rn(x, sn), __fmul_rn(z, c));  // cpu.go:382
@@ -781,6 +819,12 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     if (has_tail) load_unit<QT>(wt, a.qs, nb, tile, a.ng, a.ng, a.tail, lane, r);
   }
 
+  // the epilogue's own inputs, in flight during the prologue
+  const bool active = sp == 0 && has_tile;
+  const int tA = 2 * q, tB = 2 * q + 1;
+  const bool okA = tA < nt, okB = NT > 1 && tB < nt;
+  const EpiIn pre = epi_load<EPI>(a, tile, r, active, t0 + tA, okA, t0 + tB, okB);
+
   int ex[NT];
   stage_x<QT, NT, PRO>(a, t0, nt, xs, misc, bsum, dxs, ex);
 
@@ -810,9 +854,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     }
   }
   // ---- epilogue: lane holds rows r of the tile for tokens 2q and 2q+1
-  const bool active = sp == 0 && has_tile;
-  const int tA = 2 * q, tB = 2 * q + 1;
-  const bool okA = tA < nt, okB = NT > 1 && tB < nt;
   int eA = 0, eB = 0;
 #pragma unroll
   for (int t = 0; t < NT; t++) {
@@ -821,7 +862,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   }
   const float vA = okA ? ldexpf(acc0, -eA) : 0.f;
   const float vB = okB ? ldexpf(acc1, -eB) : 0.f;
-  row_epilogue<EPI>(a, tile, r, active, t0 + tA, okA, vA, t0 + tB, okB, vB);
+  row_epilogue<EPI>(a, tile, r, active, t0 + tA, okA, vA, t0 + tB, okB, vB, &pre);
   if (EPI == EPI_ARGMAX) {
     const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
     const bool ok = active && lr < a.rows && q == 0 && okA && vA == vA;

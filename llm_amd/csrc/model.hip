@@ -62,6 +62,7 @@ struct Model {
   int32_t *tokens = nullptr, *outb = nullptr;
   int32_t* host = nullptr;  // pinned: prompt ids in, sampled ids out
   uint32_t host_cap = 0;
+  uint8_t* bounce = nullptr;  // pinned: every copy to or from caller memory passes through it
   QMat embd, out;
   bool tied = false;
   float* out_norm = nullptr;
@@ -97,6 +98,36 @@ static int launch_rec(Model& m, const char* cls, uint64_t bytes, F&& launch) {
   LLM_HIP(hipEventRecord(r.a, m.stream));
   LLM_TRY(launch());
   LLM_HIP(hipEventRecord(r.b, m.stream));
+  return 0;
+}
+
+// Transfers between the device and caller memory go through the model's
+// pinned bounce buffer in pieces of BOUNCE_BYTES: the runtime only ever DMAs
+// to or from memory the library allocated pinned, never to pageable caller
+// memory (which it would have to lock or stage itself), and the library holds
+// no caller pointer after a call returns.
+constexpr uint64_t BOUNCE_BYTES = 1ull << 20;
+
+// n bytes device -> caller memory, on the model's stream (synchronous).
+static int copy_out(Model& m, void* dst, const void* src, uint64_t n) {
+  for (uint64_t o = 0; o < n; o += BOUNCE_BYTES) {
+    const uint64_t c = std::min(BOUNCE_BYTES, n - o);
+    LLM_HIP(hipMemcpyAsync(m.bounce, (const char*)src + o, c, hipMemcpyDeviceToHost, m.stream));
+    LLM_HIP(hipStreamSynchronize(m.stream));
+    memcpy((char*)dst + o, m.bounce, c);
+  }
+  return 0;
+}
+
+// n bytes caller memory -> device, on the model's stream (synchronous).
+static int copy_in(Model& m, void* dst, const void* src, uint64_t n) {
+  for (uint64_t o = 0; o < n; o += BOUNCE_BYTES) {
+    const uint64_t c = std::min(BOUNCE_BYTES, n - o);
+    LLM_HIP(hipStreamSynchronize(m.stream));
+    memcpy(m.bounce, (const char*)src + o, c);
+    LLM_HIP(hipMemcpyAsync((char*)dst + o, m.bounce, c, hipMemcpyHostToDevice, m.stream));
+  }
+  LLM_HIP(hipStreamSynchronize(m.stream));
   return 0;
 }
 
@@ -168,6 +199,7 @@ static void model_destroy(Model* m) {
   }
   for (void* p : m->allocs) (void)hipFree(p);
   if (m->host) (void)hipHostFree(m->host);
+  if (m->bounce) (void)hipHostFree(m->bounce);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
 }
@@ -685,11 +717,11 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
       cs[((size_t)p * hp + i) * 2] = (float)co;
       cs[((size_t)p * hp + i) * 2 + 1] = (float)sn;
     }
-  if (hipMemcpy(m->cs, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
-    return fail(set_error(LLMHIP_ERR_DEVICE, "llm: RoPE table upload failed"));
   m->host_cap = std::max<uint32_t>(m->ctx + 1, 64);
-  if (hipHostMalloc((void**)&m->host, (size_t)m->host_cap * 4, hipHostMallocDefault) != hipSuccess)
+  if (hipHostMalloc((void**)&m->host, (size_t)m->host_cap * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&m->bounce, BOUNCE_BYTES, hipHostMallocDefault) != hipSuccess)
     return fail(set_error(LLMHIP_ERR_DEVICE, "llm: hipHostMalloc failed"));
+  if ((rc = copy_in(*m, m->cs, cs.data(), cs.size() * 4)) != 0) return fail(rc);
   *out = new llmhip_model{m};
   return 0;
 }
@@ -859,10 +891,10 @@ int llmhip_model_prefill(llmhip_model* h, const int32_t* ids, int n, float* logi
   }
   m.pos = (uint32_t)n;
   m.prompted = full;
-  if (logits) LLM_HIP(hipMemcpyAsync(logits, m.logits, (size_t)m.cfg.vocab * 4, hipMemcpyDeviceToHost, m.stream));
   LLM_HIP(hipMemcpyAsync(m.host, m.tokens + n, 4, hipMemcpyDeviceToHost, m.stream));
   LLM_HIP(hipStreamSynchronize(m.stream));
   if (first) *first = m.host[0];
+  if (logits) LLM_TRY(copy_out(m, logits, m.logits, (uint64_t)m.cfg.vocab * 4));
   m.stats.tokens += n;
   return 0;
 }
@@ -915,10 +947,10 @@ int llmhip_model_peek(llmhip_model* h, const char* name, float* out, uint64_t n)
   LLM_HIP(hipStreamSynchronize(m.stream));
   if (m.kv16 && s.rfind("kvblk.", 0) == 0) {  // binary16 cache: widened on the host
     std::vector<_Float16> h(n);
-    LLM_HIP(hipMemcpy(h.data(), src, n * 2, hipMemcpyDeviceToHost));
+    LLM_TRY(copy_out(m, h.data(), src, n * 2));
     for (uint64_t i = 0; i < n; i++) out[i] = (float)h[i];
   } else {
-    LLM_HIP(hipMemcpy(out, src, n * 4, hipMemcpyDeviceToHost));
+    LLM_TRY(copy_out(m, out, src, n * 4));
   }
   m.stats.submits++;
   return 0;
