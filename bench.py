@@ -60,15 +60,12 @@ def pmc_traffic(cls):
 
 
 def copy_calibration():
-    """A plain 256 MiB device-to-device copy (one elementwise kernel): the
-    known-size reference for the FETCH_SIZE / WRITE_SIZE counters."""
-    import torch
-    x = torch.ones(64 << 20, device="cuda:0")
-    y = torch.empty_like(x)
-    torch.cuda.synchronize()
-    y.copy_(x)
-    torch.cuda.synchronize()
-    log(f"copy calibration: {x.numel() * 4} bytes read, {y.numel() * 4} bytes written")
+    """A plain 256 MiB device-to-device copy (the runtime's copy kernel,
+    __amd_rocclr_copyBuffer): the known-size reference for the FETCH_SIZE /
+    WRITE_SIZE counters."""
+    from llm_amd import kernels
+    kernels.copy_calibration(256 << 20)
+    log(f"copy calibration: {256 << 20} bytes read, {256 << 20} bytes written")
 
 
 def log(*a):
@@ -76,8 +73,7 @@ def log(*a):
 
 
 def generation(args):
-    import torch
-    from llm_amd import llm, synth
+    from llm_amd import kernels, llm, synth
     spec = synth.qwen25(seed=0)
     t0 = time.time()
     path = synth.cached(spec)
@@ -89,7 +85,7 @@ def generation(args):
     for i in range(args.warmup):
         tm = g.Generate(prompt, args.gen, -1)
         log(f"warmup {i}: prefill {tm.PromptTokens / tm.Prefill:.1f} tok/s, decode {tm.Generated / tm.Decode:.1f} tok/s")
-    torch.cuda.synchronize()
+    kernels.synchronize()
     rounds = []
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -97,7 +93,7 @@ def generation(args):
         rounds.append(tm)
         log(f"round {i}: prefill {tm.PromptTokens / tm.Prefill:.1f} tok/s, decode {tm.Generated / tm.Decode:.1f} "
             f"tok/s ({tm.Dispatches} dispatches)")
-    torch.cuda.synchronize()
+    kernels.synchronize()
     wall = time.perf_counter() - t0
     dec = sum(r.Generated for r in rounds) / sum(r.Decode for r in rounds)
     pre = sum(r.PromptTokens for r in rounds) / sum(r.Prefill for r in rounds)
@@ -147,8 +143,7 @@ def loader(args):
     parallel pread straight into pinned staging, one DMA per run on its own
     stream, the repack on the device) for the config-3 file from the page
     cache, against the pinned host-to-device copy rate measured here."""
-    import torch
-    from llm_amd import llm, synth
+    from llm_amd import kernels, llm, synth
     path = synth.cached(synth.qwen25(seed=0))
     f = llm.Parse(path)
     tensor_bytes = sum(t.Size for t in f.Tensors)
@@ -160,18 +155,7 @@ def loader(args):
         ts.append(time.perf_counter() - t0)
         g.close()
     ts = sorted(ts[1:])
-    n = 64 << 20
-    src = torch.empty(n, dtype=torch.uint8, pin_memory=True)
-    dst = torch.empty(n, dtype=torch.uint8, device="cuda")
-    for _ in range(3):
-        dst.copy_(src, non_blocking=True)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(10):
-        dst.copy_(src, non_blocking=True)
-    e1.record()
-    torch.cuda.synchronize()
-    h2d = 10 * n / e0.elapsed_time(e1) * 1e-6
+    h2d = kernels.bench_h2d(64 << 20, 10)
     med = ts[len(ts) // 2]
     res = {"seconds": round(med, 5), "min_seconds": round(ts[0], 5), "tensor_bytes": tensor_bytes,
            "gb_s": round(tensor_bytes / med * 1e-9, 2), "h2d_pinned_gb_s": round(h2d, 2),
@@ -209,20 +193,19 @@ def long_context(args):
 
 def sweep(args):
     import numpy as np
-    import torch
     from llm_amd import kernels, synth
     out = []
     for qtype, tname in ((kernels.Q4_0, "q4_0"), (kernels.Q8_0, "q8_0")):
         for rows, k in SWEEP:
             rng = np.random.default_rng([1, rows, k, qtype])
             m = kernels.QMat(qtype, rows, k, synth.quant_blocks(qtype, rows, k, rng, q8_div=8.0))
-            x = torch.randn((1, k), device="cuda:0")
-            y = torch.empty((1, rows), device="cuda:0")
+            x = kernels.DeviceBuffer.from_numpy(np.random.default_rng([2, rows, k]).standard_normal((1, k), np.float32))
+            y = kernels.DeviceBuffer(rows * 4)
             nbytes = m.gguf_bytes
-            warm = kernels.bench([m], x, y, iters=200, warmup=20)
+            warm = kernels.bench([m], x, y, 1, iters=200, warmup=20)
             copies = [m] + [m.clone() for _ in range(min(4095, max(0, -(-args.hbm_bytes // nbytes) - 1)))]
             iters = max(len(copies), 200)
-            hbm = kernels.bench(copies, x, y, iters=iters, warmup=len(copies))
+            hbm = kernels.bench(copies, x, y, 1, iters=iters, warmup=len(copies))
             out.append({"type": tname, "rows": rows, "k": k, "n": 1, "bytes": nbytes,
                         "hbm_us": round(hbm, 3), "hbm_gbps": round(nbytes / hbm * 1e-3, 1),
                         "hbm_frac": round(nbytes / hbm * 1e-3 / PEAK_HBM_GBS, 4), "copies": len(copies),
@@ -231,7 +214,9 @@ def sweep(args):
                 f"{len(copies)} copies, warm {out[-1]['warm_gbps']} GB/s")
             for c in copies:
                 c.close()
-            torch.cuda.synchronize()
+            x.close()
+            y.close()
+            kernels.synchronize()
     return out
 
 
@@ -280,8 +265,8 @@ def main():
         log("bench.py: this build measures one GPU; the path shards by independent sequences per GPU "
             "(see DESIGN.md), and no multi-GPU figure is taken")
         sys.exit(2)
-    import torch
-    if not torch.cuda.is_available():
+    from llm_amd import _lib
+    if _lib.device_count() < 1:
         log("bench.py: no GPU")
         sys.exit(2)
     if args.copy_calibration:

@@ -79,6 +79,23 @@ LLMHIP_API int llmhip_device_count(int* n);
 /* The device's limits (memory_budget = its total memory). */
 LLMHIP_API int llmhip_device_limits(int ordinal, llmhip_limits* out);
 
+/* Device memory for callers with no allocator of their own (the tests and
+ * benchmarks of the kernel-level entry points): zeroed at allocation.  Reads
+ * and writes are synchronous and pass through pinned staging, never DMA to
+ * or from caller memory.  No counterpart in the reference (its buffers are
+ * webgpu Buffers). */
+LLMHIP_API int llmhip_buffer_alloc(int ordinal, uint64_t bytes, void** out);
+LLMHIP_API void llmhip_buffer_free(void* dev);
+LLMHIP_API int llmhip_buffer_write(void* dev, const void* host, uint64_t bytes);
+LLMHIP_API int llmhip_buffer_read(void* host, const void* dev, uint64_t bytes);
+LLMHIP_API int llmhip_device_synchronize(int ordinal);
+/* Measurement helpers: the pinned host-to-device copy rate in GB/s over
+ * `iters` copies of `bytes` (the bound of the loader), and one
+ * device-to-device copy of `bytes` (a copy of known size, for scaling the
+ * FETCH_SIZE / WRITE_SIZE counters). */
+LLMHIP_API int llmhip_bench_h2d(int ordinal, uint64_t bytes, int iters, float* gbps);
+LLMHIP_API int llmhip_copy_calibration(int ordinal, uint64_t bytes);
+
 /* --------------------------------------------------- quantised matrices */
 
 /* A quantised [rows][k] matrix on one device, repacked on the device from raw

@@ -67,6 +67,13 @@ SIGNATURES = [
     ("llmhip_last_error", ctypes.c_char_p, []),
     ("llmhip_device_count", I, [ctypes.POINTER(I)]),
     ("llmhip_device_limits", I, [I, ctypes.POINTER(Limits)]),
+    ("llmhip_buffer_alloc", I, [I, U64, ctypes.POINTER(P)]),
+    ("llmhip_buffer_free", None, [P]),
+    ("llmhip_buffer_write", I, [P, P, U64]),
+    ("llmhip_buffer_read", I, [P, P, U64]),
+    ("llmhip_device_synchronize", I, [I]),
+    ("llmhip_bench_h2d", I, [I, U64, I, ctypes.POINTER(F)]),
+    ("llmhip_copy_calibration", I, [I, U64]),
     ("llmhip_qmat_create", I, [I, U32, U64, U64, ctypes.POINTER(P)]),
     ("llmhip_qmat_upload", I, [P, P, U64, U64]),
     ("llmhip_qmat_dequant", I, [P, P, P]),

@@ -2,7 +2,9 @@
 // device layer: the bounded GGUF v3 header parser (gguf/gguf.go), ConfigFrom
 // (config.go), NewGPU's streaming loader (gpu.go:465-764 with the repack now
 // on the device), Generate, PrefillLogits and Peek (gpu.go:904-1043).
+#include <execinfo.h>
 #include <fcntl.h>
+#include <signal.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
@@ -370,6 +372,49 @@ using namespace llm;
 
 // Tunables of the Go package (gpu.go:20-23,165,1046-1054).
 static int g_decode_batch = 8, g_prefill_batch = 64, g_f16kv = 0, g_exact = 0;
+
+// With LLMHIP_CRASH_TRACE set when the library loads, a SIGSEGV, SIGBUS or
+// SIGABRT first writes the native stack to stderr (frames as path(+offset),
+// for addr2line on the library), then goes to the handler that was installed
+// before (Python's faulthandler, say), or to the default action.
+namespace {
+struct sigaction g_prev_act[3];
+const int g_trace_sigs[3] = {SIGSEGV, SIGBUS, SIGABRT};
+
+void crash_trace(int sig, siginfo_t* info, void* uctx) {
+  static const char head[] = "llmhip: fatal signal, native stack:\n";
+  (void)!write(2, head, sizeof head - 1);
+  void* frames[64];
+  int n = backtrace(frames, 64);
+  backtrace_symbols_fd(frames, n, 2);
+  for (int i = 0; i < 3; i++) {
+    if (g_trace_sigs[i] != sig) continue;
+    sigaction(sig, &g_prev_act[i], nullptr);
+    if ((g_prev_act[i].sa_flags & SA_SIGINFO) && g_prev_act[i].sa_sigaction) {
+      g_prev_act[i].sa_sigaction(sig, info, uctx);
+    } else if (g_prev_act[i].sa_handler != SIG_DFL && g_prev_act[i].sa_handler != SIG_IGN) {
+      g_prev_act[i].sa_handler(sig);
+    }
+    break;
+  }
+  raise(sig);  // the default action, if the previous handler returned
+}
+
+__attribute__((constructor)) void install_crash_trace() {
+  const char* e = getenv("LLMHIP_CRASH_TRACE");
+  if (!e || !*e || *e == '0') return;
+  void* warm[2];
+  (void)backtrace(warm, 2);  // loads the unwinder now, not inside the handler
+  for (int i = 0; i < 3; i++) {
+    struct sigaction a;
+    memset(&a, 0, sizeof a);
+    a.sa_sigaction = crash_trace;
+    a.sa_flags = SA_SIGINFO | SA_ONSTACK;
+    sigemptyset(&a.sa_mask);
+    sigaction(g_trace_sigs[i], &a, &g_prev_act[i]);
+  }
+}
+}  // namespace
 static const int kMaxBatch = 16;
 
 struct llm_gguf {

@@ -196,17 +196,116 @@ int llmhip_device_limits(int ordinal, llmhip_limits* out) {
   return 0;
 }
 
+int llmhip_buffer_alloc(int ordinal, uint64_t bytes, void** out) {
+  clear_error();
+  *out = nullptr;
+  LLM_HIP(hipSetDevice(ordinal));
+  LLM_HIP(hipMalloc(out, bytes ? bytes : 1));
+  if (hipMemset(*out, 0, bytes ? bytes : 1) != hipSuccess) {
+    (void)hipFree(*out);
+    *out = nullptr;
+    return set_error(LLMHIP_ERR_DEVICE, "llm: hipMemset failed");
+  }
+  return 0;
+}
+
+void llmhip_buffer_free(void* dev) {
+  if (dev) (void)hipFree(dev);
+}
+
+// Synchronous copies between caller memory and the device in pieces through
+// a pinned staging buffer of this call.
+constexpr uint64_t BUFFER_STAGE = 4ull << 20;
+
+static int buffer_copy(void* dst, const void* src, uint64_t bytes, bool to_dev) {
+  clear_error();
+  if (!bytes) return 0;
+  uint8_t* stage = nullptr;
+  LLM_HIP(hipHostMalloc((void**)&stage, std::min(bytes, BUFFER_STAGE), hipHostMallocDefault));
+  int rc = 0;
+  for (uint64_t o = 0; o < bytes && rc == 0; o += BUFFER_STAGE) {
+    const uint64_t c = std::min(BUFFER_STAGE, bytes - o);
+    if (to_dev) {
+      memcpy(stage, (const uint8_t*)src + o, c);
+      if (hipMemcpy((uint8_t*)dst + o, stage, c, hipMemcpyHostToDevice) != hipSuccess)
+        rc = set_error(LLMHIP_ERR_DEVICE, "llm: copy to the device failed");
+    } else {
+      if (hipMemcpy(stage, (const uint8_t*)src + o, c, hipMemcpyDeviceToHost) != hipSuccess)
+        rc = set_error(LLMHIP_ERR_DEVICE, "llm: copy from the device failed");
+      else
+        memcpy((uint8_t*)dst + o, stage, c);
+    }
+  }
+  (void)hipHostFree(stage);
+  return rc;
+}
+
+int llmhip_buffer_write(void* dev, const void* host, uint64_t bytes) { return buffer_copy(dev, host, bytes, true); }
+
+int llmhip_buffer_read(void* host, const void* dev, uint64_t bytes) { return buffer_copy(host, dev, bytes, false); }
+
+int llmhip_device_synchronize(int ordinal) {
+  clear_error();
+  LLM_HIP(hipSetDevice(ordinal));
+  LLM_HIP(hipDeviceSynchronize());
+  return 0;
+}
+
+int llmhip_bench_h2d(int ordinal, uint64_t bytes, int iters, float* gbps) {
+  clear_error();
+  if (iters < 1 || bytes == 0) return set_error(LLMHIP_ERR_ARG, "llm: h2d bench of %d copies", iters);
+  LLM_HIP(hipSetDevice(ordinal));
+  uint8_t *h = nullptr, *d = nullptr;
+  hipStream_t s = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = 0;
+  float ms = 0;
+  if (hipHostMalloc((void**)&h, bytes, hipHostMallocDefault) != hipSuccess || hipMalloc((void**)&d, bytes) != hipSuccess ||
+      hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
+      hipEventCreate(&e1) != hipSuccess)
+    rc = set_error(LLMHIP_ERR_DEVICE, "llm: h2d bench setup failed");
+  for (int i = 0; i < 3 && rc == 0; i++)
+    if (hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, s) != hipSuccess) rc = LLMHIP_ERR_DEVICE;
+  if (rc == 0 && hipEventRecord(e0, s) != hipSuccess) rc = LLMHIP_ERR_DEVICE;
+  for (int i = 0; i < iters && rc == 0; i++)
+    if (hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, s) != hipSuccess) rc = LLMHIP_ERR_DEVICE;
+  if (rc == 0 && (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                  hipEventElapsedTime(&ms, e0, e1) != hipSuccess))
+    rc = LLMHIP_ERR_DEVICE;
+  if (rc == LLMHIP_ERR_DEVICE) set_error(LLMHIP_ERR_DEVICE, "llm: h2d bench failed");
+  if (s) (void)hipStreamSynchronize(s);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (s) (void)hipStreamDestroy(s);
+  if (d) (void)hipFree(d);
+  if (h) (void)hipHostFree(h);
+  if (rc == 0) *gbps = (float)((double)bytes * iters / (ms * 1e-3) * 1e-9);
+  return rc;
+}
+
+int llmhip_copy_calibration(int ordinal, uint64_t bytes) {
+  clear_error();
+  LLM_HIP(hipSetDevice(ordinal));
+  void *a = nullptr, *b = nullptr;
+  int rc = 0;
+  if (hipMalloc(&a, bytes) != hipSuccess || hipMalloc(&b, bytes) != hipSuccess || hipMemset(a, 1, bytes) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess || hipMemcpy(b, a, bytes, hipMemcpyDeviceToDevice) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess)
+    rc = set_error(LLMHIP_ERR_DEVICE, "llm: calibration copy failed");
+  if (a) (void)hipFree(a);
+  if (b) (void)hipFree(b);
+  return rc;
+}
+
+// A matrix holds only its device memory; an upload creates the matrix's
+// stream on first use and pinned staging for the duration of the call (a
+// benchmark rotates thousands of clones, which never upload).
 int llmhip_qmat_create(int ordinal, uint32_t ggml_type, uint64_t rows, uint64_t k, llmhip_qmat** out) {
   clear_error();
   *out = nullptr;
   llmhip_qmat* q = new llmhip_qmat();
   int rc = qmat_alloc(&q->m, ordinal, ggml_type, rows, k);
-  if (rc == 0 && hipStreamCreateWithFlags(&q->stream, hipStreamNonBlocking) != hipSuccess)
-    rc = set_error(LLMHIP_ERR_DEVICE, "llm: hipStreamCreate failed");
-  if (rc == 0) rc = stager_init(&q->st, ordinal, 4ull << 20, q->stream);
   if (rc != 0) {
-    stager_free(&q->st);
-    if (q->stream) (void)hipStreamDestroy(q->stream);
     qmat_release(&q->m);
     delete q;
     return rc;
@@ -217,15 +316,26 @@ int llmhip_qmat_create(int ordinal, uint32_t ggml_type, uint64_t rows, uint64_t 
 
 int llmhip_qmat_upload(llmhip_qmat* q, const void* raw, uint64_t nbytes, uint64_t byte_offset) {
   clear_error();
-  LLM_TRY(qmat_upload(&q->st, q->m, raw, nbytes, byte_offset, 0));
-  LLM_HIP(hipStreamSynchronize(q->stream));
+  LLM_HIP(hipSetDevice(q->m.device));
+  if (!q->stream) LLM_HIP(hipStreamCreateWithFlags(&q->stream, hipStreamNonBlocking));
+  int rc = stager_init(&q->st, q->m.device, 4ull << 20, q->stream);
+  if (rc == 0) rc = qmat_upload(&q->st, q->m, raw, nbytes, byte_offset, 0);
+  if (hipStreamSynchronize(q->stream) != hipSuccess && rc == 0)
+    rc = set_error(LLMHIP_ERR_DEVICE, "llm: upload failed");
+  stager_free(&q->st);
+  return rc;
+}
+
+// Work queued by an upload is complete before a product reads the matrix.
+static int qmat_ready(llmhip_qmat* q) {
+  LLM_HIP(hipSetDevice(q->m.device));
+  if (q->stream) LLM_HIP(hipStreamSynchronize(q->stream));
   return 0;
 }
 
 int llmhip_qmat_dequant(llmhip_qmat* q, float* out_dev, void* hip_stream) {
   clear_error();
-  LLM_HIP(hipSetDevice(q->m.device));
-  LLM_HIP(hipStreamSynchronize(q->stream));
+  LLM_TRY(qmat_ready(q));
   return qmat_dequant(q->m, out_dev, (hipStream_t)hip_stream);
 }
 
@@ -254,8 +364,7 @@ int llmhip_qmat_gemv(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, in
   clear_error();
   GemvArgs a;
   LLM_TRY(qmat_gemv_args(q, x_dev, y_dev, n, &a));
-  LLM_HIP(hipSetDevice(q->m.device));
-  LLM_HIP(hipStreamSynchronize(q->stream));
+  LLM_TRY(qmat_ready(q));
   return qmat_launch(q, a, accumulate ? EPI_ACC : EPI_STORE, (hipStream_t)hip_stream);
 }
 
@@ -263,8 +372,7 @@ int llmhip_qmat_gemv_q8(llmhip_qmat* q, const float* x_dev, float* y_dev, int n,
   clear_error();
   GemvArgs a;
   LLM_TRY(qmat_gemv_args(q, x_dev, y_dev, n, &a));
-  LLM_HIP(hipSetDevice(q->m.device));
-  LLM_HIP(hipStreamSynchronize(q->stream));
+  LLM_TRY(qmat_ready(q));
   return qmat_launch(q, a, EPI_STORE, (hipStream_t)hip_stream, PRO_PLAIN | PRO_Q8);
 }
 
@@ -282,7 +390,7 @@ int llmhip_qmat_bench(llmhip_qmat* const* mats, int count, const float* x_dev, f
     if (mats[i]->m.g.q.type != mats[0]->m.g.q.type || mats[i]->m.g.rows != mats[0]->m.g.rows ||
         mats[i]->m.g.k != mats[0]->m.g.k)
       return set_error(LLMHIP_ERR_ARG, "llm: bench matrices differ in shape or type");
-    LLM_HIP(hipStreamSynchronize(mats[i]->stream));
+    LLM_TRY(qmat_ready(mats[i]));
   }
   LLM_HIP(hipSetDevice(mats[0]->m.device));
   const uint32_t t = mats[0]->m.g.q.type;

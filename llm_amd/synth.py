@@ -16,9 +16,12 @@ formats of cpu.go:164-215).  Distributions:
 Each tensor draws from its own generator seeded by (model seed, crc32(name)),
 so a tensor's bytes do not depend on which other tensors the file holds.
 """
+import atexit
 import dataclasses
 import os
+import shutil
 import struct
+import tempfile
 import zlib
 
 import numpy as np
@@ -212,7 +215,7 @@ def write(path, spec, alignment=32):
         hdr += struct.pack("<IQ", qt, off)
         off = (off + size + alignment - 1) // alignment * alignment
     pad = (-len(hdr)) % alignment
-    tmp = path + ".tmp"
+    tmp = f"{path}.{os.getpid()}.tmp"  # a writer of its own, then one atomic rename
     with open(tmp, "wb") as f:
         f.write(hdr)
         f.write(b"\0" * pad)
@@ -227,9 +230,25 @@ def write(path, spec, alignment=32):
     return path
 
 
+_PRIVATE = None
+
+
+def _private_dir():
+    """A directory of this process, created on first use and removed at exit.
+    Files under a shared temporary directory with deterministic names can be
+    rewritten by another process (another test run or job on the same host)
+    between the GPU loading a model and the oracle loading it."""
+    global _PRIVATE
+    if _PRIVATE is None:
+        _PRIVATE = tempfile.mkdtemp(prefix="llm_synth_")
+        atexit.register(shutil.rmtree, _PRIVATE, True)
+    return _PRIVATE
+
+
 def cached(spec, directory=None):
-    """Write the model once into `directory` (default $LLM_SYNTH_DIR or /tmp) and reuse it."""
-    directory = directory or os.environ.get("LLM_SYNTH_DIR", "/tmp")
+    """Write the model once into `directory` (default $LLM_SYNTH_DIR, else a
+    directory of this process) and reuse it."""
+    directory = directory or os.environ.get("LLM_SYNTH_DIR") or _private_dir()
     os.makedirs(directory, exist_ok=True)
     key = zlib.crc32(repr(dataclasses.asdict(dataclasses.replace(spec, types={}))).encode()
                      + repr(sorted((k, [spec.mat_type(k, l) for l in range(spec.layers)])

@@ -108,31 +108,49 @@ def test_qwen25_f16_kv_cache(gpu):
 # independent float64 restatement of tests/test_oracle.py shows the same
 # 2.7e-3 / 3.6e-3 steps against the oracle on the same tiny-model inputs).
 # The products themselves are pinned on identical inputs at the summation
-# bound (tests/test_gemv_gpu.py::test_exact_ggml_gemv).  End to end: prompts
-# of 1-4 tokens (few codes, no flip) within 1e-4; longer runs within the flip
-# level -- EXACT_TOL on the tiny models, where one flip moves the logits by
-# 2.7e-3 to 6.6e-3 (measured, GPU and float64 restatement alike), and 5e-3 and
-# closer to the oracle's ExactGGML than to its f32 mode at the Qwen shape --
-# with greedy tokens equal up to near-ties at that level.
+# bound (tests/test_gemv_gpu.py::test_exact_ggml_gemv).  End to end every
+# run is held to the flip level -- EXACT_TOL on the tiny models, where one
+# flip moves the logits by 2.7e-3 to 6.6e-3 (measured, GPU and float64
+# restatement alike), and 5e-3 and closer to the oracle's ExactGGML than to
+# its f32 mode at the Qwen shape -- with greedy tokens equal up to near-ties
+# at that level.  A flip can happen at any prompt length: a 3-token prompt of
+# the mixed-type model was measured with its first layer's output within
+# 7.5e-9 of the oracle's and one flip in the second layer (225 of 256 rows of
+# its output 1e-4..4e-4 off, logits 4.1e-3), while the same prompts in f32
+# mode stay below 1e-6 (test_short_prompts).
 EXACT_TOL = 1e-2
 EXACT_TINY = dict(TINY, **{"qwen2-split": lambda: synth.tiny_qwen(seed=8)})
 
 
-@pytest.mark.parametrize("name", list(TINY))
-def test_exact_ggml_short(gpu, name):
-    """ExactGGML (cpu.go:15-21, 117-140, 166-214) through the decode kernels:
-    prompts of 1 to 4 tokens, logits within 1e-4 of the oracle's."""
-    from oracle import cpuref
-    spec = TINY[name]()
-    g, cpu = _open(spec, 128, exact=True)
+def _short_prompts(g, cpu, spec):
+    out = []
     for plen in (1, 2, 3, 4):
         prompt = list(synth.prompt(20 + plen, plen, spec.vocab))
         cpu.reset()
         for t in prompt:
             want = cpu.forward(t)
-        rel = rel_err(g.PrefillLogits(prompt), want)
-        print(f"prompt {plen}: logits relative error {rel:.3e}", flush=True)
-        assert rel <= LOGIT_TOL
+        out.append(rel_err(g.PrefillLogits(prompt), want))
+        print(f"prompt {plen}: logits relative error {out[-1]:.3e}", flush=True)
+    return out
+
+
+@pytest.mark.parametrize("name", list(TINY))
+def test_short_prompts(gpu, name):
+    """Prompts of 1 to 4 tokens run the decode tile kernel with 1, 2 and 4
+    token slots (one pass each): logits within 1e-4 of the oracle's."""
+    spec = TINY[name]()
+    g, cpu = _open(spec, 128)
+    assert max(_short_prompts(g, cpu, spec)) <= LOGIT_TOL
+
+
+@pytest.mark.parametrize("name", list(TINY))
+def test_exact_ggml_short(gpu, name):
+    """ExactGGML (cpu.go:15-21, 117-140, 166-214) through the decode kernels
+    with 1, 2 and 4 token slots: prompts of 1 to 4 tokens, logits within the
+    flip level of the oracle's."""
+    spec = TINY[name]()
+    g, cpu = _open(spec, 128, exact=True)
+    assert max(_short_prompts(g, cpu, spec)) <= EXACT_TOL
 
 
 @pytest.mark.parametrize("name,prompt_len,n", [("llama", 150, 40), ("qwen2", 150, 40), ("qwen2-mixed", 150, 40),
