@@ -27,6 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_MFMA_F16_TFLOPS = 2500.0  # dense f16/bf16
 METRIC = "decode & prefill tok/s at Qwen2.5-0.5B shape; Q4_0 GEMV HBM GB/s vs peak"
 SWEEP = [(576, 576), (1536, 576), (576, 1536), (896, 896), (4864, 896), (896, 4864), (151936, 896)]
 # HBM bytes per launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
@@ -136,6 +137,22 @@ def generation(args):
         "classes": classes, "step_kernel_us": step_kernel_us, "roofline": roofline,
         "gemv_aggregate_gbps": gemv_all, "dispatches_per_token": dispatches,
     }
+
+
+def prefill_roofline(tok_s):
+    """MFMA utilisation of the prefill chunks: the layers'
+    matrix FLOPs (2 per weight per token) at the measured prefill rate, against
+    MI355X's dense f16 MFMA peak."""
+    from llm_amd import synth
+    s = synth.qwen25(seed=0)
+    kvd = s.kv_heads * (s.embd // s.heads)
+    per_token = 2 * s.layers * (s.embd * (s.embd + 2 * kvd) + s.embd * s.embd + 3 * s.ff * s.embd)
+    achieved = per_token * tok_s * 1e-12
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_MFMA_F16_TFLOPS, 5), "flops_per_token": per_token,
+            "note": "layer matrix FLOPs over the whole prefill time (prep, attention and the head included); the "
+                    "products run on v_mfma_f32_16x16x32_f16 with each activation split into two f16 rows, so the "
+                    "MFMA units execute twice these FLOPs"}
 
 
 def loader(args):
@@ -286,6 +303,7 @@ def main():
         "prefill_tok_s": round(r["prefill"], 2),
         "rounds": r["rounds"],
         "roofline": r["roofline"],
+        "prefill_roofline": prefill_roofline(r["prefill"]),
         "decode_step": {"kernel_us": round(r["step_kernel_us"], 2), "wall_us": round(1e6 / r["value"], 2),
                         "dispatches_per_token": r["dispatches_per_token"],
                         "gemv_aggregate_gbps": round(r["gemv_aggregate_gbps"], 1), "classes": r["classes"]},
