@@ -1078,29 +1078,134 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
   }
 }
 
-// Prefill matrix product.  A workgroup owns two 16-row tiles and a range of
-// token groups (grid.y); its four waves split the blocks of k (split-K) and
-// add their partials in LDS in a fixed order.  A weight word is dequantised
-// once and feeds one MFMA per token group and tile; the activation operands
-// come from prep_kernel's buffer (shared by all workgroups through L2).
-constexpr int GT = 2;  // tiles per workgroup
+// Prefill matrix product.  A workgroup owns GT 16-row tiles and NG token
+// groups of 8 (grid.y walks the groups); its waves split the block groups of
+// k (split-K).  Each wave pipelines its block groups through two register
+// sets: the weights and activation operands of its next group are in flight
+// while the current one goes through the MFMA.  Every load in that loop is
+// unconditional (indices clamped into the matrix and the prepared
+// activations), so the waits count only what is needed.  A weight word is
+// dequantised once and feeds NG MFMAs per tile, an activation operand GT.
+// The waves' partials meet in LDS; wave w then adds, in wave order, the
+// (tile, token group) pairs w, w + waves, ... and runs their row epilogues.
+constexpr int GEMM_MAXW = 8;  // waves per workgroup
 
-template <uint32_t QT, int EPI, bool Q8>
-__global__ __launch_bounds__(256) void gemm_kernel(GemvArgs a) {
-  typedef QT_<QT> T;
-  __shared__ float red[3][64][GT * 8 * 2];
+// The activation side of one block group: 4 blocks x NG token groups of MFMA
+// operands, and per token block scalars where the product needs them (Q8: the
+// activation blocks' d; Q4_1: the block sums that meet m).
+template <uint32_t QT, bool Q8, int NG>
+struct XUnit {
+  h8 x[4][NG];
+  float xd[Q8 ? 4 : 1][Q8 ? NG : 1][2];
+  float xb[QT == LLMHIP_Q4_1 ? 4 : 1][QT == LLMHIP_Q4_1 ? NG : 1][2];
+};
+
+// Blocks b0 .. b0+3 (clamped to bmax) for the token groups g0 .. g0+NG-1
+// (clamped to the last prepared group).
+template <uint32_t QT, bool Q8, int NG>
+__device__ __forceinline__ void load_xunit(XUnit<QT, Q8, NG>& X, const GemvArgs& a, uint32_t b0, uint32_t bmax,
+                                           uint32_t g0, int lane, int q) {
+  const h8* xp = (const h8*)a.xp;
+  const uint32_t nb = a.nb, gl = a.tg - 1;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t b = min(b0 + j, bmax);
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+      const uint32_t gg = min(g0 + g, gl);
+      X.x[j][g] = xp[((uint64_t)gg * nb + b) * 64 + lane];
+      const uint64_t iA = (uint64_t)(gg * 8 + 2 * q) * nb + b;
+      if (Q8) {
+        X.xd[j][g][0] = a.xdx[iA];
+        X.xd[j][g][1] = a.xdx[iA + nb];
+      }
+      if (QT == LLMHIP_Q4_1) {
+        X.xb[j][g][0] = a.xbsum[iA];
+        X.xb[j][g][1] = a.xbsum[iA + nb];
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t u4c(const uint4& v, int j) {
+  return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
+}
+
+// Block j of a weight unit: the B operand, d and (Q4_1) m.  A group unit
+// holds a 4-block record; the tail unit (TAIL) holds block j in component j.
+template <uint32_t QT, bool TAIL>
+__device__ __forceinline__ void unit_block(const WUnit& u, int j, h8& B, float& d, float& m) {
+  m = 0.f;
+  if (QT == LLMHIP_Q8_0) {
+    if (TAIL) {
+      B = dq8(u4c(u.w0, j), u4c(u.w1, j));
+      d = f16_hw(u4c(u.sv, j) & 0xffff);
+    } else {
+      const uint4 ww = j < 2 ? u.w0 : u.w1;
+      B = (j % 2 == 0) ? dq8(ww.x, ww.y) : dq8(ww.z, ww.w);
+      const uint32_t sw = j < 2 ? u.sv.x : u.sv.y;
+      d = f16_hw(j % 2 == 0 ? sw & 0xffff : sw >> 16);
+    }
+  } else if (QT == LLMHIP_Q4_1) {
+    B = dq4<true>(u4c(u.w0, j));
+    const uint32_t sw = u4c(u.sv, j);
+    d = f16_hw(sw & 0xffff);
+    m = f16_hw(sw >> 16);
+  } else {
+    B = dq4<false>(u4c(u.w0, j));
+    if (TAIL) {
+      d = f16_hw(u4c(u.sv, j) & 0xffff);
+    } else {
+      const uint32_t sw = j < 2 ? u.sv.x : u.sv.y;
+      d = f16_hw(j % 2 == 0 ? sw & 0xffff : sw >> 16);
+    }
+  }
+}
+
+// The MFMAs of one unit (nblk of its 4 blocks) into acc[tile][group][token of the pair].
+template <uint32_t QT, bool Q8, int GT, int NG, bool TAIL>
+__device__ __forceinline__ void gemm_unit(float (&acc)[GT][NG][2], const WUnit (&w)[GT], const XUnit<QT, Q8, NG>& X,
+                                          int nblk) {
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    if (j >= nblk) break;
+    h8 B[GT];
+    float d[GT], mm[GT];
+#pragma unroll
+    for (int u = 0; u < GT; u++) unit_block<QT, TAIL>(w[u], j, B[u], d[u], mm[u]);
+#pragma unroll
+    for (int g = 0; g < NG; g++)
+#pragma unroll
+      for (int u = 0; u < GT; u++) {
+        const f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(X.x[j][g], B[u], f4{0, 0, 0, 0}, 0, 0, 0);
+        if (Q8) {  // ggml's block product, as in mfma_block
+          float pA = __fmul_rn(__fmul_rn(d[u], X.xd[j][g][0]), D[0] + D[1]);
+          float pB = __fmul_rn(__fmul_rn(d[u], X.xd[j][g][1]), D[2] + D[3]);
+          if (QT == LLMHIP_Q4_1) {
+            pA = __fadd_rn(pA, __fmul_rn(mm[u], X.xb[j][g][0]));
+            pB = __fadd_rn(pB, __fmul_rn(mm[u], X.xb[j][g][1]));
+          }
+          acc[u][g][0] += pA;
+          acc[u][g][1] += pB;
+        } else {
+          acc[u][g][0] += d[u] * (D[0] + D[1]);
+          acc[u][g][1] += d[u] * (D[2] + D[3]);
+          if (QT == LLMHIP_Q4_1) {
+            acc[u][g][0] += mm[u] * X.xb[j][g][0];
+            acc[u][g][1] += mm[u] * X.xb[j][g][1];
+          }
+        }
+      }
+  }
+}
+
+template <uint32_t QT, int EPI, bool Q8, int GT, int NG>
+__global__ __launch_bounds__(64 * GEMM_MAXW) void gemm_kernel(GemvArgs a) {
+  __shared__ float red[GEMM_MAXW][GT * NG * 2][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int r = lane & 15, q = lane >> 4;
-  const uint32_t nb = a.nb, TG = a.tg;
-  const uint32_t tgpw = (TG + gridDim.y - 1) / gridDim.y, g0 = blockIdx.y * tgpw;
-  const uint32_t ngr = min(tgpw, TG - min(TG, g0));  // token groups of this workgroup
-  const uint32_t tile0 = blockIdx.x * GT;
-  const h8* xp = (const h8*)a.xp;
-  float acc[GT][8][2];
-#pragma unroll
-  for (int u = 0; u < GT; u++)
-#pragma unroll
-    for (int g = 0; g < 8; g++) acc[u][g][0] = acc[u][g][1] = 0.f;
+  const uint32_t W = blockDim.x >> 6, nb = a.nb, ng = a.ng;
+  const uint32_t g0 = blockIdx.y * NG, tile0 = blockIdx.x * GT;
   bool tv[GT];
   uint32_t tt[GT];
 #pragma unroll
@@ -1108,124 +1213,70 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvArgs a) {
     tv[u] = tile0 + u < a.tiles;
     tt[u] = tv[u] ? tile0 + u : tile0;
   }
-  // one block b for both tiles: B[u] weights, d[u] / m[u] scales
-  auto block = [&](uint32_t b, const h8* B, const float* d, const float* mm) {
-#pragma unroll
-    for (int g = 0; g < 8; g++) {
-      if (g >= (int)ngr) break;
-      const h8 A = xp[((uint64_t)(g0 + g) * nb + b) * 64 + lane];
-#pragma unroll
-      for (int u = 0; u < GT; u++) {
-        f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[u], f4{0, 0, 0, 0}, 0, 0, 0);
-        if (Q8) {  // ggml's block product, as in mfma_block
-          const uint64_t iA = (uint64_t)((g0 + g) * 8 + 2 * q) * nb + b, iB = iA + nb;
-          float pA = __fmul_rn(__fmul_rn(d[u], a.xdx[iA]), D[0] + D[1]);
-          float pB = __fmul_rn(__fmul_rn(d[u], a.xdx[iB]), D[2] + D[3]);
-          if (QT == LLMHIP_Q4_1) {
-            pA = __fadd_rn(pA, __fmul_rn(mm[u], a.xbsum[iA]));
-            pB = __fadd_rn(pB, __fmul_rn(mm[u], a.xbsum[iB]));
-          }
-          acc[u][g][0] += pA;
-          acc[u][g][1] += pB;
-          continue;
-        }
-        acc[u][g][0] += d[u] * (D[0] + D[1]);
-        acc[u][g][1] += d[u] * (D[2] + D[3]);
-        if (QT == LLMHIP_Q4_1) {
-          acc[u][g][0] += mm[u] * a.xbsum[(uint64_t)((g0 + g) * 8 + 2 * q) * nb + b];
-          acc[u][g][1] += mm[u] * a.xbsum[(uint64_t)((g0 + g) * 8 + 2 * q + 1) * nb + b];
-        }
-      }
-    }
-  };
-  for (uint32_t g4 = wave; g4 < a.ng; g4 += 4) {
-    uint4 w0[GT], w1[GT], sv[GT];
-#pragma unroll
-    for (int u = 0; u < GT; u++) {
-      WUnit wu;
-      load_unit<QT>(wu, a.qs, nb, tt[u], g4, a.ng, a.tail, lane, r);
-      w0[u] = wu.w0;
-      w1[u] = wu.w1;
-      sv[u] = wu.sv;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      h8 B[GT];
-      float d[GT], mm[GT];
-#pragma unroll
-      for (int u = 0; u < GT; u++) {
-        const uint32_t wj = j == 0 ? w0[u].x : j == 1 ? w0[u].y : j == 2 ? w0[u].z : w0[u].w;
-        if (QT == LLMHIP_Q8_0) {
-          const uint4 ww = j < 2 ? w0[u] : w1[u];
-          B[u] = (j % 2 == 0) ? dq8(ww.x, ww.y) : dq8(ww.z, ww.w);
-          const uint32_t sw = j < 2 ? sv[u].x : sv[u].y;
-          d[u] = f16_hw(j % 2 == 0 ? sw & 0xffff : sw >> 16);
-          mm[u] = 0;
-        } else if (QT == LLMHIP_Q4_1) {
-          B[u] = dq4<true>(wj);
-          const uint32_t sw = j == 0 ? sv[u].x : j == 1 ? sv[u].y : j == 2 ? sv[u].z : sv[u].w;
-          d[u] = f16_hw(sw & 0xffff);
-          mm[u] = f16_hw(sw >> 16);
-        } else {
-          B[u] = dq4<false>(wj);
-          const uint32_t sw = j < 2 ? sv[u].x : sv[u].y;
-          d[u] = f16_hw(j % 2 == 0 ? sw & 0xffff : sw >> 16);
-          mm[u] = 0;
-        }
-      }
-      block(4 * g4 + j, B, d, mm);
-    }
-  }
-  if (a.tail && (a.ng % 4) == (uint32_t)wave) {
-    for (uint32_t j = 0; j < a.tail; j++) {
-      const uint32_t b = 4 * a.ng + j;
-      h8 B[GT];
-      float d[GT], mm[GT];
-#pragma unroll
-      for (int u = 0; u < GT; u++) {
-        const uint8_t* tb = a.qs + Lay<QT>::tile(tt[u], nb);
-        const uint8_t* qq = tb + Lay<QT>::qoff(b, lane, a.ng, a.tail);
-        const uint8_t* s = tb + Lay<QT>::soff(b, r, nb, a.ng, a.tail);
-        if (QT == LLMHIP_Q8_0) B[u] = dq8(*(const uint32_t*)qq, *(const uint32_t*)(qq + 4));
-        else B[u] = dq4<QT == LLMHIP_Q4_1>(*(const uint32_t*)qq);
-        d[u] = f16_hw(s[0] | s[1] << 8);
-        mm[u] = QT == LLMHIP_Q4_1 ? f16_hw(s[2] | s[3] << 8) : 0.f;
-      }
-      block(b, B, d, mm);
-    }
-  }
-  // split-K: waves 1..3 hand their partials to wave 0, which adds them in order
-  if (wave > 0) {
-#pragma unroll
-    for (int u = 0; u < GT; u++)
-#pragma unroll
-      for (int g = 0; g < 8; g++) {
-        red[wave - 1][lane][(u * 8 + g) * 2] = acc[u][g][0];
-        red[wave - 1][lane][(u * 8 + g) * 2 + 1] = acc[u][g][1];
-      }
-  }
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int w = 0; w < 3; w++)
-#pragma unroll
-    for (int u = 0; u < GT; u++)
-#pragma unroll
-      for (int g = 0; g < 8; g++) {
-        acc[u][g][0] += red[w][lane][(u * 8 + g) * 2];
-        acc[u][g][1] += red[w][lane][(u * 8 + g) * 2 + 1];
-      }
+  float acc[GT][NG][2];
 #pragma unroll
   for (int u = 0; u < GT; u++)
 #pragma unroll
-    for (int g = 0; g < 8; g++) {
-      if (g >= (int)ngr) break;
-      const uint32_t tokA = (g0 + g) * 8 + 2 * q, tokB = tokA + 1;
-      const bool okA = tokA < a.ntok, okB = tokB < a.ntok;
-      const float vA = okA ? ldexpf(acc[u][g][0], -a.xexp[tokA]) : 0.f;
-      const float vB = okB ? ldexpf(acc[u][g][1], -a.xexp[tokB]) : 0.f;
-      row_epilogue<EPI>(a, tile0 + u, r, tv[u], tokA, okA, vA, tokB, okB, vB);
+    for (int g = 0; g < NG; g++) acc[u][g][0] = acc[u][g][1] = 0.f;
+
+  // groups wave, wave + W, ...: two register sets, A and B, in turn
+  const uint32_t cnt = ng > (uint32_t)wave ? (ng - wave + W - 1) / W : 0;
+  const uint32_t glast = wave + (cnt ? cnt - 1 : 0) * W;
+  WUnit wA[GT], wB[GT];
+  XUnit<QT, Q8, NG> xA, xB;
+  auto load = [&](WUnit (&w)[GT], XUnit<QT, Q8, NG>& X, uint32_t gi) {
+#pragma unroll
+    for (int u = 0; u < GT; u++) load_group<QT>(w[u], a.qs, nb, tt[u], gi, lane, r);
+    load_xunit<QT, Q8, NG>(X, a, 4 * gi, 4 * gi + 3, g0, lane, q);
+  };
+  if (cnt) {
+    // no branch between a load and its use, and scheduling barriers, so the
+    // loads of the next group stay ahead of the current group's MFMAs
+    load(wA, xA, wave);
+    uint32_t i = 0;
+    for (; i + 1 < cnt; i += 2) {
+      load(wB, xB, wave + (i + 1) * W);
+      __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+      gemm_unit<QT, Q8, GT, NG, false>(acc, wA, xA, 4);
+      load(wA, xA, min(wave + (i + 2) * W, glast));
+      __builtin_amdgcn_sched_barrier(0);
+      gemm_unit<QT, Q8, GT, NG, false>(acc, wB, xB, 4);
     }
+    if (i < cnt) gemm_unit<QT, Q8, GT, NG, false>(acc, wA, xA, 4);
+  }
+  if (a.tail && ng % W == (uint32_t)wave) {
+    WUnit wt[GT];
+    XUnit<QT, Q8, NG> xt;
+#pragma unroll
+    for (int u = 0; u < GT; u++) load_unit<QT>(wt[u], a.qs, nb, tt[u], ng, ng, a.tail, lane, r);
+    load_xunit<QT, Q8, NG>(xt, a, 4 * ng, 4 * ng + a.tail - 1, g0, lane, q);
+    gemm_unit<QT, Q8, GT, NG, true>(acc, wt, xt, (int)a.tail);
+  }
+
+  // split-K: every wave's partials into LDS, then pair p = (tile, group) is
+  // added in wave order by wave p % W and goes through the row epilogue
+#pragma unroll
+  for (int u = 0; u < GT; u++)
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+      red[wave][(u * NG + g) * 2][lane] = acc[u][g][0];
+      red[wave][(u * NG + g) * 2 + 1][lane] = acc[u][g][1];
+    }
+  __syncthreads();
+  for (uint32_t p = wave; p < (uint32_t)(GT * NG); p += W) {
+    const uint32_t u = p / NG, g = p % NG;
+    float s0 = red[0][2 * p][lane], s1 = red[0][2 * p + 1][lane];
+    for (uint32_t w = 1; w < W; w++) {
+      s0 += red[w][2 * p][lane];
+      s1 += red[w][2 * p + 1][lane];
+    }
+    if (g0 + g >= a.tg) continue;
+    const uint32_t tokA = (g0 + g) * 8 + 2 * q, tokB = tokA + 1;
+    const bool okA = tokA < a.ntok, okB = tokB < a.ntok;
+    const float vA = okA ? ldexpf(s0, -a.xexp[tokA]) : 0.f;
+    const float vB = okB ? ldexpf(s1, -a.xexp[tokB]) : 0.f;
+    row_epilogue<EPI>(a, tile0 + u, r, tv[u], tokA, okA, vA, tokB, okB, vB);
+  }
 }
 
 // ----------------------------------------------------------- dispatch
@@ -1328,22 +1379,42 @@ int embed_launch_qt(const QMat& m, const int32_t* tokens, const uint32_t* state,
   return 0;
 }
 
+template <uint32_t QT, int EPI, bool Q8, int GT, int NG>
+static void gemm_go(const GemvArgs& a, uint32_t waves, hipStream_t s) {
+  dim3 grid((a.tiles + GT - 1) / GT, (a.tg + NG - 1) / NG);
+  hipLaunchKernelGGL((gemm_kernel<QT, EPI, Q8, GT, NG>), grid, dim3(64 * waves), 0, s, a);
+}
+
+template <uint32_t QT, int EPI>
+static void gemm_shape(const GemvArgs& a, hipStream_t s) {
+  // waves per workgroup: 8 once a wave would otherwise hold more than one block group
+  const uint32_t units = a.ng + (a.tail ? 1 : 0), waves = units > 4 ? 8 : 4;
+  // two tiles per workgroup on tall matrices (each activation operand feeds
+  // two MFMAs); four token groups where that still leaves >= 256 workgroups
+  // and the per-token block scalars do not crowd the registers
+  const bool gt2 = a.tiles >= 256;
+  const uint32_t wx = gt2 ? (a.tiles + 1) / 2 : a.tiles;
+  const bool ng4 = !a.q8 && QT != LLMHIP_Q4_1 && a.tg >= 4 && wx * ((a.tg + 3) / 4) >= 256;
+  if (a.q8) {
+    if (gt2) gemm_go<QT, EPI, true, 2, 2>(a, waves, s);
+    else gemm_go<QT, EPI, true, 1, 2>(a, waves, s);
+  } else if (ng4) {
+    if (gt2) gemm_go<QT, EPI, false, 2, 4>(a, waves, s);
+    else gemm_go<QT, EPI, false, 1, 4>(a, waves, s);
+  } else {
+    if (gt2) gemm_go<QT, EPI, false, 2, 2>(a, waves, s);
+    else gemm_go<QT, EPI, false, 1, 2>(a, waves, s);
+  }
+}
+
 template <uint32_t QT>
 int gemm_launch_qt(const GemvArgs& a, int epi, hipStream_t s) {
-  // token-group splits so that a launch has >= ~512 waves
-  uint32_t wgs = (a.tiles + GT - 1) / GT, ts = 1;
-  while (ts < a.tg && wgs * ts * 4 < 2048) ts *= 2;
-  dim3 grid(wgs, std::min(ts, a.tg));
-  switch (epi * 2 + (a.q8 ? 1 : 0)) {
-#define LLMHIP_GEMM_CASE(E)                                                                                \
-  case E * 2: hipLaunchKernelGGL((gemm_kernel<QT, E, false>), grid, dim3(256), 0, s, a); break; \
-  case E * 2 + 1: hipLaunchKernelGGL((gemm_kernel<QT, E, true>), grid, dim3(256), 0, s, a); break;
-    LLMHIP_GEMM_CASE(EPI_STORE)
-    LLMHIP_GEMM_CASE(EPI_ACC)
-    LLMHIP_GEMM_CASE(EPI_QKV)
-    LLMHIP_GEMM_CASE(EPI_GATEUP)
-    LLMHIP_GEMM_CASE(EPI_SWIGLU)
-#undef LLMHIP_GEMM_CASE
+  switch (epi) {
+    case EPI_STORE: gemm_shape<QT, EPI_STORE>(a, s); break;
+    case EPI_ACC: gemm_shape<QT, EPI_ACC>(a, s); break;
+    case EPI_QKV: gemm_shape<QT, EPI_QKV>(a, s); break;
+    case EPI_GATEUP: gemm_shape<QT, EPI_GATEUP>(a, s); break;
+    case EPI_SWIGLU: gemm_shape<QT, EPI_SWIGLU>(a, s); break;
     default: return set_error(LLMHIP_ERR_ARG, "llm: gemm: unsupported epilogue %d", epi);
   }
   LLM_HIP(hipGetLastError());

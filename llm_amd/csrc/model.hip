@@ -4,6 +4,7 @@
 // the device-side state, so a graph replays at any position.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <set>
@@ -639,9 +640,26 @@ static int graph_for(Model& m, uint32_t ntok, bool head, hipGraphExec_t* out) {
 }
 
 // One pass of ntok tokens whose first position is pos (known on the host).
+// LLMHIP_EAGER=1: passes go to the stream as direct launches instead of graph
+// replays (same kernels, arguments and order), for tools that trace kernel
+// launches but not graph replays.
+static bool eager_passes() {
+  static const bool e = [] {
+    const char* v = getenv("LLMHIP_EAGER");
+    return v && *v && strcmp(v, "0") != 0;
+  }();
+  return e;
+}
+
 static int launch_graph(Model& m, uint32_t pos, uint32_t ntok, bool head) {
   hipGraphExec_t ex;
   attn_plan(m, pos, ntok);
+  if (eager_passes()) {
+    m.dispatches = 0;
+    LLM_TRY(record_pass(m, ntok, head));
+    m.stats.dispatches += m.dispatches;
+    return 0;
+  }
   LLM_TRY(graph_for(m, ntok, head, &ex));
   LLM_HIP(hipGraphLaunch(ex, m.stream));
   m.stats.dispatches += m.graph_nodes[graph_key(ntok, m.attn_rows, m.attn_split, head)];
