@@ -962,19 +962,21 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
     if (tid == 0) a.xexp[t] = 0;
     return;
   }
-  f4 va[PMAXI], vc[PMAXI];
+  f4 va[PMAXI], vc[PMAXI], wa[PMAXI], wc[PMAXI];  // x, and the norm weights in the same round trip
   {
 #pragma unroll
     for (int k = 0; k < PMAXI; k++) {
-      uint32_t it = tid + k * 256;
-      f4 A = {0, 0, 0, 0}, C = {0, 0, 0, 0};
-      if (it < NI) {
-        const float* xr = a.x + (uint64_t)(a.xrow0 + t) * a.ldx + (it / 4) * 32 + 4 * (it % 4);
-        A = *(const f4*)xr;
-        C = *(const f4*)(xr + 16);
+      // loads without a condition, so that one wait covers them all (items
+      // past the row read the last one; the reductions skip them)
+      const uint32_t it = tid + k * 256, ic = min(it, NI - 1);
+      const float* xr = a.x + (uint64_t)(a.xrow0 + t) * a.ldx + (ic / 4) * 32 + 4 * (ic % 4);
+      va[k] = *(const f4*)xr;
+      vc[k] = *(const f4*)(xr + 16);
+      if (PRO & PRO_RMS) {
+        const float* wr = a.nw + (ic / 4) * 32 + 4 * (ic % 4);
+        wa[k] = *(const f4*)wr;
+        wc[k] = *(const f4*)(wr + 16);
       }
-      va[k] = A;
-      vc[k] = C;
     }
   }
   if (PRO & PRO_RMS) {
@@ -982,7 +984,8 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
     float ss = 0;
 #pragma unroll
     for (int k = 0; k < PMAXI; k++)
-      for (int i = 0; i < 4; i++) ss += va[k][i] * va[k][i] + vc[k][i] * vc[k][i];
+      if (tid + k * 256 < NI)
+        for (int i = 0; i < 4; i++) ss += va[k][i] * va[k][i] + vc[k][i] * vc[k][i];
     ss = wave_sum(ss);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
@@ -993,11 +996,9 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
     for (int k = 0; k < PMAXI; k++) {
       uint32_t it = tid + k * 256;
       if (it >= NI) continue;
-      const float* wr = a.nw + (it / 4) * 32 + 4 * (it % 4);
-      f4 wa = *(const f4*)wr, wc = *(const f4*)(wr + 16);
       for (int i = 0; i < 4; i++) {
-        va[k][i] = __fmul_rn(__fmul_rn(va[k][i], sc), wa[i]);
-        vc[k][i] = __fmul_rn(__fmul_rn(vc[k][i], sc), wc[i]);
+        va[k][i] = __fmul_rn(__fmul_rn(va[k][i], sc), wa[k][i]);
+        vc[k][i] = __fmul_rn(__fmul_rn(vc[k][i], sc), wc[k][i]);
       }
     }
     __syncthreads();
@@ -1038,7 +1039,8 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
   float m = 0;
 #pragma unroll
   for (int k = 0; k < PMAXI; k++)
-    for (int i = 0; i < 4; i++) m = fmaxf(m, fmaxf(fabsf(va[k][i]), fabsf(vc[k][i])));
+    if (tid + k * 256 < NI)
+      for (int i = 0; i < 4; i++) m = fmaxf(m, fmaxf(fabsf(va[k][i]), fabsf(vc[k][i])));
   m = wave_max(m);
   if (lane == 0) red[wave] = m;
   __syncthreads();
@@ -1387,20 +1389,18 @@ static void gemm_go(const GemvArgs& a, uint32_t waves, hipStream_t s) {
 
 template <uint32_t QT, int EPI>
 static void gemm_shape(const GemvArgs& a, hipStream_t s) {
-  // waves per workgroup: 8 once a wave would otherwise hold more than one block group
-  const uint32_t units = a.ng + (a.tail ? 1 : 0), waves = units > 4 ? 8 : 4;
-  // two tiles per workgroup on tall matrices (each activation operand feeds
-  // two MFMAs); four token groups where that still leaves >= 256 workgroups
-  // and the per-token block scalars do not crowd the registers
+  // Measured on MI355X at 64 tokens (prep + product, Q4_0): two token groups
+  // per workgroup beat four at every layer shape (more workgroups, lower
+  // registers: 9728x896 12.6 against 15.2 us, 896x4864 11.8 against 16.6);
+  // two tiles per workgroup pay on tall matrices (9728x896: 12.6 against 15.7
+  // with one, 14.6 with four); short matrices with many block groups take
+  // eight waves, tall ones four.
+  const uint32_t units = a.ng + (a.tail ? 1 : 0);
   const bool gt2 = a.tiles >= 256;
-  const uint32_t wx = gt2 ? (a.tiles + 1) / 2 : a.tiles;
-  const bool ng4 = !a.q8 && QT != LLMHIP_Q4_1 && a.tg >= 4 && wx * ((a.tg + 3) / 4) >= 256;
+  const uint32_t waves = units > 4 && !gt2 ? 8 : 4;
   if (a.q8) {
     if (gt2) gemm_go<QT, EPI, true, 2, 2>(a, waves, s);
     else gemm_go<QT, EPI, true, 1, 2>(a, waves, s);
-  } else if (ng4) {
-    if (gt2) gemm_go<QT, EPI, false, 2, 4>(a, waves, s);
-    else gemm_go<QT, EPI, false, 1, 4>(a, waves, s);
   } else {
     if (gt2) gemm_go<QT, EPI, false, 2, 2>(a, waves, s);
     else gemm_go<QT, EPI, false, 1, 2>(a, waves, s);
