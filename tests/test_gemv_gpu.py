@@ -60,7 +60,7 @@ def test_sweep(gpu, oracle, qtype, rows, k, n):
 @pytest.mark.parametrize("qtype", [2, 3, 8])
 @pytest.mark.parametrize("rows,k,n", [(896, 896, 1), (1152, 896, 2), (896, 4864, 3), (4864, 896, 1), (37, 96, 1),
                                       (130, 224, 2), (33, 576, 4), (896, 896, 8), (9728, 896, 64), (896, 4864, 64),
-                                      (130, 224, 5), (151936, 896, 1), (65541, 576, 1)])
+                                      (130, 224, 5), (151936, 896, 1), (65541, 576, 1), (4100, 608, 37)])
 def test_exact_ggml_gemv(gpu, oracle, qtype, rows, k, n):
     """The ExactGGML product (cpu.go:117-140, 166-214) against the oracle's,
     through the decode tile kernel (1-4 tokens), the streaming kernel (one
@@ -98,6 +98,18 @@ def test_exact_ggml_gemv(gpu, oracle, qtype, rows, k, n):
 @pytest.mark.parametrize("rows,k,n", [(16, 32, 1), (37, 96, 1), (5, 160, 3), (33, 576, 2), (130, 224, 5),
                                       (64, 4864, 4), (1, 32, 1), (17, 1312, 7)])
 def test_ragged(gpu, oracle, qtype, rows, k, n):
+    _check_gemv(gpu, oracle, qtype, rows, k, n)
+
+
+@pytest.mark.parametrize("qtype", [2, 3, 8])
+@pytest.mark.parametrize("rows,k,n", [(4100, 608, 37), (4111, 4864, 13), (4096, 160, 64), (300, 1312, 9)])
+def test_prefill_edges(gpu, oracle, qtype, rows, k, n):
+    """The prefill product's clamped indices: an odd tile count on two-tile
+    workgroups (257 tiles, the last workgroup half empty), a row count that
+    is not a multiple of 16, trailing blocks (608 = 4 groups + 3 blocks,
+    4864 = 38 groups, 160 = 1 group + 1 block, 1312 = 10 groups + 1), an odd
+    number of 8-token groups (37 tokens: 5 groups on two-group workgroups)
+    and a partial last group."""
     _check_gemv(gpu, oracle, qtype, rows, k, n)
 
 
