@@ -57,6 +57,124 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a, uint32_t ntok, ui
   }
 }
 
+// Prefill attention over chunks of 128 cache rows on the matrix cores (head
+// size 64, several tokens): a workgroup per (KV head g, chunk c, group of 64
+// queries), the queries of KV head g numbered token * GQ + (head - g * GQ).
+// The chunk's key and value rows are staged in LDS once; each of the four
+// waves owns 16 queries and forms, with v_mfma_f32_16x16x4_f32,
+//   S = Q K^T (16 queries x 128 rows, 16 steps of 4 dimensions),
+// then per query the chunk max M over its causal rows, e = exp(s*scale - M),
+// L = sum e, and O = e V (P goes through LDS into the A layout).  (M, L, O)
+// are the chunk partials attn_merge_kernel combines, as attn_kernel<SPLIT>
+// writes them; chunks at or past a query's causal bound write nothing.
+// Operand layouts of the 16x16x4 f32 MFMA: lane l holds A[l % 16][l / 16],
+// B[l / 16][l % 16] and D[4 (l / 16) + i][l % 16], i < 4.
+constexpr uint32_t AMMA_KS = 65, AMMA_VS = 80, AMMA_PS = 132;  // LDS row strides (bank-conflict free)
+
+template <bool KVH>
+__global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a, uint32_t ntok, uint32_t nchunks) {
+  constexpr uint32_t HD = 64, C = ATTN_SPLIT_ROWS;
+  __shared__ float Ks[C * AMMA_KS], Vs[C * AMMA_VS], Ps[4][16 * AMMA_PS];
+  const uint32_t GQ = a.heads / a.kv_heads, nq = ntok * GQ;
+  const uint32_t c = blockIdx.x % nchunks, rest = blockIdx.x / nchunks;
+  const uint32_t g = rest % a.kv_heads, q0 = (rest / a.kv_heads) * 64;
+  const uint32_t row0 = c * C, pos0 = a.state[0];
+  const uint32_t tlast = (min(q0 + 64, nq) - 1) / GQ;
+  if (q0 >= nq || row0 >= pos0 + tlast + 1) return;  // uniform: no query of the group reaches the chunk
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4, r = lane & 15;
+
+  // stage the chunk's rows below lim (zeros past it: masked, and 0 * V stays 0)
+  const uint32_t lim = min(a.rows, pos0 + tlast + 1);
+#pragma unroll
+  for (uint32_t k = 0; k < C * HD / 4 / 256; k++) {
+    const uint32_t idx = tid + 256 * k, row = idx / 16, c4 = idx % 16, p = row0 + row;
+    f4 kk = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+    if (p < lim) {
+      kk = kv_load4<KVH>(a.kv, (uint64_t)p * a.kvd + g * HD + 4 * c4);
+      vv = kv_load4<KVH>(a.kv, (uint64_t)a.ctx * a.kvd + (uint64_t)p * a.kvd + g * HD + 4 * c4);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) Ks[row * AMMA_KS + 4 * c4 + i] = kk[i];
+    *(f4*)&Vs[row * AMMA_VS + 4 * c4] = vv;
+  }
+
+  // this lane's A rows: query m = r of the wave, dimensions 16 grp .. 16 grp + 15
+  const uint32_t qa = min(q0 + 16 * wave + r, nq - 1), ta = qa / GQ, ha = g * GQ + qa % GQ;
+  f4 aq[4];
+  const float* qp = a.q + (uint64_t)ta * a.heads * HD + ha * HD + 16 * grp;
+#pragma unroll
+  for (int v = 0; v < 4; v++) aq[v] = *(const f4*)(qp + 4 * v);
+  // the causal bound of this lane's D rows: queries 4 grp + i of the wave
+  uint32_t nd[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t qd = q0 + 16 * wave + 4 * grp + i;
+    nd[i] = qd < nq ? pos0 + qd / GQ + 1 : 0;
+  }
+  __syncthreads();
+
+  f4 S[C / 16];
+#pragma unroll
+  for (uint32_t nt = 0; nt < C / 16; nt++) S[nt] = f4{0, 0, 0, 0};
+#pragma unroll
+  for (uint32_t j = 0; j < 16; j++) {
+    const float av = aq[j / 4][j % 4];
+#pragma unroll
+    for (uint32_t nt = 0; nt < C / 16; nt++)
+      S[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, Ks[(16 * nt + r) * AMMA_KS + 16 * grp + j], S[nt], 0, 0, 0);
+  }
+  float M[4], L[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float m = -INFINITY;
+#pragma unroll
+    for (uint32_t nt = 0; nt < C / 16; nt++) {
+      const bool ok = row0 + 16 * nt + r < nd[i];
+      S[nt][i] = ok ? S[nt][i] * a.scale : -INFINITY;
+      m = fmaxf(m, S[nt][i]);
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    M[i] = m;
+    float l = 0;
+#pragma unroll
+    for (uint32_t nt = 0; nt < C / 16; nt++) {
+      const bool ok = row0 + 16 * nt + r < nd[i];
+      const float e = ok ? expf(S[nt][i] - m) : 0.f;
+      l += e;
+      Ps[wave][(4 * grp + i) * AMMA_PS + 16 * nt + r] = e;
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o);
+    L[i] = l;
+  }
+  __syncthreads();
+
+  f4 O[HD / 16];
+#pragma unroll
+  for (uint32_t dt = 0; dt < HD / 16; dt++) O[dt] = f4{0, 0, 0, 0};
+#pragma unroll 8
+  for (uint32_t j = 0; j < C / 4; j++) {
+    const float pa = Ps[wave][r * AMMA_PS + 4 * j + grp];
+#pragma unroll
+    for (uint32_t dt = 0; dt < HD / 16; dt++)
+      O[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, Vs[(4 * j + grp) * AMMA_VS + 16 * dt + r], O[dt], 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t qd = q0 + 16 * wave + 4 * grp + i;
+    if (qd >= nq || row0 >= nd[i]) continue;
+    const uint32_t t = qd / GQ, h = g * GQ + qd % GQ;
+    const uint64_t th = (uint64_t)t * a.heads + h;
+#pragma unroll
+    for (uint32_t dt = 0; dt < HD / 16; dt++) a.pv[(th * a.smax + c) * HD + 16 * dt + r] = O[dt][i];
+    if (r == 0) {
+      a.ml[(th * a.smax + c) * 2] = M[i];
+      a.ml[(th * a.smax + c) * 2 + 1] = L[i];
+    }
+  }
+}
+
 // The chunks of one (token, head) merged (the flash-decoding combine of
 // kernels_fused.go:150-170): M = max m_c, att = sum_c e^{m_c-M} o_c / sum_c
 // e^{m_c-M} l_c, over the chunks below the causal bound.  One thread per
@@ -124,8 +242,16 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s) {
   }
   const uint32_t chunks = (a.rows + ATTN_SPLIT_ROWS - 1) / ATTN_SPLIT_ROWS;
   if (chunks > a.smax) return set_error(LLMHIP_ERR_ARG, "llm: attention: %u chunks of %u", chunks, a.smax);
-  if (a.hd == 64) attn_go<64, ATTN_SPLIT_ROWS / 32, true>(a, ntok, NI * chunks, s);
-  else attn_go<128, ATTN_SPLIT_ROWS / 32, true>(a, ntok, NI * chunks, s);
+  if (a.hd == 64 && ntok > 1) {
+    // several tokens: the matrix-core form, 64 queries of a KV head per workgroup
+    const uint32_t blocks = chunks * a.kv_heads * ((ntok * (a.heads / a.kv_heads) + 63) / 64);
+    if (a.kv16) hipLaunchKernelGGL((attn_mma_kernel<true>), dim3(blocks), dim3(256), 0, s, a, ntok, chunks);
+    else hipLaunchKernelGGL((attn_mma_kernel<false>), dim3(blocks), dim3(256), 0, s, a, ntok, chunks);
+  } else if (a.hd == 64) {
+    attn_go<64, ATTN_SPLIT_ROWS / 32, true>(a, ntok, NI * chunks, s);
+  } else {
+    attn_go<128, ATTN_SPLIT_ROWS / 32, true>(a, ntok, NI * chunks, s);
+  }
   LLM_HIP(hipGetLastError());
   if (a.hd == 64) hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(a.heads, ntok), dim3(64), 0, s, a);
   else hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(a.heads, ntok), dim3(128), 0, s, a);
