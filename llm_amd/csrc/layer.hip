@@ -84,18 +84,24 @@ __global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a, uint32_t ntok
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4, r = lane & 15;
 
   // stage the chunk's rows below lim (zeros past it: masked, and 0 * V stays 0)
-  const uint32_t lim = min(a.rows, pos0 + tlast + 1);
+  // (every load first, rows clamped below lim, so that one wait covers them)
+  const uint32_t lim = min(a.rows, pos0 + tlast + 1);  // > row0
+  constexpr uint32_t NL = C * HD / 4 / 256;
+  f4 kk[NL], vv[NL];
 #pragma unroll
-  for (uint32_t k = 0; k < C * HD / 4 / 256; k++) {
-    const uint32_t idx = tid + 256 * k, row = idx / 16, c4 = idx % 16, p = row0 + row;
-    f4 kk = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-    if (p < lim) {
-      kk = kv_load4<KVH>(a.kv, (uint64_t)p * a.kvd + g * HD + 4 * c4);
-      vv = kv_load4<KVH>(a.kv, (uint64_t)a.ctx * a.kvd + (uint64_t)p * a.kvd + g * HD + 4 * c4);
-    }
+  for (uint32_t k = 0; k < NL; k++) {
+    const uint32_t idx = tid + 256 * k, p = min(row0 + idx / 16, lim - 1), c4 = idx % 16;
+    kk[k] = kv_load4<KVH>(a.kv, (uint64_t)p * a.kvd + g * HD + 4 * c4);
+    vv[k] = kv_load4<KVH>(a.kv, (uint64_t)a.ctx * a.kvd + (uint64_t)p * a.kvd + g * HD + 4 * c4);
+  }
 #pragma unroll
-    for (int i = 0; i < 4; i++) Ks[row * AMMA_KS + 4 * c4 + i] = kk[i];
-    *(f4*)&Vs[row * AMMA_VS + 4 * c4] = vv;
+  for (uint32_t k = 0; k < NL; k++) {
+    const uint32_t idx = tid + 256 * k, row = idx / 16, c4 = idx % 16;
+    const bool in = row0 + row < lim;
+    const f4 z = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; i++) Ks[row * AMMA_KS + 4 * c4 + i] = in ? kk[k][i] : 0.f;
+    *(f4*)&Vs[row * AMMA_VS + 4 * c4] = in ? vv[k] : z;
   }
 
   // this lane's A rows: query m = r of the wave, dimensions 16 grp .. 16 grp + 15
@@ -116,12 +122,23 @@ __global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a, uint32_t ntok
   f4 S[C / 16];
 #pragma unroll
   for (uint32_t nt = 0; nt < C / 16; nt++) S[nt] = f4{0, 0, 0, 0};
+  // batches of 4 dimension steps: the batch's key operands are read from LDS
+  // before its MFMAs (scheduling barriers keep the compiler from interleaving
+  // each read with its use)
 #pragma unroll
-  for (uint32_t j = 0; j < 16; j++) {
-    const float av = aq[j / 4][j % 4];
+  for (uint32_t jb = 0; jb < 16; jb += 4) {
+    float kb[4][C / 16];
 #pragma unroll
-    for (uint32_t nt = 0; nt < C / 16; nt++)
-      S[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, Ks[(16 * nt + r) * AMMA_KS + 16 * grp + j], S[nt], 0, 0, 0);
+    for (uint32_t jj = 0; jj < 4; jj++)
+#pragma unroll
+      for (uint32_t nt = 0; nt < C / 16; nt++) kb[jj][nt] = Ks[(16 * nt + r) * AMMA_KS + 16 * grp + jb + jj];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t jj = 0; jj < 4; jj++)
+#pragma unroll
+      for (uint32_t nt = 0; nt < C / 16; nt++)
+        S[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[jb / 4][jj], kb[jj][nt], S[nt], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
   float M[4], L[4];
 #pragma unroll
@@ -153,12 +170,23 @@ __global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a, uint32_t ntok
   f4 O[HD / 16];
 #pragma unroll
   for (uint32_t dt = 0; dt < HD / 16; dt++) O[dt] = f4{0, 0, 0, 0};
-#pragma unroll 8
-  for (uint32_t j = 0; j < C / 4; j++) {
-    const float pa = Ps[wave][r * AMMA_PS + 4 * j + grp];
+  // batches of 8 row steps: the batch's operands are read from LDS before its MFMAs
+  for (uint32_t jb = 0; jb < C / 4; jb += 8) {
+    float pa[8], vb[8][HD / 16];
 #pragma unroll
-    for (uint32_t dt = 0; dt < HD / 16; dt++)
-      O[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, Vs[(4 * j + grp) * AMMA_VS + 16 * dt + r], O[dt], 0, 0, 0);
+    for (uint32_t jj = 0; jj < 8; jj++) {
+      const uint32_t j = jb + jj;
+      pa[jj] = Ps[wave][r * AMMA_PS + 4 * j + grp];
+#pragma unroll
+      for (uint32_t dt = 0; dt < HD / 16; dt++) vb[jj][dt] = Vs[(4 * j + grp) * AMMA_VS + 16 * dt + r];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t jj = 0; jj < 8; jj++)
+#pragma unroll
+      for (uint32_t dt = 0; dt < HD / 16; dt++)
+        O[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[jj], vb[jj][dt], O[dt], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
   for (int i = 0; i < 4; i++) {
