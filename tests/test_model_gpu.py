@@ -76,6 +76,19 @@ def test_attention_paths(gpu, prompt_len, heads, kv_heads, hd):
     _check(g, cpu, prompt, (320 if hd == 64 else 200) - prompt_len)
 
 
+@pytest.mark.parametrize("prompt_len,heads,kv_heads", [(520, 14, 2), (330, 8, 8), (460, 9, 3)])
+def test_prefill_attention_mma(gpu, prompt_len, heads, kv_heads):
+    """The matrix-core form of prefill attention past 256 positions: query
+    groups of 64 that cut across tokens (7, 1 and 3 query heads per KV head),
+    a last prefill chunk of 8 tokens (520 = 8 x 64 + 8), chunks whose rows
+    reach past some queries' causal bound, then decode steps over the cache
+    it wrote."""
+    spec = synth.tiny_llama(seed=40 + heads + kv_heads, embd=64 * heads, heads=heads, kv_heads=kv_heads, ctx=1024)
+    g, cpu = _open(spec, 640)
+    prompt = synth.prompt(8, prompt_len, spec.vocab)
+    _check(g, cpu, prompt, 16)
+
+
 @pytest.mark.parametrize("name,prompt_len,n", [("llama", 150, 40), ("qwen2", 150, 40), ("qwen2-split", 300, 24),
                                                ("llama-hd128", 140, 40)])
 def test_f16_kv_cache(gpu, name, prompt_len, n):
