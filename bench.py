@@ -229,6 +229,22 @@ def sweep(args):
                         "warm_us": round(warm, 3), "warm_gbps": round(nbytes / warm * 1e-3, 1)})
             log(f"gemv {tname} {rows}x{k}: HBM {out[-1]['hbm_gbps']} GB/s ({out[-1]['hbm_frac']:.1%}) over "
                 f"{len(copies)} copies, warm {out[-1]['warm_gbps']} GB/s")
+            # prefill-chunk token counts: the activation prep and the product
+            # (one launch pair) over the same rotated copies
+            for n in (8, 64):
+                xn = kernels.DeviceBuffer.from_numpy(
+                    np.random.default_rng([3, n, k]).standard_normal((n, k), np.float32))
+                yn = kernels.DeviceBuffer(n * rows * 4)
+                us = kernels.bench(copies, xn, yn, n, iters=iters, warmup=len(copies))
+                tf = 2.0 * rows * k * n / us * 1e-6
+                out.append({"type": tname, "rows": rows, "k": k, "n": n, "bytes": nbytes, "hbm_us": round(us, 3),
+                            "hbm_gbps": round(nbytes / us * 1e-3, 1),
+                            "hbm_frac": round(nbytes / us * 1e-3 / PEAK_HBM_GBS, 4), "copies": len(copies),
+                            "tflops": round(tf, 2), "mfma_frac": round(tf / PEAK_MFMA_F16_TFLOPS, 5)})
+                log(f"gemm {tname} {rows}x{k} n={n}: {us:.2f} us (prep + product), {tf:.1f} TFLOP/s, "
+                    f"weights {out[-1]['hbm_gbps']} GB/s")
+                xn.close()
+                yn.close()
             for c in copies:
                 c.close()
             x.close()
