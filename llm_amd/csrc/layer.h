@@ -20,6 +20,17 @@ struct AttnArgs {
   float scale;     // f32(1/sqrt(hd)), cpu.go:304
 };
 
+// Prefill: att also written as the output projection's prepared operands (per
+// 32-element block of a token: exponent-scaled f16 hi/lo in the product's
+// operand order, xdx = 2^-e, xbsum = the block sum, xexp = 0); xp null: not.
+struct AttnOps {
+  void* xp;
+  float* xdx;
+  float* xbsum;
+  int32_t* xexp;
+  uint32_t onb;  // blocks per token row (heads * hd / 32)
+};
+
 // Rows per chunk of the split attention kernel.
 constexpr uint32_t ATTN_SPLIT_ROWS = 128;
 
@@ -29,7 +40,7 @@ bool attn_ok(uint32_t hd);
 uint32_t attn_full_max(uint32_t hd);
 // One launch (one chunk), or two (chunks, merge).  Every position of the pass
 // (state[0] .. state[0] + ntok - 1) must be below a.rows.
-int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s);
+int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* ops = nullptr);
 int argmax_launch(const float* pv, const uint32_t* pi, uint32_t n, const float* logits, int32_t* tokens,
                   int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s);
 int advance_launch(uint32_t* state, uint32_t n, hipStream_t s);

@@ -7,6 +7,54 @@
 
 namespace llmhip {
 
+// The block-scaled operand form of att (AttnOps): v = att[t][col],
+// col = h * HD + d, held by lane d % 64 of whole waves.  Per 32-element block
+// (half a wave): the exponent e that puts the block's max magnitude in
+// [2^14, 2^15) (0 for an all-zero or non-finite block), hi = f16(v 2^e),
+// lo = f16(v 2^e - hi); item i of the block (elements 4i..4i+3 and
+// 16+4i..16+4i+3) is written by the block's lane 4i as the product's 16-byte
+// operands for token slot t % 8 of group t / 8, in the order
+// {A0, A2, C0, C2, A1, A3, C1, C3} of prep_kernel.
+__device__ __forceinline__ void emit_operand(const AttnOps& a, uint32_t t, uint32_t col, float v) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  const uint32_t lane = threadIdx.x & 63, j = lane & 31, b = col / 32;
+  float mx = fabsf(v), sum = v;
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o));
+    sum += __shfl_xor(sum, o);
+  }
+  int e = 0;
+  if (mx > 0 && mx <= 3.0e38f) {
+    int E;
+    frexpf(mx, &E);
+    e = 15 - E;
+  }
+  const float sv = ldexpf(v, e);
+  const uint32_t base = lane - j;  // the block's first lane
+  float g[8];
+  const uint32_t src[8] = {0, 2, 16, 18, 1, 3, 17, 19};
+#pragma unroll
+  for (int i = 0; i < 8; i++) g[i] = __shfl(sv, (int)(base + (j & ~3u) + src[i]));
+  if ((j & 3) == 0 && j < 16) {
+    h8 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const _Float16 hh = (_Float16)g[i];
+      hi[i] = hh;
+      lo[i] = (_Float16)(g[i] - (float)hh);
+    }
+    h8* dst = (h8*)a.xp + ((uint64_t)(t / 8) * a.onb + b) * 64 + (j / 4) * 16 + 2 * (t % 8);
+    dst[0] = hi;
+    dst[1] = lo;
+  }
+  if (j == 0) {
+    a.xdx[(uint64_t)t * a.onb + b] = ldexpf(1.f, -e);
+    a.xbsum[(uint64_t)t * a.onb + b] = sum;
+    if (col == 0) a.xexp[t] = 0;
+  }
+}
+
 // Attention over the KV cache (cpu.go:300-334), one query head per
 // workgroup of 512 threads over C = 32*J cache rows (attn_core.h).  Every
 // global load is issued before anything waits; a.rows (host-chosen, >= every
@@ -22,8 +70,8 @@ namespace llmhip {
 //   SPLIT = true: chunk c covers rows [c*C, c*C + C); writes the partials
 //     (m, l) and o = sum e v for attn_merge_kernel; chunks past the causal
 //     bound write nothing.
-template <uint32_t HD, uint32_t J, bool SPLIT, bool KVH>
-__global__ __launch_bounds__(512) void attn_kernel(AttnArgs a, uint32_t ntok, uint32_t units) {
+template <uint32_t HD, uint32_t J, bool SPLIT, bool KVH, bool EMIT = false>
+__global__ __launch_bounds__(512) void attn_kernel(AttnArgs a, uint32_t ntok, uint32_t units, AttnOps ops) {
   typedef AttnChunk<HD, J, 8, KVH> AC;
   __shared__ AttnLds<HD, 8> sm;
   const uint32_t GQ = a.heads / a.kv_heads, sb = blockIdx.x / 8;
@@ -55,6 +103,7 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a, uint32_t ntok, ui
       a.att[(uint64_t)t * a.heads * HD + h * HD + tid] = o / L;
     }
   }
+  if (EMIT && tid < HD) emit_operand(ops, t, h * HD + tid, o / L);
 }
 
 // Prefill attention over chunks of 128 cache rows on the matrix cores (head
@@ -207,8 +256,8 @@ __global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a, uint32_t ntok
 // kernels_fused.go:150-170): M = max m_c, att = sum_c e^{m_c-M} o_c / sum_c
 // e^{m_c-M} l_c, over the chunks below the causal bound.  One thread per
 // output dimension; the partials of up to 16 chunks are loaded at once.
-template <uint32_t HD>
-__global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a) {
+template <uint32_t HD, bool EMIT = false>
+__global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a, AttnOps ops) {
   const uint32_t h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
   const uint32_t n = a.state[0] + t + 1, P = (n + ATTN_SPLIT_ROWS - 1) / ATTN_SPLIT_ROWS;
   const uint64_t th = (uint64_t)t * a.heads + h;
@@ -242,6 +291,7 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a) {
     M = M2;
   }
   a.att[(uint64_t)t * a.heads * HD + h * HD + d] = o / L;
+  if (EMIT) emit_operand(ops, t, h * HD + d, o / L);
 }
 
 bool attn_ok(uint32_t hd) { return hd == 64 || hd == 128; }
@@ -249,22 +299,29 @@ bool attn_ok(uint32_t hd) { return hd == 64 || hd == 128; }
 uint32_t attn_full_max(uint32_t hd) { return hd == 64 ? 256 : 128; }
 
 template <uint32_t HD, uint32_t J, bool SPLIT>
-static void attn_go(const AttnArgs& a, uint32_t ntok, uint32_t units, hipStream_t s) {
+static void attn_go(const AttnArgs& a, uint32_t ntok, uint32_t units, hipStream_t s, const AttnOps& ops) {
   const uint32_t gq = a.heads / a.kv_heads, blocks = 8 * gq * ((units + 7) / 8);
-  if (a.kv16) hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT, true>), dim3(blocks), dim3(512), 0, s, a, ntok, units);
-  else hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT, false>), dim3(blocks), dim3(512), 0, s, a, ntok, units);
+  const dim3 g(blocks), b(512);
+  if (!SPLIT && ops.xp) {  // prefill: also the output projection's operands
+    if (a.kv16) hipLaunchKernelGGL((attn_kernel<HD, J, false, true, true>), g, b, 0, s, a, ntok, units, ops);
+    else hipLaunchKernelGGL((attn_kernel<HD, J, false, false, true>), g, b, 0, s, a, ntok, units, ops);
+    return;
+  }
+  if (a.kv16) hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT, true>), g, b, 0, s, a, ntok, units, ops);
+  else hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT, false>), g, b, 0, s, a, ntok, units, ops);
 }
 
-int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s) {
+int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* ops_in) {
   if (ntok == 0) return 0;
+  const AttnOps ops = ops_in ? *ops_in : AttnOps{nullptr, nullptr, nullptr, nullptr, 0};
   if (!attn_ok(a.hd) || a.rows == 0 || a.rows > a.ctx || a.heads % a.kv_heads)
     return set_error(LLMHIP_ERR_ARG, "llm: attention: head size %u, %u rows of %u not supported", a.hd, a.rows,
                      a.ctx);
   const uint32_t NI = ntok * a.kv_heads;
   if (!a.split) {
     if (a.rows > attn_full_max(a.hd)) return set_error(LLMHIP_ERR_ARG, "llm: attention: %u rows in one chunk", a.rows);
-    if (a.hd == 64) attn_go<64, 8, false>(a, ntok, NI, s);
-    else attn_go<128, 4, false>(a, ntok, NI, s);
+    if (a.hd == 64) attn_go<64, 8, false>(a, ntok, NI, s, ops);
+    else attn_go<128, 4, false>(a, ntok, NI, s, ops);
     LLM_HIP(hipGetLastError());
     return 0;
   }
@@ -276,13 +333,19 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s) {
     if (a.kv16) hipLaunchKernelGGL((attn_mma_kernel<true>), dim3(blocks), dim3(256), 0, s, a, ntok, chunks);
     else hipLaunchKernelGGL((attn_mma_kernel<false>), dim3(blocks), dim3(256), 0, s, a, ntok, chunks);
   } else if (a.hd == 64) {
-    attn_go<64, ATTN_SPLIT_ROWS / 32, true>(a, ntok, NI * chunks, s);
+    attn_go<64, ATTN_SPLIT_ROWS / 32, true>(a, ntok, NI * chunks, s, ops);
   } else {
-    attn_go<128, ATTN_SPLIT_ROWS / 32, true>(a, ntok, NI * chunks, s);
+    attn_go<128, ATTN_SPLIT_ROWS / 32, true>(a, ntok, NI * chunks, s, ops);
   }
   LLM_HIP(hipGetLastError());
-  if (a.hd == 64) hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(a.heads, ntok), dim3(64), 0, s, a);
-  else hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(a.heads, ntok), dim3(128), 0, s, a);
+  const dim3 mg(a.heads, ntok);
+  if (a.hd == 64) {
+    if (ops.xp) hipLaunchKernelGGL((attn_merge_kernel<64, true>), mg, dim3(64), 0, s, a, ops);
+    else hipLaunchKernelGGL((attn_merge_kernel<64, false>), mg, dim3(64), 0, s, a, ops);
+  } else {
+    if (ops.xp) hipLaunchKernelGGL((attn_merge_kernel<128, true>), mg, dim3(128), 0, s, a, ops);
+    else hipLaunchKernelGGL((attn_merge_kernel<128, false>), mg, dim3(128), 0, s, a, ops);
+  }
   LLM_HIP(hipGetLastError());
   return 0;
 }

@@ -400,13 +400,14 @@ static int gemv_rec(Model& m, const char* cls, const GemvArgs& a, uint32_t qtype
 // prologue fused.  `prep` false reuses the staging of the previous call (the
 // matrices of one mixed-type group share an input).
 static int mat_rec(Model& m, const char* cls, const char* pcls, GemvArgs a, uint32_t qtype, int pro, int epi,
-                   uint64_t bytes, bool prep = true) {
+                   uint64_t bytes, bool prep = true, bool block_scaled = false) {
   if (a.ntok < GEMM_MIN_TOKENS) return gemv_rec(m, cls, a, qtype, pro, epi, bytes);
   xprep_bind(&a, m.xprep);
   if (m.q8) {
     pro |= PRO_Q8;
     a.q8 = 1;
   }
+  if (block_scaled) a.q8 = 1;  // operands already staged per block (scale 2^-e in xdx)
   if (prep && !skipped(m, cls))
     LLM_TRY(launch_rec(m, pcls, 0, [&]() { return prep_launch(a, pro, m.stream); }));
   if (skipped(m, cls)) return 0;
@@ -469,12 +470,26 @@ static AttnArgs attn_args(const Model& m, const Layer& L) {
   return a;
 }
 
+// A prefill chunk in f32 mode has the attention write the output
+// projection's operands itself (per-block exponents), so K3 runs without its
+// activation prep.
+static bool att_operands(const Model& m, uint32_t ntok) {
+  return ntok >= GEMM_MIN_TOKENS && !m.q8 && !skipped(m, "k2") && !skipped(m, "k3");
+}
+
 static int rec_k2(Model& m, const Layer& L, uint32_t ntok) {
   if (skipped(m, "k2")) return 0;
   // KV bytes read for the last token of the pass (the decode step's one token)
   uint64_t bytes = 2ull * (m.pos + 1) * m.kvd * 4;
   if (m.attn_split) m.dispatches++;  // the merge kernel
-  return launch_rec(m, "k2", bytes, [&]() { return attn_launch(attn_args(m, L), ntok, m.stream); });
+  const AttnArgs a = attn_args(m, L);
+  if (att_operands(m, ntok)) {
+    GemvArgs g = base_args(m, L.o, ntok);
+    xprep_bind(&g, m.xprep);
+    const AttnOps ops = {g.xp, g.xdx, g.xbsum, g.xexp, g.nb};
+    return launch_rec(m, "k2", bytes, [&]() { return attn_launch(a, ntok, m.stream, &ops); });
+  }
+  return launch_rec(m, "k2", bytes, [&]() { return attn_launch(a, ntok, m.stream); });
 }
 
 // the heads' merged outputs times W_o, added to the residual
@@ -484,7 +499,8 @@ static int rec_k3(Model& m, const Layer& L, uint32_t ntok) {
   a.ldx = m.cfg.embd;
   a.y = m.x;
   a.ldy = m.cfg.embd;
-  return mat_rec(m, "k3", "p3", a, L.o.g.q.type, PRO_PLAIN, EPI_ACC, L.o.g.gguf_bytes());
+  const bool staged = att_operands(m, ntok);
+  return mat_rec(m, "k3", "p3", a, L.o.g.q.type, PRO_PLAIN, EPI_ACC, L.o.g.gguf_bytes(), !staged, staged);
 }
 
 static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
