@@ -41,7 +41,8 @@ def kernel_symbols(attn_full):
     k5 share one; rocprof tells them apart by grid size), the one-chunk or
     split attention, the streaming head."""
     return {"k1": "gemv_kernel<2u, 1, 1, 2>",
-            "k2": "attn_kernel<64u, 8u, false, false>" if attn_full else "attn_kernel<64u, 4u, true, false> + attn_merge_kernel<64u>",
+            "k2": "attn_kernel<64u, 8u, false, false, false>" if attn_full else
+                  "attn_kernel<64u, 4u, true, false, false> + attn_merge_kernel<64u, false>",
             "k3": "gemv_kernel<2u, 1, 0, 1>", "k4": "gemv_kernel<2u, 1, 1, 3>", "k5": "gemv_kernel<2u, 1, 0, 1>",
             "head": "gemv_stream_kernel<8u, 1, 4>"}
 
