@@ -266,28 +266,28 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a, AttnOps ops)
   constexpr uint32_t B = 16;
   float M = -INFINITY, L = 0, o = 0;
   for (uint32_t c0 = 0; c0 < P; c0 += B) {
+    // every load of the batch issued before any is used (chunk clamped below
+    // P; the chunks past it are skipped below), so that one wait covers them
     float mc[B], lc[B], oc[B];
 #pragma unroll
-    for (uint32_t i = 0; i < B; i++)
-      if (c0 + i < P) {
-        mc[i] = ml[2 * (c0 + i)];
-        lc[i] = ml[2 * (c0 + i) + 1];
-        oc[i] = pv[(uint64_t)(c0 + i) * HD];
-      }
+    for (uint32_t i = 0; i < B; i++) {
+      const uint32_t c = min(c0 + i, P - 1);
+      mc[i] = ml[2 * c];
+      lc[i] = ml[2 * c + 1];
+      oc[i] = pv[(uint64_t)c * HD];
+    }
     float M2 = M;
 #pragma unroll
-    for (uint32_t i = 0; i < B; i++)
-      if (c0 + i < P) M2 = fmaxf(M2, mc[i]);
+    for (uint32_t i = 0; i < B; i++) M2 = fmaxf(M2, c0 + i < P ? mc[i] : -INFINITY);
     const float r = expf(M - M2);  // 0 on the first batch (M = -inf)
     L *= r;
     o *= r;
 #pragma unroll
-    for (uint32_t i = 0; i < B; i++)
-      if (c0 + i < P) {
-        const float w = expf(mc[i] - M2);
-        L += w * lc[i];
-        o += w * oc[i];
-      }
+    for (uint32_t i = 0; i < B; i++) {
+      const float w = c0 + i < P ? expf(mc[i] - M2) : 0.f;
+      L += w * lc[i];
+      o += w * oc[i];
+    }
     M = M2;
   }
   a.att[(uint64_t)t * a.heads * HD + h * HD + d] = o / L;
