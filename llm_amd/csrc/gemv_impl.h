@@ -952,7 +952,7 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
   const uint32_t nb = a.nb, K = a.k, NI = nb * 4;
   h8* xp = (h8*)a.xp;
   const uint32_t tg = t / 8, s2 = 2 * (t % 8);
-  float* red = pl;        // [4] partials, [8] s, [9] exp
+  float* red = pl;        // [0, 4) wave sums of squares, [4, 8) wave maxima
   if (t >= a.ntok) {
     for (uint32_t it = tid; it < NI; it += 256) {
       xp[((uint64_t)tg * nb + it / 4) * 64 + (it % 4) * 16 + s2] = h8{};
@@ -989,9 +989,8 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
     ss = wave_sum(ss);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
-    if (tid == 0) red[8] = (float)(1.0 / sqrt((double)((red[0] + red[1] + red[2] + red[3]) / (float)K + a.eps)));
-    __syncthreads();
-    const float sc = red[8];
+    // every thread forms the scale from the four wave sums (same order): no second barrier
+    const float sc = (float)(1.0 / sqrt((double)((red[0] + red[1] + red[2] + red[3]) / (float)K + a.eps)));
 #pragma unroll
     for (int k = 0; k < PMAXI; k++) {
       uint32_t it = tid + k * 256;
@@ -1001,7 +1000,6 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
         vc[k][i] = __fmul_rn(__fmul_rn(vc[k][i], sc), wc[k][i]);
       }
     }
-    __syncthreads();
   }
   if (PRO & PRO_Q8) {  // quantizeQ8 per block, as in stage_x
     if (tid == 0) a.xexp[t] = 0;
@@ -1042,21 +1040,19 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
     if (tid + k * 256 < NI)
       for (int i = 0; i < 4; i++) m = fmaxf(m, fmaxf(fabsf(va[k][i]), fabsf(vc[k][i])));
   m = wave_max(m);
-  if (lane == 0) red[wave] = m;
+  if (lane == 0) red[4 + wave] = m;  // [0, 4) may still be read for the RMS scale
   __syncthreads();
-  if (tid == 0) {
-    float mm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    int e = 0;
+  // every thread forms the exponent from the four wave maxima: no second barrier
+  int ex = 0;
+  {
+    const float mm = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
     if (mm > 0 && mm <= 3.0e38f) {
       int E;
       frexpf(mm, &E);
-      e = 15 - E;
+      ex = 15 - E;
     }
-    ((int*)red)[9] = e;
-    a.xexp[t] = e;
   }
-  __syncthreads();
-  const int ex = ((int*)red)[9];
+  if (tid == 0) a.xexp[t] = ex;
 #pragma unroll
   for (int k = 0; k < PMAXI; k++) {
     uint32_t it = tid + k * 256;
