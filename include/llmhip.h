@@ -169,7 +169,9 @@ LLMHIP_API int llmhip_model_tensor(llmhip_model* m, const char* name, uint32_t g
 /* Stream raw tensor bytes [byte_offset, byte_offset+nbytes) of a declared
  * tensor (whole blocks for quantised types): streamMat / loadF32 /
  * loadGroup of gpu.go:297-407 and fused.go:108-190, with the repack, the
- * QKV and gate/up concatenation and the NEOX pairing done on the device. */
+ * QKV and gate/up concatenation and the NEOX pairing done on the device.
+ * A range overlapping bytes of the tensor uploaded before is refused
+ * (LLMHIP_ERR_ARG), so that finalize sees each byte counted once. */
 LLMHIP_API int llmhip_model_upload(llmhip_model* m, const char* name, const void* raw, uint64_t nbytes,
                                    uint64_t byte_offset);
 /* The loader's fast path: the same upload, with the nbytes read from the open
@@ -189,7 +191,8 @@ LLMHIP_API int llmhip_model_upload_file(llmhip_model* m, const char* name, int f
  * file. */
 LLMHIP_API int llmhip_model_upload_file_tensors(llmhip_model* m, int fd, uint32_t n, const char* const* names,
                                                 const uint64_t* file_offsets);
-/* Check that every needed tensor arrived in full ("llm: missing tensor"). */
+/* Check that every needed tensor arrived in full ("llm: missing tensor"):
+ * its uploaded ranges, disjoint, cover all of its bytes. */
 LLMHIP_API int llmhip_model_finalize(llmhip_model* m);
 /* Run a prompt from position 0 (prefill, gpu.go:853-900) in chunks of
  * prefill_batch tokens; optionally copy out the last token's logits (vocab
@@ -202,6 +205,10 @@ LLMHIP_API int llmhip_model_prefill(llmhip_model* m, const int32_t* ids, int n, 
 LLMHIP_API int llmhip_model_decode(llmhip_model* m, int cnt, int32_t* out);
 /* The first n 4-byte words of a named buffer as float32 (Peek, gpu.go:1018-1043):
  * x, q, att (the merged attention output), gate (the SwiGLU activations),
+ * up (the up product W_up h), h (the head's normed row: RMSNorm of the last
+ * token's residual with output_norm, formed at the call), k and v (the K and V
+ * rows the latest pass appended last, in the last layer run: K after bias and
+ * RoPE, as the cache holds them),
  * logits, state, tokens, outb, and
  * kvblk.N. (layer N's cache [2][ctx][kvd]). */
 LLMHIP_API int llmhip_model_peek(llmhip_model* m, const char* name, float* out, uint64_t n);

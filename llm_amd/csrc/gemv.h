@@ -74,6 +74,8 @@ struct GemvArgs {
   float* amax_v;  // EPI_ARGMAX: per-workgroup partials
   uint32_t* amax_i;
   const float* aux;  // EPI_SWIGLU: the gate values
+  float* up;         // EPI_GATEUP / EPI_SWIGLU: the up product u = W_up h also stored here, [t*ff + i]
+                     // (nullptr: not kept); Peek("up")
   // prefill (gemm_kernel): activations prepared once per launch by prep_kernel
   void* xp;        // [tg][nb][64 lanes] 16-byte MFMA operands (hi/lo f16 of 8 tokens)
   int32_t* xexp;   // [tg*8] power-of-two scale per token

@@ -381,11 +381,13 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
         uint64_t o = (uint64_t)tokA * a.ldy + lr;
         float gg = a.aux[o];
         a.y[o] = gg / (1.f + expf(-gg)) * vA;
+        if (a.up) a.up[o] = vA;  // after the gate was read: up may alias aux
       }
       if (okB) {
         uint64_t o = (uint64_t)tokB * a.ldy + lr;
         float gg = a.aux[o];
         a.y[o] = gg / (1.f + expf(-gg)) * vB;
+        if (a.up) a.up[o] = vB;
       }
     }
   }
@@ -431,13 +433,14 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
   }
   if (EPI == EPI_GATEUP) {
     // act = g / (1 + exp(-g)) * u (cpu.go:345); gate row i at lane r, up row i at r+8
+    // (lanes r >= 8 hold the up rows: with a.up they store them there, in the
+    // same store instruction as the activations)
     float uA = __shfl_xor(vA, 8), uB = __shfl_xor(vB, 8);
-    if (active && r < 8) {
-      uint32_t i = 8 * tile + r;
-      if (i < a.ff) {
-        if (okA) a.y[(uint64_t)tokA * a.ff + i] = vA / (1.f + expf(-vA)) * uA;
-        if (okB) a.y[(uint64_t)tokB * a.ff + i] = vB / (1.f + expf(-vB)) * uB;
-      }
+    const uint32_t i = 8 * tile + (r & 7);
+    float* dst = r < 8 ? a.y : a.up;
+    if (active && i < a.ff && dst) {
+      if (okA) dst[(uint64_t)tokA * a.ff + i] = r < 8 ? vA / (1.f + expf(-vA)) * uA : vA;
+      if (okB) dst[(uint64_t)tokB * a.ff + i] = r < 8 ? vB / (1.f + expf(-vB)) * uB : vB;
     }
   }
 }

@@ -44,5 +44,8 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* 
 int argmax_launch(const float* pv, const uint32_t* pi, uint32_t n, const float* logits, int32_t* tokens,
                   int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s);
 int advance_launch(uint32_t* state, uint32_t n, hipStream_t s);
+// out[i] = x[i] * s * w[i], s = f32(1/sqrt(f64(sum x^2 / n + eps))) (rmsNorm, cpu.go:81-98), one
+// workgroup; n <= 16384.  Not on the forward pass (the matrix kernels fuse it): Peek("h").
+int rmsnorm_launch(const float* x, const float* w, uint32_t n, float eps, float* out, hipStream_t s);
 
 }  // namespace llmhip

@@ -436,6 +436,27 @@ __global__ void advance_kernel(uint32_t* state, uint32_t n) {
   }
 }
 
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                      uint32_t n, float eps, float* __restrict__ out) {
+  __shared__ float part[4];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  float ss = 0;
+  for (uint32_t i = tid; i < n; i += 256) ss += x[i] * x[i];
+  ss = rows_sum4(row_sum16(ss));
+  if (lane == 0) part[wave] = ss;
+  __syncthreads();
+  const float t = (part[0] + part[1]) + (part[2] + part[3]);
+  const float sc = (float)(1.0 / sqrt((double)(t / (float)n + eps)));
+  for (uint32_t i = tid; i < n; i += 256) out[i] = __fmul_rn(__fmul_rn(x[i], sc), w[i]);
+}
+
+int rmsnorm_launch(const float* x, const float* w, uint32_t n, float eps, float* out, hipStream_t s) {
+  if (n == 0 || n > 16384) return set_error(LLMHIP_ERR_ARG, "llm: rmsnorm of %u elements", n);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, s, x, w, n, eps, out);
+  LLM_HIP(hipGetLastError());
+  return 0;
+}
+
 int advance_launch(uint32_t* state, uint32_t n, hipStream_t s) {
   hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, s, state, n);
   LLM_HIP(hipGetLastError());

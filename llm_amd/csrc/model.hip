@@ -4,6 +4,7 @@
 // the device-side state, so a graph replays at any position.
 #include <algorithm>
 #include <cmath>
+#include <iterator>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -19,9 +20,42 @@ namespace llmhip {
 struct TensorInfo {
   uint32_t type = 0;
   std::vector<uint64_t> dims;
-  uint64_t size = 0, received = 0;
+  uint64_t size = 0, received = 0;  // received: bytes covered by the uploads so far
+  std::map<uint64_t, uint64_t> got;  // the uploaded byte ranges, start -> end, disjoint
   bool used = false;
 };
+
+// Refuses a range [off, off + n) of tensor `name` that overlaps one uploaded
+// before (a second upload of the same bytes would let finalize accept a tensor
+// part of which was never written).
+static int check_range(const TensorInfo& t, const char* name, uint64_t off, uint64_t n) {
+  if (n == 0) return 0;
+  auto it = t.got.upper_bound(off);  // first range starting after off
+  const bool before = it != t.got.begin() && std::prev(it)->second > off;
+  const bool after = it != t.got.end() && it->first < off + n;
+  if (before || after)
+    return set_error(LLMHIP_ERR_ARG, "llm: upload of %s bytes [%llu, %llu) overlaps bytes already uploaded", name,
+                     (unsigned long long)off, (unsigned long long)(off + n));
+  return 0;
+}
+
+// Records an accepted range (check_range passed), merging it with its neighbours.
+static void add_range(TensorInfo& t, uint64_t off, uint64_t n) {
+  if (n == 0) return;
+  uint64_t a = off, b = off + n;
+  auto it = t.got.lower_bound(a);
+  if (it != t.got.begin() && std::prev(it)->second == a) {
+    --it;
+    a = it->first;
+    it = t.got.erase(it);
+  }
+  if (it != t.got.end() && it->first == b) {
+    b = it->second;
+    t.got.erase(it);
+  }
+  t.got[a] = b;
+  t.received += n;
+}
 
 struct Layer {
   QMat qkv[3];
@@ -56,8 +90,11 @@ struct Model {
   bool sizing = false;
   hipStream_t stream = nullptr;
   Stager st;
+  // gbuf: the up product of the pass's last layer ([pm][ff], Peek "up"; the
+  // gate values in between when gate and up have different types); h: the
+  // head's normed row, formed on demand by Peek("h")
   float *x = nullptr, *q = nullptr, *act = nullptr, *gbuf = nullptr, *logits = nullptr, *pv = nullptr,
-        *ml = nullptr, *amax_v = nullptr, *cs = nullptr, *att = nullptr;
+        *ml = nullptr, *amax_v = nullptr, *cs = nullptr, *att = nullptr, *h = nullptr;
   void* xprep = nullptr;  // prepared activations of a prefill chunk
   uint32_t *amax_i = nullptr, *state = nullptr;
   int32_t *tokens = nullptr, *outb = nullptr;
@@ -79,6 +116,7 @@ struct Model {
   int layers_limit = 0;
   std::set<std::string> skip;
   uint32_t pos = 0;  // host mirror of state[0] (== state[1])
+  uint32_t last_row = 0;     // the row of x holding the last token of the latest pass
   uint32_t attn_rows = 0;    // pass being recorded: cache rows its attention reads
   bool attn_split = false;   // ... and whether it runs in chunks merged by a second kernel
   bool prompted = false;
@@ -511,6 +549,7 @@ static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
     a.ldx = c.embd;
     a.nw = L.ffn_norm;
     a.y = m.act;
+    a.up = m.gbuf;
     a.ff = c.ff;
     return mat_rec(m, "k4", "p4", a, L.gu[0].g.q.type, PRO_RMS, EPI_GATEUP, L.gu[0].g.gguf_bytes());
   }
@@ -528,6 +567,7 @@ static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
   u.y = m.act;
   u.ldy = c.ff;
   u.aux = m.gbuf;
+  u.up = m.gbuf;
   return mat_rec(m, "k4", "p4", u, L.gu[1].g.q.type, PRO_RMS, EPI_SWIGLU, L.gu[1].g.gguf_bytes(), false);
 }
 
@@ -670,6 +710,7 @@ static bool eager_passes() {
 static int launch_graph(Model& m, uint32_t pos, uint32_t ntok, bool head) {
   hipGraphExec_t ex;
   attn_plan(m, pos, ntok);
+  m.last_row = ntok - 1;
   if (eager_passes()) {
     m.dispatches = 0;
     LLM_TRY(record_pass(m, ntok, head));
@@ -738,7 +779,7 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
       (rc = dalloc_n(*m, &m->ml, pm * H * m->smax * 2)) || (rc = dalloc_n(*m, &m->state, 2)) ||
       (rc = dalloc_n(*m, &m->tokens, (uint64_t)m->ctx + 1)) || (rc = dalloc_n(*m, &m->outb, 1)) ||
       (rc = dalloc(*m, &m->xprep, xprep_bytes(m->pm, (uint32_t)std::max(c.embd, c.ff)))) ||
-      (rc = dalloc_n(*m, &m->cs, (uint64_t)m->ctx * c.head_dim)))
+      (rc = dalloc_n(*m, &m->cs, (uint64_t)m->ctx * c.head_dim)) || (rc = dalloc_n(*m, &m->h, E)))
     return fail(rc);
   // RoPE table in double precision, gpu.go:524-534 (and cpu.go:374-375)
   std::vector<float> cs((size_t)m->ctx * c.head_dim);
@@ -810,6 +851,7 @@ static int upload_from(Model& m, const char* name, const Source& src, uint64_t n
   if (!m.allocated) LLM_TRY(allocate(m));
   if (off + nbytes > t.size)
     return set_error(LLMHIP_ERR_ARG, "llm: upload of %s runs past its %llu bytes", name, (unsigned long long)t.size);
+  LLM_TRY(check_range(t, name, off, nbytes));
   QMat* q;
   uint64_t row_off;
   float* f;
@@ -822,7 +864,7 @@ static int upload_from(Model& m, const char* name, const Source& src, uint64_t n
     LLM_TRY(qmat_upload(&m.st, *q, src, nbytes, off, row_off));
   else
     LLM_TRY(f32_upload(&m.st, f, src, nbytes, off));
-  t.received += nbytes;
+  add_range(t, off, nbytes);
   return 0;
 }
 
@@ -847,6 +889,10 @@ int llmhip_model_upload_file_tensors(llmhip_model* h, int fd, uint32_t n, const 
     if (it == m.tensors.end()) return set_error(LLMHIP_ERR_ARG, "llm: tensor %s was not declared", names[i]);
     TensorInfo& t = it->second;
     if (!t.used) continue;
+    LLM_TRY(check_range(t, names[i], 0, t.size));
+    for (uint32_t j = 0; j < i; j++)
+      if (strcmp(names[j], names[i]) == 0)
+        return set_error(LLMHIP_ERR_ARG, "llm: tensor %s listed twice in one upload", names[i]);
     if (!m.allocated) LLM_TRY(allocate(m));
     StagePiece p{};
     QMat* q;
@@ -870,7 +916,7 @@ int llmhip_model_upload_file_tensors(llmhip_model* h, int fd, uint32_t n, const 
   LLM_HIP(hipSetDevice(m.device));
   if (!m.st.cap) LLM_TRY(stager_init(&m.st, m.device, MODEL_STAGE_BYTES, m.stream));
   LLM_TRY(stage_file_runs(&m.st, fd, sorted.data(), sorted.size()));
-  for (size_t i = 0; i < ps.size(); i++) owner[i]->received += ps[i].bytes;
+  for (size_t i = 0; i < ps.size(); i++) add_range(*owner[i], ps[i].off, ps[i].bytes);
   return 0;
 }
 
@@ -888,6 +934,8 @@ int llmhip_model_finalize(llmhip_model* h) {
   clear_error();
   Model& m = *h->m;
   if (!m.allocated) LLM_TRY(allocate(m));
+  // every used tensor covered in full: its uploads are disjoint, so the bytes
+  // received count each byte once
   for (auto& kv : m.tensors)
     if (kv.second.used && kv.second.received < kv.second.size)
       return set_error(LLMHIP_ERR_FORMAT, "llm: tensor %s: %llu of %llu bytes uploaded", kv.first.c_str(),
@@ -960,10 +1008,30 @@ int llmhip_model_peek(llmhip_model* h, const char* name, float* out, uint64_t n)
   uint64_t cap = 0;
   std::string s = name;
   const uint64_t E = m.cfg.embd, F = m.cfg.ff;
+  bool kv_row = false;  // src is an element offset into a cache of binary16 or f32 values
   if (s == "x") { src = m.x; cap = m.pm * E; }
   else if (s == "q") { src = m.q; cap = m.pm * E; }
   else if (s == "att") { src = m.att; cap = m.pm * E; }
   else if (s == "gate" || s == "act") { src = m.act; cap = m.pm * F; }
+  else if (s == "up") { src = m.gbuf; cap = m.pm * F; }
+  else if (s == "h") {
+    // the head's input (recordHead's rms, fused.go:269-275): RMSNorm of the
+    // last token's residual row with output_norm, formed here from x
+    if (!m.allocated) return set_error(LLMHIP_ERR_STATE, "llm: no buffer \"h\" before the weights are loaded");
+    LLM_HIP(hipSetDevice(m.device));
+    LLM_TRY(rmsnorm_launch(m.x + (uint64_t)m.last_row * E, m.out_norm, (uint32_t)E, m.cfg.eps, m.h, m.stream));
+    src = m.h;
+    cap = E;
+  } else if (s == "k" || s == "v") {
+    // the K or V row the latest pass appended last: the last layer run, the
+    // last position (as stored in the cache: K after bias and RoPE)
+    const int nl = m.layers_limit > 0 && m.layers_limit < m.cfg.layers ? m.layers_limit : m.cfg.layers;
+    if (m.allocated && m.pos > 0 && nl > 0) {
+      src = (const void*)(uintptr_t)(((uint64_t)(s == "v") * m.ctx + (m.pos - 1)) * m.kvd);
+      kv_row = true;
+      cap = m.kvd;
+    }
+  }
   else if (s == "logits") { src = m.logits; cap = m.cfg.vocab; }
   else if (s == "state") { src = m.state; cap = 2; }
   else if (s == "tokens") { src = m.tokens; cap = m.ctx + 1; }
@@ -975,11 +1043,22 @@ int llmhip_model_peek(llmhip_model* h, const char* name, float* out, uint64_t n)
       cap = 2ull * m.ctx * m.kvd;
     }
   }
-  if (!src) return set_error(LLMHIP_ERR_ARG, "llm: no buffer \"%s\"", name);
+  if (!src && !kv_row) return set_error(LLMHIP_ERR_ARG, "llm: no buffer \"%s\"", name);
   if (n > cap) return set_error(LLMHIP_ERR_ARG, "llm: buffer \"%s\" holds %llu words", name, (unsigned long long)cap);
   LLM_HIP(hipSetDevice(m.device));
   LLM_HIP(hipStreamSynchronize(m.stream));
-  if (m.kv16 && s.rfind("kvblk.", 0) == 0) {  // binary16 cache: widened on the host
+  if (kv_row) {  // src: the row's element offset in the last layer's cache
+    const int nl = m.layers_limit > 0 && m.layers_limit < m.cfg.layers ? m.layers_limit : m.cfg.layers;
+    const uint64_t e = (uint64_t)(uintptr_t)src;
+    const char* kv = (const char*)m.layers[nl - 1].kv;
+    if (m.kv16) {
+      std::vector<_Float16> hv(n);
+      LLM_TRY(copy_out(m, hv.data(), kv + e * 2, n * 2));
+      for (uint64_t i = 0; i < n; i++) out[i] = (float)hv[i];
+    } else {
+      LLM_TRY(copy_out(m, out, kv + e * 4, n * 4));
+    }
+  } else if (m.kv16 && s.rfind("kvblk.", 0) == 0) {  // binary16 cache: widened on the host
     std::vector<_Float16> h(n);
     LLM_TRY(copy_out(m, h.data(), src, n * 2));
     for (uint64_t i = 0; i < n; i++) out[i] = (float)h[i];

@@ -514,6 +514,8 @@ struct cpuref_model {
   size_t ntensors;
   float **k, **v;
   float* last_x;
+  float* last_h;  /* the head's input of the last token (rmsNorm with output_norm) */
+  float* last_u;  /* the up product of the last layer run, last token */
 };
 typedef struct cpuref_model cpuref_model;
 
@@ -554,6 +556,8 @@ static void model_free(cpuref_model* m) {
   free(m->tensors);
   free(m->file);
   free(m->last_x);
+  free(m->last_h);
+  free(m->last_u);
   free(m);
 }
 
@@ -689,6 +693,8 @@ EXPORT int cpuref_load(const char* path, int max_ctx, cpuref_model** out) {
     m->v[l] = (float*)calloc(kv ? kv : 1, 4);
   }
   m->last_x = (float*)calloc((size_t)m->c.embd, 4);
+  m->last_h = (float*)calloc((size_t)m->c.embd, 4);
+  m->last_u = (float*)calloc((size_t)m->c.ff, 4);
   *out = m;
   return 0;
 }
@@ -703,6 +709,17 @@ EXPORT void cpuref_set_max_layers(cpuref_model* m, int n) { m->max_layers = n; }
 EXPORT void cpuref_reset(cpuref_model* m) { m->pos = 0; } /* Reset, cpu.go:64 */
 EXPORT int cpuref_pos(cpuref_model* m) { return m->pos; }  /* Pos, cpu.go:67 */
 EXPORT void cpuref_last_x(cpuref_model* m, float* out) { memcpy(out, m->last_x, (size_t)m->c.embd * 4); }
+/* Intermediate values of the last Forward (copies only; the trace surface the
+ * reference's GPU Peek exposes, gpu.go:1015-1043): the head's normed row, the
+ * last layer's up product, and a cached K or V row. */
+EXPORT void cpuref_last_h(cpuref_model* m, float* out) { memcpy(out, m->last_h, (size_t)m->c.embd * 4); }
+EXPORT void cpuref_last_up(cpuref_model* m, float* out) { memcpy(out, m->last_u, (size_t)m->c.ff * 4); }
+EXPORT int cpuref_kv_row(cpuref_model* m, int layer, int pos, int v, float* out) {
+  int kvd = m->c.kv_heads * m->c.head_dim;
+  if (layer < 0 || layer >= m->c.layers || pos < 0 || pos >= m->pos) return fail("llm: no cache row%s", "");
+  memcpy(out, (v ? m->v[layer] : m->k[layer]) + (size_t)pos * kvd, (size_t)kvd * 4);
+  return 0;
+}
 EXPORT int cpuref_max_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();
@@ -874,6 +891,7 @@ EXPORT int cpuref_forward(cpuref_model* m, int32_t tok, float* logits) {
     rc = -1;
   } else {
     memcpy(m->last_x, x, (size_t)c.embd * 4);
+    if (nl > 0) memcpy(m->last_u, u, (size_t)c.ff * 4);
     if (m->max_layers != 0 && m->max_layers < c.layers) {
       m->pos++;
       rc = 0;
@@ -884,6 +902,7 @@ EXPORT int cpuref_forward(cpuref_model* m, int32_t tok, float* logits) {
         rc = -1;
       } else {
         cpuref_rmsnorm(h, x, (const float*)on->data, c.embd, c.eps);
+        memcpy(m->last_h, h, (size_t)c.embd * 4);
         if (mv(m, logits, h, out, PREP(h, c.embd))) rc = -1;
         else {
           m->pos++;

@@ -62,6 +62,9 @@ def lib():
         L.cpuref_reset.argtypes = [P]
         L.cpuref_pos.argtypes = [P]
         L.cpuref_last_x.argtypes = [P, P]
+        L.cpuref_last_h.argtypes = [P, P]
+        L.cpuref_last_up.argtypes = [P, P]
+        L.cpuref_kv_row.argtypes = [P, I, I, I, P]
         L.cpuref_forward.argtypes = [P, ctypes.c_int32, P]
         L.cpuref_tensor.argtypes = [P, ctypes.c_char_p, ctypes.POINTER(P), ctypes.POINTER(ctypes.c_uint64),
                                     ctypes.POINTER(ctypes.c_uint32), P]
@@ -189,6 +192,25 @@ class CPU:
     def last_x(self):
         out = np.empty(self.cfg.embd, np.float32)
         lib().cpuref_last_x(self._h, _p(out))
+        return out
+
+    def last_h(self):
+        """The head's input row of the last forward (rmsNorm with output_norm)."""
+        out = np.empty(self.cfg.embd, np.float32)
+        lib().cpuref_last_h(self._h, _p(out))
+        return out
+
+    def last_up(self):
+        """The up product of the last layer the last forward ran."""
+        out = np.empty(self.cfg.ff, np.float32)
+        lib().cpuref_last_up(self._h, _p(out))
+        return out
+
+    def kv_row(self, layer, pos, v=False):
+        """The cached K (v False) or V row of a layer at a position."""
+        out = np.empty(self.cfg.kv_heads * self.cfg.head_dim, np.float32)
+        if lib().cpuref_kv_row(self._h, layer, pos, int(v), _p(out)) != 0:
+            raise RuntimeError(lib().cpuref_error().decode())
         return out
 
     def tensor(self, name):

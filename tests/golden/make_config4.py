@@ -5,8 +5,11 @@ the C restatement of cpu.go; row- and head-parallel runs are bit-identical
 to single-threaded ones).  Writes tests/golden/config4.json: the prompt seed,
 every CPU token, and at each step the runner-up token and the CPU logit gap
 to it, so a GPU divergence can be judged by the near-tie rule without
-re-running the CPU.  Run:  python tests/golden/make_config4.py [threads]
+re-running the CPU; and tests/golden/config4_logits.npz: all vocab step-1
+logits of the CPU (f32, compressed), whose sha256 the JSON records.
+Run:  python tests/golden/make_config4.py [threads]
 """
+import hashlib
 import json
 import os
 import sys
@@ -34,6 +37,10 @@ def main():
         logits = cpu.forward(t)
         if i % 256 == 0:
             print(f"prompt {i}/{PROMPT} {time.time() - t0:.0f}s", flush=True)
+    here = os.path.dirname(os.path.abspath(__file__))
+    npz = os.path.join(here, "config4_logits.npz")
+    np.savez_compressed(npz, logits=logits.astype(np.float32))
+    digest = hashlib.sha256(logits.astype("<f4").tobytes()).hexdigest()
     steps = []
     first_top = None
     while len(steps) < GEN:
@@ -49,8 +56,8 @@ def main():
         if len(steps) % 64 == 0:
             print(f"gen {len(steps)}/{GEN} {time.time() - t0:.0f}s", flush=True)
     out = {"spec": "synth.qwen25_mixed(seed=0)", "prompt_seed": SEED, "prompt": PROMPT, "generate": GEN, "ctx": CTX,
-           "first_top16": first_top, "steps": steps}
-    dst = os.path.join(os.path.dirname(os.path.abspath(__file__)), "config4.json")
+           "first_top16": first_top, "logits_sha256": digest, "logits_file": os.path.basename(npz), "steps": steps}
+    dst = os.path.join(here, "config4.json")
     json.dump(out, open(dst, "w"), separators=(",", ":"))
     print(f"wrote {dst} in {time.time() - t0:.0f}s")
 

@@ -1,10 +1,13 @@
 """BASELINE config 4 on the GPU: the Qwen2.5-0.5B shape at long context (a
 2048-token prompt in 32 prefill chunks, 512 greedy tokens, context 4096, f32 KV
 cache ~100 MB) with the baseline type mix (Q4_1 ffn_down on odd layers, Q8_0
-head), against golden CPU-oracle tokens (tests/golden/config4.json, written by
-tests/golden/make_config4.py); and the extended mix (Q8_0 and Q4_1 on every
-kind of matrix) at the same shape against the oracle run here.
+head), against golden CPU-oracle results written by tests/golden/make_config4.py:
+every step-1 logit (tests/golden/config4_logits.npz, the check of
+examples/generate/main.go:159-165: max|gpu - cpu| / max|cpu| <= 1e-4) and the
+512 greedy tokens (tests/golden/config4.json); and the extended mix (Q8_0 and
+Q4_1 on every kind of matrix) at the same shape against the oracle run here.
 """
+import hashlib
 import json
 import os
 
@@ -17,6 +20,7 @@ from tests.parity import LOGIT_TOL, cpu_greedy, greedy_parity, gpu_generate, rel
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config4.json")
+LOGITS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config4_logits.npz")
 
 
 def test_config4_long_context(gpu):
@@ -27,11 +31,16 @@ def test_config4_long_context(gpu):
     print(f"config 4: {path}, prompt {gold['prompt']}, generate {gold['generate']}, ctx {gold['ctx']}", flush=True)
     g = llm.NewGPU(0, None, path, gold["ctx"])
     prompt = [int(t) for t in synth.prompt(gold["prompt_seed"], gold["prompt"], spec.vocab)]
-    # step-1 logits: the CPU's 16 largest, within the tolerance of max|logits|
+    # step-1 logits: all of them, within the tolerance of max|logits|
+    cpu = np.load(LOGITS)["logits"]
+    assert hashlib.sha256(cpu.astype("<f4").tobytes()).hexdigest() == gold["logits_sha256"]
+    assert cpu.shape == (spec.vocab,) and float(np.max(np.abs(cpu))) == gold["steps"][0]["maxabs"]
     logits = g.PrefillLogits(prompt)
-    maxabs = gold["steps"][0]["maxabs"]
+    rel = rel_err(logits, cpu)
+    print(f"config 4: step-1 logits relative error {rel:.3e} over {cpu.size}", flush=True)
+    assert rel <= LOGIT_TOL
     for i, v in gold["first_top16"]:
-        assert abs(float(logits[i]) - v) <= LOGIT_TOL * maxabs, (i, float(logits[i]), v)
+        assert float(cpu[i]) == v
     want = [s["tok"] for s in gold["steps"]]
     done, ties = 0, 0
     while done < len(want):

@@ -176,3 +176,58 @@ def test_loader_refusals(gpu, tmp_path):
     bad.write_bytes(data[: len(data) - 100])
     with pytest.raises(LLMError):
         llm.NewGPU(0, None, str(bad), 64)
+
+
+def test_upload_coverage(gpu):
+    """Upload completeness counts covered bytes, not received bytes: a range
+    that overlaps one uploaded before is refused (so a tensor half of which
+    came twice is never taken as complete), a tensor listed twice in one
+    batched call is refused, and finalize accepts the model once every byte
+    arrived exactly once (its logits then equal the fast loader's)."""
+    from llm_amd import _lib, llm
+    from llm_amd._lib import LLMError
+    spec = synth.tiny_llama(seed=4, layers=3)
+    path = synth.cached(spec)
+    L, f, cfg, m = _create(path, 64)
+    fd = os.open(path, os.O_RDONLY)
+    try:
+        t = next(t for t in f.Tensors if t.Type == 2 and t.Name.startswith("blk.1."))
+        bb = BLOCK[2][1]
+        half = t.Size // bb // 2 * bb
+        base = f.DataOffset + t.Offset
+
+        def up(a, n):
+            llm.check(L.llmhip_model_upload_file(m, t.Name.encode(), fd, base + a, n, a))
+
+        up(0, half)
+        for a, n in ((0, half), (bb, bb), (half - bb, 2 * bb), (0, t.Size)):
+            with pytest.raises(LLMError) as e:
+                up(a, n)
+            assert e.value.kind == "ARG" and "overlaps" in str(e.value), (a, n)
+        with pytest.raises(LLMError) as e:  # the same tensor twice in one batch
+            names = (ctypes.c_char_p * 2)(b"output_norm.weight", b"output_norm.weight")
+            o = f.DataOffset + f.Tensor("output_norm.weight")[0].Offset
+            offs = (ctypes.c_uint64 * 2)(o, o)
+            llm.check(L.llmhip_model_upload_file_tensors(m, fd, 2, names, offs))
+        assert e.value.kind == "ARG" and "twice" in str(e.value)
+        # everything else, then t's second half in two pieces (adjacent ranges merge)
+        rest = [x for x in f.Tensors if x.Name != t.Name]
+        names = (ctypes.c_char_p * len(rest))(*[x.Name.encode() for x in rest])
+        offs = (ctypes.c_uint64 * len(rest))(*[f.DataOffset + x.Offset for x in rest])
+        llm.check(L.llmhip_model_upload_file_tensors(m, fd, len(rest), names, offs))
+        with pytest.raises(LLMError) as e:  # half of t still missing
+            llm.check(L.llmhip_model_finalize(m))
+        assert e.value.kind == "FORMAT" and t.Name in str(e.value)
+        mid = half + (t.Size - half) // bb // 2 * bb
+        up(mid, t.Size - mid)
+        up(half, mid - half)
+        llm.check(L.llmhip_model_finalize(m))
+        g = llm.NewGPU(0, None, path, 64)
+        prompt = synth.prompt(5, 9, spec.vocab)
+        want = _prefill(_lib.lib(), g._m, spec.vocab, prompt)
+        got = _prefill(L, m, spec.vocab, prompt)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        g.close()
+    finally:
+        os.close(fd)
+        L.llmhip_model_free(m)

@@ -271,6 +271,41 @@ def test_state_and_tokens(gpu):
     assert s.dispatches > 0 and s.submits > 0
 
 
+@pytest.mark.parametrize("name", ["qwen2", "qwen2-mixed"])
+def test_peek_buffers(gpu, name):
+    """Peek's trace buffers (gpu.go:513-516, 1015-1043) against the oracle's
+    values of the same pass, after a two-chunk prefill and after decode steps:
+    h (the head's input: RMSNorm of the last residual row with output_norm),
+    up (the last layer's up product, through the fused gate/up epilogue and,
+    for gate and up of different types, the SwiGLU one), k and v (the cache
+    rows the pass appended last, in the last layer)."""
+    spec = TINY[name]()
+    g, cpu = _open(spec, 256)
+    L, E, F, kvd = spec.layers, spec.embd, spec.ff, spec.kvd
+    prompt = [int(t) for t in synth.prompt(8, 70, spec.vocab)]
+
+    def check(fed, last_row):
+        cpu.reset()
+        for t in fed:
+            cpu.forward(t)
+        h = g.Peek("h", E)
+        up = g.Peek("up", (last_row + 1) * F)[last_row * F:]
+        k, v = g.Peek("k", kvd), g.Peek("v", kvd)
+        errs = [rel_err(h, cpu.last_h()), rel_err(up, cpu.last_up()),
+                rel_err(k, cpu.kv_row(L - 1, len(fed) - 1)), rel_err(v, cpu.kv_row(L - 1, len(fed) - 1, v=True))]
+        print(f"{len(fed)} tokens fed: h {errs[0]:.2e} up {errs[1]:.2e} k {errs[2]:.2e} v {errs[3]:.2e}", flush=True)
+        assert max(errs) <= 1e-5
+        kv = g.Peek(f"kvblk.{L - 1}.", 2 * 256 * kvd).reshape(2, 256, kvd)
+        assert np.array_equal(k, kv[0, len(fed) - 1]) and np.array_equal(v, kv[1, len(fed) - 1])
+
+    g.PrefillLogits(prompt)  # chunks of 64 and 6 tokens: the last pass's last token is row 5
+    check(prompt, 5)
+    out = gpu_generate(g, prompt, 5)  # the prefill, then 4 decode steps of one token
+    check(prompt + out[:4], 0)
+    with pytest.raises(Exception):
+        g.Peek("h", E + 1)
+
+
 def test_refusals(gpu):
     from llm_amd import llm
     from llm_amd._lib import LLMError

@@ -6,6 +6,7 @@ mistake in it: the reference's own known values and invariants
 numpy's IEEE conversions, and independent float64 formulations (vectorised
 numpy, written from the mathematics rather than from cpu.go's loop order).
 """
+import os
 import struct
 
 import numpy as np
@@ -429,3 +430,18 @@ def test_threaded_forward_bit_identical():
     for t in toks:
         la, lb = a.forward(t), b.forward(t)
     assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
+def test_config4_golden_consistent():
+    """The committed config-4 fixtures agree with each other: the logits file
+    is the one the JSON's hash names, its argmax (the oracle's Argmax rule) is
+    the first greedy token, its 16 largest are the recorded ones."""
+    import hashlib
+    import json
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    gold = json.load(open(os.path.join(here, "config4.json")))
+    l = np.load(os.path.join(here, gold["logits_file"]))["logits"]
+    assert hashlib.sha256(l.astype("<f4").tobytes()).hexdigest() == gold["logits_sha256"]
+    assert cpuref.argmax(l) == gold["steps"][0]["tok"]
+    assert [[int(i), float(v)] for i, v in gold["first_top16"]] == [[int(i), float(l[i])] for i, _ in gold["first_top16"]]
+    assert float(np.max(np.abs(l))) == gold["steps"][0]["maxabs"]
