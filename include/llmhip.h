@@ -116,6 +116,18 @@ LLMHIP_API int llmhip_qmat_dequant(llmhip_qmat* m, float* out_dev, void* hip_str
 /* y_dev[n][rows] (+)= W x_dev[n][k] for n tokens (1 <= n <= 64), in f32:
  * the matvec of cpu.go:143-222 for each token.  accumulate != 0 adds into y. */
 LLMHIP_API int llmhip_qmat_gemv(llmhip_qmat* m, const float* x_dev, float* y_dev, int n, int accumulate, void* hip_stream);
+/* llmhip_qmat_gemv without any allocation, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, hosts that
+ * forbid it).  No counterpart in the reference.  Products of 5 or more tokens
+ * stage their activations in one static device array per GPU (about 2.2 MB,
+ * held until the process ends) instead of a buffer the matrix allocates:
+ * k at most LLMHIP_NOALLOC_MAX_K (LLMHIP_ERR_ARG above it), n at most 64.
+ * Every call on a GPU shares that GPU's array, so calls that overlap on one GPU
+ * (on different streams, or from different threads) race; calls in one stream
+ * are ordered and safe.  Same kernels and results as llmhip_qmat_gemv. */
+#define LLMHIP_NOALLOC_MAX_K 8192
+LLMHIP_API int llmhip_qmat_gemv_noalloc(llmhip_qmat* m, const float* x_dev, float* y_dev, int n, int accumulate,
+                                        void* hip_stream);
 /* The ExactGGML form (cpu.go:117-140, 166-214): each token's x quantised to
  * Q8_0 blocks (Q8_1 for Q4_1 weights) as quantizeQ8 does, then ggml's integer
  * block products scaled by d_w * d_x (+ m_w * s_x); y_dev = the result. */

@@ -78,6 +78,7 @@ SIGNATURES = [
     ("llmhip_qmat_upload", I, [P, P, U64, U64]),
     ("llmhip_qmat_dequant", I, [P, P, P]),
     ("llmhip_qmat_gemv", I, [P, P, P, I, I, P]),
+    ("llmhip_qmat_gemv_noalloc", I, [P, P, P, I, I, P]),
     ("llmhip_qmat_gemv_q8", I, [P, P, P, I, P]),
     ("llmhip_qmat_bytes", U64, [P]),
     ("llmhip_qmat_gguf_bytes", U64, [P]),

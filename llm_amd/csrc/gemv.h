@@ -85,10 +85,11 @@ struct GemvArgs {
   uint32_t q8;     // the prepared activations are Q8 blocks (PRO_Q8): gemm_kernel's block products
 };
 
-// Bytes of the prepared-activation buffers for ntok tokens of k inputs.
-inline uint64_t xprep_bytes(uint32_t ntok, uint32_t k) {
-  uint64_t tg = (ntok + 7) / 8, nb = k / 32;
-  return tg * nb * 64 * 16 + tg * 8 * 4 + 2 * tg * 8 * nb * 4 + 4 * 256;
+// Bytes of the prepared-activation buffers for ntok tokens of k inputs
+// (room for xprep_bind's rounding of each part to 256 bytes included).
+constexpr uint64_t xprep_bytes(uint32_t ntok, uint32_t k) {
+  return ((uint64_t)ntok + 7) / 8 * (k / 32) * 64 * 16 + ((uint64_t)ntok + 7) / 8 * 8 * 4 +
+         2 * (((uint64_t)ntok + 7) / 8) * 8 * (k / 32) * 4 + 4 * 256;
 }
 // Point a.xp / a.xexp / a.xbsum / a.xdx into one buffer of xprep_bytes.
 inline void xprep_bind(GemvArgs* a, void* buf) {

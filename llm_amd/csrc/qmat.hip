@@ -351,13 +351,44 @@ static int qmat_gemv_args(llmhip_qmat* q, const float* x, float* y, int n, GemvA
   return 0;
 }
 
-static int qmat_launch(llmhip_qmat* q, GemvArgs& a, int epi, hipStream_t s, int pro = PRO_PLAIN) {
+// One product: the decode kernel below GEMM_MIN_TOKENS tokens, else the
+// prefill pair, whose prepared activations go to `xprep` (xprep_bytes(64, k)
+// bytes; nullptr: the matrix's own buffer, allocated on first use).
+static int qmat_launch(llmhip_qmat* q, GemvArgs& a, int epi, hipStream_t s, int pro = PRO_PLAIN,
+                       void* xprep = nullptr) {
   if (a.ntok < GEMM_MIN_TOKENS) return gemv_launch(a, q->m.g.q.type, pro, epi, s);
-  if (!q->xprep) LLM_HIP(hipMalloc(&q->xprep, xprep_bytes(64, (uint32_t)q->m.g.k)));
-  xprep_bind(&a, q->xprep);
+  if (!xprep) {
+    if (!q->xprep) LLM_HIP(hipMalloc(&q->xprep, xprep_bytes(64, (uint32_t)q->m.g.k)));
+    xprep = q->xprep;
+  }
+  xprep_bind(&a, xprep);
   a.q8 = (pro & PRO_Q8) ? 1 : 0;
   LLM_TRY(prep_launch(a, pro, s));
   return gemm_launch(a, q->m.g.q.type, epi, s);
+}
+
+// The scratch of llmhip_qmat_gemv_noalloc: the prepared activations of up to
+// 64 tokens of k <= LLMHIP_NOALLOC_MAX_K, one copy per device for the life of
+// the process.  Host code uses the address noalloc_scratch() returns for the
+// current device, never the array's name (a host-side stand-in).
+static __device__ __align__(256) uint8_t scratch[xprep_bytes(64, LLMHIP_NOALLOC_MAX_K)];
+
+static std::mutex g_scratch_mu;
+static std::vector<void*> g_scratch_at;  // per device ordinal, from hipGetSymbolAddress
+
+static int noalloc_scratch(int device, void** out) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (device < 0) return set_error(LLMHIP_ERR_ARG, "llm: device %d", device);
+  if ((size_t)device >= g_scratch_at.size()) g_scratch_at.resize((size_t)device + 1, nullptr);
+  if (!g_scratch_at[(size_t)device]) {
+    LLM_HIP(hipSetDevice(device));  // the address is per device: look it up with the device current
+    void* p = nullptr;
+    LLM_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return set_error(LLMHIP_ERR_DEVICE, "llm: no device address for the scratch array");
+    g_scratch_at[(size_t)device] = p;
+  }
+  *out = g_scratch_at[(size_t)device];
+  return 0;
 }
 
 int llmhip_qmat_gemv(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, int accumulate, void* hip_stream) {
@@ -366,6 +397,20 @@ int llmhip_qmat_gemv(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, in
   LLM_TRY(qmat_gemv_args(q, x_dev, y_dev, n, &a));
   LLM_TRY(qmat_ready(q));
   return qmat_launch(q, a, accumulate ? EPI_ACC : EPI_STORE, (hipStream_t)hip_stream);
+}
+
+int llmhip_qmat_gemv_noalloc(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, int accumulate,
+                             void* hip_stream) {
+  clear_error();
+  if (q->m.g.k > LLMHIP_NOALLOC_MAX_K)
+    return set_error(LLMHIP_ERR_ARG, "llm: gemv_noalloc: k=%llu is above its scratch's maximum of %u",
+                     (unsigned long long)q->m.g.k, (unsigned)LLMHIP_NOALLOC_MAX_K);
+  GemvArgs a;
+  LLM_TRY(qmat_gemv_args(q, x_dev, y_dev, n, &a));
+  void* xp = nullptr;
+  if (a.ntok >= GEMM_MIN_TOKENS) LLM_TRY(noalloc_scratch(q->m.device, &xp));
+  LLM_TRY(qmat_ready(q));
+  return qmat_launch(q, a, accumulate ? EPI_ACC : EPI_STORE, (hipStream_t)hip_stream, PRO_PLAIN, xp);
 }
 
 int llmhip_qmat_gemv_q8(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, void* hip_stream) {
