@@ -254,30 +254,61 @@ def sweep(args):
     return out
 
 
-def cpu_baseline(args):
-    """The CPU oracle (C restatement of cpu.go, row-parallel, bit-identical to
-    single-threaded) on a bounded sample of the same workload."""
-    from llm_amd import synth
+def _cpu_model():
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def _oracle_decode(cpu, prompt, seconds, ctx):
+    """(prefill tok/s over the prompt, decode tok/s, decode tokens) of the
+    oracle, decoding greedily for about `seconds` after the prompt."""
     from oracle import cpuref
-    spec = synth.qwen25(seed=0)
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
-    cpu = cpuref.CPU(synth.cached(spec), args.ctx, threads=threads)
-    prompt = list(synth.prompt(0, 8, spec.vocab))
     t0 = time.perf_counter()
     for t in prompt:
         logits = cpu.forward(t)
     pre = len(prompt) / (time.perf_counter() - t0)
     n = 0
     t0 = time.perf_counter()
-    while (time.perf_counter() - t0 < args.cpu_seconds or n < 4) and len(prompt) + n < args.ctx:
+    while (time.perf_counter() - t0 < seconds or n < 4) and len(prompt) + n < ctx:
         logits = cpu.forward(cpuref.argmax(logits))
         n += 1
-    dec = n / (time.perf_counter() - t0)
-    log(f"cpu oracle ({threads} threads): prefill {pre:.2f} tok/s, decode {dec:.2f} tok/s over {n} tokens")
-    return {"value": round(dec, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"qwen2.5-0.5b shape (same seeded model), 8 prompt tokens then {n} greedy decode tokens "
-                      f"(~{args.cpu_seconds:.0f}s), decode tok/s of the row-parallel oracle",
-            "prefill_tok_s": round(pre, 3)}
+    return pre, n / (time.perf_counter() - t0), n
+
+
+def cpu_baseline(args):
+    """The CPU oracle (the C restatement of cpu.go, -O2 -ffp-contract=off) on
+    a bounded sample of the same workload: single-threaded, as cpu.go's
+    Forward runs on one goroutine (cpu.go:225) -- the `value` -- and
+    row-parallel over the host's cores (bit-identical results) beside it."""
+    from llm_amd import synth
+    from oracle import cpuref
+    spec = synth.qwen25(seed=0)
+    path = synth.cached(spec)
+    prompt = list(synth.prompt(0, 8, spec.vocab))
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = min(affinity or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
+    cpu = cpuref.CPU(path, args.ctx, threads=1)
+    pre1, dec1, n1 = _oracle_decode(cpu, prompt, args.cpu_seconds, args.ctx)
+    cpu.close()
+    cpu = cpuref.CPU(path, args.ctx, threads=threads)
+    pre, dec, n = _oracle_decode(cpu, prompt, args.cpu_seconds, args.ctx)
+    cpu.close()
+    log(f"cpu oracle: 1 thread decode {dec1:.2f} tok/s ({n1} tokens); {threads} threads decode {dec:.2f} tok/s "
+        f"({n} tokens); host {_cpu_model()}, {os.cpu_count()} CPUs, {affinity} in this process's affinity")
+    return {"value": round(dec1, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"qwen2.5-0.5b shape (the same seeded model), 8 prompt tokens then {n1} greedy decode tokens "
+                      f"(~{args.cpu_seconds:.0f}s) on one thread, decode tok/s",
+            "prefill_tok_s": round(pre1, 3),
+            "row_parallel": {"value": round(dec, 3), "unit": "tok/s", "cores": threads, "prefill_tok_s": round(pre, 3),
+                             "sample": f"the same, {n} decode tokens, matvec rows and attention heads over "
+                                       f"{threads} threads"},
+            "host": {"cpu_model": _cpu_model(), "nproc": os.cpu_count(), "affinity": affinity}}
 
 
 def main():
