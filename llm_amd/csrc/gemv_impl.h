@@ -618,19 +618,22 @@ struct WUnit {
 // Load group g (< ng) of tile t of the matrix at wq.  The layer matrices use
 // ordinary (cacheable) loads; the streaming kernel's are non-temporal, so the
 // one-pass read of the vocabulary head does not push the layers out of cache.
+// With `real` false the unit is not needed: every lane reads the tile's first
+// bytes (one cache line), so the load stays unconditional and costs nothing.
 template <uint32_t QT, bool STREAM = false>
 __device__ __forceinline__ void load_group(WUnit& u, const uint8_t* wq, uint32_t nb, uint32_t t, uint32_t g,
-                                           int lane, int r) {
+                                           int lane, int r, bool real = true) {
   typedef Lay<QT> LY;
   const uint8_t* tb = wq + LY::tile(t, nb);
+  const uint32_t ql = real ? g * LY::QG + lane * 16 : 0;
   if (STREAM) {
-    u.w0 = ld_stream16(tb + g * LY::QG + lane * 16);
-    if (QT == LLMHIP_Q8_0) u.w1 = ld_stream16(tb + g * LY::QG + 1024 + lane * 16);
+    u.w0 = ld_stream16(tb + ql);
+    if (QT == LLMHIP_Q8_0) u.w1 = ld_stream16(tb + ql + (real ? 1024 : 0));
   } else {
-    u.w0 = *(const uint4*)(tb + g * LY::QG + lane * 16);
-    if (QT == LLMHIP_Q8_0) u.w1 = *(const uint4*)(tb + g * LY::QG + 1024 + lane * 16);
+    u.w0 = *(const uint4*)(tb + ql);
+    if (QT == LLMHIP_Q8_0) u.w1 = *(const uint4*)(tb + ql + (real ? 1024 : 0));
   }
-  const uint8_t* sp = tb + 16 * nb * LY::QB + g * 64 * LY::SB + r * 4 * LY::SB;
+  const uint8_t* sp = tb + (real ? 16 * nb * LY::QB + g * 64 * LY::SB + r * 4 * LY::SB : 0);
   if (QT == LLMHIP_Q4_1) {
     u.sv = *(const uint4*)sp;
   } else {
@@ -776,100 +779,6 @@ __device__ __forceinline__ void argmax_partial(const GemvArgs& a, float* misc, f
       }
     a.amax_v[blockIdx.x] = bv;
     a.amax_i[blockIdx.x] = bi;
-  }
-}
-
-// The decode matrix-vector product (and up to 4 tokens): waves of a
-// workgroup own 16-row tiles, `split` waves share a tile's block groups
-// (split-K, added in a fixed order through LDS).  The first batch of up to
-// four of a wave's units is loaded before the activation prologue, so the
-// weight and activation round trips overlap (up to two tokens: with four, the
-// registers held across the prologue would spill).
-template <uint32_t QT, int NT, int PRO, int EPI>
-__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
-  typedef QT_<QT> T;
-  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  const uint32_t bd = blockDim.x, nwv = bd >> 6;
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const uint32_t t0 = blockIdx.y * NT;
-  const int nt = min((int)NT, (int)(a.ntok - t0));
-  const uint32_t nb = a.nb;
-  constexpr bool Q8 = (PRO & PRO_Q8) != 0;
-  const Lds L = lds_layout(NT, QT, nb, nwv, Q8);
-  h8* xs = (h8*)(lds + L.xs);
-  float* misc = (float*)(lds + L.misc);  // [0,64) sum-of-squares partials, [64,128) max partials, then argmax
-  float* bsum = (float*)(lds + L.bsum);
-  float* dxs = (float*)(lds + L.dx);
-
-  constexpr bool HOIST = NT <= 2;
-  const uint32_t split = a.split, tpw = nwv / split;
-  const uint32_t lt = wave / split, sp = wave % split;
-  const uint32_t tile = blockIdx.x * tpw + lt;
-  const bool has_tile = tile < a.tiles;
-  const int r = lane & 15, q = lane >> 4;  // B/D column (row in tile), k-group / D row group
-  const int slot = lane & 15;              // A row: token slot
-  // this wave's groups: sp, sp + split, ... below ng; the tail goes to wave ng % split
-  const uint32_t cnt = has_tile && a.ng > sp ? (a.ng - sp + split - 1) / split : 0;
-  const bool has_tail = has_tile && a.tail && (a.ng % split) == sp;
-  WUnit w[4], wt;
-  auto load_batch = [&](uint32_t i0) {
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-      if (i0 + u < cnt) load_group<QT>(w[u], a.qs, nb, tile, sp + (i0 + u) * split, lane, r);
-  };
-  if (HOIST) {
-    load_batch(0);
-    if (has_tail) load_unit<QT>(wt, a.qs, nb, tile, a.ng, a.ng, a.tail, lane, r);
-  }
-
-  // the epilogue's own inputs, in flight during the prologue
-  const bool active = sp == 0 && has_tile;
-  const int tA = 2 * q, tB = 2 * q + 1;
-  const bool okA = tA < nt, okB = NT > 1 && tB < nt;
-  const EpiIn pre = epi_load<EPI>(a, tile, r, active, t0 + tA, okA, t0 + tB, okB);
-
-  int ex[NT];
-  stage_x<QT, NT, PRO>(a, t0, nt, xs, misc, bsum, dxs, ex);
-
-  float acc0 = 0, acc1 = 0;
-  for (uint32_t i0 = 0; i0 < cnt; i0 += 4) {
-    if (i0 > 0 || !HOIST) load_batch(i0);
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-      if (i0 + u < cnt)
-        unit_mfma<QT, NT, Q8>(w[u], sp + (i0 + u) * split, a.ng, a.tail, xs, bsum, dxs, nb, q, slot, acc0, acc1);
-  }
-  if (has_tail) {
-    if (!HOIST) load_unit<QT>(wt, a.qs, nb, tile, a.ng, a.ng, a.tail, lane, r);
-    unit_mfma<QT, NT, Q8>(wt, a.ng, a.ng, a.tail, xs, bsum, dxs, nb, q, slot, acc0, acc1);
-  }
-  // ---- split-K: partial sums of the waves of a tile, added in a fixed order
-  if (split > 1) {
-    float* part = (float*)(lds + L.part);
-    part[(wave * 64 + lane) * 2] = acc0;
-    part[(wave * 64 + lane) * 2 + 1] = acc1;
-    __syncthreads();
-    if (sp == 0) {
-      for (uint32_t s = 1; s < split; s++) {
-        acc0 += part[((wave + s) * 64 + lane) * 2];
-        acc1 += part[((wave + s) * 64 + lane) * 2 + 1];
-      }
-    }
-  }
-  // ---- epilogue: lane holds rows r of the tile for tokens 2q and 2q+1
-  int eA = 0, eB = 0;
-#pragma unroll
-  for (int t = 0; t < NT; t++) {
-    if (t == tA) eA = ex[t];
-    if (t == tB) eB = ex[t];
-  }
-  const float vA = okA ? ldexpf(acc0, -eA) : 0.f;
-  const float vB = okB ? ldexpf(acc1, -eB) : 0.f;
-  row_epilogue<EPI>(a, tile, r, active, t0 + tA, okA, vA, t0 + tB, okB, vB, &pre);
-  if (EPI == EPI_ARGMAX) {
-    const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
-    const bool ok = active && lr < a.rows && q == 0 && okA && vA == vA;
-    argmax_partial(a, misc, ok ? vA : -INFINITY, ok ? lr : 0xffffffffu);
   }
 }
 
@@ -1280,11 +1189,389 @@ __global__ __launch_bounds__(64 * GEMM_MAXW) void gemm_kernel(GemvArgs a) {
   }
 }
 
+// ------------------------------------------------------- the decode kernel
+
+// The decode matrix-vector product (1, 2 or 4 tokens).  Waves of a workgroup
+// own 16-row tiles; `split` waves share a tile's block groups (split-K, added
+// in a fixed order through LDS at the end).  Each wave stages only the
+// activations its own units need, in its own part of LDS, with no barrier:
+// a batch of up to UB units (groups of four blocks), one DPP row of 16 lanes
+// per unit, lane = item (block b, k-group iq: elements 4iq..4iq+3 and
+// 16+4iq..16+4iq+3 of the block).  Each unit and token gets its own power of
+// two 2^e (the unit's largest magnitude in [2^14, 2^15)), the scaled values are
+// split exactly into f16 hi + lo, written to the wave's LDS in MFMA operand
+// order and read back by the operand lanes.  RMSNorm (cpu.go:81-98) takes the
+// sum of squares of the whole row, which every wave reduces itself.  Loads are
+// issued rows, then activation items, then weights: they return in order, so
+// the staging overlaps the weights' round trip.
+constexpr int UB = 4;  // units per staging batch: one 16-lane DPP row each
+
+// LDS of one wave: A operands [unit][block][k-group][slot] h8 (slots 2t, 2t+1:
+// hi, lo of token t), then [unit][block][token] floats: the block sums of x
+// (Q4_1) and the activation block scales (PRO_Q8).
+template <int NT>
+struct WaveLds {
+  static constexpr uint32_t S = 2 * NT;
+  static constexpr uint32_t OPS = UB * 16 * S * 16;
+  static constexpr uint32_t TAB = UB * 4 * NT * 4;
+  static constexpr uint32_t BYTES = OPS + 2 * TAB;
+};
+
+// Bytes of LDS of a decode-kernel launch: the waves' own staging, the split-K
+// partials, and 128 floats of workgroup scratch (the argmax partials).
+__host__ __device__ inline uint32_t decode_lds(int nt, uint32_t waves) {
+  const uint32_t per = nt == 1 ? WaveLds<1>::BYTES : nt == 2 ? WaveLds<2>::BYTES : WaveLds<4>::BYTES;
+  return waves * per + waves * 64 * 2 * 4 + 128 * 4;
+}
+
+// One lane's activation item of a staging batch, for each token: x (and the
+// norm weights), zero where the item does not exist.  With four units per
+// batch a lane loads both halves of its item (elements 4iq..4iq+3 in xa,
+// 16+4iq..16+4iq+3 in xc); with two, lanes 0-31 load the first halves of the
+// two units' items and lanes 32-63 the second (one load instruction per
+// array instead of two), in xa, and staging swaps them across.
+template <int NT, bool RMS>
+struct Items {
+  f4 xa[NT], xc[NT], wa, wc;
+};
+
+// Issue the item loads of the batch whose units start at i0 (group sp +
+// i * split for unit i < cnt; with TAILU the tail, blocks < tail).  Absent
+// items read one address for the whole wave, so the loads are unconditional.
+template <int NT, int PRO, bool TAILU, int NU>
+__device__ __forceinline__ void load_items(Items<NT, (PRO & PRO_RMS) != 0>& it, const GemvArgs& a, uint32_t t0, int nt,
+                                           uint32_t i0, uint32_t cnt, uint32_t sp, uint32_t split, int lane) {
+  const uint32_t u = NU == 4 ? lane >> 4 : (lane >> 4) & 1, b = (lane >> 2) & 3, iq = lane & 3;
+  const uint32_t half = NU == 4 ? 0 : lane >> 5;
+  const uint32_t i = i0 + u;
+  const bool ok = TAILU ? (u == 0 && b < a.tail) : i < cnt;
+  const uint32_t g = TAILU ? a.ng : sp + i * split;
+  const uint32_t e0 = ok ? (g * 4 + b) * 32 + 4 * iq + 16 * half : 0;
+  const f4 z = {0, 0, 0, 0};
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const float* xr = a.x + (uint64_t)(a.xrow0 + t0 + min(t, nt - 1)) * a.ldx + e0;
+    const f4 A = *(const f4*)xr;
+    it.xa[t] = ok && t < nt ? A : z;
+    if (NU == 4) {
+      const f4 C = *(const f4*)(xr + 16);
+      it.xc[t] = ok && t < nt ? C : z;
+    }
+  }
+  if (PRO & PRO_RMS) {
+    const f4 A = *(const f4*)(a.nw + e0);
+    it.wa = ok ? A : z;
+    if (NU == 4) {
+      const f4 C = *(const f4*)(a.nw + e0 + 16);
+      it.wc = ok ? C : z;
+    }
+  }
+}
+
+// With two units per batch: each lane's other half, from the lane 32 away.
+__device__ __forceinline__ f4 other_half(const f4& v, int lane) {
+  f4 o;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint32_t x = __float_as_uint(v[k]);
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    o[k] = __uint_as_float(lane < 32 ? r[1] : r[0]);
+  }
+  return o;
+}
+
+// Stage a batch from its loaded items: RMSNorm's h = (x s) w, then per unit
+// and token the scale and the f16 hi + lo split (or, for PRO_Q8, quantizeQ8
+// per block of 32, cpu.go:117-140), into the wave's LDS.  ex[u][t] receives
+// the exponent of unit u, token t (wave-uniform).  Call with the whole wave.
+template <uint32_t QT, int NT, int PRO, int NU>
+__device__ __forceinline__ void stage_items(const Items<NT, (PRO & PRO_RMS) != 0>& it, const float (&rs)[NT], int lane,
+                                            h8* ops, float* sums, float* dxs, int (&ex)[UB][NT]) {
+  constexpr int S = 2 * NT;
+  const uint32_t u = NU == 4 ? lane >> 4 : (lane >> 4) & 1, b = (lane >> 2) & 3, iq = lane & 3;
+  const bool writer = NU == 4 || lane < 32;  // two units: lanes 32-63 hold copies
+  h8* dst = ops + ((u * 4 + b) * 4 + iq) * S;
+  f4 wA = {0, 0, 0, 0}, wC = {0, 0, 0, 0};
+  if (PRO & PRO_RMS) {
+    if (NU == 4) {
+      wA = it.wa;
+      wC = it.wc;
+    } else {
+      const f4 o = other_half(it.wa, lane);
+      wA = lane < 32 ? it.wa : o;
+      wC = lane < 32 ? o : it.wa;
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    f4 A = it.xa[t], C = it.xc[t];
+    if (NU == 2) {
+      const f4 o = other_half(it.xa[t], lane);
+      A = lane < 32 ? it.xa[t] : o;
+      C = lane < 32 ? o : it.xa[t];
+    }
+    if (PRO & PRO_RMS) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        A[k] = __fmul_rn(__fmul_rn(A[k], rs[t]), wA[k]);  // cpu.go:96
+        C[k] = __fmul_rn(__fmul_rn(C[k], rs[t]), wC[k]);
+      }
+    }
+    const float v[8] = {A[0], A[2], C[0], C[2], A[1], A[3], C[1], C[3]};
+    if (PRO & PRO_Q8) {
+      // a block's four items sit in four consecutive lanes
+      float am = 0;
+#pragma unroll
+      for (int k = 0; k < 8; k++) am = fmaxf(am, fabsf(v[k]));
+      am = fmaxf(am, __shfl_xor(am, 1));
+      am = fmaxf(am, __shfl_xor(am, 2));
+      const float d = __fdiv_rn(am, 127.f);
+      const float id = d != 0.f ? __fdiv_rn(1.f, d) : 0.f;
+      h8 hi;
+      int qs = 0;
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const float qv = roundf(__fmul_rn(v[k], id));
+        hi[k] = (_Float16)qv;
+        qs += (int)qv;
+      }
+      qs += __shfl_xor(qs, 1);
+      qs += __shfl_xor(qs, 2);
+      if (writer) {
+        dst[2 * t] = hi;
+        dst[2 * t + 1] = h8{};
+        if (iq == 0) {
+          dxs[(u * 4 + b) * NT + t] = (float)to_f16(d);
+          if (QT == LLMHIP_Q4_1) sums[(u * 4 + b) * NT + t] = (float)to_f16(__fmul_rn(d, (float)qs));
+        }
+      }
+#pragma unroll
+      for (int w = 0; w < UB; w++) ex[w][t] = 0;
+      continue;
+    }
+    float m = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(v[k]));
+    m = row_max16(m);  // the unit's largest magnitude (its 16 lanes)
+    int e = 0;
+    if (m > 0 && m <= 3.0e38f) {
+      int E;
+      frexpf(m, &E);
+      e = 15 - E;
+    }
+    h8 hi, lo;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const float sv = ldexpf(v[k], e);
+      const _Float16 h = (_Float16)sv;
+      hi[k] = h;
+      lo[k] = (_Float16)(sv - (float)h);
+    }
+    if (writer) {
+      dst[2 * t] = hi;
+      dst[2 * t + 1] = lo;
+    }
+    if (QT == LLMHIP_Q4_1) {
+      // block sums sum_j x_j (cpu.go:196-198), unscaled
+      float sx = (A[0] + A[1] + A[2] + A[3]) + (C[0] + C[1] + C[2] + C[3]);
+      sx += __shfl_xor(sx, 1);
+      sx += __shfl_xor(sx, 2);
+      if (writer && iq == 0) sums[(u * 4 + b) * NT + t] = sx;
+    }
+#pragma unroll
+    for (int w = 0; w < UB; w++) ex[w][t] = __builtin_amdgcn_readlane(e, 16 * (w % NU));
+  }
+}
+
+// The MFMAs of unit u of a staged batch: group blocks 0..3, or the tail's
+// blocks 0..tail-1 (TAIL).  Lane (row r, group q) adds to acc0 / acc1 the
+// products of tokens 2q / 2q + 1: d_w 2^-e sum_j (hi + lo)_j w_j per block
+// (+ m_w sum_j x_j for Q4_1), or for PRO_Q8 ggml's d_w d_x sum_j q_j w_j
+// (+ m_w s_x), rounded as cpu.go:174-210 rounds it.
+template <uint32_t QT, int NT, bool Q8, bool TAIL>
+__device__ __forceinline__ void unit_products(const WUnit& w, uint32_t u, int nblk, const h8* ops, const float* sums,
+                                              const float* dxs, const int (&ex)[UB][NT], int q, int slot, float& acc0,
+                                              float& acc1) {
+  constexpr int S = 2 * NT;
+  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+  const int tA = min(2 * q, NT - 1), tB = min(2 * q + 1, NT - 1);
+  const bool okA = 2 * q < NT, okB = 2 * q + 1 < NT;
+  float uA = 0, uB = 0, mA = 0, mB = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    if (j >= nblk) break;
+    const u4v X = __builtin_bit_cast(u4v, ops[((u * 4 + j) * 4 + q) * S + min(slot, S - 1)]);
+    const h8 A = __builtin_bit_cast(h8, X & (slot < S ? ~0u : 0u));
+    h8 B;
+    float d, m;
+    unit_block<QT, TAIL>(w, j, B, d, m);
+    const f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4{0, 0, 0, 0}, 0, 0, 0);
+    const uint32_t bi = (u * 4 + j) * NT;
+    if (Q8) {
+      float pA = __fmul_rn(__fmul_rn(d, dxs[bi + tA]), D[0] + D[1]);
+      float pB = __fmul_rn(__fmul_rn(d, dxs[bi + tB]), D[2] + D[3]);
+      if (QT == LLMHIP_Q4_1) {
+        pA = __fadd_rn(pA, __fmul_rn(m, sums[bi + tA]));
+        pB = __fadd_rn(pB, __fmul_rn(m, sums[bi + tB]));
+      }
+      acc0 += okA ? pA : 0.f;
+      if (NT > 1) acc1 += okB ? pB : 0.f;
+    } else {
+      uA += d * (D[0] + D[1]);
+      if (NT > 1) uB += d * (D[2] + D[3]);
+      if (QT == LLMHIP_Q4_1) {
+        mA += m * sums[bi + tA];
+        if (NT > 1) mB += m * sums[bi + tB];
+      }
+    }
+  }
+  if (!Q8) {
+    // undo the unit's scale of each token (ex[u][t] is wave-uniform)
+    const int eA = NT == 4 && q == 1 ? ex[u][min(2, NT - 1)] : ex[u][0];
+    const int eB = NT == 4 && q == 1 ? ex[u][min(3, NT - 1)] : ex[u][min(1, NT - 1)];
+    acc0 += okA ? ldexpf(uA, -eA) + mA : 0.f;
+    if (NT > 1) acc1 += okB ? ldexpf(uB, -eB) + mB : 0.f;
+  }
+}
+
+template <uint32_t QT, int NT, int PRO, int EPI, int NU>
+__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
+  typedef WaveLds<NT> WL;
+  constexpr bool Q8 = (PRO & PRO_Q8) != 0, RMS = (PRO & PRO_RMS) != 0;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const uint32_t nwv = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const uint32_t t0 = blockIdx.y * NT;
+  const int nt = min((int)NT, (int)(a.ntok - t0));
+  const uint32_t nb = a.nb, ng = a.ng;
+  unsigned char* wl = lds + wave * WL::BYTES;
+  h8* ops = (h8*)wl;
+  float* sums = (float*)(wl + WL::OPS);
+  float* dxs = (float*)(wl + WL::OPS + WL::TAB);
+  float* part = (float*)(lds + nwv * WL::BYTES);
+  float* misc = part + nwv * 64 * 2;  // [0, 64): RMS partials; [80, 112): argmax partials
+
+  const uint32_t split = a.split, tpw = nwv / split;
+  const uint32_t lt = wave / split, sp = wave % split;
+  const uint32_t tile = min(blockIdx.x * tpw + lt, a.tiles - 1);
+  const bool has_tile = blockIdx.x * tpw + lt < a.tiles;
+  const int r = lane & 15, q = lane >> 4, slot = lane & 15;
+  // this wave's units: groups sp, sp + split, ... below ng, then the tail (wave ng % split)
+  const uint32_t cnt = has_tile && ng > sp ? (ng - sp + split - 1) / split : 0;
+  const bool has_tail = has_tile && a.tail && (ng % split) == sp;
+
+  // the epilogue's own inputs, in flight during the prologue
+  const bool active = sp == 0 && has_tile;
+  const int tA = 2 * q, tB = 2 * q + 1;
+  const bool okA = tA < nt, okB = NT > 1 && tB < nt;
+  const EpiIn pre = epi_load<EPI>(a, tile, r, active, t0 + tA, okA, t0 + tB, okB);
+
+  // RMSNorm's sum of squares: the workgroup's waves load the row between
+  // them (two float4s per lane and token at once: rows up to 512 * waves floats)
+  constexpr int RV = 2;
+  const uint32_t K4 = a.k / 4;
+  f4 rv[RMS ? NT : 1][RMS ? RV : 1];
+  if (RMS) {
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int v = 0; v < RV; v++) {
+        const uint32_t c = min(wave * 64 + lane + 64 * nwv * v, K4 - 1);
+        rv[t][v] = *(const f4*)(a.x + (uint64_t)(a.xrow0 + t0 + min(t, nt - 1)) * a.ldx + 4 * c);
+      }
+  }
+  // the first batch: activation items, then weights (they return in that order)
+  Items<NT, RMS> it, itt;
+  WUnit w[NU], wt;
+  load_items<NT, PRO, false, NU>(it, a, t0, nt, 0, cnt, sp, split, lane);
+#pragma unroll
+  for (int u = 0; u < NU; u++) load_group<QT>(w[u], a.qs, nb, tile, sp + u * split, lane, r, (uint32_t)u < cnt);
+  if (NT == 1 && has_tail) {  // (several tokens: loaded when the tail comes, to hold fewer registers)
+    load_items<NT, PRO, true, NU>(itt, a, t0, nt, 0, cnt, sp, split, lane);
+    load_unit<QT>(wt, a.qs, nb, tile, ng, ng, a.tail, lane, r);
+  }
+  float rs[NT];
+  if (RMS) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      float ss = 0;
+#pragma unroll
+      for (int v = 0; v < RV; v++)
+        if (wave * 64 + lane + 64 * nwv * v < K4)
+          ss += rv[t][v][0] * rv[t][v][0] + rv[t][v][1] * rv[t][v][1] + rv[t][v][2] * rv[t][v][2] +
+                rv[t][v][3] * rv[t][v][3];
+      for (uint32_t c = wave * 64 + lane + 64 * nwv * RV; c < K4; c += 64 * nwv) {  // longer rows
+        const f4 x4 = *(const f4*)(a.x + (uint64_t)(a.xrow0 + t0 + min(t, nt - 1)) * a.ldx + 4 * c);
+        ss += x4[0] * x4[0] + x4[1] * x4[1] + x4[2] * x4[2] + x4[3] * x4[3];
+      }
+      ss = wave_sum_dpp(ss);
+      if (lane == 0) misc[wave * NT + t] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      float ss = 0;
+      for (uint32_t v = 0; v < nwv; v++) ss += misc[v * NT + t];  // every thread, the same order
+      rs[t] = t < nt ? (float)(1.0 / sqrt((double)(ss / (float)a.k + a.eps))) : 0.f;  // cpu.go:90-95
+    }
+  }
+
+  float acc0 = 0, acc1 = 0;
+  int ex[UB][NT];
+  for (uint32_t i0 = 0; i0 < cnt; i0 += NU) {
+    if (i0 > 0) {
+      load_items<NT, PRO, false, NU>(it, a, t0, nt, i0, cnt, sp, split, lane);
+#pragma unroll
+      for (int u = 0; u < NU; u++) load_group<QT>(w[u], a.qs, nb, tile, sp + (i0 + u) * split, lane, r, i0 + u < cnt);
+    }
+    stage_items<QT, NT, PRO, NU>(it, rs, lane, ops, sums, dxs, ex);
+#pragma unroll
+    for (int u = 0; u < NU; u++)
+      if (i0 + u < cnt) unit_products<QT, NT, Q8, false>(w[u], u, 4, ops, sums, dxs, ex, q, slot, acc0, acc1);
+  }
+  if (has_tail) {
+    if (NT > 1) {
+      load_items<NT, PRO, true, NU>(itt, a, t0, nt, 0, cnt, sp, split, lane);
+      load_unit<QT>(wt, a.qs, nb, tile, ng, ng, a.tail, lane, r);
+    }
+    stage_items<QT, NT, PRO, NU>(itt, rs, lane, ops, sums, dxs, ex);
+    unit_products<QT, NT, Q8, true>(wt, 0, (int)a.tail, ops, sums, dxs, ex, q, slot, acc0, acc1);
+  }
+  // ---- split-K: partial sums of the waves of a tile, added in a fixed order
+  // (every partial read issued before the sums)
+  if (split > 1) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    f2* p2 = (f2*)part;
+    p2[wave * 64 + lane] = f2{acc0, acc1};
+    __syncthreads();
+    if (sp == 0) {
+      f2 pv[15];
+#pragma unroll
+      for (int k = 0; k < 15; k++) pv[k] = p2[(wave + min((uint32_t)k + 1, split - 1)) * 64 + lane];
+#pragma unroll
+      for (int k = 0; k < 15; k++)
+        if ((uint32_t)k + 1 < split) {
+          acc0 += pv[k][0];
+          acc1 += pv[k][1];
+        }
+    }
+  }
+  // ---- epilogue: lane holds rows r of the tile for tokens 2q and 2q+1
+  const float vA = okA ? acc0 : 0.f;
+  const float vB = okB ? acc1 : 0.f;
+  row_epilogue<EPI>(a, tile, r, active, t0 + tA, okA, vA, t0 + tB, okB, vB, &pre);
+  if (EPI == EPI_ARGMAX) {
+    const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
+    const bool ok = active && lr < a.rows && q == 0 && okA && vA == vA;
+    argmax_partial(a, misc, ok ? vA : -INFINITY, ok ? lr : 0xffffffffu);
+  }
+}
+
 // ----------------------------------------------------------- dispatch
 
-template <uint32_t QT, int NT, int PRO, int EPI>
-static int launch_one(const GemvArgs& a, dim3 grid, uint32_t lds, hipStream_t s) {
-  auto k = gemv_kernel<QT, NT, PRO, EPI>;
+template <uint32_t QT, int NT, int PRO, int EPI, int NU>
+static int launch_nu(const GemvArgs& a, dim3 grid, uint32_t lds, hipStream_t s) {
+  auto k = gemv_kernel<QT, NT, PRO, EPI, NU>;
   static bool big = false;
   if (lds > 65536 && !big) {
     LLM_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
@@ -1293,6 +1580,15 @@ static int launch_one(const GemvArgs& a, dim3 grid, uint32_t lds, hipStream_t s)
   hipLaunchKernelGGL(k, grid, dim3(64 * a.waves), lds, s, a);
   LLM_HIP(hipGetLastError());
   return 0;
+}
+
+// Units a wave stages per batch: two when no wave has more than two groups
+// (no load is issued for a third or fourth), else four.
+template <uint32_t QT, int NT, int PRO, int EPI>
+static int launch_one(const GemvArgs& a, dim3 grid, uint32_t lds, hipStream_t s) {
+  const uint32_t per_wave = (a.ng + a.split - 1) / a.split;
+  if (per_wave <= 2) return launch_nu<QT, NT, PRO, EPI, 2>(a, grid, lds, s);
+  return launch_nu<QT, NT, PRO, EPI, 4>(a, grid, lds, s);
 }
 
 template <uint32_t QT, int NT, int Q>
@@ -1338,15 +1634,15 @@ int gemv_launch_qt(const GemvArgs& a, int pro, int epi, hipStream_t s) {
     return set_error(LLMHIP_ERR_ARG, "llm: gemv: no streaming form of prologue/epilogue %d/%d", pro, epi);
   }
   int nt = a.ntok <= 1 ? 1 : a.ntok <= 2 ? 2 : 4;
-  Lds L = lds_layout(nt, QT, a.nb, a.waves, (pro & PRO_Q8) != 0);
-  if (L.total > 160 * 1024)
-    return set_error(LLMHIP_ERR_ARG, "llm: gemv: k=%u needs %u bytes of LDS", a.k, L.total);
+  const uint32_t lds = decode_lds(nt, a.waves);
+  if (lds > 160 * 1024)
+    return set_error(LLMHIP_ERR_ARG, "llm: gemv: %u waves of %d tokens need %u bytes of LDS", a.waves, nt, lds);
   if (epi == EPI_ARGMAX && a.ntok != 1) return set_error(LLMHIP_ERR_ARG, "llm: gemv: argmax epilogue needs one token");
   dim3 grid(gemv_groups(a), (a.ntok + nt - 1) / nt);
   switch (nt) {
-    case 1: return launch_nt<QT, 1>(a, pro, epi, grid, L.total, s);
-    case 2: return launch_nt<QT, 2>(a, pro, epi, grid, L.total, s);
-    default: return launch_nt<QT, 4>(a, pro, epi, grid, L.total, s);
+    case 1: return launch_nt<QT, 1>(a, pro, epi, grid, lds, s);
+    case 2: return launch_nt<QT, 2>(a, pro, epi, grid, lds, s);
+    default: return launch_nt<QT, 4>(a, pro, epi, grid, lds, s);
   }
 }
 
