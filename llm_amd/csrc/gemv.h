@@ -117,7 +117,8 @@ int gemv_launch(const GemvArgs& a, uint32_t qtype, int pro, int epi, hipStream_t
 uint32_t gemv_groups(const GemvArgs& a);
 // Picks the split-K factor (waves per tile) and the waves per workgroup.
 void gemv_pick(uint32_t tiles, uint32_t ng, uint32_t tail, uint32_t nb, uint32_t* split, uint32_t* waves);
-// Picks the streaming form for a one-token launch: workgroups (0: none) and waves per workgroup.
+// Picks the streaming form for a one-token launch: workgroups (0: none: fewer than
+// GEMV_STREAM_MIN_TILES tiles, or tail blocks) and waves per workgroup.
 void gemv_pick_stream(uint32_t tiles, uint32_t nb, uint32_t* wgs, uint32_t* waves);
 // Tiles from which one-token launches stream.
 constexpr uint32_t GEMV_STREAM_MIN_TILES = 4096;

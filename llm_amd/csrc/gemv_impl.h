@@ -242,6 +242,31 @@ __device__ __forceinline__ h8 dq4(uint32_t w) {
   return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
+// dq4 with its masks and the 0x6400 exponent held in registers: gfx9's
+// three-operand encoding takes no literal, so with the constants as literals
+// each (w & mask) | 0x6400.. is two instructions; from registers it is one
+// v_and_or_b32 (the exponent bits and the masks do not overlap).
+struct Dq4K {
+  uint32_t m0, m1, magic;
+};
+__device__ __forceinline__ Dq4K dq4_consts() {
+  Dq4K k{0x000F000Fu, 0x00F000F0u, 0x64006400u};
+  asm volatile("" : "+s"(k.m0), "+s"(k.m1), "+v"(k.magic));
+  return k;
+}
+template <bool Q41>
+__device__ __forceinline__ h8 dq4k(uint32_t w, const Dq4K& k) {
+  const h2 lo_off = Q41 ? h2{(_Float16)-1024, (_Float16)-1024} : h2{(_Float16)-1032, (_Float16)-1032};
+  const h2 hi_off = Q41 ? h2{(_Float16)-64, (_Float16)-64} : h2{(_Float16)-72, (_Float16)-72};
+  const h2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const uint32_t w8 = w >> 8;
+  h2 a = as_h2((w & k.m0) | k.magic) + lo_off;
+  h2 b = as_h2((w & k.m1) | k.magic) * s16 + hi_off;
+  h2 c = as_h2((w8 & k.m0) | k.magic) + lo_off;
+  h2 d = as_h2((w8 & k.m1) | k.magic) * s16 + hi_off;
+  return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
 // Two repacked Q8_0 words as eight f16 weights in the same element order:
 // bytes 0 and 2 of a word form one pair, bytes 1 and 3 the other.  With
 // the sign bit flipped a byte is i8+128; 0x64 above it gives 1024+i8+128.
@@ -620,7 +645,7 @@ struct WUnit {
 // one-pass read of the vocabulary head does not push the layers out of cache.
 // With `real` false the unit is not needed: every lane reads the tile's first
 // bytes (one cache line), so the load stays unconditional and costs nothing.
-template <uint32_t QT, bool STREAM = false>
+template <uint32_t QT, bool STREAM = false, bool SCALES = true>
 __device__ __forceinline__ void load_group(WUnit& u, const uint8_t* wq, uint32_t nb, uint32_t t, uint32_t g,
                                            int lane, int r, bool real = true) {
   typedef Lay<QT> LY;
@@ -633,6 +658,7 @@ __device__ __forceinline__ void load_group(WUnit& u, const uint8_t* wq, uint32_t
     u.w0 = *(const uint4*)(tb + ql);
     if (QT == LLMHIP_Q8_0) u.w1 = *(const uint4*)(tb + ql + (real ? 1024 : 0));
   }
+  if (!SCALES) return;
   const uint8_t* sp = tb + (real ? 16 * nb * LY::QB + g * 64 * LY::SB + r * 4 * LY::SB : 0);
   if (QT == LLMHIP_Q4_1) {
     u.sv = *(const uint4*)sp;
@@ -640,6 +666,34 @@ __device__ __forceinline__ void load_group(WUnit& u, const uint8_t* wq, uint32_t
     uint2 x2 = *(const uint2*)sp;
     u.sv = uint4{x2.x, x2.y, 0, 0};
   }
+}
+
+// The scales of groups 4h .. 4h+3 of tile t (no tail blocks), one load for
+// four groups: lane L holds row L % 16 of group 4h + L / 16 (groups past
+// NG - 1 read group NG - 1 again).  `real` false: one lane-invariant line.
+template <uint32_t QT, int NG>
+__device__ __forceinline__ uint4 load_scales4(const uint8_t* wq, uint32_t nb, uint32_t t, int h, int lane,
+                                              bool real) {
+  typedef Lay<QT> LY;
+  constexpr uint32_t SR = 4 * LY::SB;  // one row's scale bytes in a group
+  const uint32_t g = min(4 * h + (lane >> 4), NG - 1);
+  const uint8_t* sp = wq + LY::tile(t, nb) + (real ? 16 * nb * LY::QB + g * 16 * SR + (lane & 15) * SR : 0);
+  if (SR == 16) return *(const uint4*)sp;
+  const uint2 x = *(const uint2*)sp;
+  return uint4{x.x, x.y, 0, 0};
+}
+
+// Group g's scales of row r, as load_group leaves them in WUnit::sv, from
+// the four-group load that holds them (lane 16 (g % 4) + r).
+template <uint32_t QT>
+__device__ __forceinline__ uint4 group_scales(const uint4& s4, int g, int r) {
+  const int src = (16 * (g & 3) + r) * 4;
+  uint4 v;
+  v.x = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)s4.x);
+  v.y = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)s4.y);
+  v.z = QT == LLMHIP_Q4_1 ? (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)s4.z) : 0u;
+  v.w = QT == LLMHIP_Q4_1 ? (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)s4.w) : 0u;
+  return v;
 }
 
 // Load unit g (< ng: a group, == ng: the tail) of tile t of the matrix at wq.
@@ -708,12 +762,11 @@ __device__ __forceinline__ void mfma_block(const h8* xs, const float* bsum, cons
   }
 }
 
-// The blocks of unit g of a tile (see WUnit).
+// The four blocks of group g of a tile (see WUnit).
 template <uint32_t QT, int NT, bool Q8 = false>
-__device__ __forceinline__ void unit_mfma(const WUnit& u, uint32_t g, uint32_t ng, uint32_t tail, const h8* xs,
-                                          const float* bsum, const float* dxs, uint32_t nb, int q, int slot,
-                                          float& acc0, float& acc1) {
-  if (g < ng) {
+__device__ __forceinline__ void group_mfma(const WUnit& u, uint32_t g, const h8* xs, const float* bsum,
+                                           const float* dxs, uint32_t nb, int q, int slot, float& acc0, float& acc1) {
+  {
     const uint32_t b0 = 4 * g;
     if (QT == LLMHIP_Q8_0) {
       mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 0, dq8(u.w0.x, u.w0.y), u.sv.x & 0xffff, 0, acc0, acc1);
@@ -735,18 +788,36 @@ __device__ __forceinline__ void unit_mfma(const WUnit& u, uint32_t g, uint32_t n
       mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 2, dq4<false>(u.w0.z), u.sv.y & 0xffff, 0, acc0, acc1);
       mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b0 + 3, dq4<false>(u.w0.w), u.sv.y >> 16, 0, acc0, acc1);
     }
-    return;
   }
-  const uint32_t q0[3] = {u.w0.x, u.w0.y, u.w0.z}, q1[3] = {u.w1.x, u.w1.y, u.w1.z}, s[3] = {u.sv.x, u.sv.y, u.sv.z};
-#pragma unroll
-  for (uint32_t j = 0; j < 3; j++) {
-    if (j >= tail) continue;
-    const uint32_t b = 4 * ng + j;
-    if (QT == LLMHIP_Q8_0)
-      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b, dq8(q0[j], q1[j]), s[j] & 0xffff, 0, acc0, acc1);
-    else
-      mfma_block<QT, NT, Q8>(xs, bsum, dxs, nb, q, slot, b, dq4<QT == LLMHIP_Q4_1>(q0[j]), s[j] & 0xffff, s[j] >> 16,
-                             acc0, acc1);
+}
+
+// group_mfma for one token with f32 activations whose MFMA operands are
+// already in registers (xa: the group's four blocks, slots past hi/lo zero).
+// Only lanes of q == 0 hold the token's sums; the others accumulate values
+// the epilogue drops, so no per-lane selects.
+template <uint32_t QT>
+__device__ __forceinline__ void group_pre(const WUnit& u, uint32_t g, const h8* xa, const float* bsum,
+                                          const Dq4K& K, float& acc) {
+  auto blk = [&](int j, h8 B, uint32_t dbits, uint32_t mbits) {
+    const f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], B, f4{0, 0, 0, 0}, 0, 0, 0);
+    acc += f16_hw(dbits) * (D[0] + D[1]);
+    if (QT == LLMHIP_Q4_1) acc += f16_hw(mbits) * bsum[4 * g + j];
+  };
+  if (QT == LLMHIP_Q8_0) {
+    blk(0, dq8(u.w0.x, u.w0.y), u.sv.x & 0xffff, 0);
+    blk(1, dq8(u.w0.z, u.w0.w), u.sv.x >> 16, 0);
+    blk(2, dq8(u.w1.x, u.w1.y), u.sv.y & 0xffff, 0);
+    blk(3, dq8(u.w1.z, u.w1.w), u.sv.y >> 16, 0);
+  } else if (QT == LLMHIP_Q4_1) {
+    blk(0, dq4k<true>(u.w0.x, K), u.sv.x & 0xffff, u.sv.x >> 16);
+    blk(1, dq4k<true>(u.w0.y, K), u.sv.y & 0xffff, u.sv.y >> 16);
+    blk(2, dq4k<true>(u.w0.z, K), u.sv.z & 0xffff, u.sv.z >> 16);
+    blk(3, dq4k<true>(u.w0.w, K), u.sv.w & 0xffff, u.sv.w >> 16);
+  } else {
+    blk(0, dq4k<false>(u.w0.x, K), u.sv.x & 0xffff, 0);
+    blk(1, dq4k<false>(u.w0.y, K), u.sv.x >> 16, 0);
+    blk(2, dq4k<false>(u.w0.z, K), u.sv.y & 0xffff, 0);
+    blk(3, dq4k<false>(u.w0.w, K), u.sv.y >> 16, 0);
   }
 }
 
@@ -783,20 +854,27 @@ __device__ __forceinline__ void argmax_partial(const GemvArgs& a, float* misc, f
 }
 
 // Large matrices at one token (the vocabulary head; the 151936-row sweep
-// shape): a grid of a few workgroups per CU, the activations staged once per
-// workgroup, and each of the W waves of the grid streaming its tiles w,
-// w + W, w + 2W, ... as a sequence of units (ng groups, then the tail) with
-// the next R units always in flight: unit i+R is loaded as soon as unit i has
-// gone through the MFMA.  A tile's row epilogue runs after its last unit.
+// shape; k a multiple of 128, no tail blocks): a grid of a few workgroups per
+// CU, the activations staged once per workgroup, and each of the W waves of
+// the grid streaming the groups of its tiles w, w + W, w + 2W, ... in order.
+// Every refill is issued (those past the wave's last tile read one line for
+// the whole wave), so the compiler's wait before each group can count the
+// loads issued after it -- on gfx9 stores count too, so the loop is shaped to
+// make every count static:
+//  NG > 0 (NG groups per tile): one loop iteration is one tile; group g is
+//    taken from ring slot g and the slot refilled with group g of the wave's
+//    next tile at once, so a whole tile (NG groups) is always in flight; the
+//    tile's row epilogue ends the iteration.
+//  NG == 0 (any ng): a ring of STREAM_RING groups, the epilogue after a tile's
+//    last group (in flight between tiles it drains to the epilogue's stores).
 constexpr int STREAM_RING = 4;
-template <uint32_t QT, int PRO, int EPI>
+template <uint32_t QT, int PRO, int EPI, int NG>
 __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
-  constexpr int R = STREAM_RING;
-  typedef QT_<QT> T;
+  constexpr int R = NG > 0 ? NG : STREAM_RING;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const uint32_t nwv = blockDim.x >> 6;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const uint32_t nb = a.nb, ng = a.ng, tail = a.tail;
+  const uint32_t nb = a.nb, ng = NG > 0 ? NG : a.ng;
   constexpr bool Q8 = (PRO & PRO_Q8) != 0;
   const Lds L = lds_layout(1, QT, nb, nwv, Q8);
   h8* xs = (h8*)(lds + L.xs);
@@ -805,43 +883,109 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
   float* dxs = (float*)(lds + L.dx);
   const int r = lane & 15, q = lane >> 4, slot = lane & 15;
   const uint32_t W = gridDim.x * nwv, gw = blockIdx.x * nwv + wave;
-  const uint32_t upt = ng + (tail ? 1 : 0);
   const uint32_t ntw = gw < a.tiles ? (a.tiles - 1 - gw) / W + 1 : 0;
-  const uint32_t U = ntw * upt;
+  const uint32_t U = ntw * ng;
   WUnit w[R];
-  auto fetch = [&](uint32_t i, WUnit& u) {
-    const uint32_t tile = gw + (i / upt) * W;
-    load_unit<QT, true>(u, a.qs, nb, tile, i % upt, ng, tail, lane, r);
-  };
-#pragma unroll
-  for (int d = 0; d < R; d++)
-    if ((uint32_t)d < U) fetch(d, w[d]);
-
-  int ex[1];
-  stage_x<QT, 1, PRO>(a, 0, 1, xs, misc, bsum, dxs, ex);
-
   float acc0 = 0, acc1 = 0, bv = -INFINITY;
   uint32_t bi = 0xffffffffu;
-  for (uint32_t i0 = 0; i0 < U; i0 += R) {
+  int ex[1];
+  // the row epilogue of the wave's tile j (argmax partials in bv / bi)
+  auto finish = [&](uint32_t j) {
+    const uint32_t tile = gw + j * W;
+    const float v = q == 0 ? ldexpf(acc0, -ex[0]) : 0.f;
+    row_epilogue<EPI>(a, tile, r, true, 0, q == 0, v, 1, false, 0.f);
+    if (EPI == EPI_ARGMAX) {
+      const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
+      if (q == 0 && lr < a.rows && v == v && amax_better(v, lr, bv, bi)) {
+        bv = v;
+        bi = lr;
+      }
+    }
+    acc0 = acc1 = 0;
+  };
+  if (NG > 0) {
+    // A tile's scales come in one load per four groups, handed to the lanes
+    // that need them by ds_bpermute (2 loads a tile instead of NG).  They are
+    // double-buffered: tile j's load goes out at group 0 of tile j - 1, so
+    // group 0's wait covers only its own quants and those scales.  Two tiles
+    // per loop trip keep each buffer in fixed registers.
+    constexpr int NS = NG > 0 ? (NG + 3) / 4 : 1;
+    uint4 scA[NS], scB[NS];
+    auto load_sc = [&](uint4(&sc)[NS], uint32_t t, bool real) {
 #pragma unroll
-    for (int d = 0; d < R; d++) {
-      const uint32_t i = i0 + d;
-      if (i >= U) break;
-      const uint32_t g = i % upt;
-      unit_mfma<QT, 1, Q8>(w[d], g, ng, tail, xs, bsum, dxs, nb, q, slot, acc0, acc1);
-      if (i + R < U) fetch(i + R, w[d]);
-      if (g == upt - 1) {  // the tile is complete
-        const uint32_t tile = gw + (i / upt) * W;
-        const float v = q == 0 ? ldexpf(acc0, -ex[0]) : 0.f;
-        row_epilogue<EPI>(a, tile, r, true, 0, q == 0, v, 1, false, 0.f);
-        if (EPI == EPI_ARGMAX) {
-          const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
-          if (q == 0 && lr < a.rows && v == v && amax_better(v, lr, bv, bi)) {
-            bv = v;
-            bi = lr;
-          }
+      for (int h = 0; h < NS; h++) sc[h] = load_scales4<QT, NG>(a.qs, nb, t, h, lane, real);
+    };
+    const uint32_t t0 = min(gw, a.tiles - 1);
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+      load_group<QT, true, false>(w[g], a.qs, nb, t0, g, lane, r, ntw > 0);
+      if (g == 0) load_sc(scA, t0, ntw > 0);
+    }
+    stage_x<QT, 1, PRO>(a, 0, 1, xs, misc, bsum, dxs, ex);
+    // f32 activations: every block's MFMA operand read and masked once
+    constexpr int NX = Q8 ? 1 : 4 * (NG > 0 ? NG : 1);
+    h8 xa[NX];
+    const Dq4K K = dq4_consts();
+    if (!Q8) {
+      typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int b = 0; b < NX; b++) {
+        const u4v X = __builtin_bit_cast(u4v, xs[(b * 4 + q) * 2 + min(slot, 1)]);
+        xa[b] = __builtin_bit_cast(h8, X & (slot < 2 ? ~0u : 0u));
+      }
+    }
+    auto run_tile = [&](uint32_t j, const uint4(&cur)[NS], uint4(&nxt)[NS]) {
+      const uint32_t next = min(gw + (j + 1) * W, a.tiles - 1);
+      const bool more = j + 1 < ntw;
+#pragma unroll
+      for (int g = 0; g < NG; g++) {
+        w[g].sv = group_scales<QT>(cur[g / 4], g, r);
+        if (Q8)
+          group_mfma<QT, 1, Q8>(w[g], g, xs, bsum, dxs, nb, q, slot, acc0, acc1);
+        else
+          group_pre<QT>(w[g], g, xa + 4 * g, bsum, K, acc0);
+        // the slot's last use (the block scales) before its refill, and the
+        // refill issued there: no register copy of a load still in flight
+        // (the empty asm keeps the scaled sums from sinking into the epilogue)
+        asm volatile("" : "+v"(acc0), "+v"(acc1));
+        __builtin_amdgcn_sched_barrier(0);
+        load_group<QT, true, false>(w[g], a.qs, nb, next, g, lane, r, more);
+        if (g == 0) load_sc(nxt, next, more);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      finish(j);
+    };
+    uint32_t j = 0;
+    for (; j + 1 < ntw; j += 2) {
+      run_tile(j, scA, scB);
+      run_tile(j + 1, scB, scA);
+    }
+    if (j < ntw) run_tile(j, scA, scB);
+  } else {
+    uint32_t jf = 0, gf = 0;  // the next group to load: the wave's tile jf, group gf
+    auto fetch = [&](WUnit& u, uint32_t i) {
+      load_group<QT, true>(u, a.qs, nb, min(gw + jf * W, a.tiles - 1), gf, lane, r, i < U);
+      if (++gf == ng) {
+        gf = 0;
+        jf++;
+      }
+    };
+#pragma unroll
+    for (int d = 0; d < R; d++) fetch(w[d], d);
+    stage_x<QT, 1, PRO>(a, 0, 1, xs, misc, bsum, dxs, ex);
+    uint32_t jc = 0, gc = 0;  // the group in the MFMA: tile jc, group gc
+    for (uint32_t i0 = 0; i0 < U; i0 += R) {
+#pragma unroll
+      for (int d = 0; d < R; d++) {
+        const uint32_t i = i0 + d;
+        if (i >= U) break;
+        group_mfma<QT, 1, Q8>(w[d], gc, xs, bsum, dxs, nb, q, slot, acc0, acc1);
+        fetch(w[d], i + R);
+        if (++gc == ng) {  // the tile is complete
+          finish(jc);
+          gc = 0;
+          jc++;
         }
-        acc0 = acc1 = 0;
       }
     }
   }
@@ -1615,7 +1759,11 @@ static int launch_nt(const GemvArgs& a, int pro, int epi, dim3 grid, uint32_t ld
 template <uint32_t QT, int PRO, int EPI>
 static int launch_stream(const GemvArgs& a, hipStream_t s) {
   const Lds L = lds_layout(1, QT, a.nb, a.swaves, (PRO & PRO_Q8) != 0);
-  hipLaunchKernelGGL((gemv_stream_kernel<QT, PRO, EPI>), dim3(a.stream), dim3(64 * a.swaves), L.total, s, a);
+  const dim3 g(a.stream), b(64 * a.swaves);
+  switch (a.ng) {  // a whole tile in flight per wave where its groups fit the registers
+    case 7: hipLaunchKernelGGL((gemv_stream_kernel<QT, PRO, EPI, 7>), g, b, L.total, s, a); break;
+    default: hipLaunchKernelGGL((gemv_stream_kernel<QT, PRO, EPI, 0>), g, b, L.total, s, a);
+  }
   LLM_HIP(hipGetLastError());
   return 0;
 }

@@ -77,12 +77,15 @@ void gemv_bind(GemvArgs* a, const QMat& m) {
 void gemv_pick_stream(uint32_t tiles, uint32_t nb, uint32_t* wgs, uint32_t* waves) {
   *wgs = 0;
   *waves = 4;
-  if (tiles < GEMV_STREAM_MIN_TILES) return;
+  if (tiles < GEMV_STREAM_MIN_TILES || nb % 4) return;  // tail blocks: the tile kernel
   uint32_t w = 4;  // the prologue stages at most two 8-element items per thread
   while (w < 8 && nb * 4 > 2 * 64 * w) w *= 2;
   if (nb * 4 > 2 * 64 * w) return;  // k > 8192: the tile kernel
-  // about 16 waves per CU (4 per SIMD), each streaming several tiles
-  *wgs = std::min((tiles + w - 1) / w, 4096u / w);
+  // about 16 waves per CU (4 per SIMD), each streaming several tiles; at
+  // nb == 28 (k = 896) each wave keeps a whole tile in flight and the
+  // activations in registers, which leaves room for 8 waves per CU
+  const uint32_t total = nb == 28 ? 2048u : 4096u;
+  *wgs = std::min((tiles + w - 1) / w, total / w);
   *waves = w;
 }
 

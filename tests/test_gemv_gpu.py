@@ -121,10 +121,13 @@ def test_q41_shapes(gpu, oracle, qtype, rows, k, n):
 
 
 @pytest.mark.parametrize("qtype", [2, 3, 8])
-@pytest.mark.parametrize("rows,k", [(65541, 576), (70000, 224), (65536, 4864)])
+@pytest.mark.parametrize("rows,k", [(65541, 896), (70000, 512), (65536, 4864), (65541, 576), (70000, 224)])
 def test_stream_shapes(gpu, oracle, qtype, rows, k):
-    """One-token launches of 4096 tiles or more take the streaming kernel:
-    ragged rows, 1-3 tail blocks, and a k that needs 8 waves per workgroup."""
+    """One-token launches of 4096 tiles or more whose k is whole 4-block
+    groups take the streaming kernel: ragged rows at k = 896 (one tile's 7
+    groups in flight per wave), 4 groups per tile (the ring form), and a k
+    that needs 8 waves per workgroup.  With tail blocks (576 = 4 groups + 2
+    blocks, 224 = 7 blocks) the same launch takes the tile kernel."""
     _check_gemv(gpu, oracle, qtype, rows, k, 1)
 
 
