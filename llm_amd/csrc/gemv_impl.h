@@ -228,30 +228,18 @@ __global__ void embed_kernel(const uint8_t* __restrict__ wq, uint64_t tiles, uin
 // Word w of a Q4 block (byte i: element 4w+i low nibble, 16+4w+i high) as
 // eight f16 weights in the order 4w, 4w+2, 16+4w, 16+4w+2, 4w+1, 4w+3,
 // 16+4w+1, 16+4w+3.  0x6400|n is the f16 1024+n; a nibble in bits 4-7 gives
-// 1024+16n, scaled back by 1/16.  Every step is exact.
-template <bool Q41>
-__device__ __forceinline__ h8 dq4(uint32_t w) {
-  const h2 lo_off = Q41 ? h2{(_Float16)-1024, (_Float16)-1024} : h2{(_Float16)-1032, (_Float16)-1032};
-  const h2 hi_off = Q41 ? h2{(_Float16)-64, (_Float16)-64} : h2{(_Float16)-72, (_Float16)-72};
-  const h2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
-  uint32_t w8 = w >> 8;
-  h2 a = as_h2((w & 0x000F000Fu) | 0x64006400u) + lo_off;
-  h2 b = as_h2((w & 0x00F000F0u) | 0x64006400u) * s16 + hi_off;
-  h2 c = as_h2((w8 & 0x000F000Fu) | 0x64006400u) + lo_off;
-  h2 d = as_h2((w8 & 0x00F000F0u) | 0x64006400u) * s16 + hi_off;
-  return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
-// dq4 with its masks and the 0x6400 exponent held in registers: gfx9's
-// three-operand encoding takes no literal, so with the constants as literals
-// each (w & mask) | 0x6400.. is two instructions; from registers it is one
-// v_and_or_b32 (the exponent bits and the masks do not overlap).
+// 1024+16n, scaled back by 1/16.  Every step is exact.  The masks and the
+// 0x6400 exponent are held in registers: gfx9's three-operand encoding takes
+// no literal, so with literal constants each (w & mask) | 0x6400.. would be
+// two instructions; from registers it is one v_and_or_b32 (the exponent bits
+// and the masks do not overlap).
 struct Dq4K {
   uint32_t m0, m1, magic;
 };
 __device__ __forceinline__ Dq4K dq4_consts() {
   Dq4K k{0x000F000Fu, 0x00F000F0u, 0x64006400u};
-  asm volatile("" : "+s"(k.m0), "+s"(k.m1), "+v"(k.magic));
+  // not volatile: identical copies merge and leave loops
+  asm("" : "+s"(k.m0), "+s"(k.m1), "+v"(k.magic));
   return k;
 }
 template <bool Q41>
@@ -264,6 +252,21 @@ __device__ __forceinline__ h8 dq4k(uint32_t w, const Dq4K& k) {
   h2 b = as_h2((w & k.m1) | k.magic) * s16 + hi_off;
   h2 c = as_h2((w8 & k.m0) | k.magic) + lo_off;
   h2 d = as_h2((w8 & k.m1) | k.magic) * s16 + hi_off;
+  return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// The same with literal constants (measured faster in the decode tile kernel,
+// whose per-unit code the register form reschedules for the worse).
+template <bool Q41>
+__device__ __forceinline__ h8 dq4(uint32_t w) {
+  const h2 lo_off = Q41 ? h2{(_Float16)-1024, (_Float16)-1024} : h2{(_Float16)-1032, (_Float16)-1032};
+  const h2 hi_off = Q41 ? h2{(_Float16)-64, (_Float16)-64} : h2{(_Float16)-72, (_Float16)-72};
+  const h2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const uint32_t w8 = w >> 8;
+  h2 a = as_h2((w & 0x000F000Fu) | 0x64006400u) + lo_off;
+  h2 b = as_h2((w & 0x00F000F0u) | 0x64006400u) * s16 + hi_off;
+  h2 c = as_h2((w8 & 0x000F000Fu) | 0x64006400u) + lo_off;
+  h2 d = as_h2((w8 & 0x00F000F0u) | 0x64006400u) * s16 + hi_off;
   return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
@@ -1187,7 +1190,8 @@ __device__ __forceinline__ uint32_t u4c(const uint4& v, int j) {
 
 // Block j of a weight unit: the B operand, d and (Q4_1) m.  A group unit
 // holds a 4-block record; the tail unit (TAIL) holds block j in component j.
-template <uint32_t QT, bool TAIL>
+// RK: the nibble dequantiser on register constants (dq4k).
+template <uint32_t QT, bool TAIL, bool RK = false>
 __device__ __forceinline__ void unit_block(const WUnit& u, int j, h8& B, float& d, float& m) {
   m = 0.f;
   if (QT == LLMHIP_Q8_0) {
@@ -1201,12 +1205,12 @@ __device__ __forceinline__ void unit_block(const WUnit& u, int j, h8& B, float& 
       d = f16_hw(j % 2 == 0 ? sw & 0xffff : sw >> 16);
     }
   } else if (QT == LLMHIP_Q4_1) {
-    B = dq4<true>(u4c(u.w0, j));
+    B = RK ? dq4k<true>(u4c(u.w0, j), dq4_consts()) : dq4<true>(u4c(u.w0, j));
     const uint32_t sw = u4c(u.sv, j);
     d = f16_hw(sw & 0xffff);
     m = f16_hw(sw >> 16);
   } else {
-    B = dq4<false>(u4c(u.w0, j));
+    B = RK ? dq4k<false>(u4c(u.w0, j), dq4_consts()) : dq4<false>(u4c(u.w0, j));
     if (TAIL) {
       d = f16_hw(u4c(u.sv, j) & 0xffff);
     } else {
@@ -1226,7 +1230,7 @@ __device__ __forceinline__ void gemm_unit(float (&acc)[GT][NG][2], const WUnit (
     h8 B[GT];
     float d[GT], mm[GT];
 #pragma unroll
-    for (int u = 0; u < GT; u++) unit_block<QT, TAIL>(w[u], j, B[u], d[u], mm[u]);
+    for (int u = 0; u < GT; u++) unit_block<QT, TAIL, true>(w[u], j, B[u], d[u], mm[u]);
 #pragma unroll
     for (int g = 0; g < NG; g++)
 #pragma unroll
