@@ -210,8 +210,12 @@ def long_context(args):
 
 
 def sweep(args):
+    """Config 1: each shape's launches back to back in a hipGraph (captured
+    once, replayed), over rotated copies > 640 MB for HBM and one copy for the
+    warm figure; with LLMHIP_EAGER=1 (kernel tracing) as stream launches."""
     import numpy as np
     from llm_amd import kernels, synth
+    graph = os.environ.get("LLMHIP_EAGER", "") not in ("1", "true")
     out = []
     for qtype, tname in ((kernels.Q4_0, "q4_0"), (kernels.Q8_0, "q8_0")):
         for rows, k in SWEEP:
@@ -220,14 +224,16 @@ def sweep(args):
             x = kernels.DeviceBuffer.from_numpy(np.random.default_rng([2, rows, k]).standard_normal((1, k), np.float32))
             y = kernels.DeviceBuffer(rows * 4)
             nbytes = m.gguf_bytes
-            warm = kernels.bench([m], x, y, 1, iters=200, warmup=20)
+            warm = kernels.bench([m], x, y, 1, iters=200, warmup=20, graph=graph)
             copies = [m] + [m.clone() for _ in range(min(4095, max(0, -(-args.hbm_bytes // nbytes) - 1)))]
             iters = max(len(copies), 200)
-            hbm = kernels.bench(copies, x, y, 1, iters=iters, warmup=len(copies))
+            hbm = kernels.bench(copies, x, y, 1, iters=iters, warmup=len(copies), graph=graph)
+            stream = kernels.bench(copies, x, y, 1, iters=iters, warmup=len(copies))
             out.append({"type": tname, "rows": rows, "k": k, "n": 1, "bytes": nbytes,
                         "hbm_us": round(hbm, 3), "hbm_gbps": round(nbytes / hbm * 1e-3, 1),
                         "hbm_frac": round(nbytes / hbm * 1e-3 / PEAK_HBM_GBS, 4), "copies": len(copies),
-                        "warm_us": round(warm, 3), "warm_gbps": round(nbytes / warm * 1e-3, 1)})
+                        "warm_us": round(warm, 3), "warm_gbps": round(nbytes / warm * 1e-3, 1),
+                        "launch": "graph" if graph else "stream", "stream_hbm_us": round(stream, 3)})
             log(f"gemv {tname} {rows}x{k}: HBM {out[-1]['hbm_gbps']} GB/s ({out[-1]['hbm_frac']:.1%}) over "
                 f"{len(copies)} copies, warm {out[-1]['warm_gbps']} GB/s")
             # prefill-chunk token counts: the activation prep and the product
@@ -236,7 +242,7 @@ def sweep(args):
                 xn = kernels.DeviceBuffer.from_numpy(
                     np.random.default_rng([3, n, k]).standard_normal((n, k), np.float32))
                 yn = kernels.DeviceBuffer(n * rows * 4)
-                us = kernels.bench(copies, xn, yn, n, iters=iters, warmup=len(copies))
+                us = kernels.bench(copies, xn, yn, n, iters=iters, warmup=len(copies), graph=graph)
                 tf = 2.0 * rows * k * n / us * 1e-6
                 out.append({"type": tname, "rows": rows, "k": k, "n": n, "bytes": nbytes, "hbm_us": round(us, 3),
                             "hbm_gbps": round(nbytes / us * 1e-3, 1),
@@ -251,6 +257,34 @@ def sweep(args):
             x.close()
             y.close()
             kernels.synchronize()
+    return out
+
+
+def one_gemv(args):
+    """One sweep shape alone (the --gemv option): the same rotated copies and
+    stream launches as the sweep's stream figure, so that a profiler's kernel
+    trace and counters cover exactly these launches."""
+    import numpy as np
+    from llm_amd import kernels, synth
+    spec = args.gemv.split(":")
+    types = {"q4_0": kernels.Q4_0, "q8_0": kernels.Q8_0, "q4_1": kernels.Q4_1}
+    qtype = types[spec[0]]
+    rows, k = (int(v) for v in spec[1].split("x"))
+    n = int(spec[2]) if len(spec) > 2 else 1
+    rng = np.random.default_rng([1, rows, k, qtype])
+    m = kernels.QMat(qtype, rows, k, synth.quant_blocks(qtype, rows, k, rng, q8_div=8.0))
+    x = kernels.DeviceBuffer.from_numpy(np.random.default_rng([2, rows, k]).standard_normal((n, k), np.float32))
+    y = kernels.DeviceBuffer(n * rows * 4)
+    nbytes = m.gguf_bytes
+    copies = [m] + [m.clone() for _ in range(min(4095, max(0, -(-args.hbm_bytes // nbytes) - 1)))]
+    iters = max(len(copies), 100)
+    us = kernels.bench(copies, x, y, n, iters=iters, warmup=len(copies))
+    out = {"type": spec[0], "rows": rows, "k": k, "n": n, "bytes": nbytes, "copies": len(copies),
+           "launches": iters + len(copies), "stream_us": round(us, 3), "gbps": round(nbytes / us * 1e-3, 1)}
+    for c in copies:
+        c.close()
+    x.close()
+    y.close()
     return out
 
 
@@ -325,6 +359,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--copy-calibration", action="store_true", help="only run the counter calibration copy")
+    ap.add_argument("--gemv", metavar="TYPE:ROWSxK[:N]",
+                    help="only one sweep shape (q4_0 / q8_0 / q4_1), rotated copies over stream launches, "
+                         "for a profiler: e.g. q4_0:151936x896")
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py: this build measures one GPU; the path shards by independent sequences per GPU "
@@ -336,6 +373,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.gemv:
+        print(json.dumps(one_gemv(args)), flush=True)
         return
     g, r = generation(args)
     g.close()

@@ -143,6 +143,13 @@ LLMHIP_API uint64_t llmhip_qmat_gguf_bytes(const llmhip_qmat* m);
  * the weights come from HBM. */
 LLMHIP_API int llmhip_qmat_bench(llmhip_qmat* const* mats, int count, const float* x_dev, float* y_dev, int n, int iters,
                       int warmup, void* hip_stream, float* avg_us);
+/* The same measured over hipGraph replays: the launches (cycling through the
+ * `count` matrices, at least 16 per graph) are captured once on `hip_stream`
+ * (a stream of its own when null) after `warmup` direct launches, and the
+ * graph is replayed until `iters` launches are timed.  No counterpart in the
+ * reference (a measurement entry point, as the reference's bench mode is). */
+LLMHIP_API int llmhip_qmat_bench_graph(llmhip_qmat* const* mats, int count, const float* x_dev, float* y_dev, int n,
+                                       int iters, int warmup, void* hip_stream, float* avg_us);
 /* A copy of m on the same device (device-to-device): rotating copies whose
  * total exceeds the Infinity Cache makes a benchmark read HBM. */
 LLMHIP_API int llmhip_qmat_clone(const llmhip_qmat* m, llmhip_qmat** out);

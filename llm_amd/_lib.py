@@ -83,6 +83,7 @@ SIGNATURES = [
     ("llmhip_qmat_bytes", U64, [P]),
     ("llmhip_qmat_gguf_bytes", U64, [P]),
     ("llmhip_qmat_bench", I, [ctypes.POINTER(P), I, P, P, I, I, I, P, ctypes.POINTER(F)]),
+    ("llmhip_qmat_bench_graph", I, [ctypes.POINTER(P), I, P, P, I, I, I, P, ctypes.POINTER(F)]),
     ("llmhip_qmat_clone", I, [P, ctypes.POINTER(P)]),
     ("llmhip_qmat_free", None, [P]),
     ("llmhip_model_create", I, [I, ctypes.POINTER(Limits), ctypes.POINTER(Config), I, I, ctypes.POINTER(P)]),

@@ -798,11 +798,11 @@ __device__ __forceinline__ void group_mfma(const WUnit& u, uint32_t g, const h8*
 // already in registers (xa: the group's four blocks, slots past hi/lo zero).
 // Only lanes of q == 0 hold the token's sums; the others accumulate values
 // the epilogue drops, so no per-lane selects.
-template <uint32_t QT>
+template <uint32_t QT, int XS = 1>
 __device__ __forceinline__ void group_pre(const WUnit& u, uint32_t g, const h8* xa, const float* bsum,
                                           const Dq4K& K, float& acc) {
   auto blk = [&](int j, h8 B, uint32_t dbits, uint32_t mbits) {
-    const f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], B, f4{0, 0, 0, 0}, 0, 0, 0);
+    const f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j * XS], B, f4{0, 0, 0, 0}, 0, 0, 0);
     acc += f16_hw(dbits) * (D[0] + D[1]);
     if (QT == LLMHIP_Q4_1) acc += f16_hw(mbits) * bsum[4 * g + j];
   };
@@ -907,26 +907,29 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
     acc0 = acc1 = 0;
   };
   if (NG > 0) {
-    // A tile's scales come in one load per four groups, handed to the lanes
-    // that need them by ds_bpermute (2 loads a tile instead of NG).  They are
-    // double-buffered: tile j's load goes out at group 0 of tile j - 1, so
-    // group 0's wait covers only its own quants and those scales.  Two tiles
-    // per loop trip keep each buffer in fixed registers.
+    // The wave's next tile is in flight while it computes the current one:
+    // its quants in wt (group g refilled as soon as group g is consumed) and
+    // its scales (one load per four groups, handed to the lanes that need
+    // them by ds_bpermute) in sc, refilled at the tile's start once the
+    // tile's NG groups of scales are extracted.
     constexpr int NS = NG > 0 ? (NG + 3) / 4 : 1;
-    uint4 scA[NS], scB[NS];
-    auto load_sc = [&](uint4(&sc)[NS], uint32_t t, bool real) {
+    constexpr int NGX = NG > 0 ? NG : 1;
+    WUnit wt[NGX];
+    uint4 sc[NS];
+    auto load_sc = [&](uint32_t t, bool real) {
 #pragma unroll
       for (int h = 0; h < NS; h++) sc[h] = load_scales4<QT, NG>(a.qs, nb, t, h, lane, real);
     };
-    const uint32_t t0 = min(gw, a.tiles - 1);
+    {
+      const uint32_t t0 = min(gw, a.tiles - 1);
+      load_sc(t0, ntw > 0);
 #pragma unroll
-    for (int g = 0; g < NG; g++) {
-      load_group<QT, true, false>(w[g], a.qs, nb, t0, g, lane, r, ntw > 0);
-      if (g == 0) load_sc(scA, t0, ntw > 0);
+      for (int g = 0; g < NG; g++) load_group<QT, true, false>(wt[g], a.qs, nb, t0, g, lane, r, ntw > 0);
     }
     stage_x<QT, 1, PRO>(a, 0, 1, xs, misc, bsum, dxs, ex);
-    // f32 activations: every block's MFMA operand read and masked once
-    constexpr int NX = Q8 ? 1 : 4 * (NG > 0 ? NG : 1);
+    // f32 activations: every block's MFMA operand read from LDS and masked
+    // once, into registers
+    constexpr int NX = Q8 ? 1 : 4 * NGX;
     h8 xa[NX];
     const Dq4K K = dq4_consts();
     if (!Q8) {
@@ -937,33 +940,32 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
         xa[b] = __builtin_bit_cast(h8, X & (slot < 2 ? ~0u : 0u));
       }
     }
-    auto run_tile = [&](uint32_t j, const uint4(&cur)[NS], uint4(&nxt)[NS]) {
+    for (uint32_t j = 0; j < ntw; j++) {
       const uint32_t next = min(gw + (j + 1) * W, a.tiles - 1);
       const bool more = j + 1 < ntw;
+      uint4 sv[NGX];
+#pragma unroll
+      for (int g = 0; g < NG; g++) sv[g] = group_scales<QT>(sc[g / 4], g, r);
+      __builtin_amdgcn_sched_barrier(0);
+      load_sc(next, more);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int g = 0; g < NG; g++) {
-        w[g].sv = group_scales<QT>(cur[g / 4], g, r);
+        wt[g].sv = sv[g];
         if (Q8)
-          group_mfma<QT, 1, Q8>(w[g], g, xs, bsum, dxs, nb, q, slot, acc0, acc1);
+          group_mfma<QT, 1, Q8>(wt[g], g, xs, bsum, dxs, nb, q, slot, acc0, acc1);
         else
-          group_pre<QT>(w[g], g, xa + 4 * g, bsum, K, acc0);
-        // the slot's last use (the block scales) before its refill, and the
-        // refill issued there: no register copy of a load still in flight
-        // (the empty asm keeps the scaled sums from sinking into the epilogue)
+          group_pre<QT>(wt[g], g, xa + 4 * g, bsum, K, acc0);
+        // the slot's last use before its refill, and the refill issued there:
+        // no register copy of a load still in flight (the empty asm keeps the
+        // scaled sums from sinking into the epilogue)
         asm volatile("" : "+v"(acc0), "+v"(acc1));
         __builtin_amdgcn_sched_barrier(0);
-        load_group<QT, true, false>(w[g], a.qs, nb, next, g, lane, r, more);
-        if (g == 0) load_sc(nxt, next, more);
+        load_group<QT, true, false>(wt[g], a.qs, nb, next, g, lane, r, more);
         __builtin_amdgcn_sched_barrier(0);
       }
       finish(j);
-    };
-    uint32_t j = 0;
-    for (; j + 1 < ntw; j += 2) {
-      run_tile(j, scA, scB);
-      run_tile(j + 1, scB, scA);
     }
-    if (j < ntw) run_tile(j, scA, scB);
   } else {
     uint32_t jf = 0, gf = 0;  // the next group to load: the wave's tile jf, group gf
     auto fetch = [&](WUnit& u, uint32_t i) {

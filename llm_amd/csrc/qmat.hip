@@ -459,6 +459,66 @@ int llmhip_qmat_bench(llmhip_qmat* const* mats, int count, const float* x_dev, f
   return 0;
 }
 
+int llmhip_qmat_bench_graph(llmhip_qmat* const* mats, int count, const float* x_dev, float* y_dev, int n,
+                            int iters, int warmup, void* hip_stream, float* avg_us) {
+  clear_error();
+  if (count < 1 || iters < 1) return set_error(LLMHIP_ERR_ARG, "llm: bench of %d matrices, %d iterations", count, iters);
+  std::vector<GemvArgs> args((size_t)count);
+  for (int i = 0; i < count; i++) {
+    LLM_TRY(qmat_gemv_args(mats[i], x_dev, y_dev, n, &args[i]));
+    if (mats[i]->m.g.q.type != mats[0]->m.g.q.type || mats[i]->m.g.rows != mats[0]->m.g.rows ||
+        mats[i]->m.g.k != mats[0]->m.g.k)
+      return set_error(LLMHIP_ERR_ARG, "llm: bench matrices differ in shape or type");
+    LLM_TRY(qmat_ready(mats[i]));
+  }
+  LLM_HIP(hipSetDevice(mats[0]->m.device));
+  hipStream_t s = (hipStream_t)hip_stream;
+  bool own = false;
+  if (!s) {  // the legacy stream cannot be captured
+    LLM_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    own = true;
+  }
+  hipGraph_t g = nullptr;
+  hipGraphExec_t ex = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = 0;
+  // direct launches first: they make what a first launch allocates (the
+  // prefill pair's activation buffer), which a capture must not
+  for (int i = 0; i < std::max(warmup, count) && rc == 0; i++) rc = qmat_launch(mats[i % count], args[i % count], EPI_STORE, s);
+  if (rc == 0 && hipStreamSynchronize(s) != hipSuccess) rc = set_error(LLMHIP_ERR_DEVICE, "llm: warmup failed");
+  const int per = std::max(count, 16);  // launches per graph, cycling through the matrices
+  if (rc == 0) {
+    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+      rc = set_error(LLMHIP_ERR_DEVICE, "llm: stream capture failed");
+    } else {
+      for (int i = 0; i < per && rc == 0; i++) rc = qmat_launch(mats[i % count], args[i % count], EPI_STORE, s);
+      const hipError_t e = hipStreamEndCapture(s, &g);
+      if (rc == 0 && e != hipSuccess) rc = set_error(LLMHIP_ERR_DEVICE, "llm: capture failed: %s", hipGetErrorString(e));
+    }
+  }
+  if (rc == 0 && hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) != hipSuccess)
+    rc = set_error(LLMHIP_ERR_DEVICE, "llm: graph instantiate failed");
+  if (rc == 0 && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
+    rc = set_error(LLMHIP_ERR_DEVICE, "llm: hipEventCreate failed");
+  const int reps = (iters + per - 1) / per;
+  float ms = 0;
+  if (rc == 0) {
+    bool ok = hipGraphLaunch(ex, s) == hipSuccess && hipStreamSynchronize(s) == hipSuccess;  // one untimed replay
+    ok = ok && hipEventRecord(e0, s) == hipSuccess;
+    for (int r = 0; r < reps && ok; r++) ok = hipGraphLaunch(ex, s) == hipSuccess;
+    ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+         hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+    if (!ok) rc = set_error(LLMHIP_ERR_DEVICE, "llm: graph replay failed");
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (ex) (void)hipGraphExecDestroy(ex);
+  if (g) (void)hipGraphDestroy(g);
+  if (own) (void)hipStreamDestroy(s);
+  if (rc == 0) *avg_us = ms * 1000.f / (float)(reps * per);
+  return rc;
+}
+
 int llmhip_qmat_clone(const llmhip_qmat* q, llmhip_qmat** out) {
   clear_error();
   *out = nullptr;

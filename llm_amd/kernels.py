@@ -146,12 +146,14 @@ class QMat:
             pass
 
 
-def bench(mats, x, y, n, iters, warmup=10):
+def bench(mats, x, y, n, iters, warmup=10, graph=False):
     """Average microseconds of one gemv of n tokens, cycling back-to-back
-    through `mats`, on device buffers x and y."""
+    through `mats`, on device buffers x and y: stream launches, or (graph)
+    replays of a hipGraph of the launches."""
     arr = (ctypes.c_void_p * len(mats))(*[m._h.value for m in mats])
     us = ctypes.c_float()
-    check(lib().llmhip_qmat_bench(arr, len(mats), x.ptr, y.ptr, int(n), iters, warmup, None, ctypes.byref(us)))
+    fn = lib().llmhip_qmat_bench_graph if graph else lib().llmhip_qmat_bench
+    check(fn(arr, len(mats), x.ptr, y.ptr, int(n), iters, warmup, None, ctypes.byref(us)))
     return us.value
 
 

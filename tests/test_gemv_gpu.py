@@ -229,3 +229,24 @@ def test_upload_in_pieces(gpu, oracle):
     x = _x(1, k, 1)
     y = m.gemv(x)
     assert _rel(y, oracle.matvec(2, raw, rows, k, x[0])[None]) <= TOL
+
+
+@pytest.mark.parametrize("n", [1, 8])
+def test_bench_graph(gpu, oracle, n):
+    """The sweep's graph-replay measurement (llmhip_qmat_bench_graph) runs the
+    same product: after the replays y holds the gemv of the last matrix."""
+    from llm_amd import kernels
+    qtype, rows, k = 2, 65541, 896  # 1-token launches take the streaming kernel
+    raw = _raw(qtype, rows, k, 21)
+    m = kernels.QMat(qtype, rows, k, raw)
+    c = m.clone()
+    x = _x(n, k, 21)
+    xb = kernels.DeviceBuffer.from_numpy(x)
+    yb = kernels.DeviceBuffer(n * rows * 4)
+    us = kernels.bench([m, c], xb, yb, n, iters=40, warmup=2, graph=True)
+    assert us > 0
+    y = yb.numpy(np.float32, (n, rows))
+    want = np.stack([oracle.matvec(qtype, raw, rows, k, x[t], threads=16) for t in range(n)])
+    assert _rel(y, want) <= TOL
+    for b in (xb, yb, c, m):
+        b.close()
