@@ -37,28 +37,37 @@ PMC_SUMMARY = os.path.join(ROOT, "profiles", "pmc_decode_qwen25.txt")
 
 def kernel_symbols(attn_full):
     """Device symbol of each decode kernel class of the config-3 model (Q4_0
-    layers, Q8_0 head): gemv_kernel<type, tokens, prologue, epilogue> (k3 and
-    k5 share one; rocprof tells them apart by grid size), the one-chunk or
-    split attention, the streaming head."""
-    return {"k1": "gemv_kernel<2u, 1, 1, 2>",
+    layers, Q8_0 head): gemv_kernel<type, tokens, prologue, epilogue, units
+    per staging batch>, the one-chunk or split attention, the streaming head
+    <type, prologue, epilogue, groups per tile>."""
+    return {"k1": "gemv_kernel<2u, 1, 1, 2, 2>",
             "k2": "attn_kernel<64u, 8u, false, false, false>" if attn_full else
                   "attn_kernel<64u, 4u, true, false, false> + attn_merge_kernel<64u, false>",
-            "k3": "gemv_kernel<2u, 1, 0, 1>", "k4": "gemv_kernel<2u, 1, 1, 3>", "k5": "gemv_kernel<2u, 1, 0, 1>",
-            "head": "gemv_stream_kernel<8u, 1, 4>"}
+            "k3": "gemv_kernel<2u, 1, 0, 1, 2>", "k4": "gemv_kernel<2u, 1, 1, 3, 2>", "k5": "gemv_kernel<2u, 1, 0, 1, 4>",
+            "head": "gemv_stream_kernel<8u, 1, 4, 7>"}
 
 
 def pmc_traffic(cls):
     """HBM bytes per launch of a decode kernel class from the committed
-    rocprofv3 counter summary (lines `traffic_bytes <class> <bytes>`), or None."""
+    rocprofv3 counter summary (lines `traffic_bytes <class> <bytes>`), and
+    whether that summary measured the kernel sources of this tree (its
+    `sources_hash` line against llm_amd.profsum.sources_hash()).  A stale
+    figure is not reported: (None, reason)."""
+    from llm_amd import profsum
+    want, got, value = profsum.sources_hash(), None, None
     try:
         with open(PMC_SUMMARY) as f:
             for line in f:
                 p = line.split()
+                if len(p) == 2 and p[0] == "sources_hash":
+                    got = p[1]
                 if len(p) == 3 and p[0] == "traffic_bytes" and p[1] == cls:
-                    return int(p[2])
+                    value = int(p[2])
     except OSError:
-        pass
-    return None
+        return None, "no counter summary"
+    if got != want:
+        return None, f"{os.path.relpath(PMC_SUMMARY, ROOT)} measured sources {got}, this tree is {want}"
+    return value, f"{os.path.relpath(PMC_SUMMARY, ROOT)} (sources {got})"
 
 
 def copy_calibration():
@@ -126,9 +135,10 @@ def generation(args):
     dom = max(classes, key=lambda k: classes[k]["us_per_token"])
     d = classes[dom]
     achieved = d["bytes"] / d["avg_us"] * 1e-3
+    traffic, source = pmc_traffic(dom)
     roofline = {"bound": "hbm", "kernel": dom, "symbol": syms[dom], "achieved": round(achieved, 1),
                 "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                "traffic": pmc_traffic(dom), "bytes_per_launch": d["bytes"], "avg_us": d["avg_us"]}
+                "traffic": traffic, "traffic_source": source, "bytes_per_launch": d["bytes"], "avg_us": d["avg_us"]}
     w = [k for k in classes if k != "k2"]
     gemv_all = sum(classes[k]["bytes"] * classes[k]["launches_per_token"] for k in w) / \
         sum(classes[k]["us_per_token"] for k in w) * 1e-3
@@ -260,13 +270,13 @@ def sweep(args):
     return out
 
 
-def one_gemv(args):
-    """One sweep shape alone (the --gemv option): the same rotated copies and
-    stream launches as the sweep's stream figure, so that a profiler's kernel
-    trace and counters cover exactly these launches."""
+def one_gemv(spec, hbm_bytes):
+    """One sweep shape alone (the --gemv option), TYPE:ROWSxK[:N]: the same
+    rotated copies and stream launches as the sweep's stream figure, so that a
+    profiler's kernel trace and counters cover exactly these launches."""
     import numpy as np
     from llm_amd import kernels, synth
-    spec = args.gemv.split(":")
+    spec = spec.split(":")
     types = {"q4_0": kernels.Q4_0, "q8_0": kernels.Q8_0, "q4_1": kernels.Q4_1}
     qtype = types[spec[0]]
     rows, k = (int(v) for v in spec[1].split("x"))
@@ -276,9 +286,10 @@ def one_gemv(args):
     x = kernels.DeviceBuffer.from_numpy(np.random.default_rng([2, rows, k]).standard_normal((n, k), np.float32))
     y = kernels.DeviceBuffer(n * rows * 4)
     nbytes = m.gguf_bytes
-    copies = [m] + [m.clone() for _ in range(min(4095, max(0, -(-args.hbm_bytes // nbytes) - 1)))]
+    copies = [m] + [m.clone() for _ in range(min(4095, max(0, -(-hbm_bytes // nbytes) - 1)))]
     iters = max(len(copies), 100)
     us = kernels.bench(copies, x, y, n, iters=iters, warmup=len(copies))
+    log(f"gemv {spec[0]} {rows}x{k} n={n}: {us:.2f} us over {len(copies)} copies")
     out = {"type": spec[0], "rows": rows, "k": k, "n": n, "bytes": nbytes, "copies": len(copies),
            "launches": iters + len(copies), "stream_us": round(us, 3), "gbps": round(nbytes / us * 1e-3, 1)}
     for c in copies:
@@ -359,9 +370,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--copy-calibration", action="store_true", help="only run the counter calibration copy")
-    ap.add_argument("--gemv", metavar="TYPE:ROWSxK[:N]",
-                    help="only one sweep shape (q4_0 / q8_0 / q4_1), rotated copies over stream launches, "
-                         "for a profiler: e.g. q4_0:151936x896")
+    ap.add_argument("--gemv", metavar="TYPE:ROWSxK[:N][,...]",
+                    help="only these sweep shapes (q4_0 / q8_0 / q4_1), in order, each over rotated copies with "
+                         "stream launches, for a profiler: e.g. q4_0:151936x896,q8_0:896x896:64")
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py: this build measures one GPU; the path shards by independent sequences per GPU "
@@ -375,7 +386,7 @@ def main():
         copy_calibration()
         return
     if args.gemv:
-        print(json.dumps(one_gemv(args)), flush=True)
+        print(json.dumps([one_gemv(spec, args.hbm_bytes) for spec in args.gemv.split(",")]), flush=True)
         return
     g, r = generation(args)
     g.close()
