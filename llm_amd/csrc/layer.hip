@@ -257,9 +257,9 @@ __global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a, uint32_t ntok
 // e^{m_c-M} l_c, over the chunks below the causal bound.  One thread per
 // output dimension; the partials of up to 16 chunks are loaded at once.
 template <uint32_t HD, bool EMIT = false>
-__global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a, AttnOps ops) {
+__global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a, AttnOps ops, uint32_t crows) {
   const uint32_t h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
-  const uint32_t n = a.state[0] + t + 1, P = (n + ATTN_SPLIT_ROWS - 1) / ATTN_SPLIT_ROWS;
+  const uint32_t n = a.state[0] + t + 1, P = (n + crows - 1) / crows;
   const uint64_t th = (uint64_t)t * a.heads + h;
   const float* ml = a.ml + th * a.smax * 2;
   const float* pv = a.pv + th * a.smax * HD + d;
@@ -325,26 +325,28 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* 
     LLM_HIP(hipGetLastError());
     return 0;
   }
-  const uint32_t chunks = (a.rows + ATTN_SPLIT_ROWS - 1) / ATTN_SPLIT_ROWS;
+  const uint32_t crows = ntok == 1 ? ATTN_DECODE_ROWS : ATTN_SPLIT_ROWS;
+  const uint32_t chunks = (a.rows + crows - 1) / crows;
   if (chunks > a.smax) return set_error(LLMHIP_ERR_ARG, "llm: attention: %u chunks of %u", chunks, a.smax);
-  if (a.hd == 64 && ntok > 1) {
+  if (ntok == 1) {
+    if (a.hd == 64) attn_go<64, ATTN_DECODE_ROWS / 32, true>(a, ntok, NI * chunks, s, ops);
+    else attn_go<128, ATTN_DECODE_ROWS / 32, true>(a, ntok, NI * chunks, s, ops);
+  } else if (a.hd == 64) {
     // several tokens: the matrix-core form, 64 queries of a KV head per workgroup
     const uint32_t blocks = chunks * a.kv_heads * ((ntok * (a.heads / a.kv_heads) + 63) / 64);
     if (a.kv16) hipLaunchKernelGGL((attn_mma_kernel<true>), dim3(blocks), dim3(256), 0, s, a, ntok, chunks);
     else hipLaunchKernelGGL((attn_mma_kernel<false>), dim3(blocks), dim3(256), 0, s, a, ntok, chunks);
-  } else if (a.hd == 64) {
-    attn_go<64, ATTN_SPLIT_ROWS / 32, true>(a, ntok, NI * chunks, s, ops);
   } else {
     attn_go<128, ATTN_SPLIT_ROWS / 32, true>(a, ntok, NI * chunks, s, ops);
   }
   LLM_HIP(hipGetLastError());
   const dim3 mg(a.heads, ntok);
   if (a.hd == 64) {
-    if (ops.xp) hipLaunchKernelGGL((attn_merge_kernel<64, true>), mg, dim3(64), 0, s, a, ops);
-    else hipLaunchKernelGGL((attn_merge_kernel<64, false>), mg, dim3(64), 0, s, a, ops);
+    if (ops.xp) hipLaunchKernelGGL((attn_merge_kernel<64, true>), mg, dim3(64), 0, s, a, ops, crows);
+    else hipLaunchKernelGGL((attn_merge_kernel<64, false>), mg, dim3(64), 0, s, a, ops, crows);
   } else {
-    if (ops.xp) hipLaunchKernelGGL((attn_merge_kernel<128, true>), mg, dim3(128), 0, s, a, ops);
-    else hipLaunchKernelGGL((attn_merge_kernel<128, false>), mg, dim3(128), 0, s, a, ops);
+    if (ops.xp) hipLaunchKernelGGL((attn_merge_kernel<128, true>), mg, dim3(128), 0, s, a, ops, crows);
+    else hipLaunchKernelGGL((attn_merge_kernel<128, false>), mg, dim3(128), 0, s, a, ops, crows);
   }
   LLM_HIP(hipGetLastError());
   return 0;
