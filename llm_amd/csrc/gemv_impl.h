@@ -824,6 +824,42 @@ __device__ __forceinline__ void group_pre(const WUnit& u, uint32_t g, const h8* 
   }
 }
 
+// group_pre with the four blocks' MFMAs chained through one accumulator:
+// xa[j] holds block j's hi and lo in slots 2j and 2j + 1 (zero elsewhere),
+// so block j's sums land in those slots and lane (r, q) holds blocks 2q and
+// 2q + 1 of row r (q < 2; lanes of q >= 2 hold zeros).  The scales follow:
+// one add and one FMA per pair of blocks instead of per block.  The row's
+// total is split between lanes q = 0 and 1 (added at the tile's end).
+template <uint32_t QT>
+__device__ __forceinline__ void group_chain(const WUnit& u, uint32_t g, const h8* xa, const float* bsum,
+                                            const Dq4K& K, int q, float& acc) {
+  h8 B[4];
+  if (QT == LLMHIP_Q8_0) {
+    B[0] = dq8(u.w0.x, u.w0.y);
+    B[1] = dq8(u.w0.z, u.w0.w);
+    B[2] = dq8(u.w1.x, u.w1.y);
+    B[3] = dq8(u.w1.z, u.w1.w);
+  } else {
+    B[0] = dq4k<QT == LLMHIP_Q4_1>(u.w0.x, K);
+    B[1] = dq4k<QT == LLMHIP_Q4_1>(u.w0.y, K);
+    B[2] = dq4k<QT == LLMHIP_Q4_1>(u.w0.z, K);
+    B[3] = dq4k<QT == LLMHIP_Q4_1>(u.w0.w, K);
+  }
+  f4 D = {0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < 4; j++) D = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], B[j], D, 0, 0, 0);
+  const bool hi = (q & 1) != 0;
+  if (QT == LLMHIP_Q4_1) {  // d, m of blocks 2q and 2q + 1
+    const uint32_t s0 = hi ? u.sv.z : u.sv.x, s1 = hi ? u.sv.w : u.sv.y;
+    const uint32_t b0 = 4 * g + 2 * (q & 1);
+    acc += f16_hw(s0 & 0xffff) * (D[0] + D[1]) + f16_hw(s1 & 0xffff) * (D[2] + D[3]);
+    acc += f16_hw(s0 >> 16) * bsum[b0] + f16_hw(s1 >> 16) * bsum[b0 + 1];
+  } else {  // d of blocks 2q and 2q + 1 in one word
+    const uint32_t sw = hi ? u.sv.y : u.sv.x;
+    acc += f16_hw(sw & 0xffff) * (D[0] + D[1]) + f16_hw(sw >> 16) * (D[2] + D[3]);
+  }
+}
+
 // Greedy-sampling partials: (max, lowest index) over the rows a workgroup saw
 // (NaN never wins, cpu.go:389-397), written to amax_v/amax_i[blockIdx.x];
 // argmax_kernel combines the workgroups'.  Called by every thread.
@@ -895,6 +931,7 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
   // the row epilogue of the wave's tile j (argmax partials in bv / bi)
   auto finish = [&](uint32_t j) {
     const uint32_t tile = gw + j * W;
+    if (NG > 0 && !Q8) acc0 += __shfl_xor(acc0, 16);  // group_chain: lanes q = 0 and 1 hold halves
     const float v = q == 0 ? ldexpf(acc0, -ex[0]) : 0.f;
     row_epilogue<EPI>(a, tile, r, true, 0, q == 0, v, 1, false, 0.f);
     if (EPI == EPI_ARGMAX) {
@@ -932,12 +969,14 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
     constexpr int NX = Q8 ? 1 : 4 * NGX;
     h8 xa[NX];
     const Dq4K K = dq4_consts();
-    if (!Q8) {
+    if (!Q8) {  // block b in slots 2 (b % 4) and 2 (b % 4) + 1 (group_chain)
       typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 #pragma unroll
       for (int b = 0; b < NX; b++) {
-        const u4v X = __builtin_bit_cast(u4v, xs[(b * 4 + q) * 2 + min(slot, 1)]);
-        xa[b] = __builtin_bit_cast(h8, X & (slot < 2 ? ~0u : 0u));
+        const int sl = slot - 2 * (b % 4);
+        const bool in = sl == 0 || sl == 1;
+        const u4v X = __builtin_bit_cast(u4v, xs[(b * 4 + q) * 2 + (in ? sl : 0)]);
+        xa[b] = __builtin_bit_cast(h8, X & (in ? ~0u : 0u));
       }
     }
     for (uint32_t j = 0; j < ntw; j++) {
@@ -955,7 +994,7 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
         if (Q8)
           group_mfma<QT, 1, Q8>(wt[g], g, xs, bsum, dxs, nb, q, slot, acc0, acc1);
         else
-          group_pre<QT>(wt[g], g, xa + 4 * g, bsum, K, acc0);
+          group_chain<QT>(wt[g], g, xa + 4 * g, bsum, K, q, acc0);
         // the slot's last use before its refill, and the refill issued there:
         // no register copy of a load still in flight (the empty asm keeps the
         // scaled sums from sinking into the epilogue)
