@@ -852,11 +852,14 @@ __device__ __forceinline__ void group_chain(const WUnit& u, uint32_t g, const h8
   if (QT == LLMHIP_Q4_1) {  // d, m of blocks 2q and 2q + 1
     const uint32_t s0 = hi ? u.sv.z : u.sv.x, s1 = hi ? u.sv.w : u.sv.y;
     const uint32_t b0 = 4 * g + 2 * (q & 1);
-    acc += f16_hw(s0 & 0xffff) * (D[0] + D[1]) + f16_hw(s1 & 0xffff) * (D[2] + D[3]);
-    acc += f16_hw(s0 >> 16) * bsum[b0] + f16_hw(s1 >> 16) * bsum[b0 + 1];
+    acc = fmaf(f16_hw(s0 & 0xffff), D[0] + D[1], acc);
+    acc = fmaf(f16_hw(s1 & 0xffff), D[2] + D[3], acc);
+    acc = fmaf(f16_hw(s0 >> 16), bsum[b0], acc);
+    acc = fmaf(f16_hw(s1 >> 16), bsum[b0 + 1], acc);
   } else {  // d of blocks 2q and 2q + 1 in one word
     const uint32_t sw = hi ? u.sv.y : u.sv.x;
-    acc += f16_hw(sw & 0xffff) * (D[0] + D[1]) + f16_hw(sw >> 16) * (D[2] + D[3]);
+    acc = fmaf(f16_hw(sw & 0xffff), D[0] + D[1], acc);
+    acc = fmaf(f16_hw(sw >> 16), D[2] + D[3], acc);
   }
 }
 
