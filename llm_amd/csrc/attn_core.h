@@ -25,10 +25,10 @@ __device__ __forceinline__ f4 kv_load4(const float* kv, uint64_t i) {
   return f4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
 }
 
-template <uint32_t HD, uint32_t NW>
+template <uint32_t HD, uint32_t NW, uint32_t QN = 1>
 struct AttnLds {
-  float m[NW], l[NW];
-  f4 o[NW * 16 * (HD / 64)];
+  float m[QN][NW], l[QN][NW];
+  f4 o[QN][NW * 16 * (HD / 64)];
 };
 
 template <uint32_t HD, uint32_t J, uint32_t NW, bool KVH>
@@ -76,11 +76,11 @@ struct AttnChunk {
       m = fmaxf(m, sj[j]);
     }
     m = rows_max4(m);
-    if (lane == 0) sm.m[wave] = m;
+    if (lane == 0) sm.m[0][wave] = m;
     __syncthreads();
-    float M = sm.m[0];
+    float M = sm.m[0][0];
 #pragma unroll
-    for (uint32_t w = 1; w < NW; w++) M = fmaxf(M, sm.m[w]);
+    for (uint32_t w = 1; w < NW; w++) M = fmaxf(M, sm.m[0][w]);
     f4 acc[V4];
 #pragma unroll
     for (uint32_t v = 0; v < V4; v++) acc[v] = f4{0, 0, 0, 0};
@@ -105,8 +105,8 @@ struct AttnChunk {
       }
     if (lane < 16)
 #pragma unroll
-      for (uint32_t v = 0; v < V4; v++) sm.o[(wave * 16 + cl) * V4 + v] = acc[v];
-    if (lane == 0) sm.l[wave] = l;
+      for (uint32_t v = 0; v < V4; v++) sm.o[0][(wave * 16 + cl) * V4 + v] = acc[v];
+    if (lane == 0) sm.l[0][wave] = l;
     __syncthreads();
     *M_out = M;
     float L = 0, o = 0;
@@ -114,12 +114,90 @@ struct AttnChunk {
       const uint32_t fi = tid / 4, ci = fi % 16, vi = fi / 16, k = tid % 4;
 #pragma unroll
       for (uint32_t w = 0; w < NW; w++) {
-        L += sm.l[w];
-        o += sm.o[(w * 16 + ci) * V4 + vi][k];
+        L += sm.l[0][w];
+        o += sm.o[0][(w * 16 + ci) * V4 + vi][k];
       }
     }
     *L_out = L;
     *o_out = o;
+  }
+
+  // reduce for QN queries of one head over the same rows (several tokens of a
+  // prefill chunk): query i has its slice q[i] and its causal bound n[i]; out
+  // per query as reduce's.  The same two barriers for all QN.
+  template <uint32_t QN>
+  __device__ __forceinline__ void reduce_n(const f4 (&q)[QN][V4], uint32_t row0, const uint32_t (&n)[QN],
+                                           float scale, AttnLds<HD, NW, QN>& sm, float (&M_out)[QN],
+                                           float (&L_out)[QN], float (&o_out)[QN]) const {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id(), cl = lane & 15, slot = tid >> 4;
+    float sj[QN][J], m[QN];
+#pragma unroll
+    for (uint32_t i = 0; i < QN; i++) {
+      m[i] = -INFINITY;
+#pragma unroll
+      for (uint32_t j = 0; j < J; j++) {
+        const uint32_t p = row0 + slot + S * j;
+        float d = 0;
+#pragma unroll
+        for (uint32_t v = 0; v < V4; v++)
+          d += q[i][v][0] * kr[j][v][0] + q[i][v][1] * kr[j][v][1] + q[i][v][2] * kr[j][v][2] +
+               q[i][v][3] * kr[j][v][3];
+        d = row_sum16(d);
+        sj[i][j] = p < n[i] ? d * scale : -INFINITY;
+        m[i] = fmaxf(m[i], sj[i][j]);
+      }
+      m[i] = rows_max4(m[i]);
+      if (lane == 0) sm.m[i][wave] = m[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t i = 0; i < QN; i++) {
+      float M = sm.m[i][0];
+#pragma unroll
+      for (uint32_t w = 1; w < NW; w++) M = fmaxf(M, sm.m[i][w]);
+      M_out[i] = M;
+      f4 acc[V4];
+#pragma unroll
+      for (uint32_t v = 0; v < V4; v++) acc[v] = f4{0, 0, 0, 0};
+      float l = 0;
+#pragma unroll
+      for (uint32_t j = 0; j < J; j++) {
+        const uint32_t p = row0 + slot + S * j;
+        if (p < n[i]) {
+          const float e = expf(sj[i][j] - M);
+          l += e;
+#pragma unroll
+          for (uint32_t v = 0; v < V4; v++) acc[v] += e * vr[j][v];
+        }
+      }
+      l = rows_sum4(l);
+#pragma unroll
+      for (uint32_t v = 0; v < V4; v++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          acc[v][k] += __shfl_xor(acc[v][k], 16);
+          acc[v][k] += __shfl_xor(acc[v][k], 32);
+        }
+      if (lane < 16)
+#pragma unroll
+        for (uint32_t v = 0; v < V4; v++) sm.o[i][(wave * 16 + cl) * V4 + v] = acc[v];
+      if (lane == 0) sm.l[i][wave] = l;
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t i = 0; i < QN; i++) {
+      float L = 0, o = 0;
+      if (tid < HD) {
+        const uint32_t fi = tid / 4, ci = fi % 16, vi = fi / 16, k = tid % 4;
+#pragma unroll
+        for (uint32_t w = 0; w < NW; w++) {
+          L += sm.l[i][w];
+          o += sm.o[i][(w * 16 + ci) * V4 + vi][k];
+        }
+      }
+      L_out[i] = L;
+      o_out[i] = o;
+    }
   }
 };
 

@@ -106,6 +106,43 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a, uint32_t ntok, ui
   if (EMIT && tid < HD) emit_operand(ops, t, h * HD + tid, o / L);
 }
 
+// The one-chunk attention for QN tokens of a pass at once: a workgroup per
+// (token group of QN, KV head) and query head, as attn_kernel maps units to
+// XCDs, loads the rows once for its QN queries (AttnChunk::reduce_n), each
+// with its own causal bound; outputs (and, EMIT, the O product's operands)
+// as attn_kernel<SPLIT = false> writes them.
+template <uint32_t HD, uint32_t J, bool KVH, bool EMIT, uint32_t QN>
+__global__ __launch_bounds__(512) void attn_multi_kernel(AttnArgs a, uint32_t ntok, uint32_t units, AttnOps ops) {
+  typedef AttnChunk<HD, J, 8, KVH> AC;
+  __shared__ AttnLds<HD, 8, QN> sm;
+  const uint32_t GQ = a.heads / a.kv_heads, sb = blockIdx.x / 8;
+  const uint32_t u = 8 * (sb / GQ) + blockIdx.x % 8;
+  if (u >= units) return;
+  const uint32_t tp = u / a.kv_heads, g = u % a.kv_heads, h = g * GQ + sb % GQ;
+  const uint32_t tid = threadIdx.x, cl = tid & 15;
+  f4 q[QN][AC::V4];
+  uint32_t n[QN];
+#pragma unroll
+  for (uint32_t i = 0; i < QN; i++) {
+    const uint32_t t = min(tp * QN + i, ntok - 1);
+    const float* qp = a.q + (uint64_t)t * a.heads * HD + h * HD + 4 * cl;
+#pragma unroll
+    for (uint32_t v = 0; v < AC::V4; v++) q[i][v] = *(const f4*)(qp + 64 * v);
+    n[i] = a.state[0] + t + 1;
+  }
+  AC rows;
+  rows.load(a.kv, a.kvd, a.ctx, g, 0, a.rows);
+  float M[QN], L[QN], o[QN];
+  rows.template reduce_n<QN>(q, 0, n, a.scale, sm, M, L, o);
+#pragma unroll
+  for (uint32_t i = 0; i < QN; i++) {
+    const uint32_t t = tp * QN + i;
+    if (t >= ntok) break;  // uniform
+    if (tid < HD) a.att[(uint64_t)t * a.heads * HD + h * HD + tid] = o[i] / L[i];
+    if (EMIT && tid < HD) emit_operand(ops, t, h * HD + tid, o[i] / L[i]);
+  }
+}
+
 // Prefill attention over chunks of 128 cache rows on the matrix cores (head
 // size 64, several tokens): a workgroup per (KV head g, chunk c, group of 64
 // queries), the queries of KV head g numbered token * GQ + (head - g * GQ).
@@ -320,7 +357,19 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* 
   const uint32_t NI = ntok * a.kv_heads;
   if (!a.split) {
     if (a.rows > attn_full_max(a.hd)) return set_error(LLMHIP_ERR_ARG, "llm: attention: %u rows in one chunk", a.rows);
-    if (a.hd == 64) attn_go<64, 8, false>(a, ntok, NI, s, ops);
+    if (a.hd == 64 && ntok > 1) {
+      // two tokens per workgroup (measured: prefill 53.8k -> 54.8k tok/s; four: 53.4k)
+      constexpr uint32_t QN = 2;
+      const uint32_t units = (ntok + QN - 1) / QN * a.kv_heads, gq = a.heads / a.kv_heads;
+      const dim3 g(8 * gq * ((units + 7) / 8)), b(512);
+      if (a.kv16) {
+        if (ops.xp) hipLaunchKernelGGL((attn_multi_kernel<64, 8, true, true, QN>), g, b, 0, s, a, ntok, units, ops);
+        else hipLaunchKernelGGL((attn_multi_kernel<64, 8, true, false, QN>), g, b, 0, s, a, ntok, units, ops);
+      } else {
+        if (ops.xp) hipLaunchKernelGGL((attn_multi_kernel<64, 8, false, true, QN>), g, b, 0, s, a, ntok, units, ops);
+        else hipLaunchKernelGGL((attn_multi_kernel<64, 8, false, false, QN>), g, b, 0, s, a, ntok, units, ops);
+      }
+    } else if (a.hd == 64) attn_go<64, 8, false>(a, ntok, NI, s, ops);
     else attn_go<128, 4, false>(a, ntok, NI, s, ops);
     LLM_HIP(hipGetLastError());
     return 0;
