@@ -1699,14 +1699,28 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       ss = wave_sum_dpp(ss);
       if (lane == 0) misc[wave * NT + t] = ss;
     }
-    __syncthreads();
+  }
+  // cpu.go:90-95, from the waves' partial sums (every thread, the same order)
+  auto rms_scales = [&]() {
 #pragma unroll
     for (int t = 0; t < NT; t++) {
       float ss = 0;
-      for (uint32_t v = 0; v < nwv; v++) ss += misc[v * NT + t];  // every thread, the same order
-      rs[t] = t < nt ? (float)(1.0 / sqrt((double)(ss / (float)a.k + a.eps))) : 0.f;  // cpu.go:90-95
+      for (uint32_t v = 0; v < nwv; v++) ss += misc[v * NT + t];
+      rs[t] = t < nt ? (float)(1.0 / sqrt((double)(ss / (float)a.k + a.eps))) : 0.f;
     }
+  };
+  // LATE (f32 activations): the units are staged as x * w and the products
+  // scaled by each token's 1/rms at the end, so no wave waits for the
+  // others' sums before its products.  PRO_Q8 quantises x * s * w itself and
+  // needs s first.
+  constexpr bool LATE = RMS && !Q8;
+  if (RMS && !LATE) {
+    __syncthreads();
+    rms_scales();
   }
+  if (LATE)
+#pragma unroll
+    for (int t = 0; t < NT; t++) rs[t] = 1.f;
 
   float acc0 = 0, acc1 = 0;
   int ex[UB][NT];
@@ -1728,6 +1742,12 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     }
     stage_items<QT, NT, PRO, NU>(itt, rs, lane, ops, sums, dxs, ex);
     unit_products<QT, NT, Q8, true>(wt, 0, (int)a.tail, ops, sums, dxs, ex, q, slot, acc0, acc1);
+  }
+  if (LATE) {
+    __syncthreads();  // every wave's sum of squares is in misc
+    rms_scales();
+    acc0 *= rs[min(2 * q, NT - 1)];
+    acc1 *= rs[min(2 * q + 1, NT - 1)];
   }
   // ---- split-K: partial sums of the waves of a tile, added in a fixed order
   // (every partial read issued before the sums)
