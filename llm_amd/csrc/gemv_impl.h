@@ -1082,18 +1082,30 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
       }
     }
   }
+  // f32 mode with RMSNorm: the largest |x * w| goes through the same barrier
+  // as the sum of squares (the exponent below needs only the magnitude of
+  // max |x * s * w| = s * max |x * w|, s > 0), so the prep has one barrier
+  float mw = 0;
   if (PRO & PRO_RMS) {
     // cpu.go:90-96
     float ss = 0;
 #pragma unroll
     for (int k = 0; k < PMAXI; k++)
       if (tid + k * 256 < NI)
-        for (int i = 0; i < 4; i++) ss += va[k][i] * va[k][i] + vc[k][i] * vc[k][i];
+        for (int i = 0; i < 4; i++) {
+          ss += va[k][i] * va[k][i] + vc[k][i] * vc[k][i];
+          mw = fmaxf(mw, fmaxf(fabsf(va[k][i] * wa[k][i]), fabsf(vc[k][i] * wc[k][i])));
+        }
     ss = wave_sum(ss);
     if (lane == 0) red[wave] = ss;
+    if (!(PRO & PRO_Q8)) {
+      mw = wave_max(mw);
+      if (lane == 0) red[4 + wave] = mw;
+    }
     __syncthreads();
     // every thread forms the scale from the four wave sums (same order): no second barrier
     const float sc = (float)(1.0 / sqrt((double)((red[0] + red[1] + red[2] + red[3]) / (float)K + a.eps)));
+    mw = sc * fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
 #pragma unroll
     for (int k = 0; k < PMAXI; k++) {
       uint32_t it = tid + k * 256;
@@ -1137,18 +1149,21 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
     }
     return;
   }
-  float m = 0;
+  float mm = mw;
+  if (!(PRO & PRO_RMS)) {
+    float m = 0;
 #pragma unroll
-  for (int k = 0; k < PMAXI; k++)
-    if (tid + k * 256 < NI)
-      for (int i = 0; i < 4; i++) m = fmaxf(m, fmaxf(fabsf(va[k][i]), fabsf(vc[k][i])));
-  m = wave_max(m);
-  if (lane == 0) red[4 + wave] = m;  // [0, 4) may still be read for the RMS scale
-  __syncthreads();
-  // every thread forms the exponent from the four wave maxima: no second barrier
+    for (int k = 0; k < PMAXI; k++)
+      if (tid + k * 256 < NI)
+        for (int i = 0; i < 4; i++) m = fmaxf(m, fmaxf(fabsf(va[k][i]), fabsf(vc[k][i])));
+    m = wave_max(m);
+    if (lane == 0) red[4 + wave] = m;
+    __syncthreads();
+    // every thread forms the exponent from the four wave maxima: no second barrier
+    mm = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+  }
   int ex = 0;
   {
-    const float mm = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
     if (mm > 0 && mm <= 3.0e38f) {
       int E;
       frexpf(mm, &E);
