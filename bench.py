@@ -42,7 +42,7 @@ def kernel_symbols(attn_full):
     <type, prologue, epilogue, groups per tile>."""
     return {"k1": "gemv_kernel<2u, 1, 1, 2, 2>",
             "k2": "attn_kernel<64u, 8u, false, false, false>" if attn_full else
-                  "attn_kernel<64u, 4u, true, false, false> + attn_merge_kernel<64u, false>",
+                  "attn_kernel<64u, 8u, true, false, false>",
             "k3": "gemv_kernel<2u, 1, 0, 1, 2>", "k4": "gemv_kernel<2u, 1, 1, 3, 2>", "k5": "gemv_kernel<2u, 1, 0, 1, 4>",
             "head": "gemv_stream_kernel<8u, 1, 4, 7>"}
 
@@ -212,7 +212,10 @@ def long_context(args):
     res = {"workload": "BASELINE config 4: qwen2.5-0.5b shape, Q4_1 ffn_down on odd layers, Q8_0 head, 2048-token "
                        "prompt, 512 greedy tokens, ctx 4096",
            "prefill_tok_s": round(tm.PromptTokens / tm.Prefill, 1), "decode_tok_s": round(tm.Generated / tm.Decode, 1),
-           "attention_at_end": {"avg_us": round(us, 2), "kv_bytes": nbytes, "gbps": round(nbytes / us * 1e-3, 1)},
+           "attention_at_end": {"avg_us": round(us, 2), "kv_bytes": nbytes, "gbps": round(nbytes / us * 1e-3, 1),
+                                "note": "the split attention kernel (chunks of 256 rows); their merge runs in the "
+                                        "output projection's prologue, so classes_at_end.k3 carries it (k3 merges "
+                                        "nothing at config 3: decode_step.classes.k3)"},
            "classes_at_end": classes}
     log(f"long context: prefill {res['prefill_tok_s']} tok/s, decode {res['decode_tok_s']} tok/s, "
         f"attention {us:.1f} us for {nbytes} KV bytes")

@@ -31,7 +31,19 @@ enum Prologue : int {
   PRO_RMS = 1,    // RMSNorm(x[t]) * nw  (cpu.go:81-98), recomputed per workgroup
   PRO_Q8 = 2,     // flag: the input then quantised to Q8_0 / Q8_1 blocks and the products formed
                   // as ggml's CPU backend forms them (the ExactGGML mode, cpu.go:117-140, 166-214)
+  PRO_MERGE = 4,  // one token, f32: x[e] is the attention output of head e / hd, merged from the
+                  // split attention's chunk partials (mpv, mml) as attn_merge_kernel merges them;
+                  // the bits from PRO_MERGE_SHIFT up hold how many chunks (merge_pro)
 };
+// Chunks of partials the merging prologue combines: all of them loaded at
+// once, an even count from 2 to MERGE_MAX_CHUNKS chosen per pass (the chunks
+// its attention rows can have), so that no load waits for the position.
+constexpr uint32_t MERGE_MAX_CHUNKS = 16;
+constexpr int PRO_MERGE_SHIFT = 3;
+constexpr int merge_pro(uint32_t chunks) { return PRO_MERGE | (int)(((chunks + 1) / 2 - 1) << PRO_MERGE_SHIFT); }
+constexpr uint32_t merge_chunks(int pro) {
+  return (pro & PRO_MERGE) ? 2 * (((uint32_t)pro >> PRO_MERGE_SHIFT) & 7) + 2 : 0;
+}
 
 enum Epilogue : int {
   EPI_STORE = 0,   // y[t*ldy + row] = v
@@ -76,6 +88,12 @@ struct GemvArgs {
   const float* aux;  // EPI_SWIGLU: the gate values
   float* up;         // EPI_GATEUP / EPI_SWIGLU: the up product u = W_up h also stored here, [t*ff + i]
                      // (nullptr: not kept); Peek("up")
+  // PRO_MERGE: the split attention's partials ([heads][msmax][hd] sums of e*v, [heads][msmax][2]
+  // max and sum of e) over chunks of mrows positions; the merged row also goes to matt (tile 0)
+  const float* mpv;
+  const float* mml;
+  uint32_t msmax, mrows;
+  float* matt;
   // prefill (gemm_kernel): activations prepared once per launch by prep_kernel
   void* xp;        // [tg][nb][64 lanes] 16-byte MFMA operands (hi/lo f16 of 8 tokens)
   int32_t* xexp;   // [tg*8] power-of-two scale per token

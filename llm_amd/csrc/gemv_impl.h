@@ -1437,17 +1437,26 @@ __host__ __device__ inline uint32_t decode_lds(int nt, uint32_t waves) {
 // 16+4iq..16+4iq+3 in xc); with two, lanes 0-31 load the first halves of the
 // two units' items and lanes 32-63 the second (one load instruction per
 // array instead of two), in xa, and staging swaps them across.
-template <int NT, bool RMS>
+// MC chunks (PRO_MERGE, one token): instead of x, each chunk's (max, sum of
+// e) of the item's head and its partial sums of e*v for the item's elements;
+// P, the chunks below the causal bound; merge_items forms xa / xc from them.
+template <int NT, bool RMS, uint32_t MC = 0>
 struct Items {
   f4 xa[NT], xc[NT], wa, wc;
+  float mc[MC ? MC : 1], lc[MC ? MC : 1];
+  f4 oa[MC ? MC : 1], oc[MC ? MC : 1];
+  uint32_t P, e0;
+  bool ok;
 };
+template <int NT, int PRO>
+using ItemsOf = Items<NT, (PRO & PRO_RMS) != 0, merge_chunks(PRO)>;
 
 // Issue the item loads of the batch whose units start at i0 (group sp +
 // i * split for unit i < cnt; with TAILU the tail, blocks < tail).  Absent
 // items read one address for the whole wave, so the loads are unconditional.
 template <int NT, int PRO, bool TAILU, int NU>
-__device__ __forceinline__ void load_items(Items<NT, (PRO & PRO_RMS) != 0>& it, const GemvArgs& a, uint32_t t0, int nt,
-                                           uint32_t i0, uint32_t cnt, uint32_t sp, uint32_t split, int lane) {
+__device__ __forceinline__ void load_items(ItemsOf<NT, PRO>& it, const GemvArgs& a, uint32_t t0, int nt, uint32_t i0,
+                                           uint32_t cnt, uint32_t sp, uint32_t split, int lane) {
   const uint32_t u = NU == 4 ? lane >> 4 : (lane >> 4) & 1, b = (lane >> 2) & 3, iq = lane & 3;
   const uint32_t half = NU == 4 ? 0 : lane >> 5;
   const uint32_t i = i0 + u;
@@ -1455,6 +1464,27 @@ __device__ __forceinline__ void load_items(Items<NT, (PRO & PRO_RMS) != 0>& it, 
   const uint32_t g = TAILU ? a.ng : sp + i * split;
   const uint32_t e0 = ok ? (g * 4 + b) * 32 + 4 * iq + 16 * half : 0;
   const f4 z = {0, 0, 0, 0};
+  if constexpr ((PRO & PRO_MERGE) != 0) {
+    // one token: the head of elements e0.. (and e0 + 16..), its chunks
+    static_assert(NT == 1, "merging prologue: one token");
+    const uint32_t h = e0 / a.hd, d = e0 % a.hd;
+    const float* ml = a.mml + (uint64_t)h * a.msmax * 2;
+    const float* pv = a.mpv + (uint64_t)h * a.msmax * a.hd + d;
+#pragma unroll
+    for (uint32_t c = 0; c < merge_chunks(PRO); c++) {
+      typedef float f2 __attribute__((ext_vector_type(2)));
+      const uint32_t cc = min(c, a.msmax - 1);
+      const f2 v = *(const f2*)(ml + 2 * cc);
+      it.mc[c] = v[0];
+      it.lc[c] = v[1];
+      it.oa[c] = *(const f4*)(pv + (uint64_t)cc * a.hd);
+      if (NU == 4) it.oc[c] = *(const f4*)(pv + (uint64_t)cc * a.hd + 16);
+    }
+    it.P = (a.state[0] + a.mrows) / a.mrows;  // chunks holding positions 0 .. pos
+    it.e0 = e0;
+    it.ok = ok;
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     const float* xr = a.x + (uint64_t)(a.xrow0 + t0 + min(t, nt - 1)) * a.ldx + e0;
@@ -1475,6 +1505,44 @@ __device__ __forceinline__ void load_items(Items<NT, (PRO & PRO_RMS) != 0>& it, 
   }
 }
 
+// PRO_MERGE: the item's attention outputs from its loaded chunk partials, in
+// attn_merge_kernel's order (one batch of chunks from M = -inf, L = o = 0:
+// M = max m_c, w_c = e^{m_c - M}, L = sum w_c l_c, o = sum w_c o_c, o / L);
+// chunks at or past P are left out.  keep: also store them to matt.
+template <int PRO, int NU>
+__device__ __forceinline__ void merge_items(ItemsOf<1, PRO>& it, const GemvArgs& a, bool keep) {
+  constexpr uint32_t MC = merge_chunks(PRO);
+  float M = -INFINITY;
+#pragma unroll
+  for (uint32_t c = 0; c < MC; c++) M = fmaxf(M, c < it.P ? it.mc[c] : -INFINITY);
+  float L = 0;
+  f4 oA = {0, 0, 0, 0}, oC = {0, 0, 0, 0};
+#pragma unroll
+  for (uint32_t c = 0; c < MC; c++) {
+    const bool in = c < it.P;
+    const float w = in ? expf(it.mc[c] - M) : 0.f;
+    L += w * (in ? it.lc[c] : 0.f);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      oA[k] += w * (in ? it.oa[c][k] : 0.f);
+      if (NU == 4) oC[k] += w * (in ? it.oc[c][k] : 0.f);
+    }
+  }
+  const f4 z = {0, 0, 0, 0};
+  f4 A, C;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    A[k] = oA[k] / L;
+    C[k] = oC[k] / L;
+  }
+  it.xa[0] = it.ok ? A : z;
+  if (NU == 4) it.xc[0] = it.ok ? C : z;
+  if (keep && it.ok) {
+    *(f4*)(a.matt + it.e0) = A;
+    if (NU == 4) *(f4*)(a.matt + it.e0 + 16) = C;
+  }
+}
+
 // With two units per batch: each lane's other half, from the lane 32 away.
 __device__ __forceinline__ f4 other_half(const f4& v, int lane) {
   f4 o;
@@ -1492,7 +1560,7 @@ __device__ __forceinline__ f4 other_half(const f4& v, int lane) {
 // per block of 32, cpu.go:117-140), into the wave's LDS.  ex[u][t] receives
 // the exponent of unit u, token t (wave-uniform).  Call with the whole wave.
 template <uint32_t QT, int NT, int PRO, int NU>
-__device__ __forceinline__ void stage_items(const Items<NT, (PRO & PRO_RMS) != 0>& it, const float (&rs)[NT], int lane,
+__device__ __forceinline__ void stage_items(const ItemsOf<NT, PRO>& it, const float (&rs)[NT], int lane,
                                             h8* ops, float* sums, float* dxs, int (&ex)[UB][NT]) {
   constexpr int S = 2 * NT;
   const uint32_t u = NU == 4 ? lane >> 4 : (lane >> 4) & 1, b = (lane >> 2) & 3, iq = lane & 3;
@@ -1641,8 +1709,10 @@ __device__ __forceinline__ void unit_products(const WUnit& w, uint32_t u, int nb
   }
 }
 
+// (the merging prologue holds every chunk's partials in registers: at most
+// 8 waves per workgroup, so that 256 VGPRs are there for it)
 template <uint32_t QT, int NT, int PRO, int EPI, int NU>
-__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(GemvArgs a) {
   typedef WaveLds<NT> WL;
   constexpr bool Q8 = (PRO & PRO_Q8) != 0, RMS = (PRO & PRO_RMS) != 0;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
@@ -1662,6 +1732,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   const uint32_t lt = wave / split, sp = wave % split;
   const uint32_t tile = min(blockIdx.x * tpw + lt, a.tiles - 1);
   const bool has_tile = blockIdx.x * tpw + lt < a.tiles;
+  const bool keep = blockIdx.x * tpw + lt == 0;  // PRO_MERGE: tile 0's waves also store the merged row
   const int r = lane & 15, q = lane >> 4, slot = lane & 15;
   // this wave's units: groups sp, sp + split, ... below ng, then the tail (wave ng % split)
   const uint32_t cnt = has_tile && ng > sp ? (ng - sp + split - 1) / split : 0;
@@ -1688,7 +1759,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       }
   }
   // the first batch: activation items, then weights (they return in that order)
-  Items<NT, RMS> it, itt;
+  ItemsOf<NT, PRO> it, itt;
   WUnit w[NU], wt;
   load_items<NT, PRO, false, NU>(it, a, t0, nt, 0, cnt, sp, split, lane);
 #pragma unroll
@@ -1745,6 +1816,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int u = 0; u < NU; u++) load_group<QT>(w[u], a.qs, nb, tile, sp + (i0 + u) * split, lane, r, i0 + u < cnt);
     }
+    if constexpr ((PRO & PRO_MERGE) != 0) merge_items<PRO, NU>(it, a, keep);
     stage_items<QT, NT, PRO, NU>(it, rs, lane, ops, sums, dxs, ex);
 #pragma unroll
     for (int u = 0; u < NU; u++)
@@ -1755,6 +1827,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       load_items<NT, PRO, true, NU>(itt, a, t0, nt, 0, cnt, sp, split, lane);
       load_unit<QT>(wt, a.qs, nb, tile, ng, ng, a.tail, lane, r);
     }
+    if constexpr ((PRO & PRO_MERGE) != 0) merge_items<PRO, NU>(itt, a, keep);
     stage_items<QT, NT, PRO, NU>(itt, rs, lane, ops, sums, dxs, ex);
     unit_products<QT, NT, Q8, true>(wt, 0, (int)a.tail, ops, sums, dxs, ex, q, slot, acc0, acc1);
   }
@@ -1821,6 +1894,22 @@ static int launch_one(const GemvArgs& a, dim3 grid, uint32_t lds, hipStream_t s)
 template <uint32_t QT, int NT, int Q>
 static int launch_nt_q(const GemvArgs& a, int pro, int epi, dim3 grid, uint32_t lds, hipStream_t s) {
   constexpr int PP = PRO_PLAIN | Q, PR = PRO_RMS | Q;
+  if (pro & PRO_MERGE) {  // two units per staging batch (more would spill the partials)
+    if constexpr (Q == 0 && NT == 1)
+      if (epi == EPI_ACC && !(pro & (PRO_RMS | PRO_Q8)) && a.waves <= 8 && (a.ng + a.split - 1) / a.split <= 2)
+        switch (merge_chunks(pro)) {
+          case 2: return launch_nu<QT, 1, merge_pro(2), EPI_ACC, 2>(a, grid, lds, s);
+          case 4: return launch_nu<QT, 1, merge_pro(4), EPI_ACC, 2>(a, grid, lds, s);
+          case 6: return launch_nu<QT, 1, merge_pro(6), EPI_ACC, 2>(a, grid, lds, s);
+          case 8: return launch_nu<QT, 1, merge_pro(8), EPI_ACC, 2>(a, grid, lds, s);
+          case 10: return launch_nu<QT, 1, merge_pro(10), EPI_ACC, 2>(a, grid, lds, s);
+          case 12: return launch_nu<QT, 1, merge_pro(12), EPI_ACC, 2>(a, grid, lds, s);
+          case 14: return launch_nu<QT, 1, merge_pro(14), EPI_ACC, 2>(a, grid, lds, s);
+          case 16: return launch_nu<QT, 1, merge_pro(16), EPI_ACC, 2>(a, grid, lds, s);
+        }
+    return set_error(LLMHIP_ERR_ARG,
+                     "llm: gemv: the merging prologue is for one f32 token into EPI_ACC, <= 8 waves, <= 2 units each");
+  }
   switch ((pro & PRO_RMS) * 8 + epi) {
     case PRO_PLAIN * 8 + EPI_STORE: return launch_one<QT, NT, PP, EPI_STORE>(a, grid, lds, s);
     case PRO_PLAIN * 8 + EPI_ACC: return launch_one<QT, NT, PP, EPI_ACC>(a, grid, lds, s);

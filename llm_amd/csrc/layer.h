@@ -42,8 +42,10 @@ bool attn_ok(uint32_t hd);
 // Positions the one-chunk kernel covers.
 uint32_t attn_full_max(uint32_t hd);
 // One launch (one chunk), or two (chunks, merge).  Every position of the pass
-// (state[0] .. state[0] + ntok - 1) must be below a.rows.
-int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* ops = nullptr);
+// (state[0] .. state[0] + ntok - 1) must be below a.rows.  merge false (one
+// token, chunks): the merge is left to the output projection's prologue
+// (PRO_MERGE).
+int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* ops = nullptr, bool merge = true);
 int argmax_launch(const float* pv, const uint32_t* pi, uint32_t n, const float* logits, int32_t* tokens,
                   int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s);
 int advance_launch(uint32_t* state, uint32_t n, hipStream_t s);

@@ -348,7 +348,7 @@ static void attn_go(const AttnArgs& a, uint32_t ntok, uint32_t units, hipStream_
   else hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT, false>), g, b, 0, s, a, ntok, units, ops);
 }
 
-int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* ops_in) {
+int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* ops_in, bool merge) {
   if (ntok == 0) return 0;
   const AttnOps ops = ops_in ? *ops_in : AttnOps{nullptr, nullptr, nullptr, nullptr, 0};
   if (!attn_ok(a.hd) || a.rows == 0 || a.rows > a.ctx || a.heads % a.kv_heads)
@@ -389,6 +389,10 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* 
     attn_go<128, ATTN_SPLIT_ROWS / 32, true>(a, ntok, NI * chunks, s, ops);
   }
   LLM_HIP(hipGetLastError());
+  if (!merge) {
+    if (ntok != 1 || ops.xp) return set_error(LLMHIP_ERR_ARG, "llm: attention: only one token's merge is left out");
+    return 0;
+  }
   const dim3 mg(a.heads, ntok);
   if (a.hd == 64) {
     if (ops.xp) hipLaunchKernelGGL((attn_merge_kernel<64, true>), mg, dim3(64), 0, s, a, ops, crows);

@@ -515,12 +515,24 @@ static bool att_operands(const Model& m, uint32_t ntok) {
   return ntok >= GEMM_MIN_TOKENS && !m.q8 && !skipped(m, "k2") && !skipped(m, "k3");
 }
 
+// A one-token pass with the split attention leaves the merge of the chunk
+// partials to the output projection's prologue (PRO_MERGE: no merge kernel)
+// where the partials fit its loads and registers; f32 activations only.
+static bool merge_in_k3(const Model& m, const Layer& L, uint32_t ntok) {
+  if (ntok != 1 || !m.attn_split || m.q8) return false;
+  GemvArgs a;
+  gemv_bind(&a, L.o);
+  return (m.attn_rows + ATTN_DECODE_ROWS - 1) / ATTN_DECODE_ROWS <= MERGE_MAX_CHUNKS && a.waves <= 8 && !a.stream &&
+         (a.ng + a.split - 1) / a.split <= 2;
+}
+
 static int rec_k2(Model& m, const Layer& L, uint32_t ntok) {
   if (skipped(m, "k2")) return 0;
   // KV bytes read for the last token of the pass (the decode step's one token)
   uint64_t bytes = 2ull * (m.pos + 1) * m.kvd * 4;
-  if (m.attn_split) m.dispatches++;  // the merge kernel
   const AttnArgs a = attn_args(m, L);
+  if (merge_in_k3(m, L, ntok)) return launch_rec(m, "k2", bytes, [&]() { return attn_launch(a, ntok, m.stream, nullptr, false); });
+  if (m.attn_split) m.dispatches++;  // the merge kernel
   if (att_operands(m, ntok)) {
     GemvArgs g = base_args(m, L.o, ntok);
     xprep_bind(&g, m.xprep);
@@ -537,6 +549,15 @@ static int rec_k3(Model& m, const Layer& L, uint32_t ntok) {
   a.ldx = m.cfg.embd;
   a.y = m.x;
   a.ldy = m.cfg.embd;
+  if (merge_in_k3(m, L, ntok)) {
+    a.mpv = m.pv;
+    a.mml = m.ml;
+    a.msmax = m.smax;
+    a.mrows = ATTN_DECODE_ROWS;
+    a.matt = m.att;  // Peek("att")
+    const uint32_t chunks = (m.attn_rows + ATTN_DECODE_ROWS - 1) / ATTN_DECODE_ROWS;
+    return gemv_rec(m, "k3", a, L.o.g.q.type, merge_pro(chunks), EPI_ACC, L.o.g.gguf_bytes());
+  }
   const bool staged = att_operands(m, ntok);
   return mat_rec(m, "k3", "p3", a, L.o.g.q.type, PRO_PLAIN, EPI_ACC, L.o.g.gguf_bytes(), !staged, staged);
 }

@@ -516,6 +516,7 @@ struct cpuref_model {
   float* last_x;
   float* last_h;  /* the head's input of the last token (rmsNorm with output_norm) */
   float* last_u;  /* the up product of the last layer run, last token */
+  float* last_a;  /* the attention output of the last layer run, last token */
 };
 typedef struct cpuref_model cpuref_model;
 
@@ -558,6 +559,7 @@ static void model_free(cpuref_model* m) {
   free(m->last_x);
   free(m->last_h);
   free(m->last_u);
+  free(m->last_a);
   free(m);
 }
 
@@ -695,6 +697,7 @@ EXPORT int cpuref_load(const char* path, int max_ctx, cpuref_model** out) {
   m->last_x = (float*)calloc((size_t)m->c.embd, 4);
   m->last_h = (float*)calloc((size_t)m->c.embd, 4);
   m->last_u = (float*)calloc((size_t)m->c.ff, 4);
+  m->last_a = (float*)calloc((size_t)m->c.heads * m->c.head_dim, 4);
   *out = m;
   return 0;
 }
@@ -714,6 +717,10 @@ EXPORT void cpuref_last_x(cpuref_model* m, float* out) { memcpy(out, m->last_x, 
  * last layer's up product, and a cached K or V row. */
 EXPORT void cpuref_last_h(cpuref_model* m, float* out) { memcpy(out, m->last_h, (size_t)m->c.embd * 4); }
 EXPORT void cpuref_last_up(cpuref_model* m, float* out) { memcpy(out, m->last_u, (size_t)m->c.ff * 4); }
+/* the last layer's attention output (cpu.go:300-334), the reference's Peek("att") */
+EXPORT void cpuref_last_att(cpuref_model* m, float* out) {
+  memcpy(out, m->last_a, (size_t)m->c.heads * m->c.head_dim * 4);
+}
 EXPORT int cpuref_kv_row(cpuref_model* m, int layer, int pos, int v, float* out) {
   int kvd = m->c.kv_heads * m->c.head_dim;
   if (layer < 0 || layer >= m->c.layers || pos < 0 || pos >= m->pos) return fail("llm: no cache row%s", "");
@@ -892,6 +899,7 @@ EXPORT int cpuref_forward(cpuref_model* m, int32_t tok, float* logits) {
   } else {
     memcpy(m->last_x, x, (size_t)c.embd * 4);
     if (nl > 0) memcpy(m->last_u, u, (size_t)c.ff * 4);
+    if (nl > 0) memcpy(m->last_a, att, (size_t)c.heads * c.head_dim * 4);
     if (m->max_layers != 0 && m->max_layers < c.layers) {
       m->pos++;
       rc = 0;

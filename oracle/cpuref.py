@@ -64,6 +64,7 @@ def lib():
         L.cpuref_last_x.argtypes = [P, P]
         L.cpuref_last_h.argtypes = [P, P]
         L.cpuref_last_up.argtypes = [P, P]
+        L.cpuref_last_att.argtypes = [P, P]
         L.cpuref_kv_row.argtypes = [P, I, I, I, P]
         L.cpuref_forward.argtypes = [P, ctypes.c_int32, P]
         L.cpuref_tensor.argtypes = [P, ctypes.c_char_p, ctypes.POINTER(P), ctypes.POINTER(ctypes.c_uint64),
@@ -204,6 +205,12 @@ class CPU:
         """The up product of the last layer the last forward ran."""
         out = np.empty(self.cfg.ff, np.float32)
         lib().cpuref_last_up(self._h, _p(out))
+        return out
+
+    def last_att(self):
+        """The attention output of the last layer the last forward ran (cpu.go:300-334)."""
+        out = np.empty(self.cfg.heads * self.cfg.head_dim, np.float32)
+        lib().cpuref_last_att(self._h, _p(out))
         return out
 
     def kv_row(self, layer, pos, v=False):

@@ -67,13 +67,36 @@ def test_tiny_parity(gpu, name):
 def test_attention_paths(gpu, prompt_len, heads, kv_heads, hd):
     """Both attention forms and the switch between them: passes whose
     positions are all below 256 (head size 64) or 128 (head size 128) run one
-    chunk per query head, later ones chunks of 128 rows merged by a second
-    kernel; prefill chunks and decode steps on both sides, for 1, 2, 4 and 8
-    query heads per KV head and head sizes 64 and 128."""
+    chunk per query head, later ones chunks (prefill: 128 rows, merged by a
+    second kernel; decode: 256 rows, merged in the output projection's
+    prologue); prefill chunks and decode steps on both sides, for 1, 2, 4 and
+    8 query heads per KV head and head sizes 64 and 128."""
     spec = synth.tiny_llama(seed=6 + heads + kv_heads + hd, embd=hd * heads, heads=heads, kv_heads=kv_heads)
     g, cpu = _open(spec, 512)
     prompt = synth.prompt(7, prompt_len, spec.vocab)
     _check(g, cpu, prompt, (320 if hd == 64 else 200) - prompt_len)
+
+
+@pytest.mark.parametrize("hd,ctx,prompt_len", [(64, 512, 300), (128, 512, 150), (64, 4096, 2100)])
+def test_att_merged_in_projection(gpu, hd, ctx, prompt_len):
+    """One-token passes past the one-chunk bound run the split attention and
+    merge its chunk partials in the output projection's prologue (no merge
+    kernel): 2, 2 and 10 chunks of 256 rows here.  Peek("att") -- the last
+    layer's merged attention output, which the projection's first tile also
+    stores -- against the oracle's after the last of four decode steps, and
+    the tokens against the oracle's."""
+    spec = synth.tiny_qwen(seed=11 + hd, embd=4 * hd, ctx=max(ctx, 1024))
+    g, cpu = _open(spec, ctx)
+    prompt = [int(t) for t in synth.prompt(9, prompt_len, spec.vocab)]
+    out = gpu_generate(g, prompt, 4)
+    cpu.reset()
+    for t in prompt + out[:3]:
+        cpu.forward(t)
+    rel = rel_err(g.Peek("att", spec.embd), cpu.last_att())
+    print(f"att after decode at position {prompt_len + 2}: {rel:.2e}", flush=True)
+    assert rel <= 1e-5
+    toks, lgs = cpu_greedy(cpu, prompt, 4)
+    greedy_parity(g, prompt, toks, lgs)
 
 
 @pytest.mark.parametrize("prompt_len,heads,kv_heads", [(520, 14, 2), (330, 8, 8), (460, 9, 3)])
