@@ -76,6 +76,7 @@ struct GemvArgs {
   // epilogue
   float* y;
   uint32_t ldy;
+  const float* yin;  // EPI_ACC: the residual read (nullptr: y itself)
   const float* bias;  // QKV biases, logical row order (nullptr: none)
   const float* cs;    // RoPE table [pos][hd/2][cos, sin]
   float* kv;          // this layer's cache [2][ctx][kvd], f32 or (kv16) binary16

@@ -364,8 +364,9 @@ __device__ __forceinline__ EpiIn epi_load(const GemvArgs& a, uint32_t tile, int 
   const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
   if (!active || lr >= a.rows) return e;
   if (EPI == EPI_ACC) {
-    if (okA) e.yA = a.y[(uint64_t)tokA * a.ldy + lr];
-    if (okB) e.yB = a.y[(uint64_t)tokB * a.ldy + lr];
+    const float* yr = a.yin ? a.yin : a.y;
+    if (okA) e.yA = yr[(uint64_t)tokA * a.ldy + lr];
+    if (okB) e.yB = yr[(uint64_t)tokB * a.ldy + lr];
   }
   if (EPI == EPI_QKV) {
     const uint32_t lf = a.row_base + lr;

@@ -2,6 +2,7 @@
 #pragma once
 
 #include "common.h"
+#include "gemv.h"
 
 namespace llmhip {
 
@@ -46,8 +47,13 @@ uint32_t attn_full_max(uint32_t hd);
 // token, chunks): the merge is left to the output projection's prologue
 // (PRO_MERGE).
 int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* ops = nullptr, bool merge = true);
+// Greedy sampling from the head's per-workgroup partials, the token written
+// to tokens[step + adv] and out[0], the state advanced by adv; with embd and
+// xn also the sampled token's embedding row into xn (the input of the next
+// one-token pass, which then runs no embedding kernel).
 int argmax_launch(const float* pv, const uint32_t* pi, uint32_t n, const float* logits, int32_t* tokens,
-                  int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s);
+                  int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s, const QMat* embd = nullptr,
+                  float* xn = nullptr);
 int advance_launch(uint32_t* state, uint32_t n, hipStream_t s);
 // out[i] = x[i] * s * w[i], s = f32(1/sqrt(f64(sum x^2 / n + eps))) (rmsNorm, cpu.go:81-98), one
 // workgroup; n <= 16384.  Not on the forward pass (the matrix kernels fuse it): Peek("h").

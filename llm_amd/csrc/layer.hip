@@ -2,6 +2,7 @@
 // (one chunk, or chunks of positions merged by a second kernel), greedy
 // sampling and the state advance.
 #include "attn_core.h"
+#include "gemv_impl.h"
 #include "layer.h"
 #include "wave.h"
 
@@ -405,21 +406,23 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* 
   return 0;
 }
 
-// Greedy sampling (cpu.go:389-397): the lowest index of the largest logit,
-// NaN never wins, and a NaN logit 0 is never displaced.  Combines the
-// per-workgroup partials of the head's matvec (all loads in flight at once),
-// writes the token to tokens[step + adv] and out[0] (kernels.go:389-392),
-// then advances (pos, step) by adv (kernels.go:397-415).
-__device__ __forceinline__ bool amax_better(float v, uint32_t i, float bv, uint32_t bi) {
-  return i != 0xffffffffu && (bi == 0xffffffffu || v > bv || (v == bv && i < bi));
-}
-
+// Greedy sampling (cpu.go:389-397): the lowest index of the largest logit
+// (amax_better), NaN never wins, and a NaN logit 0 is never displaced.
+// Combines the per-workgroup partials of the head's matvec (all loads in
+// flight at once), writes the token to tokens[step + adv] and out[0]
+// (kernels.go:389-392), then advances (pos, step) by adv (kernels.go:397-415).
+// QT (the embedding's type; 0: none): then the sampled token's embedding row
+// (kernels.go:19-73) also goes to xn, for the next one-token pass.
+template <uint32_t QT>
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
                                                       uint32_t n, const float* __restrict__ logits,
                                                       int32_t* __restrict__ tokens, int32_t* __restrict__ outb,
-                                                      uint32_t* __restrict__ state, uint32_t adv) {
+                                                      uint32_t* __restrict__ state, uint32_t adv,
+                                                      const uint8_t* __restrict__ eq, uint64_t etiles, uint32_t enb,
+                                                      uint32_t eng, uint32_t etail, float* __restrict__ xn) {
   __shared__ float sv[16];
   __shared__ uint32_t si[16];
+  __shared__ uint32_t tok;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id(), nw = blockDim.x >> 6;
   constexpr int U = 8;
   float v[U];
@@ -473,12 +476,34 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
     outb[0] = (int32_t)bi;
     state[0] += adv;
     state[1] = step + adv;
+    tok = bi;
+  }
+  if (QT != 0) {
+    __syncthreads();
+    const uint32_t row = tok;
+    for (uint32_t b = tid; b < enb; b += blockDim.x) {
+      float v[32];
+      dequant_block<QT>(eq, etiles, enb, eng, etail, row, b, v);
+      for (int j = 0; j < 32; j++) xn[b * 32 + j] = v[j];
+    }
   }
 }
 
 int argmax_launch(const float* pv, const uint32_t* pi, uint32_t n, const float* logits, int32_t* tokens,
-                  int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s) {
-  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, pv, pi, n, logits, tokens, outb, state, adv);
+                  int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s, const QMat* e, float* xn) {
+  const dim3 g(1), b(1024);
+  if (!e || !xn) {
+    hipLaunchKernelGGL(argmax_kernel<0>, g, b, 0, s, pv, pi, n, logits, tokens, outb, state, adv, nullptr, 0ull, 0u,
+                       0u, 0u, nullptr);
+  } else if (e->g.q.type == LLMHIP_Q4_0) {
+    hipLaunchKernelGGL(argmax_kernel<LLMHIP_Q4_0>, g, b, 0, s, pv, pi, n, logits, tokens, outb, state, adv, e->qs,
+                       (uint64_t)e->g.tiles, e->g.nb, e->g.ng, e->g.tail, xn);
+  } else if (e->g.q.type == LLMHIP_Q8_0) {
+    hipLaunchKernelGGL(argmax_kernel<LLMHIP_Q8_0>, g, b, 0, s, pv, pi, n, logits, tokens, outb, state, adv, e->qs,
+                       (uint64_t)e->g.tiles, e->g.nb, e->g.ng, e->g.tail, xn);
+  } else {
+    return set_error(LLMHIP_ERR_TYPE, "llm: embedding type %u", e->g.q.type);
+  }
   LLM_HIP(hipGetLastError());
   return 0;
 }

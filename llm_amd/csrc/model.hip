@@ -93,8 +93,10 @@ struct Model {
   // gbuf: the up product of the pass's last layer ([pm][ff], Peek "up"; the
   // gate values in between when gate and up have different types); h: the
   // head's normed row, formed on demand by Peek("h")
+  // xn: the embedding row of the token the last head pass sampled, which the
+  // sampling kernel writes: the input of the next one-token pass
   float *x = nullptr, *q = nullptr, *act = nullptr, *gbuf = nullptr, *logits = nullptr, *pv = nullptr,
-        *ml = nullptr, *amax_v = nullptr, *cs = nullptr, *att = nullptr, *h = nullptr;
+        *ml = nullptr, *amax_v = nullptr, *cs = nullptr, *att = nullptr, *h = nullptr, *xn = nullptr;
   void* xprep = nullptr;  // prepared activations of a prefill chunk
   uint32_t *amax_i = nullptr, *state = nullptr;
   int32_t *tokens = nullptr, *outb = nullptr;
@@ -119,6 +121,7 @@ struct Model {
   uint32_t last_row = 0;     // the row of x holding the last token of the latest pass
   uint32_t attn_rows = 0;    // pass being recorded: cache rows its attention reads
   bool attn_split = false;   // ... and whether it runs in chunks merged by a second kernel
+  bool embed_in = true;      // ... and whether it embeds its tokens (else its one input row is xn)
   bool prompted = false;
   uint32_t dispatches = 0;  // counter while recording
   std::vector<ProfRec>* prof = nullptr;  // eager profiling: events around every launch
@@ -469,7 +472,7 @@ static int rec_k1(Model& m, const Layer& L, uint32_t ntok) {
   const llmhip_config& c = m.cfg;
   for (int i = 0; i < L.nqkv; i++) {
     GemvArgs a = base_args(m, L.qkv[i], ntok);
-    a.x = m.x;
+    a.x = m.cur_layer == 0 && !m.embed_in ? m.xn : m.x;
     a.ldx = c.embd;
     a.nw = L.attn_norm;
     a.y = m.q;
@@ -549,6 +552,7 @@ static int rec_k3(Model& m, const Layer& L, uint32_t ntok) {
   a.ldx = m.cfg.embd;
   a.y = m.x;
   a.ldy = m.cfg.embd;
+  if (m.cur_layer == 0 && !m.embed_in) a.yin = m.xn;  // the residual stream starts at the embedding row
   if (merge_in_k3(m, L, ntok)) {
     a.mpv = m.pv;
     a.mml = m.ml;
@@ -633,17 +637,22 @@ static int rec_head(Model& m, uint32_t xrow, uint32_t adv) {
   LLM_TRY(gemv_rec(m, "head", a, w.g.q.type, PRO_RMS, EPI_ARGMAX, w.g.gguf_bytes()));
   if (skipped(m, "argmax")) return rec_adv(m, adv);
   uint32_t groups = gemv_groups(a);
+  const bool emb = !skipped(m, "embed");  // the next one-token pass's input row
   return launch_rec(m, "argmax", 8ull * groups, [&]() {
-    return argmax_launch(m.amax_v, m.amax_i, groups, m.logits, m.tokens, m.outb, m.state, adv, m.stream);
+    return argmax_launch(m.amax_v, m.amax_i, groups, m.logits, m.tokens, m.outb, m.state, adv, m.stream,
+                         emb ? &m.embd : nullptr, emb ? m.xn : nullptr);
   });
 }
 
 
 // One pass of ntok tokens at positions state[0] .. state[0]+ntok-1: the
-// embedding, the layers, and (head) the logits and the sampled token of the
-// last one, which goes to tokens[step + ntok]; state advances by ntok.
-static int record_pass(Model& m, uint32_t ntok, bool head) {
-  if (!skipped(m, "embed")) {
+// embedding (embed_in; else the one token's row is xn, which the previous
+// head pass's sampling kernel wrote), the layers, and (head) the logits and
+// the sampled token of the last one, which goes to tokens[step + ntok], its
+// embedding row to xn; state advances by ntok.
+static int record_pass(Model& m, uint32_t ntok, bool head, bool embed_in) {
+  m.embed_in = embed_in || ntok != 1;
+  if (m.embed_in && !skipped(m, "embed")) {
     m.cur_layer = -1;
     uint64_t row = (uint64_t)m.embd.g.nb * m.embd.g.q.block_bytes;
     LLM_TRY(launch_rec(m, "embed", row * ntok,
@@ -684,13 +693,13 @@ static void attn_plan(Model& m, uint32_t pos, uint32_t ntok) {
   m.attn_split = true;
 }
 
-static uint64_t graph_key(uint32_t ntok, uint32_t rows, bool split, bool head) {
-  return ((uint64_t)ntok << 32) | ((uint64_t)rows << 2) | (split ? 2 : 0) | (head ? 1 : 0);
+static uint64_t graph_key(uint32_t ntok, uint32_t rows, bool split, bool head, bool embed_in) {
+  return ((uint64_t)ntok << 32) | ((uint64_t)rows << 3) | (embed_in ? 4 : 0) | (split ? 2 : 0) | (head ? 1 : 0);
 }
 
 // Capture record_pass into a graph (once per key).
-static int graph_for(Model& m, uint32_t ntok, bool head, hipGraphExec_t* out) {
-  uint64_t key = graph_key(ntok, m.attn_rows, m.attn_split, head);
+static int graph_for(Model& m, uint32_t ntok, bool head, bool embed_in, hipGraphExec_t* out) {
+  uint64_t key = graph_key(ntok, m.attn_rows, m.attn_split, head, embed_in);
   auto it = m.chunk_exec.find(key);
   if (it != m.chunk_exec.end()) {
     *out = it->second;
@@ -699,7 +708,7 @@ static int graph_for(Model& m, uint32_t ntok, bool head, hipGraphExec_t* out) {
   hipGraph_t g = nullptr;
   m.dispatches = 0;
   LLM_HIP(hipStreamBeginCapture(m.stream, hipStreamCaptureModeThreadLocal));
-  int rc = record_pass(m, ntok, head);
+  int rc = record_pass(m, ntok, head, embed_in);
   hipError_t e = hipStreamEndCapture(m.stream, &g);
   if (rc != 0) {
     if (g) (void)hipGraphDestroy(g);
@@ -728,19 +737,22 @@ static bool eager_passes() {
   return e;
 }
 
-static int launch_graph(Model& m, uint32_t pos, uint32_t ntok, bool head) {
+// embed_in false: a decode step, whose input row the previous pass's sampling
+// kernel wrote to xn.
+static int launch_graph(Model& m, uint32_t pos, uint32_t ntok, bool head, bool embed_in) {
   hipGraphExec_t ex;
   attn_plan(m, pos, ntok);
   m.last_row = ntok - 1;
+  embed_in = embed_in || ntok != 1;
   if (eager_passes()) {
     m.dispatches = 0;
-    LLM_TRY(record_pass(m, ntok, head));
+    LLM_TRY(record_pass(m, ntok, head, embed_in));
     m.stats.dispatches += m.dispatches;
     return 0;
   }
-  LLM_TRY(graph_for(m, ntok, head, &ex));
+  LLM_TRY(graph_for(m, ntok, head, embed_in, &ex));
   LLM_HIP(hipGraphLaunch(ex, m.stream));
-  m.stats.dispatches += m.graph_nodes[graph_key(ntok, m.attn_rows, m.attn_split, head)];
+  m.stats.dispatches += m.graph_nodes[graph_key(ntok, m.attn_rows, m.attn_split, head, embed_in)];
   return 0;
 }
 
@@ -800,7 +812,8 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
       (rc = dalloc_n(*m, &m->ml, pm * H * m->smax * 2)) || (rc = dalloc_n(*m, &m->state, 2)) ||
       (rc = dalloc_n(*m, &m->tokens, (uint64_t)m->ctx + 1)) || (rc = dalloc_n(*m, &m->outb, 1)) ||
       (rc = dalloc(*m, &m->xprep, xprep_bytes(m->pm, (uint32_t)std::max(c.embd, c.ff)))) ||
-      (rc = dalloc_n(*m, &m->cs, (uint64_t)m->ctx * c.head_dim)) || (rc = dalloc_n(*m, &m->h, E)))
+      (rc = dalloc_n(*m, &m->cs, (uint64_t)m->ctx * c.head_dim)) || (rc = dalloc_n(*m, &m->h, E)) ||
+      (rc = dalloc_n(*m, &m->xn, E)))
     return fail(rc);
   // RoPE table in double precision, gpu.go:524-534 (and cpu.go:374-375)
   std::vector<float> cs((size_t)m->ctx * c.head_dim);
@@ -989,7 +1002,7 @@ int llmhip_model_prefill(llmhip_model* h, const int32_t* ids, int n, float* logi
   bool full = m.layers_limit == 0 || m.layers_limit >= m.cfg.layers;
   for (int a = 0; a < n; a += (int)m.pm) {
     int b = std::min(a + (int)m.pm, n);
-    LLM_TRY(launch_graph(m, (uint32_t)a, (uint32_t)(b - a), b == n));
+    LLM_TRY(launch_graph(m, (uint32_t)a, (uint32_t)(b - a), b == n, true));
     m.stats.submits++;
   }
   m.pos = (uint32_t)n;
@@ -1012,7 +1025,7 @@ int llmhip_model_decode(llmhip_model* h, int cnt, int32_t* out) {
                      m.pos);
   LLM_HIP(hipSetDevice(m.device));
   uint32_t first = m.pos;
-  for (int j = 0; j < cnt; j++) LLM_TRY(launch_graph(m, first + (uint32_t)j, 1, true));
+  for (int j = 0; j < cnt; j++) LLM_TRY(launch_graph(m, first + (uint32_t)j, 1, true, false));
   LLM_HIP(hipMemcpyAsync(m.host, m.tokens + first + 1, (size_t)cnt * 4, hipMemcpyDeviceToHost, m.stream));
   LLM_HIP(hipStreamSynchronize(m.stream));
   memcpy(out, m.host, (size_t)cnt * 4);
@@ -1218,7 +1231,7 @@ int llmhip_model_profile(llmhip_model* h, int tokens, llmhip_kernel_time* out, i
     std::vector<ProfRec> recs;
     m.prof = &recs;
     attn_plan(m, m.pos, 1);
-    rc = record_pass(m, 1, true);
+    rc = record_pass(m, 1, true, false);
     m.prof = nullptr;
     if (hipStreamSynchronize(m.stream) != hipSuccess && rc == 0)
       rc = set_error(LLMHIP_ERR_DEVICE, "llm: profile step failed");
