@@ -55,6 +55,8 @@ int argmax_launch(const float* pv, const uint32_t* pi, uint32_t n, const float* 
                   int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s, const QMat* embd = nullptr,
                   float* xn = nullptr);
 int advance_launch(uint32_t* state, uint32_t n, hipStream_t s);
+// state = (p, p) (a prefill chunk on a lane of its own).
+int set_state_launch(uint32_t* state, uint32_t p, hipStream_t s);
 // out[i] = x[i] * s * w[i], s = f32(1/sqrt(f64(sum x^2 / n + eps))) (rmsNorm, cpu.go:81-98), one
 // workgroup; n <= 16384.  Not on the forward pass (the matrix kernels fuse it): Peek("h").
 int rmsnorm_launch(const float* x, const float* w, uint32_t n, float eps, float* out, hipStream_t s);

@@ -537,6 +537,20 @@ int rmsnorm_launch(const float* x, const float* w, uint32_t n, float eps, float*
   return 0;
 }
 
+// state = (p, p): a prefill chunk's first position, on its own lane
+__global__ void set_state_kernel(uint32_t* state, uint32_t p) {
+  if (threadIdx.x == 0) {
+    state[0] = p;
+    state[1] = p;
+  }
+}
+
+int set_state_launch(uint32_t* state, uint32_t p, hipStream_t s) {
+  hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(64), 0, s, state, p);
+  LLM_HIP(hipGetLastError());
+  return 0;
+}
+
 int advance_launch(uint32_t* state, uint32_t n, hipStream_t s) {
   hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, s, state, n);
   LLM_HIP(hipGetLastError());

@@ -78,6 +78,16 @@ struct ProfRec {
   hipEvent_t a, b;
 };
 
+// What one lane of a prefill wavefront owns: its stream, its activation and
+// staging buffers, and its device-side position (the KV cache is shared:
+// chunks write disjoint rows).  The model's own fields are lane 0.
+struct Lane {
+  hipStream_t stream = nullptr;
+  float *x = nullptr, *q = nullptr, *att = nullptr, *act = nullptr, *gbuf = nullptr, *pv = nullptr, *ml = nullptr;
+  void* xprep = nullptr;
+  uint32_t* state = nullptr;
+};
+
 struct Model {
   int device = 0;
   llmhip_limits lim{};
@@ -112,7 +122,7 @@ struct Model {
   bool kv16 = false;  // binary16 KV cache (the F16KV mode of cpu.go:22-24)
   bool q8 = false;    // ExactGGML (cpu.go:15-21): every matrix input quantised to Q8 blocks, binary16 cache
   hipGraphExec_t decode_exec = nullptr;
-  std::map<uint64_t, hipGraphExec_t> chunk_exec;  // key: graph_key(ntok, attn_rows, attn_split, head)
+  std::map<uint64_t, hipGraphExec_t> chunk_exec;  // key: graph_key (pass or segment, lane, shape)
   std::map<uint64_t, uint32_t> graph_nodes;       // dispatches per graph key
   llmhip_stats stats{};
   int layers_limit = 0;
@@ -126,6 +136,12 @@ struct Model {
   uint32_t dispatches = 0;  // counter while recording
   std::vector<ProfRec>* prof = nullptr;  // eager profiling: events around every launch
   int cur_layer = -1;
+  // the prefill wavefront's second lane, swapped into the fields above while
+  // its work is recorded (use_lane); an event per segment of chunk c in set
+  // c % 4 (prefill_wavefront)
+  Lane alt;
+  int lane = 0;
+  std::vector<hipEvent_t> seg_done[4];
 };
 
 // Brackets one launch with HIP events on the model's stream when profiling.
@@ -229,7 +245,11 @@ static void model_destroy(Model* m) {
   if (!m) return;
   (void)hipSetDevice(m->device);
   if (m->stream) (void)hipStreamSynchronize(m->stream);
+  if (m->alt.stream) (void)hipStreamSynchronize(m->alt.stream);
   destroy_graphs(*m);
+  for (auto& v : m->seg_done)
+    for (hipEvent_t e : v) (void)hipEventDestroy(e);
+  if (m->alt.stream) (void)hipStreamDestroy(m->alt.stream);
   stager_free(&m->st);
   qmat_release(&m->embd);
   qmat_release(&m->out);
@@ -645,35 +665,83 @@ static int rec_head(Model& m, uint32_t xrow, uint32_t adv) {
 }
 
 
+// LLMHIP_EAGER=1: passes go to the stream as direct launches instead of graph
+// replays (same kernels, arguments and order), for tools that trace kernel
+// launches but not graph replays.
+static bool eager_passes() {
+  static const bool e = [] {
+    const char* v = getenv("LLMHIP_EAGER");
+    return v && *v && strcmp(v, "0") != 0;
+  }();
+  return e;
+}
+
+// Layers a pass runs (Layers, gpu.go:143-146); fewer than all: no head.
+static int pass_layers(const Model& m, bool* head) {
+  int nl = m.cfg.layers;
+  if (m.layers_limit != 0 && m.layers_limit < nl) {
+    nl = std::max(m.layers_limit, 0);
+    *head = false;
+  }
+  return nl;
+}
+
+// Segment s (0 .. layers) of a pass: s = 0 the embedding and layer 0's K1;
+// then layer s-1's K2..K5 and layer s's K1; the last, the last layer's K2..K5
+// and the head (or the advance).  A segment ends with the K1 that appends its
+// layer's cache rows, which is what a later chunk's attention waits for.
+static int record_segment(Model& m, uint32_t ntok, bool head, bool embed_in, int s) {
+  m.embed_in = embed_in || ntok != 1;
+  const int nl = pass_layers(m, &head);
+  if (s == 0 && m.embed_in && !skipped(m, "embed")) {
+    m.cur_layer = -1;
+    uint64_t row = (uint64_t)m.embd.g.nb * m.embd.g.q.block_bytes;
+    LLM_TRY(launch_rec(m, "embed", row * ntok,
+                       [&]() { return embed_launch(m.embd, m.tokens, m.state, m.x, ntok, m.stream); }));
+  }
+  if (s >= 1 && s <= nl) {
+    const Layer& L = m.layers[s - 1];
+    m.cur_layer = s - 1;
+    LLM_TRY(rec_k2(m, L, ntok));
+    LLM_TRY(rec_k3(m, L, ntok));
+    LLM_TRY(rec_k4(m, L, ntok));
+    LLM_TRY(rec_k5(m, L, ntok));
+  }
+  if (s < nl) {
+    m.cur_layer = s;
+    LLM_TRY(rec_k1(m, m.layers[s], ntok));
+  }
+  if (s == nl) return head ? rec_head(m, ntok - 1, ntok) : rec_adv(m, ntok);
+  return 0;
+}
+
 // One pass of ntok tokens at positions state[0] .. state[0]+ntok-1: the
 // embedding (embed_in; else the one token's row is xn, which the previous
 // head pass's sampling kernel wrote), the layers, and (head) the logits and
 // the sampled token of the last one, which goes to tokens[step + ntok], its
 // embedding row to xn; state advances by ntok.
 static int record_pass(Model& m, uint32_t ntok, bool head, bool embed_in) {
-  m.embed_in = embed_in || ntok != 1;
-  if (m.embed_in && !skipped(m, "embed")) {
-    m.cur_layer = -1;
-    uint64_t row = (uint64_t)m.embd.g.nb * m.embd.g.q.block_bytes;
-    LLM_TRY(launch_rec(m, "embed", row * ntok,
-                       [&]() { return embed_launch(m.embd, m.tokens, m.state, m.x, ntok, m.stream); }));
-  }
-  int nl = m.cfg.layers;
-  if (m.layers_limit != 0 && m.layers_limit < nl) {
-    nl = std::max(m.layers_limit, 0);
-    head = false;
-  }
-  for (int l = 0; l < nl; l++) {
-    const Layer& L = m.layers[l];
-    m.cur_layer = l;
-    LLM_TRY(rec_k1(m, L, ntok));
-    LLM_TRY(rec_k2(m, L, ntok));
-    LLM_TRY(rec_k3(m, L, ntok));
-    LLM_TRY(rec_k4(m, L, ntok));
-    LLM_TRY(rec_k5(m, L, ntok));
-  }
-  if (head) return rec_head(m, ntok - 1, ntok);
-  return rec_adv(m, ntok);
+  bool h = head;
+  const int nl = pass_layers(m, &h);
+  for (int s = 0; s <= nl; s++) LLM_TRY(record_segment(m, ntok, head, embed_in, s));
+  return 0;
+}
+
+// Swap lane k's buffers and stream into the model's fields (lane 0 is theirs).
+static void use_lane(Model& m, int k) {
+  if (m.lane == k) return;
+  Lane& a = m.alt;
+  std::swap(m.stream, a.stream);
+  std::swap(m.x, a.x);
+  std::swap(m.q, a.q);
+  std::swap(m.att, a.att);
+  std::swap(m.act, a.act);
+  std::swap(m.gbuf, a.gbuf);
+  std::swap(m.pv, a.pv);
+  std::swap(m.ml, a.ml);
+  std::swap(m.xprep, a.xprep);
+  std::swap(m.state, a.state);
+  m.lane = k;
 }
 
 // The attention of a pass of ntok tokens from position pos: one chunk while
@@ -693,13 +761,16 @@ static void attn_plan(Model& m, uint32_t pos, uint32_t ntok) {
   m.attn_split = true;
 }
 
-static uint64_t graph_key(uint32_t ntok, uint32_t rows, bool split, bool head, bool embed_in) {
-  return ((uint64_t)ntok << 32) | ((uint64_t)rows << 3) | (embed_in ? 4 : 0) | (split ? 2 : 0) | (head ? 1 : 0);
+// seg: -1 the whole pass, else one segment (of the lane whose buffers the
+// model holds)
+static uint64_t graph_key(const Model& m, uint32_t ntok, bool head, bool embed_in, int seg) {
+  return ((uint64_t)(seg + 1) << 48) | ((uint64_t)m.lane << 44) | ((uint64_t)ntok << 32) |
+         ((uint64_t)m.attn_rows << 3) | (embed_in ? 4 : 0) | (m.attn_split ? 2 : 0) | (head ? 1 : 0);
 }
 
-// Capture record_pass into a graph (once per key).
-static int graph_for(Model& m, uint32_t ntok, bool head, bool embed_in, hipGraphExec_t* out) {
-  uint64_t key = graph_key(ntok, m.attn_rows, m.attn_split, head, embed_in);
+// Capture record_pass (seg -1) or one segment into a graph (once per key).
+static int graph_for(Model& m, uint32_t ntok, bool head, bool embed_in, int seg, hipGraphExec_t* out) {
+  uint64_t key = graph_key(m, ntok, head, embed_in, seg);
   auto it = m.chunk_exec.find(key);
   if (it != m.chunk_exec.end()) {
     *out = it->second;
@@ -708,7 +779,7 @@ static int graph_for(Model& m, uint32_t ntok, bool head, bool embed_in, hipGraph
   hipGraph_t g = nullptr;
   m.dispatches = 0;
   LLM_HIP(hipStreamBeginCapture(m.stream, hipStreamCaptureModeThreadLocal));
-  int rc = record_pass(m, ntok, head, embed_in);
+  int rc = seg < 0 ? record_pass(m, ntok, head, embed_in) : record_segment(m, ntok, head, embed_in, seg);
   hipError_t e = hipStreamEndCapture(m.stream, &g);
   if (rc != 0) {
     if (g) (void)hipGraphDestroy(g);
@@ -726,16 +797,6 @@ static int graph_for(Model& m, uint32_t ntok, bool head, bool embed_in, hipGraph
 }
 
 // One pass of ntok tokens whose first position is pos (known on the host).
-// LLMHIP_EAGER=1: passes go to the stream as direct launches instead of graph
-// replays (same kernels, arguments and order), for tools that trace kernel
-// launches but not graph replays.
-static bool eager_passes() {
-  static const bool e = [] {
-    const char* v = getenv("LLMHIP_EAGER");
-    return v && *v && strcmp(v, "0") != 0;
-  }();
-  return e;
-}
 
 // embed_in false: a decode step, whose input row the previous pass's sampling
 // kernel wrote to xn.
@@ -750,10 +811,86 @@ static int launch_graph(Model& m, uint32_t pos, uint32_t ntok, bool head, bool e
     m.stats.dispatches += m.dispatches;
     return 0;
   }
-  LLM_TRY(graph_for(m, ntok, head, embed_in, &ex));
+  LLM_TRY(graph_for(m, ntok, head, embed_in, -1, &ex));
   LLM_HIP(hipGraphLaunch(ex, m.stream));
-  m.stats.dispatches += m.graph_nodes[graph_key(ntok, m.attn_rows, m.attn_split, head, embed_in)];
+  m.stats.dispatches += m.graph_nodes[graph_key(m, ntok, head, embed_in, -1)];
   return 0;
+}
+
+// Lanes of the prefill wavefront (LLMHIP_PREFILL_LANES=1: one, for
+// comparison).
+static int prefill_lanes() {
+  static const int n = [] {
+    const char* v = getenv("LLMHIP_PREFILL_LANES");
+    return v && *v == '1' ? 1 : 2;
+  }();
+  return n;
+}
+
+// A prompt of several chunks as a wavefront over two lanes: chunk c runs on
+// lane (C-1-c) % 2 (the last on lane 0, whose buffers Peek and decode use),
+// from its own position (set_state), as graph segments of one layer each
+// (record_segment); segment s of chunk c waits for segment s-1 of chunk c-1,
+// which appended the cache rows of layer s-1 that its attention reads (the
+// chunks before that ran earlier on either lane).  The two chunks of a pair
+// are enqueued segment by segment in turn, so that the second starts one
+// segment behind the first rather than after the host has enqueued all of
+// the first; chunk c's events are set c % 4, so that every wait names the
+// record of the chunk right before.  Two chunks' layers then run at once
+// where one chunk's kernels leave the GPU idle.
+static int prefill_wavefront(Model& m, uint32_t n) {
+  const uint32_t C = (n + m.pm - 1) / m.pm;
+  hipEvent_t start = m.seg_done[0].back();
+  LLM_HIP(hipEventRecord(start, m.stream));  // the prompt upload and state reset
+  LLM_HIP(hipStreamWaitEvent(m.alt.stream, start, 0));
+  int rc = 0;
+  auto chunk = [&](uint32_t c, uint32_t* a, uint32_t* ntok, bool* head) {
+    *a = c * m.pm;
+    const uint32_t b = std::min(*a + m.pm, n);
+    *ntok = b - *a;
+    *head = b == n;
+    use_lane(m, (int)((C - 1 - c) & 1));
+    attn_plan(m, *a, *ntok);
+    m.last_row = *ntok - 1;
+  };
+  for (uint32_t c0 = 0; c0 < C && rc == 0; c0 += 2) {
+    const uint32_t cn = std::min(C - c0, 2u);
+    bool h0 = true;
+    const int nl = pass_layers(m, &h0);
+    for (int s = 0; s <= nl && rc == 0; s++) {
+      for (uint32_t c = c0; c < c0 + cn && rc == 0; c++) {
+        uint32_t a, ntok;
+        bool head;
+        chunk(c, &a, &ntok, &head);
+        if (s == 0) {
+          rc = set_state_launch(m.state, a, m.stream);
+          m.stats.submits++;
+        }
+        if (rc == 0 && c > 0 && s >= 1 && hipStreamWaitEvent(m.stream, m.seg_done[(c - 1) & 3][s - 1], 0) != hipSuccess)
+          rc = set_error(LLMHIP_ERR_DEVICE, "llm: prefill: stream wait failed");
+        if (rc == 0 && eager_passes()) {
+          m.dispatches = 0;
+          rc = record_segment(m, ntok, head, true, s);
+          m.stats.dispatches += m.dispatches;
+        } else if (rc == 0) {
+          hipGraphExec_t ex;
+          rc = graph_for(m, ntok, head, true, s, &ex);
+          if (rc == 0 && hipGraphLaunch(ex, m.stream) != hipSuccess)
+            rc = set_error(LLMHIP_ERR_DEVICE, "llm: prefill: graph launch failed");
+          if (rc == 0) m.stats.dispatches += m.graph_nodes[graph_key(m, ntok, head, true, s)];
+        }
+        if (rc == 0 && hipEventRecord(m.seg_done[c & 3][s], m.stream) != hipSuccess)
+          rc = set_error(LLMHIP_ERR_DEVICE, "llm: prefill: event record failed");
+      }
+    }
+  }
+  use_lane(m, 0);
+  // lane 0 goes on after lane 1's last work
+  hipEvent_t end = m.seg_done[1].back();
+  if (hipEventRecord(end, m.alt.stream) != hipSuccess || hipStreamWaitEvent(m.stream, end, 0) != hipSuccess)
+    rc = rc ? rc : set_error(LLMHIP_ERR_DEVICE, "llm: prefill: lane join failed");
+  m.last_row = (n - 1) % m.pm;
+  return rc;
 }
 
 }  // namespace llmhip
@@ -815,6 +952,23 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
       (rc = dalloc_n(*m, &m->cs, (uint64_t)m->ctx * c.head_dim)) || (rc = dalloc_n(*m, &m->h, E)) ||
       (rc = dalloc_n(*m, &m->xn, E)))
     return fail(rc);
+  {  // the second prefill lane
+    Lane& a = m->alt;
+    if (hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking) != hipSuccess)
+      return fail(set_error(LLMHIP_ERR_DEVICE, "llm: hipStreamCreate failed"));
+    if ((rc = dalloc_n(*m, &a.x, pm * E)) || (rc = dalloc_n(*m, &a.q, pm * E)) || (rc = dalloc_n(*m, &a.att, pm * E)) ||
+        (rc = dalloc_n(*m, &a.act, pm * F)) || (rc = dalloc_n(*m, &a.gbuf, pm * F)) ||
+        (rc = dalloc_n(*m, &a.pv, pm * H * m->smax * c.head_dim)) || (rc = dalloc_n(*m, &a.ml, pm * H * m->smax * 2)) ||
+        (rc = dalloc(*m, &a.xprep, xprep_bytes(m->pm, (uint32_t)std::max(c.embd, c.ff)))) ||
+        (rc = dalloc_n(*m, &a.state, 2)))
+      return fail(rc);
+    for (auto& v : m->seg_done) {
+      v.resize((size_t)c.layers + 1);
+      for (hipEvent_t& e : v)
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess)
+          return fail(set_error(LLMHIP_ERR_DEVICE, "llm: hipEventCreate failed"));
+    }
+  }
   // RoPE table in double precision, gpu.go:524-534 (and cpu.go:374-375)
   std::vector<float> cs((size_t)m->ctx * c.head_dim);
   const int hp = c.head_dim / 2;
@@ -1000,10 +1154,14 @@ int llmhip_model_prefill(llmhip_model* h, const int32_t* ids, int n, float* logi
   memcpy(m.host, ids, (size_t)n * 4);
   LLM_HIP(hipMemcpyAsync(m.tokens, m.host, (size_t)n * 4, hipMemcpyHostToDevice, m.stream));
   bool full = m.layers_limit == 0 || m.layers_limit >= m.cfg.layers;
-  for (int a = 0; a < n; a += (int)m.pm) {
-    int b = std::min(a + (int)m.pm, n);
-    LLM_TRY(launch_graph(m, (uint32_t)a, (uint32_t)(b - a), b == n, true));
-    m.stats.submits++;
+  if ((uint32_t)n > m.pm && prefill_lanes() == 2) {
+    LLM_TRY(prefill_wavefront(m, (uint32_t)n));
+  } else {
+    for (int a = 0; a < n; a += (int)m.pm) {
+      int b = std::min(a + (int)m.pm, n);
+      LLM_TRY(launch_graph(m, (uint32_t)a, (uint32_t)(b - a), b == n, true));
+      m.stats.submits++;
+    }
   }
   m.pos = (uint32_t)n;
   m.prompted = full;
