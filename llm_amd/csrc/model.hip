@@ -686,12 +686,11 @@ static int pass_layers(const Model& m, bool* head) {
   return nl;
 }
 
-// Segment s (0 .. layers) of a pass: s = 0 the embedding and layer 0's K1;
+// Slot s (0 .. layers) of a pass: s = 0 the embedding and layer 0's K1;
 // then layer s-1's K2..K5 and layer s's K1; the last, the last layer's K2..K5
-// and the head (or the advance).  A segment ends with the K1 that appends its
+// and the head (or the advance).  A slot ends with the K1 that appends its
 // layer's cache rows, which is what a later chunk's attention waits for.
-static int record_segment(Model& m, uint32_t ntok, bool head, bool embed_in, int s) {
-  m.embed_in = embed_in || ntok != 1;
+static int record_slot(Model& m, uint32_t ntok, bool head, int s) {
   const int nl = pass_layers(m, &head);
   if (s == 0 && m.embed_in && !skipped(m, "embed")) {
     m.cur_layer = -1;
@@ -715,15 +714,30 @@ static int record_segment(Model& m, uint32_t ntok, bool head, bool embed_in, int
   return 0;
 }
 
+// Segments of G slots (layers) of a pass of nl layers, and segment g: slots
+// [g G, (g + 1) G).
+static int segments(int nl, int G) { return (nl + G) / G; }
+static int record_segment(Model& m, uint32_t ntok, bool head, bool embed_in, int g, int G) {
+  m.embed_in = embed_in || ntok != 1;
+  bool h = head;
+  const int nl = pass_layers(m, &h);
+  for (int s = g * G; s < std::min((g + 1) * G, nl + 1); s++) LLM_TRY(record_slot(m, ntok, head, s));
+  return 0;
+}
+// The segment of the previous chunk that segment g waits for: the one whose
+// slots append the rows of the latest layer whose attention g runs (-1: none).
+static int segment_dep(int g, int G) { return (g * G + G - 2) / G; }
+
 // One pass of ntok tokens at positions state[0] .. state[0]+ntok-1: the
 // embedding (embed_in; else the one token's row is xn, which the previous
 // head pass's sampling kernel wrote), the layers, and (head) the logits and
 // the sampled token of the last one, which goes to tokens[step + ntok], its
 // embedding row to xn; state advances by ntok.
 static int record_pass(Model& m, uint32_t ntok, bool head, bool embed_in) {
+  m.embed_in = embed_in || ntok != 1;
   bool h = head;
   const int nl = pass_layers(m, &h);
-  for (int s = 0; s <= nl; s++) LLM_TRY(record_segment(m, ntok, head, embed_in, s));
+  for (int s = 0; s <= nl; s++) LLM_TRY(record_slot(m, ntok, head, s));
   return 0;
 }
 
@@ -761,16 +775,16 @@ static void attn_plan(Model& m, uint32_t pos, uint32_t ntok) {
   m.attn_split = true;
 }
 
-// seg: -1 the whole pass, else one segment (of the lane whose buffers the
-// model holds)
-static uint64_t graph_key(const Model& m, uint32_t ntok, bool head, bool embed_in, int seg) {
-  return ((uint64_t)(seg + 1) << 48) | ((uint64_t)m.lane << 44) | ((uint64_t)ntok << 32) |
+// seg: -1 the whole pass, else segment seg of G layers (of the lane whose
+// buffers the model holds)
+static uint64_t graph_key(const Model& m, uint32_t ntok, bool head, bool embed_in, int seg, int G = 0) {
+  return ((uint64_t)(seg + 1) << 49) | ((uint64_t)G << 45) | ((uint64_t)m.lane << 44) | ((uint64_t)ntok << 32) |
          ((uint64_t)m.attn_rows << 3) | (embed_in ? 4 : 0) | (m.attn_split ? 2 : 0) | (head ? 1 : 0);
 }
 
 // Capture record_pass (seg -1) or one segment into a graph (once per key).
-static int graph_for(Model& m, uint32_t ntok, bool head, bool embed_in, int seg, hipGraphExec_t* out) {
-  uint64_t key = graph_key(m, ntok, head, embed_in, seg);
+static int graph_for(Model& m, uint32_t ntok, bool head, bool embed_in, int seg, int G, hipGraphExec_t* out) {
+  uint64_t key = graph_key(m, ntok, head, embed_in, seg, G);
   auto it = m.chunk_exec.find(key);
   if (it != m.chunk_exec.end()) {
     *out = it->second;
@@ -779,7 +793,7 @@ static int graph_for(Model& m, uint32_t ntok, bool head, bool embed_in, int seg,
   hipGraph_t g = nullptr;
   m.dispatches = 0;
   LLM_HIP(hipStreamBeginCapture(m.stream, hipStreamCaptureModeThreadLocal));
-  int rc = seg < 0 ? record_pass(m, ntok, head, embed_in) : record_segment(m, ntok, head, embed_in, seg);
+  int rc = seg < 0 ? record_pass(m, ntok, head, embed_in) : record_segment(m, ntok, head, embed_in, seg, G);
   hipError_t e = hipStreamEndCapture(m.stream, &g);
   if (rc != 0) {
     if (g) (void)hipGraphDestroy(g);
@@ -811,9 +825,9 @@ static int launch_graph(Model& m, uint32_t pos, uint32_t ntok, bool head, bool e
     m.stats.dispatches += m.dispatches;
     return 0;
   }
-  LLM_TRY(graph_for(m, ntok, head, embed_in, -1, &ex));
+  LLM_TRY(graph_for(m, ntok, head, embed_in, -1, 0, &ex));
   LLM_HIP(hipGraphLaunch(ex, m.stream));
-  m.stats.dispatches += m.graph_nodes[graph_key(m, ntok, head, embed_in, -1)];
+  m.stats.dispatches += m.graph_nodes[graph_key(m, ntok, head, embed_in, -1, 0)];
   return 0;
 }
 
@@ -829,10 +843,10 @@ static int prefill_lanes() {
 
 // A prompt of several chunks as a wavefront over two lanes: chunk c runs on
 // lane (C-1-c) % 2 (the last on lane 0, whose buffers Peek and decode use),
-// from its own position (set_state), as graph segments of one layer each
-// (record_segment); segment s of chunk c waits for segment s-1 of chunk c-1,
-// which appended the cache rows of layer s-1 that its attention reads (the
-// chunks before that ran earlier on either lane).  The two chunks of a pair
+// from its own position (set_state), as graph segments of G layers
+// (record_segment); segment g of chunk c waits for the segment of chunk c-1
+// that appended the cache rows of the latest layer whose attention g runs
+// (segment_dep; the chunks before c-1 ran earlier on either lane).  The two chunks of a pair
 // are enqueued segment by segment in turn, so that the second starts one
 // segment behind the first rather than after the host has enqueued all of
 // the first; chunk c's events are set c % 4, so that every wait names the
@@ -853,11 +867,15 @@ static int prefill_wavefront(Model& m, uint32_t n) {
     attn_plan(m, *a, *ntok);
     m.last_row = *ntok - 1;
   };
+  // segments of three layers for a two-chunk prompt, where the second chunk's
+  // lag of one segment weighs most; six for longer ones, where fewer graph
+  // launches weigh more (measured: configs 3 and 4 at one to eight layers)
+  const int G = C <= 2 ? 3 : 6;
   for (uint32_t c0 = 0; c0 < C && rc == 0; c0 += 2) {
     const uint32_t cn = std::min(C - c0, 2u);
     bool h0 = true;
-    const int nl = pass_layers(m, &h0);
-    for (int s = 0; s <= nl && rc == 0; s++) {
+    const int ns = segments(pass_layers(m, &h0), G);
+    for (int s = 0; s < ns && rc == 0; s++) {
       for (uint32_t c = c0; c < c0 + cn && rc == 0; c++) {
         uint32_t a, ntok;
         bool head;
@@ -866,18 +884,19 @@ static int prefill_wavefront(Model& m, uint32_t n) {
           rc = set_state_launch(m.state, a, m.stream);
           m.stats.submits++;
         }
-        if (rc == 0 && c > 0 && s >= 1 && hipStreamWaitEvent(m.stream, m.seg_done[(c - 1) & 3][s - 1], 0) != hipSuccess)
+        const int dep = segment_dep(s, G);
+        if (rc == 0 && c > 0 && dep >= 0 && hipStreamWaitEvent(m.stream, m.seg_done[(c - 1) & 3][dep], 0) != hipSuccess)
           rc = set_error(LLMHIP_ERR_DEVICE, "llm: prefill: stream wait failed");
         if (rc == 0 && eager_passes()) {
           m.dispatches = 0;
-          rc = record_segment(m, ntok, head, true, s);
+          rc = record_segment(m, ntok, head, true, s, G);
           m.stats.dispatches += m.dispatches;
         } else if (rc == 0) {
           hipGraphExec_t ex;
-          rc = graph_for(m, ntok, head, true, s, &ex);
+          rc = graph_for(m, ntok, head, true, s, G, &ex);
           if (rc == 0 && hipGraphLaunch(ex, m.stream) != hipSuccess)
             rc = set_error(LLMHIP_ERR_DEVICE, "llm: prefill: graph launch failed");
-          if (rc == 0) m.stats.dispatches += m.graph_nodes[graph_key(m, ntok, head, true, s)];
+          if (rc == 0) m.stats.dispatches += m.graph_nodes[graph_key(m, ntok, head, true, s, G)];
         }
         if (rc == 0 && hipEventRecord(m.seg_done[c & 3][s], m.stream) != hipSuccess)
           rc = set_error(LLMHIP_ERR_DEVICE, "llm: prefill: event record failed");
