@@ -22,6 +22,7 @@ import csv
 import hashlib
 import json
 import os
+import re
 import statistics
 import subprocess
 import sys
@@ -221,20 +222,26 @@ def summarize(out):
            f"{live['decode_step']['kernel_us']} us of {live['decode_step']['wall_us']} us per token; traced run: "
            f"decode {traced['value']} tok/s.", "",
            "Prefill kernels of the traced run (64-token chunks of configs 3 and 4; grid = threads x workgroups "
-           "along y), by total time:", "", "| symbol | grid | launches | median us | mean |", "|---|---|---|---|---|"]
+           "along y), by total time. Prompts of two or more chunks run as a two-lane wavefront, two chunks' kernels "
+           "at once, so a duration here includes the other lane's load:", "",
+           "| symbol | grid | launches | median us | mean |", "|---|---|---|---|---|"]
     for (n, gx, gy), v in sorted(by.items(), key=lambda kv: -sum(kv[1])):
-        if any(k in n for k in ("gemm", "prep", "attn_mma")) or (n.startswith("attn_kernel") and "true>" in n):
+        if any(k in n for k in ("gemm", "prep", "attn_mma", "attn_multi")) or (n.startswith("attn_kernel") and "true>" in n):
             st = stats(v)
             md.append(f"| `{n}` | {gx // gy}x{gy} | {st['n']} | {st['median']:.2f} | {st['mean']:.2f} |")
     lc = live.get("long_context")
     if lc:
+        k3e, k3 = lc["classes_at_end"]["k3"]["avg_us"], live["decode_step"]["classes"]["k3"]["avg_us"]
         md += ["", f"Config 4 (2048-token prompt, 512 tokens, ctx 4096), live: prefill {lc['prefill_tok_s']} tok/s, "
-               f"decode {lc['decode_tok_s']} tok/s; at the last position the attention (split kernel + merge) "
+               f"decode {lc['decode_tok_s']} tok/s; at the last position the split attention kernel "
                f"{lc['attention_at_end']['avg_us']} us for {lc['attention_at_end']['kv_bytes']} KV bytes "
-               f"({lc['attention_at_end']['gbps']} GB/s). Traced decode attention kernels of the run:", "",
+               f"({lc['attention_at_end']['gbps']} GB/s); its chunks are merged in the output projection's prologue, "
+               f"K3 {k3e} us there against {k3} us at config 3. Traced decode attention kernels and the merging "
+               "K3 (prologue argument 4 + 8 (chunks / 2 - 1)) of the run:", "",
                "| symbol | grid | launches | median us | mean |", "|---|---|---|---|---|"]
         for (n, gx, gy), v in sorted(by.items(), key=lambda kv: -sum(kv[1])):
-            if n.startswith("attn_kernel") and "true, false, false" in n or n.startswith("attn_merge_kernel<64u, false"):
+            mk3 = re.match(r"gemv_kernel<\w+, 1, (\d+), 1, 2>", n)
+            if (n.startswith("attn_kernel") and "true, false, false" in n) or (mk3 and int(mk3.group(1)) >= 4):
                 st = stats(v)
                 md.append(f"| `{n}` | {gx // gy}x{gy} | {st['n']} | {st['median']:.2f} | {st['mean']:.2f} |")
     write(os.path.join(PROFILES, "decode_kernels_qwen25.md"), md)
