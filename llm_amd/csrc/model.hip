@@ -80,7 +80,8 @@ struct ProfRec {
 
 // What one lane of a prefill wavefront owns: its stream, its activation and
 // staging buffers, and its device-side position (the KV cache is shared:
-// chunks write disjoint rows).  The model's own fields are lane 0.
+// chunks write disjoint rows).  Lane 0 is the model's own fields.
+constexpr int LANES = 3;
 struct Lane {
   hipStream_t stream = nullptr;
   float *x = nullptr, *q = nullptr, *att = nullptr, *act = nullptr, *gbuf = nullptr, *pv = nullptr, *ml = nullptr;
@@ -136,12 +137,14 @@ struct Model {
   uint32_t dispatches = 0;  // counter while recording
   std::vector<ProfRec>* prof = nullptr;  // eager profiling: events around every launch
   int cur_layer = -1;
-  // the prefill wavefront's second lane, swapped into the fields above while
-  // its work is recorded (use_lane); an event per segment of chunk c in set
-  // c % 4 (prefill_wavefront)
-  Lane alt;
+  // the prefill wavefront's lanes (lane 0: the fields above), whose buffers
+  // use_lane puts into those fields while their work is recorded; an event per
+  // segment of chunk c in set c % (LANES + 1), and per lane its start and end
+  // (prefill_wavefront)
+  Lane lanes[LANES];
   int lane = 0;
-  std::vector<hipEvent_t> seg_done[4];
+  std::vector<hipEvent_t> seg_done[LANES + 1];
+  hipEvent_t lane_ev[LANES] = {};
 };
 
 // Brackets one launch with HIP events on the model's stream when profiling.
@@ -245,11 +248,15 @@ static void model_destroy(Model* m) {
   if (!m) return;
   (void)hipSetDevice(m->device);
   if (m->stream) (void)hipStreamSynchronize(m->stream);
-  if (m->alt.stream) (void)hipStreamSynchronize(m->alt.stream);
+  for (int k = 1; k < LANES; k++)
+    if (m->lanes[k].stream) (void)hipStreamSynchronize(m->lanes[k].stream);
   destroy_graphs(*m);
   for (auto& v : m->seg_done)
     for (hipEvent_t e : v) (void)hipEventDestroy(e);
-  if (m->alt.stream) (void)hipStreamDestroy(m->alt.stream);
+  for (hipEvent_t e : m->lane_ev)
+    if (e) (void)hipEventDestroy(e);
+  for (int k = 1; k < LANES; k++)
+    if (m->lanes[k].stream) (void)hipStreamDestroy(m->lanes[k].stream);
   stager_free(&m->st);
   qmat_release(&m->embd);
   qmat_release(&m->out);
@@ -741,20 +748,20 @@ static int record_pass(Model& m, uint32_t ntok, bool head, bool embed_in) {
   return 0;
 }
 
-// Swap lane k's buffers and stream into the model's fields (lane 0 is theirs).
+// Put lane k's buffers and stream into the model's fields.
 static void use_lane(Model& m, int k) {
   if (m.lane == k) return;
-  Lane& a = m.alt;
-  std::swap(m.stream, a.stream);
-  std::swap(m.x, a.x);
-  std::swap(m.q, a.q);
-  std::swap(m.att, a.att);
-  std::swap(m.act, a.act);
-  std::swap(m.gbuf, a.gbuf);
-  std::swap(m.pv, a.pv);
-  std::swap(m.ml, a.ml);
-  std::swap(m.xprep, a.xprep);
-  std::swap(m.state, a.state);
+  const Lane& a = m.lanes[k];
+  m.stream = a.stream;
+  m.x = a.x;
+  m.q = a.q;
+  m.att = a.att;
+  m.act = a.act;
+  m.gbuf = a.gbuf;
+  m.pv = a.pv;
+  m.ml = a.ml;
+  m.xprep = a.xprep;
+  m.state = a.state;
   m.lane = k;
 }
 
@@ -778,7 +785,7 @@ static void attn_plan(Model& m, uint32_t pos, uint32_t ntok) {
 // seg: -1 the whole pass, else segment seg of G layers (of the lane whose
 // buffers the model holds)
 static uint64_t graph_key(const Model& m, uint32_t ntok, bool head, bool embed_in, int seg, int G = 0) {
-  return ((uint64_t)(seg + 1) << 49) | ((uint64_t)G << 45) | ((uint64_t)m.lane << 44) | ((uint64_t)ntok << 32) |
+  return ((uint64_t)(seg + 1) << 50) | ((uint64_t)G << 46) | ((uint64_t)m.lane << 44) | ((uint64_t)ntok << 32) |
          ((uint64_t)m.attn_rows << 3) | (embed_in ? 4 : 0) | (m.attn_split ? 2 : 0) | (head ? 1 : 0);
 }
 
@@ -831,48 +838,56 @@ static int launch_graph(Model& m, uint32_t pos, uint32_t ntok, bool head, bool e
   return 0;
 }
 
-// Lanes of the prefill wavefront (LLMHIP_PREFILL_LANES=1: one, for
-// comparison).
+// Lanes of the prefill wavefront, at most (LLMHIP_PREFILL_LANES=1 or 2: that
+// many, for comparison).
 static int prefill_lanes() {
   static const int n = [] {
     const char* v = getenv("LLMHIP_PREFILL_LANES");
-    return v && *v == '1' ? 1 : 2;
+    return v && (*v == '1' || *v == '2') ? *v - '0' : LANES;
   }();
   return n;
 }
 
-// A prompt of several chunks as a wavefront over two lanes: chunk c runs on
-// lane (C-1-c) % 2 (the last on lane 0, whose buffers Peek and decode use),
+// A prompt of several chunks as a wavefront over L lanes (two for two
+// chunks, three for more: measured, two and three whole prefills run at once
+// reach 1.55x and 1.84x the throughput of one, four 1.58x): chunk c runs on
+// lane (C-1-c) % L (the last on lane 0, whose buffers Peek and decode use),
 // from its own position (set_state), as graph segments of G layers
 // (record_segment); segment g of chunk c waits for the segment of chunk c-1
 // that appended the cache rows of the latest layer whose attention g runs
-// (segment_dep; the chunks before c-1 ran earlier on either lane).  The two chunks of a pair
-// are enqueued segment by segment in turn, so that the second starts one
-// segment behind the first rather than after the host has enqueued all of
-// the first; chunk c's events are set c % 4, so that every wait names the
-// record of the chunk right before.  Two chunks' layers then run at once
-// where one chunk's kernels leave the GPU idle.
+// (segment_dep; the chunks before c-1 ran earlier on its lane or were waited
+// for by c-1).  The chunks of a group of L are enqueued segment by segment in
+// turn, so that each starts one segment behind the one before rather than
+// after the host has enqueued all of it; chunk c's events are set
+// c % (LANES + 1), so that every wait names the record of the chunk right
+// before.  Several chunks' layers then run at once where one chunk's kernels
+// leave the GPU idle.
 static int prefill_wavefront(Model& m, uint32_t n) {
   const uint32_t C = (n + m.pm - 1) / m.pm;
-  hipEvent_t start = m.seg_done[0].back();
-  LLM_HIP(hipEventRecord(start, m.stream));  // the prompt upload and state reset
-  LLM_HIP(hipStreamWaitEvent(m.alt.stream, start, 0));
+  const uint32_t L = std::min<uint32_t>(std::min<uint32_t>(C, 3), (uint32_t)prefill_lanes());
+  constexpr uint32_t S = LANES + 1;
+  LLM_HIP(hipEventRecord(m.lane_ev[0], m.lanes[0].stream));  // the prompt upload and state reset
+  for (uint32_t k = 1; k < L; k++) LLM_HIP(hipStreamWaitEvent(m.lanes[k].stream, m.lane_ev[0], 0));
   int rc = 0;
   auto chunk = [&](uint32_t c, uint32_t* a, uint32_t* ntok, bool* head) {
     *a = c * m.pm;
     const uint32_t b = std::min(*a + m.pm, n);
     *ntok = b - *a;
     *head = b == n;
-    use_lane(m, (int)((C - 1 - c) & 1));
+    use_lane(m, (int)((C - 1 - c) % L));
     attn_plan(m, *a, *ntok);
     m.last_row = *ntok - 1;
   };
   // segments of three layers for a two-chunk prompt, where the second chunk's
   // lag of one segment weighs most; six for longer ones, where fewer graph
-  // launches weigh more (measured: configs 3 and 4 at one to eight layers)
+  // launches weigh more (measured: configs 3 and 4 at one to eight layers).
+  // With three lanes chunk c-2 runs on another stream: its rows are ready for
+  // chunk c because c-1 waited for the same segment of it, which holds them
+  // only when a segment has two or more layers (segment_dep(g) = g).
   const int G = C <= 2 ? 3 : 6;
-  for (uint32_t c0 = 0; c0 < C && rc == 0; c0 += 2) {
-    const uint32_t cn = std::min(C - c0, 2u);
+  static_assert(LANES <= 3, "the event sets and the G >= 2 argument are for at most three lanes");
+  for (uint32_t c0 = 0; c0 < C && rc == 0; c0 += L) {
+    const uint32_t cn = std::min(C - c0, L);
     bool h0 = true;
     const int ns = segments(pass_layers(m, &h0), G);
     for (int s = 0; s < ns && rc == 0; s++) {
@@ -885,7 +900,7 @@ static int prefill_wavefront(Model& m, uint32_t n) {
           m.stats.submits++;
         }
         const int dep = segment_dep(s, G);
-        if (rc == 0 && c > 0 && dep >= 0 && hipStreamWaitEvent(m.stream, m.seg_done[(c - 1) & 3][dep], 0) != hipSuccess)
+        if (rc == 0 && c > 0 && dep >= 0 && hipStreamWaitEvent(m.stream, m.seg_done[(c - 1) % S][dep], 0) != hipSuccess)
           rc = set_error(LLMHIP_ERR_DEVICE, "llm: prefill: stream wait failed");
         if (rc == 0 && eager_passes()) {
           m.dispatches = 0;
@@ -898,16 +913,17 @@ static int prefill_wavefront(Model& m, uint32_t n) {
             rc = set_error(LLMHIP_ERR_DEVICE, "llm: prefill: graph launch failed");
           if (rc == 0) m.stats.dispatches += m.graph_nodes[graph_key(m, ntok, head, true, s, G)];
         }
-        if (rc == 0 && hipEventRecord(m.seg_done[c & 3][s], m.stream) != hipSuccess)
+        if (rc == 0 && hipEventRecord(m.seg_done[c % S][s], m.stream) != hipSuccess)
           rc = set_error(LLMHIP_ERR_DEVICE, "llm: prefill: event record failed");
       }
     }
   }
   use_lane(m, 0);
-  // lane 0 goes on after lane 1's last work
-  hipEvent_t end = m.seg_done[1].back();
-  if (hipEventRecord(end, m.alt.stream) != hipSuccess || hipStreamWaitEvent(m.stream, end, 0) != hipSuccess)
-    rc = rc ? rc : set_error(LLMHIP_ERR_DEVICE, "llm: prefill: lane join failed");
+  // lane 0 goes on after the other lanes' last work
+  for (uint32_t k = 1; k < L; k++)
+    if (hipEventRecord(m.lane_ev[k], m.lanes[k].stream) != hipSuccess ||
+        hipStreamWaitEvent(m.stream, m.lane_ev[k], 0) != hipSuccess)
+      rc = rc ? rc : set_error(LLMHIP_ERR_DEVICE, "llm: prefill: lane join failed");
   m.last_row = (n - 1) % m.pm;
   return rc;
 }
@@ -971,16 +987,23 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
       (rc = dalloc_n(*m, &m->cs, (uint64_t)m->ctx * c.head_dim)) || (rc = dalloc_n(*m, &m->h, E)) ||
       (rc = dalloc_n(*m, &m->xn, E)))
     return fail(rc);
-  {  // the second prefill lane
-    Lane& a = m->alt;
-    if (hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking) != hipSuccess)
-      return fail(set_error(LLMHIP_ERR_DEVICE, "llm: hipStreamCreate failed"));
-    if ((rc = dalloc_n(*m, &a.x, pm * E)) || (rc = dalloc_n(*m, &a.q, pm * E)) || (rc = dalloc_n(*m, &a.att, pm * E)) ||
-        (rc = dalloc_n(*m, &a.act, pm * F)) || (rc = dalloc_n(*m, &a.gbuf, pm * F)) ||
-        (rc = dalloc_n(*m, &a.pv, pm * H * m->smax * c.head_dim)) || (rc = dalloc_n(*m, &a.ml, pm * H * m->smax * 2)) ||
-        (rc = dalloc(*m, &a.xprep, xprep_bytes(m->pm, (uint32_t)std::max(c.embd, c.ff)))) ||
-        (rc = dalloc_n(*m, &a.state, 2)))
-      return fail(rc);
+  {  // the prefill lanes: lane 0 is the model's own buffers
+    m->lanes[0] = Lane{m->stream, m->x, m->q, m->att, m->act, m->gbuf, m->pv, m->ml, m->xprep, m->state};
+    for (int k = 1; k < LANES; k++) {
+      Lane& a = m->lanes[k];
+      if (hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking) != hipSuccess)
+        return fail(set_error(LLMHIP_ERR_DEVICE, "llm: hipStreamCreate failed"));
+      if ((rc = dalloc_n(*m, &a.x, pm * E)) || (rc = dalloc_n(*m, &a.q, pm * E)) ||
+          (rc = dalloc_n(*m, &a.att, pm * E)) || (rc = dalloc_n(*m, &a.act, pm * F)) ||
+          (rc = dalloc_n(*m, &a.gbuf, pm * F)) || (rc = dalloc_n(*m, &a.pv, pm * H * m->smax * c.head_dim)) ||
+          (rc = dalloc_n(*m, &a.ml, pm * H * m->smax * 2)) ||
+          (rc = dalloc(*m, &a.xprep, xprep_bytes(m->pm, (uint32_t)std::max(c.embd, c.ff)))) ||
+          (rc = dalloc_n(*m, &a.state, 2)))
+        return fail(rc);
+    }
+    for (hipEvent_t& e : m->lane_ev)
+      if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess)
+        return fail(set_error(LLMHIP_ERR_DEVICE, "llm: hipEventCreate failed"));
     for (auto& v : m->seg_done) {
       v.resize((size_t)c.layers + 1);
       for (hipEvent_t& e : v)
@@ -1173,7 +1196,7 @@ int llmhip_model_prefill(llmhip_model* h, const int32_t* ids, int n, float* logi
   memcpy(m.host, ids, (size_t)n * 4);
   LLM_HIP(hipMemcpyAsync(m.tokens, m.host, (size_t)n * 4, hipMemcpyHostToDevice, m.stream));
   bool full = m.layers_limit == 0 || m.layers_limit >= m.cfg.layers;
-  if ((uint32_t)n > m.pm && prefill_lanes() == 2) {
+  if ((uint32_t)n > m.pm && prefill_lanes() > 1) {
     LLM_TRY(prefill_wavefront(m, (uint32_t)n));
   } else {
     for (int a = 0; a < n; a += (int)m.pm) {
