@@ -782,8 +782,8 @@ static void attn_plan(Model& m, uint32_t pos, uint32_t ntok) {
   m.attn_split = true;
 }
 
-// seg: -1 the whole pass, else segment seg of G layers (of the lane whose
-// buffers the model holds)
+// seg: -1 the whole pass (G > 1: G passes of one token, a decode submit),
+// else segment seg of G layers (of the lane whose buffers the model holds)
 static uint64_t graph_key(const Model& m, uint32_t ntok, bool head, bool embed_in, int seg, int G = 0) {
   return ((uint64_t)(seg + 1) << 50) | ((uint64_t)G << 46) | ((uint64_t)m.lane << 44) | ((uint64_t)ntok << 32) |
          ((uint64_t)m.attn_rows << 3) | (embed_in ? 4 : 0) | (m.attn_split ? 2 : 0) | (head ? 1 : 0);
@@ -800,7 +800,9 @@ static int graph_for(Model& m, uint32_t ntok, bool head, bool embed_in, int seg,
   hipGraph_t g = nullptr;
   m.dispatches = 0;
   LLM_HIP(hipStreamBeginCapture(m.stream, hipStreamCaptureModeThreadLocal));
-  int rc = seg < 0 ? record_pass(m, ntok, head, embed_in) : record_segment(m, ntok, head, embed_in, seg, G);
+  int rc = 0;
+  if (seg >= 0) rc = record_segment(m, ntok, head, embed_in, seg, G);
+  for (int i = 0; seg < 0 && i < std::max(G, 1) && rc == 0; i++) rc = record_pass(m, ntok, head, embed_in);
   hipError_t e = hipStreamEndCapture(m.stream, &g);
   if (rc != 0) {
     if (g) (void)hipGraphDestroy(g);
@@ -835,6 +837,26 @@ static int launch_graph(Model& m, uint32_t pos, uint32_t ntok, bool head, bool e
   LLM_TRY(graph_for(m, ntok, head, embed_in, -1, 0, &ex));
   LLM_HIP(hipGraphLaunch(ex, m.stream));
   m.stats.dispatches += m.graph_nodes[graph_key(m, ntok, head, embed_in, -1, 0)];
+  return 0;
+}
+
+// cnt one-token decode passes from position pos as one graph (a submit, at
+// most 15 passes): its attention variant is the last position's, and the
+// earlier tokens stop at their own causal bound (the kernels read the
+// position from the device).
+static int launch_decode(Model& m, uint32_t pos, uint32_t cnt) {
+  attn_plan(m, pos + cnt - 1, 1);
+  m.last_row = 0;
+  if (eager_passes()) {
+    m.dispatches = 0;
+    for (uint32_t i = 0; i < cnt; i++) LLM_TRY(record_pass(m, 1, true, false));
+    m.stats.dispatches += m.dispatches;
+    return 0;
+  }
+  hipGraphExec_t ex;
+  LLM_TRY(graph_for(m, 1, true, false, -1, (int)cnt, &ex));
+  LLM_HIP(hipGraphLaunch(ex, m.stream));
+  m.stats.dispatches += m.graph_nodes[graph_key(m, 1, true, false, -1, (int)cnt)];
   return 0;
 }
 
@@ -1225,7 +1247,7 @@ int llmhip_model_decode(llmhip_model* h, int cnt, int32_t* out) {
                      m.pos);
   LLM_HIP(hipSetDevice(m.device));
   uint32_t first = m.pos;
-  for (int j = 0; j < cnt; j++) LLM_TRY(launch_graph(m, first + (uint32_t)j, 1, true, false));
+  for (int j = 0; j < cnt; j += 8) LLM_TRY(launch_decode(m, first + (uint32_t)j, (uint32_t)std::min(cnt - j, 8)));
   LLM_HIP(hipMemcpyAsync(m.host, m.tokens + first + 1, (size_t)cnt * 4, hipMemcpyDeviceToHost, m.stream));
   LLM_HIP(hipStreamSynchronize(m.stream));
   memcpy(out, m.host, (size_t)cnt * 4);
