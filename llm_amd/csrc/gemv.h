@@ -35,6 +35,10 @@ enum Prologue : int {
                   // split attention's chunk partials (mpv, mml) as attn_merge_kernel merges them;
                   // the bits from PRO_MERGE_SHIFT up hold how many chunks (merge_pro)
 };
+// Flag (one token, with PRO_RMS): the input row is x + xpart[0] + xpart[xpartstride]
+// (the residual and the two k-halves of the previous down projection, added in
+// that order; kparts), and workgroup 0 stores that sum to xout.
+constexpr int PRO_XSUM = 64;
 // Chunks of partials the merging prologue combines: all of them loaded at
 // once, an even count from 2 to MERGE_MAX_CHUNKS chosen per pass (the chunks
 // its attention rows can have), so that no load waits for the position.
@@ -89,6 +93,13 @@ struct GemvArgs {
   const float* aux;  // EPI_SWIGLU: the gate values
   float* up;         // EPI_GATEUP / EPI_SWIGLU: the up product u = W_up h also stored here, [t*ff + i]
                      // (nullptr: not kept); Peek("up")
+  // one token, EPI_STORE: kparts (1 or 2) workgroups per tile group, part p summing block groups
+  // [p ng / kparts, (p + 1) ng / kparts) (the tail with the last) into y + p * pstride
+  uint32_t kparts, pstride;
+  // PRO_XSUM: the partial rows added to x, and where workgroup 0 stores the sum
+  const float* xpart;
+  uint32_t xpartstride;
+  float* xout;
   // PRO_MERGE: the split attention's partials ([heads][msmax][hd] sums of e*v, [heads][msmax][2]
   // max and sum of e) over chunks of mrows positions; the merged row also goes to matt (tile 0)
   const float* mpv;

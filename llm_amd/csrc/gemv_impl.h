@@ -399,7 +399,7 @@ __device__ __forceinline__ EpiIn epi_load(const GemvArgs& a, uint32_t tile, int 
 template <int EPI>
 __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, int r, bool active, uint32_t tokA,
                                              bool okA, float vA, uint32_t tokB, bool okB, float vB,
-                                             const EpiIn* pre = nullptr) {
+                                             const EpiIn* pre = nullptr, float* yo = nullptr) {
   const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
   const bool rvalid = active && lr < a.rows;
   const EpiIn e = pre ? *pre : epi_load<EPI>(a, tile, r, active, tokA, okA, tokB, okB);
@@ -421,9 +421,10 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
     }
   }
   if (EPI == EPI_STORE || EPI == EPI_ACC || EPI == EPI_ARGMAX) {
+    float* Y = yo ? yo : a.y;  // yo: a k-part's own output row
     if (rvalid) {
-      if (okA) a.y[(uint64_t)tokA * a.ldy + lr] = EPI == EPI_ACC ? e.yA + vA : vA;
-      if (okB) a.y[(uint64_t)tokB * a.ldy + lr] = EPI == EPI_ACC ? e.yB + vB : vB;
+      if (okA) Y[(uint64_t)tokA * a.ldy + lr] = EPI == EPI_ACC ? e.yA + vA : vA;
+      if (okB) Y[(uint64_t)tokB * a.ldy + lr] = EPI == EPI_ACC ? e.yB + vB : vB;
     }
   }
   if (EPI == EPI_QKV) {
@@ -1489,10 +1490,19 @@ __device__ __forceinline__ void load_items(ItemsOf<NT, PRO>& it, const GemvArgs&
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     const float* xr = a.x + (uint64_t)(a.xrow0 + t0 + min(t, nt - 1)) * a.ldx + e0;
-    const f4 A = *(const f4*)xr;
+    f4 A = *(const f4*)xr;
+    if constexpr ((PRO & PRO_XSUM) != 0) {  // one token: (x + p0) + p1
+      static_assert(NT == 1, "PRO_XSUM: one token");
+      const f4 P0 = *(const f4*)(a.xpart + e0), P1 = *(const f4*)(a.xpart + a.xpartstride + e0);
+      A = (A + P0) + P1;
+    }
     it.xa[t] = ok && t < nt ? A : z;
     if (NU == 4) {
-      const f4 C = *(const f4*)(xr + 16);
+      f4 C = *(const f4*)(xr + 16);
+      if constexpr ((PRO & PRO_XSUM) != 0) {
+        const f4 P0 = *(const f4*)(a.xpart + e0 + 16), P1 = *(const f4*)(a.xpart + a.xpartstride + e0 + 16);
+        C = (C + P0) + P1;
+      }
       it.xc[t] = ok && t < nt ? C : z;
     }
   }
@@ -1730,17 +1740,23 @@ __global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(Ge
   float* misc = part + nwv * 64 * 2;  // [0, 64): RMS partials; [80, 112): argmax partials
 
   const uint32_t split = a.split, tpw = nwv / split;
-  const uint32_t lt = wave / split, sp = wave % split;
-  const uint32_t tile = min(blockIdx.x * tpw + lt, a.tiles - 1);
-  const bool has_tile = blockIdx.x * tpw + lt < a.tiles;
-  const bool keep = blockIdx.x * tpw + lt == 0;  // PRO_MERGE: tile 0's waves also store the merged row
+  const uint32_t lt = wave / split;
+  // k in parts (one token): workgroup x = (tile group) * kparts + part; part p
+  // runs block groups [g0, g1), the last one the tail too, into its own row
+  const uint32_t kp = a.kparts > 1 ? a.kparts : 1, kpart = blockIdx.x % kp, bx = blockIdx.x / kp;
+  const uint32_t g0 = kpart * ng / kp, g1 = (kpart + 1) * ng / kp;
+  const uint32_t tile = min(bx * tpw + lt, a.tiles - 1);
+  const bool has_tile = bx * tpw + lt < a.tiles;
+  const bool keep = bx * tpw + lt == 0;  // PRO_MERGE: tile 0's waves also store the merged row
   const int r = lane & 15, q = lane >> 4, slot = lane & 15;
-  // this wave's units: groups sp, sp + split, ... below ng, then the tail (wave ng % split)
-  const uint32_t cnt = has_tile && ng > sp ? (ng - sp + split - 1) / split : 0;
-  const bool has_tail = has_tile && a.tail && (ng % split) == sp;
+  // this wave's units: groups sp = g0 + sw, sp + split, ... below g1, then the
+  // tail (the last part's wave (g1 - g0) % split)
+  const uint32_t sw = wave % split, sp = g0 + sw, gn = g1 - g0;
+  const uint32_t cnt = has_tile && gn > sw ? (gn - sw + split - 1) / split : 0;
+  const bool has_tail = has_tile && a.tail && kpart == kp - 1 && (gn % split) == sw;
 
   // the epilogue's own inputs, in flight during the prologue
-  const bool active = sp == 0 && has_tile;
+  const bool active = sw == 0 && has_tile;
   const int tA = 2 * q, tB = 2 * q + 1;
   const bool okA = tA < nt, okB = NT > 1 && tB < nt;
   const EpiIn pre = epi_load<EPI>(a, tile, r, active, t0 + tA, okA, t0 + tB, okB);
@@ -1757,6 +1773,8 @@ __global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(Ge
       for (int v = 0; v < RV; v++) {
         const uint32_t c = min(wave * 64 + lane + 64 * nwv * v, K4 - 1);
         rv[t][v] = *(const f4*)(a.x + (uint64_t)(a.xrow0 + t0 + min(t, nt - 1)) * a.ldx + 4 * c);
+        if constexpr ((PRO & PRO_XSUM) != 0)  // one token, k <= 512 * waves (host-checked)
+          rv[t][v] = (rv[t][v] + *(const f4*)(a.xpart + 4 * c)) + *(const f4*)(a.xpart + a.xpartstride + 4 * c);
       }
   }
   // the first batch: activation items, then weights (they return in that order)
@@ -1786,6 +1804,11 @@ __global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(Ge
       ss = wave_sum_dpp(ss);
       if (lane == 0) misc[wave * NT + t] = ss;
     }
+    if constexpr ((PRO & PRO_XSUM) != 0)  // the summed residual row, for the layer's K3
+      if (blockIdx.x == 0)
+#pragma unroll
+        for (int v = 0; v < RV; v++)
+          if (wave * 64 + lane + 64 * nwv * v < K4) *(f4*)(a.xout + 4 * (wave * 64 + lane + 64 * nwv * v)) = rv[0][v];
   }
   // cpu.go:90-95, from the waves' partial sums (every thread, the same order)
   auto rms_scales = [&]() {
@@ -1845,7 +1868,7 @@ __global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(Ge
     f2* p2 = (f2*)part;
     p2[wave * 64 + lane] = f2{acc0, acc1};
     __syncthreads();
-    if (sp == 0) {
+    if (sw == 0) {
       f2 pv[15];
 #pragma unroll
       for (int k = 0; k < 15; k++) pv[k] = p2[(wave + min((uint32_t)k + 1, split - 1)) * 64 + lane];
@@ -1860,7 +1883,8 @@ __global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(Ge
   // ---- epilogue: lane holds rows r of the tile for tokens 2q and 2q+1
   const float vA = okA ? acc0 : 0.f;
   const float vB = okB ? acc1 : 0.f;
-  row_epilogue<EPI>(a, tile, r, active, t0 + tA, okA, vA, t0 + tB, okB, vB, &pre);
+  row_epilogue<EPI>(a, tile, r, active, t0 + tA, okA, vA, t0 + tB, okB, vB, &pre,
+                    kp > 1 ? a.y + kpart * a.pstride : nullptr);
   if (EPI == EPI_ARGMAX) {
     const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
     const bool ok = active && lr < a.rows && q == 0 && okA && vA == vA;
@@ -1887,7 +1911,8 @@ static int launch_nu(const GemvArgs& a, dim3 grid, uint32_t lds, hipStream_t s) 
 // (no load is issued for a third or fourth), else four.
 template <uint32_t QT, int NT, int PRO, int EPI>
 static int launch_one(const GemvArgs& a, dim3 grid, uint32_t lds, hipStream_t s) {
-  const uint32_t per_wave = (a.ng + a.split - 1) / a.split;
+  const uint32_t kp = a.kparts > 1 ? a.kparts : 1;  // a part's share of the groups
+  const uint32_t per_wave = ((a.ng + kp - 1) / kp + a.split - 1) / a.split;
   if (per_wave <= 2) return launch_nu<QT, NT, PRO, EPI, 2>(a, grid, lds, s);
   return launch_nu<QT, NT, PRO, EPI, 4>(a, grid, lds, s);
 }
@@ -1895,6 +1920,14 @@ static int launch_one(const GemvArgs& a, dim3 grid, uint32_t lds, hipStream_t s)
 template <uint32_t QT, int NT, int Q>
 static int launch_nt_q(const GemvArgs& a, int pro, int epi, dim3 grid, uint32_t lds, hipStream_t s) {
   constexpr int PP = PRO_PLAIN | Q, PR = PRO_RMS | Q;
+  if (pro & PRO_XSUM) {
+    if constexpr (NT == 1)
+      if ((pro & PRO_RMS) && epi == EPI_QKV) {
+        if (Q == 0) return launch_one<QT, 1, PRO_RMS | PRO_XSUM, EPI_QKV>(a, grid, lds, s);
+        return launch_one<QT, 1, PRO_RMS | PRO_Q8 | PRO_XSUM, EPI_QKV>(a, grid, lds, s);
+      }
+    return set_error(LLMHIP_ERR_ARG, "llm: gemv: the summing prologue is for one token into EPI_QKV");
+  }
   if (pro & PRO_MERGE) {  // two units per staging batch (more would spill the partials)
     if constexpr (Q == 0 && NT == 1)
       if (epi == EPI_ACC && !(pro & (PRO_RMS | PRO_Q8)) && a.waves <= 8 && (a.ng + a.split - 1) / a.split <= 2)

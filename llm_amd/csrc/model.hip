@@ -108,6 +108,13 @@ struct Model {
   // sampling kernel writes: the input of the next one-token pass
   float *x = nullptr, *q = nullptr, *act = nullptr, *gbuf = nullptr, *logits = nullptr, *pv = nullptr,
         *ml = nullptr, *amax_v = nullptr, *cs = nullptr, *att = nullptr, *h = nullptr, *xn = nullptr;
+  // kpart: rows 0 and 1 the two k-halves of a one-token pass's down
+  // projection, which the next layer's K1 adds to the residual x and stores,
+  // summed, to row 2, where that layer's K3 takes its residual from (x itself
+  // is never written by a launch that reads it).  k5_split: the K5 just
+  // recorded stored halves; xsum_ready: the K1 just recorded stored the sum.
+  float* kpart = nullptr;
+  bool k5_split = false, xsum_ready = false;
   void* xprep = nullptr;  // prepared activations of a prefill chunk
   uint32_t *amax_i = nullptr, *state = nullptr;
   int32_t *tokens = nullptr, *outb = nullptr;
@@ -500,6 +507,13 @@ static int rec_k1(Model& m, const Layer& L, uint32_t ntok) {
   for (int i = 0; i < L.nqkv; i++) {
     GemvArgs a = base_args(m, L.qkv[i], ntok);
     a.x = m.cur_layer == 0 && !m.embed_in ? m.xn : m.x;
+    int pro = PRO_RMS;
+    if (m.k5_split) {  // the residual is x + the previous down projection's two halves
+      a.xpart = m.kpart;
+      a.xpartstride = c.embd;
+      a.xout = m.kpart + 2 * c.embd;  // each launch's workgroup 0 stores the (same) sum there
+      pro |= PRO_XSUM;
+    }
     a.ldx = c.embd;
     a.nw = L.attn_norm;
     a.y = m.q;
@@ -512,8 +526,10 @@ static int rec_k1(Model& m, const Layer& L, uint32_t ntok) {
     a.ctx = m.ctx;
     a.neox = c.rope_neox;
     a.row_base = L.qkv_base[i];
-    LLM_TRY(mat_rec(m, "k1", "p1", a, L.qkv_type[i], PRO_RMS, EPI_QKV, L.qkv[i].g.gguf_bytes(), i == 0));
+    LLM_TRY(mat_rec(m, "k1", "p1", a, L.qkv_type[i], pro, EPI_QKV, L.qkv[i].g.gguf_bytes(), i == 0));
   }
+  m.xsum_ready = m.k5_split;
+  m.k5_split = false;
   return 0;
 }
 
@@ -580,6 +596,8 @@ static int rec_k3(Model& m, const Layer& L, uint32_t ntok) {
   a.y = m.x;
   a.ldy = m.cfg.embd;
   if (m.cur_layer == 0 && !m.embed_in) a.yin = m.xn;  // the residual stream starts at the embedding row
+  if (m.xsum_ready) a.yin = m.kpart + 2 * m.cfg.embd;  // x + the previous layer's down halves (K1 summed them)
+  m.xsum_ready = false;
   if (merge_in_k3(m, L, ntok)) {
     a.mpv = m.pv;
     a.mml = m.ml;
@@ -623,11 +641,24 @@ static int rec_k4(Model& m, const Layer& L, uint32_t ntok) {
   return mat_rec(m, "k4", "p4", u, L.gu[1].g.q.type, PRO_RMS, EPI_SWIGLU, L.gu[1].g.gguf_bytes(), false);
 }
 
-static int rec_k5(Model& m, const Layer& L, uint32_t ntok) {
+// split: a one-token pass whose next layer's K1 follows in the same pass
+// stores the product's two k-halves to kpart instead of adding it to x (twice
+// the workgroups for the long down rows; that K1 adds them, in order, to x).
+static int rec_k5(Model& m, const Layer& L, uint32_t ntok, bool split = false) {
   GemvArgs a = base_args(m, L.down, ntok);
   a.x = m.act;
   a.ldx = m.cfg.ff;
   a.y = m.x;
+  // (the summing prologue holds the whole row in two float4s per lane: k <= 512 * 4 waves)
+  split = split && ntok == 1 && !m.q8 && !a.stream && a.ng >= 2 && m.cfg.embd <= 2048 && !skipped(m, "k5") &&
+          !skipped(m, "k1");
+  if (split) {
+    a.kparts = 2;
+    a.y = m.kpart;
+    a.pstride = m.cfg.embd;
+    m.k5_split = true;
+    return gemv_rec(m, "k5", a, L.down.g.q.type, PRO_PLAIN, EPI_STORE, L.down.g.gguf_bytes());
+  }
   a.ldy = m.cfg.embd;
   return mat_rec(m, "k5", "p5", a, L.down.g.q.type, PRO_PLAIN, EPI_ACC, L.down.g.gguf_bytes());
 }
@@ -711,7 +742,7 @@ static int record_slot(Model& m, uint32_t ntok, bool head, int s) {
     LLM_TRY(rec_k2(m, L, ntok));
     LLM_TRY(rec_k3(m, L, ntok));
     LLM_TRY(rec_k4(m, L, ntok));
-    LLM_TRY(rec_k5(m, L, ntok));
+    LLM_TRY(rec_k5(m, L, ntok, s < nl));  // split when this slot's K1 adds the halves
   }
   if (s < nl) {
     m.cur_layer = s;
@@ -840,8 +871,8 @@ static int launch_graph(Model& m, uint32_t pos, uint32_t ntok, bool head, bool e
   return 0;
 }
 
-// cnt one-token decode passes from position pos as one graph (a submit, at
-// most 15 passes): its attention variant is the last position's, and the
+// cnt one-token decode passes from position pos as one graph (part of a
+// submit, at most 15 passes): its attention variant is the last position's, and the
 // earlier tokens stop at their own causal bound (the kernels read the
 // position from the device).
 static int launch_decode(Model& m, uint32_t pos, uint32_t cnt) {
@@ -1007,7 +1038,7 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
       (rc = dalloc_n(*m, &m->tokens, (uint64_t)m->ctx + 1)) || (rc = dalloc_n(*m, &m->outb, 1)) ||
       (rc = dalloc(*m, &m->xprep, xprep_bytes(m->pm, (uint32_t)std::max(c.embd, c.ff)))) ||
       (rc = dalloc_n(*m, &m->cs, (uint64_t)m->ctx * c.head_dim)) || (rc = dalloc_n(*m, &m->h, E)) ||
-      (rc = dalloc_n(*m, &m->xn, E)))
+      (rc = dalloc_n(*m, &m->xn, E)) || (rc = dalloc_n(*m, &m->kpart, 3 * E)))
     return fail(rc);
   {  // the prefill lanes: lane 0 is the model's own buffers
     m->lanes[0] = Lane{m->stream, m->x, m->q, m->att, m->act, m->gbuf, m->pv, m->ml, m->xprep, m->state};
@@ -1247,7 +1278,9 @@ int llmhip_model_decode(llmhip_model* h, int cnt, int32_t* out) {
                      m.pos);
   LLM_HIP(hipSetDevice(m.device));
   uint32_t first = m.pos;
-  for (int j = 0; j < cnt; j += 8) LLM_TRY(launch_decode(m, first + (uint32_t)j, (uint32_t)std::min(cnt - j, 8)));
+  // four passes per graph (measured, decode tok/s at configs 4 / 3: one 1514 / 1751, two 1510 / 1759,
+  // four 1508 / 1762, eight 1476 / 1765)
+  for (int j = 0; j < cnt; j += 4) LLM_TRY(launch_decode(m, first + (uint32_t)j, (uint32_t)std::min(cnt - j, 4)));
   LLM_HIP(hipMemcpyAsync(m.host, m.tokens + first + 1, (size_t)cnt * 4, hipMemcpyDeviceToHost, m.stream));
   LLM_HIP(hipStreamSynchronize(m.stream));
   memcpy(out, m.host, (size_t)cnt * 4);
@@ -1410,7 +1443,9 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
     if (k == "k2") return rec_k2(m, ly, 1);
     if (k == "k3") return rec_k3(m, ly, 1);
     if (k == "k4") return rec_k4(m, ly, 1);
-    return rec_k5(m, ly, 1);
+    const int rc5 = rec_k5(m, ly, 1, i % L < L - 1);  // as in the pass: halves but for the last layer
+    m.k5_split = false;
+    return rc5;
   };
   uint64_t b = 0;
   const Layer& L0 = m.layers[0];

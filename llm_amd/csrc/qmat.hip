@@ -105,7 +105,7 @@ void gemv_pick(uint32_t tiles, uint32_t ng, uint32_t tail, uint32_t nb, uint32_t
 uint32_t gemv_groups(const GemvArgs& a) {
   if (a.stream && a.ntok == 1) return a.stream;
   uint32_t tpw = a.waves / a.split;
-  return (a.tiles + tpw - 1) / tpw;
+  return (a.tiles + tpw - 1) / tpw * (a.kparts > 1 ? a.kparts : 1);
 }
 
 int gemv_launch(const GemvArgs& a, uint32_t qtype, int pro, int epi, hipStream_t s) {
@@ -114,6 +114,10 @@ int gemv_launch(const GemvArgs& a, uint32_t qtype, int pro, int epi, hipStream_t
     return set_error(LLMHIP_ERR_ARG, "llm: gemv: split %u over %u waves", a.split, a.waves);
   if ((uint64_t)a.nb * 4 > 2ull * 64 * a.waves)
     return set_error(LLMHIP_ERR_ARG, "llm: gemv: k=%u is too long for %u waves", a.k, a.waves);
+  if (a.kparts > 1 && (a.ntok != 1 || a.stream || a.kparts > 2 || a.ng < a.kparts || epi != EPI_STORE))
+    return set_error(LLMHIP_ERR_ARG, "llm: gemv: k in %u parts is for one token's tile-kernel store", a.kparts);
+  if ((pro & PRO_XSUM) && (a.ntok != 1 || a.k > 512u * a.waves))
+    return set_error(LLMHIP_ERR_ARG, "llm: gemv: the summing prologue is for one token, k <= 512 * waves");
   switch (qtype) {
     case LLMHIP_Q4_0: return gemv_launch_qt<LLMHIP_Q4_0>(a, pro, epi, s);
     case LLMHIP_Q4_1: return gemv_launch_qt<LLMHIP_Q4_1>(a, pro, epi, s);
