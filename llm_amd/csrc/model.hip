@@ -1439,7 +1439,12 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
       const QMat& w = m.tied ? m.embd : m.out;
       return gemv_launch(head_args(m, 0, 0), w.g.q.type, PRO_RMS | (m.q8 ? PRO_Q8 : 0), EPI_ARGMAX, m.stream);
     }
-    if (k == "k1") return rec_k1(m, ly, 1);
+    if (k == "k1") {  // as in the pass: after layer 0 the previous down projection's halves are added
+      m.k5_split = i % L > 0 && m.cfg.embd <= 2048 && !m.q8;
+      const int rc1 = rec_k1(m, ly, 1);
+      m.xsum_ready = false;
+      return rc1;
+    }
     if (k == "k2") return rec_k2(m, ly, 1);
     if (k == "k3") return rec_k3(m, ly, 1);
     if (k == "k4") return rec_k4(m, ly, 1);
