@@ -52,6 +52,43 @@ __device__ __forceinline__ uint4 ld_stream16(const uint8_t* p) {
   return uint4{v[0], v[1], v[2], v[3]};
 }
 
+// The work of warm-up workgroup j of a launch carrying p (Prefetch, gemv.h):
+// launched as workgroup (j, 1) of a grid of `own` x 2, it runs on XCD
+// c = (own + j) % 8 (workgroups are numbered x-fastest) and, with
+// the other wgs / 8 workgroups of that XCD, touches the lines of the consumer
+// workgroups x = c, c + 8, ...: tile group x / kparts, part x % kparts, whose
+// block groups [g0, g1) (the last part: through the tile's end) are quant
+// bytes [g0 qg, g1 qg) and scale bytes sbase + [g0 sg, g1 sg).  Four loads
+// per thread are in flight at once; the values are only kept alive.
+__device__ __forceinline__ void prefetch_run(const Prefetch& p, uint32_t j) {
+  const uint32_t c = (p.own + j) % XCDS, per = p.wgs / XCDS, k = j / XCDS;
+  const uint32_t nx = p.cgrid > c ? (p.cgrid - c + XCDS - 1) / XCDS : 0;
+  const uint32_t lines = p.tpw * p.lpt, items = nx * lines, step = per * blockDim.x;
+  uint32_t acc = 0;
+  for (uint32_t f0 = k * blockDim.x + threadIdx.x; f0 < items; f0 += 4 * step) {
+    uint32_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint32_t f = f0 + u * step;
+      uint64_t off = 0;  // an in-bounds line (the first) where an item has none
+      if (f < items) {
+        const uint32_t x = c + XCDS * (f / lines), l = f % lines;
+        const uint32_t part = x % p.kparts, t = x / p.kparts * p.tpw + l / p.lpt, lt = l % p.lpt;
+        const bool last = part == p.kparts - 1;
+        const uint32_t g0 = part * p.ng / p.kparts, g1 = (part + 1) * p.ng / p.kparts;
+        const uint32_t q0 = g0 * p.qg, q1 = last ? p.sbase : g1 * p.qg;
+        const uint32_t s0 = p.sbase + g0 * p.sg, s1 = last ? p.tile_bytes : p.sbase + g1 * p.sg;
+        const uint32_t nq = (q1 - q0 + 127) / 128;
+        const uint32_t o = lt < nq ? q0 + 128 * lt : s0 + 128 * (lt - nq);
+        if (t < p.tiles && o < (lt < nq ? q1 : s1)) off = (uint64_t)t * p.tile_bytes + (o & ~3u);
+      }
+      v[u] = *(const uint32_t*)(p.qs + off);
+    }
+    acc += v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+  asm volatile("" ::"v"(acc));
+}
+
 // ------------------------------------------------------------ row maps
 
 __host__ __device__ inline uint32_t pos_of_row(uint32_t lr, uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1,
@@ -375,7 +412,7 @@ __device__ __forceinline__ EpiIn epi_load(const GemvArgs& a, uint32_t tile, int 
       const uint32_t hd = a.hd, hp = hd / 2;
       const uint32_t j = lf < a.nq ? lf : lf - a.nq, w = j % hd;
       const uint32_t i = a.neox ? w % hp : w / 2;
-      const uint32_t p0 = a.state[0];
+      const uint32_t p0 = state_pos(a.state);
       if (okA) {
         const uint64_t o = ((uint64_t)(p0 + tokA) * hp + i) * 2;
         e.cA = a.cs[o];
@@ -440,7 +477,7 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
     float oA = __shfl_xor(vA, pm), oB = __shfl_xor(vB, pm);
     if (rvalid) {
       const uint32_t hd = a.hd, hp = hd / 2;
-      const uint32_t p0 = a.state[0];
+      const uint32_t p0 = state_pos(a.state);
       for (int u = 0; u < 2; u++) {
         if (!(u ? okB : okA)) continue;
         uint32_t tok = u ? tokB : tokA;
@@ -1482,7 +1519,7 @@ __device__ __forceinline__ void load_items(ItemsOf<NT, PRO>& it, const GemvArgs&
       it.oa[c] = *(const f4*)(pv + (uint64_t)cc * a.hd);
       if (NU == 4) it.oc[c] = *(const f4*)(pv + (uint64_t)cc * a.hd + 16);
     }
-    it.P = (a.state[0] + a.mrows) / a.mrows;  // chunks holding positions 0 .. pos
+    it.P = (state_pos(a.state) + a.mrows) / a.mrows;  // chunks holding positions 0 .. pos
     it.e0 = e0;
     it.ok = ok;
     return;
@@ -1722,12 +1759,42 @@ __device__ __forceinline__ void unit_products(const WUnit& w, uint32_t u, int nb
 
 // (the merging prologue holds every chunk's partials in registers: at most
 // 8 waves per workgroup, so that 256 VGPRs are there for it)
+// One field of each 64-byte line of the arguments a one-token launch reads,
+// routed through an empty asm whose results the kernel then uses, so that
+// all of them are loaded in one round at the kernel's start: every first
+// touch of a line misses the scalar cache, and left to the compiler the
+// loads follow the branches that use them, three or four dependent rounds of
+// a few hundred ns before the first activation load is issued.  After this
+// round the other fields' loads hit the cache.
+// Lines 2 (the epilogue's outputs) and 4 (the merging and summing
+// prologues') only where the variant reads them: a line nobody reads costs a
+// miss of its own.
+template <int PRO, int EPI>
+__device__ __forceinline__ void touch_args(GemvArgs& a) {
+  static_assert(offsetof(GemvArgs, qs) < 64 && offsetof(GemvArgs, x) / 64 == 1 && offsetof(GemvArgs, ldy) / 64 == 2 &&
+                    offsetof(GemvArgs, kparts) / 64 == 3 && offsetof(GemvArgs, xout) / 64 == 4 &&
+                    offsetof(GemvArgs, mpv) / 64 == 4 && offsetof(GemvArgs, ff) / 64 == 3 &&
+                    offsetof(GemvArgs, up) / 64 == 3,
+                "one field of each argument line");
+  constexpr bool L2 = EPI != EPI_GATEUP, L4 = (PRO & (PRO_MERGE | PRO_XSUM)) != 0;
+  if constexpr (L2 && L4) asm volatile("" : "+s"(a.qs), "+s"(a.x), "+s"(a.ldy), "+s"(a.kparts), "+s"(a.mpv));
+  if constexpr (L2 && !L4) asm volatile("" : "+s"(a.qs), "+s"(a.x), "+s"(a.ldy), "+s"(a.kparts));
+  if constexpr (!L2 && L4) asm volatile("" : "+s"(a.qs), "+s"(a.x), "+s"(a.kparts), "+s"(a.mpv));
+  if constexpr (!L2 && !L4) asm volatile("" : "+s"(a.qs), "+s"(a.x), "+s"(a.kparts));
+}
+
 template <uint32_t QT, int NT, int PRO, int EPI, int NU>
-__global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(GemvArgs a_in) {
+  if (NT == 1 && blockIdx.y != 0) {  // the L2 warm-up row (a one-token launch has one row of its own)
+    if (blockIdx.x < a_in.pf.wgs) prefetch_run(a_in.pf, blockIdx.x);
+    return;
+  }
+  GemvArgs a = a_in;
+  if (NT == 1) touch_args<PRO, EPI>(a);
   typedef WaveLds<NT> WL;
   constexpr bool Q8 = (PRO & PRO_Q8) != 0, RMS = (PRO & PRO_RMS) != 0;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  const uint32_t nwv = blockDim.x >> 6;
+  const uint32_t nwv = a.waves;  // the launch's blockDim.x / 64
   const int lane = threadIdx.x & 63, wave = wave_id();
   const uint32_t t0 = blockIdx.y * NT;
   const int nt = min((int)NT, (int)(a.ntok - t0));
@@ -1755,12 +1822,6 @@ __global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(Ge
   const uint32_t cnt = has_tile && gn > sw ? (gn - sw + split - 1) / split : 0;
   const bool has_tail = has_tile && a.tail && kpart == kp - 1 && (gn % split) == sw;
 
-  // the epilogue's own inputs, in flight during the prologue
-  const bool active = sw == 0 && has_tile;
-  const int tA = 2 * q, tB = 2 * q + 1;
-  const bool okA = tA < nt, okB = NT > 1 && tB < nt;
-  const EpiIn pre = epi_load<EPI>(a, tile, r, active, t0 + tA, okA, t0 + tB, okB);
-
   // RMSNorm's sum of squares: the workgroup's waves load the row between
   // them (two float4s per lane and token at once: rows up to 512 * waves floats)
   constexpr int RV = 2;
@@ -1787,6 +1848,12 @@ __global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(Ge
     load_items<NT, PRO, true, NU>(itt, a, t0, nt, 0, cnt, sp, split, lane);
     load_unit<QT>(wt, a.qs, nb, tile, ng, ng, a.tail, lane, r);
   }
+  // the epilogue's own inputs (issued after the prologue's: the RoPE rows wait
+  // for the position), in flight during the products
+  const bool active = sw == 0 && has_tile;
+  const int tA = 2 * q, tB = 2 * q + 1;
+  const bool okA = tA < nt, okB = NT > 1 && tB < nt;
+  const EpiIn pre = epi_load<EPI>(a, tile, r, active, t0 + tA, okA, t0 + tB, okB);
   float rs[NT];
   if (RMS) {
 #pragma unroll
@@ -1993,6 +2060,15 @@ int gemv_launch_qt(const GemvArgs& a, int pro, int epi, hipStream_t s) {
     return set_error(LLMHIP_ERR_ARG, "llm: gemv: %u waves of %d tokens need %u bytes of LDS", a.waves, nt, lds);
   if (epi == EPI_ARGMAX && a.ntok != 1) return set_error(LLMHIP_ERR_ARG, "llm: gemv: argmax epilogue needs one token");
   dim3 grid(gemv_groups(a), (a.ntok + nt - 1) / nt);
+  if (a.pf.wgs) {  // the warm-up workgroups: a second row after the launch's own (at most as many)
+    if (nt != 1 || epi == EPI_ARGMAX || a.pf.wgs % XCDS || !a.pf.qs)
+      return set_error(LLMHIP_ERR_ARG, "llm: gemv: an L2 warm-up rides on a one-token launch, in groups of 8");
+    GemvArgs b = a;
+    b.pf.own = grid.x;
+    b.pf.wgs = std::min(a.pf.wgs, grid.x / XCDS * XCDS);
+    if (b.pf.wgs) grid.y = 2;
+    return launch_nt<QT, 1>(b, pro, epi, grid, lds, s);
+  }
   switch (nt) {
     case 1: return launch_nt<QT, 1>(a, pro, epi, grid, lds, s);
     case 2: return launch_nt<QT, 2>(a, pro, epi, grid, lds, s);

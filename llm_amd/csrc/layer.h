@@ -19,6 +19,7 @@ struct AttnArgs {
   uint32_t split;  // 0: one chunk (rows <= attn_full_max(hd)); 1: chunks (ATTN_SPLIT_ROWS; one token ATTN_DECODE_ROWS) + merge
   uint32_t kv16;   // the cache holds binary16 values (F16KV)
   float scale;     // f32(1/sqrt(hd)), cpu.go:304
+  Prefetch pf;     // one token: an L2 warm-up for a later launch (attn_kernel carries it)
 };
 
 // Prefill: att also written as the output projection's prepared operands (per

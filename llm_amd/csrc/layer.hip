@@ -72,7 +72,15 @@ __device__ __forceinline__ void emit_operand(const AttnOps& a, uint32_t t, uint3
 //     (m, l) and o = sum e v for attn_merge_kernel; chunks past the causal
 //     bound write nothing.
 template <uint32_t HD, uint32_t J, bool SPLIT, bool KVH, bool EMIT = false>
-__global__ __launch_bounds__(512) void attn_kernel(AttnArgs a, uint32_t ntok, uint32_t units, AttnOps ops) {
+__global__ __launch_bounds__(512) void attn_kernel(AttnArgs a_in, uint32_t ntok, uint32_t units, AttnOps ops) {
+  if (blockIdx.y != 0) {  // the L2 warm-up row
+    if (blockIdx.x < a_in.pf.wgs) prefetch_run(a_in.pf, blockIdx.x);
+    return;
+  }
+  // both lines of the arguments it reads in one round of scalar loads (as gemv_kernel's touch_args)
+  static_assert(offsetof(AttnArgs, heads) < 64 && offsetof(AttnArgs, rows) / 64 == 1, "argument lines");
+  AttnArgs a = a_in;
+  asm volatile("" : "+s"(a.heads), "+s"(a.rows));
   typedef AttnChunk<HD, J, 8, KVH> AC;
   __shared__ AttnLds<HD, 8> sm;
   const uint32_t GQ = a.heads / a.kv_heads, sb = blockIdx.x / 8;
@@ -88,7 +96,7 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a, uint32_t ntok, ui
   for (uint32_t v = 0; v < AC::V4; v++) q[v] = *(const f4*)(qp + 64 * v);
   AC rows;
   rows.load(a.kv, a.kvd, a.ctx, g, row0, a.rows);
-  const uint32_t n = a.state[0] + t + 1;
+  const uint32_t n = state_pos(a.state) + t + 1;
   if (SPLIT && row0 >= n) return;  // uniform over the workgroup
   float M, L, o;
   rows.reduce(q, row0, n, a.scale, sm, &M, &L, &o);
@@ -129,7 +137,7 @@ __global__ __launch_bounds__(512) void attn_multi_kernel(AttnArgs a, uint32_t nt
     const float* qp = a.q + (uint64_t)t * a.heads * HD + h * HD + 4 * cl;
 #pragma unroll
     for (uint32_t v = 0; v < AC::V4; v++) q[i][v] = *(const f4*)(qp + 64 * v);
-    n[i] = a.state[0] + t + 1;
+    n[i] = state_pos(a.state) + t + 1;
   }
   AC rows;
   rows.load(a.kv, a.kvd, a.ctx, g, 0, a.rows);
@@ -165,7 +173,7 @@ __global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a, uint32_t ntok
   const uint32_t GQ = a.heads / a.kv_heads, nq = ntok * GQ;
   const uint32_t c = blockIdx.x % nchunks, rest = blockIdx.x / nchunks;
   const uint32_t g = rest % a.kv_heads, q0 = (rest / a.kv_heads) * 64;
-  const uint32_t row0 = c * C, pos0 = a.state[0];
+  const uint32_t row0 = c * C, pos0 = state_pos(a.state);
   const uint32_t tlast = (min(q0 + 64, nq) - 1) / GQ;
   if (q0 >= nq || row0 >= pos0 + tlast + 1) return;  // uniform: no query of the group reaches the chunk
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4, r = lane & 15;
@@ -297,7 +305,7 @@ __global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a, uint32_t ntok
 template <uint32_t HD, bool EMIT = false>
 __global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a, AttnOps ops, uint32_t crows) {
   const uint32_t h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
-  const uint32_t n = a.state[0] + t + 1, P = (n + crows - 1) / crows;
+  const uint32_t n = state_pos(a.state) + t + 1, P = (n + crows - 1) / crows;
   const uint64_t th = (uint64_t)t * a.heads + h;
   const float* ml = a.ml + th * a.smax * 2;
   const float* pv = a.pv + th * a.smax * HD + d;
@@ -339,6 +347,15 @@ uint32_t attn_full_max(uint32_t hd) { return hd == 64 ? 256 : 128; }
 template <uint32_t HD, uint32_t J, bool SPLIT>
 static void attn_go(const AttnArgs& a, uint32_t ntok, uint32_t units, hipStream_t s, const AttnOps& ops) {
   const uint32_t gq = a.heads / a.kv_heads, blocks = 8 * gq * ((units + 7) / 8);
+  if (a.pf.wgs && blocks >= XCDS) {  // the warm-up workgroups: a second row (at most as many)
+    AttnArgs c = a;
+    c.pf.own = blocks;
+    c.pf.wgs = std::min(a.pf.wgs, blocks / XCDS * XCDS);
+    const dim3 g(blocks, 2), b(512);
+    if (a.kv16) hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT, true>), g, b, 0, s, c, ntok, units, ops);
+    else hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT, false>), g, b, 0, s, c, ntok, units, ops);
+    return;
+  }
   const dim3 g(blocks), b(512);
   if (!SPLIT && ops.xp) {  // prefill: also the output projection's operands
     if (a.kv16) hipLaunchKernelGGL((attn_kernel<HD, J, false, true, true>), g, b, 0, s, a, ntok, units, ops);
@@ -355,6 +372,8 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* 
   if (!attn_ok(a.hd) || a.rows == 0 || a.rows > a.ctx || a.heads % a.kv_heads)
     return set_error(LLMHIP_ERR_ARG, "llm: attention: head size %u, %u rows of %u not supported", a.hd, a.rows,
                      a.ctx);
+  if (a.pf.wgs && (ntok != 1 || ops.xp || a.pf.wgs % XCDS || !a.pf.qs))
+    return set_error(LLMHIP_ERR_ARG, "llm: attention: an L2 warm-up rides on a one-token launch, in groups of 8");
   const uint32_t NI = ntok * a.kv_heads;
   if (!a.split) {
     if (a.rows > attn_full_max(a.hd)) return set_error(LLMHIP_ERR_ARG, "llm: attention: %u rows in one chunk", a.rows);

@@ -502,6 +502,44 @@ static GemvArgs base_args(const Model& m, const QMat& q, uint32_t ntok) {
   return a;
 }
 
+// The L2 warm-up a launch of a one-token pass carries (Prefetch): K1 that of
+// its layer's K3, K2 that of K4, K3 that of K5 and K5 that of the next
+// layer's K1, each launch's idle CUs reading the next-but-one launch's weights
+// into the L2 of the XCD that will read them.  LLMHIP_L2_WARM=0 (read once):
+// none, for comparison.
+static bool l2_warm() {
+  static const bool on = [] {
+    const char* v = getenv("LLMHIP_L2_WARM");
+    return !(v && strcmp(v, "0") == 0);
+  }();
+  return on;
+}
+
+static Prefetch warm_for(const Model& m, const QMat& q, uint32_t ntok, uint32_t threads, uint32_t kparts = 1) {
+  Prefetch p;
+  memset(&p, 0, sizeof p);
+  if (ntok != 1 || !l2_warm()) return p;
+  GemvArgs c = base_args(m, q, 1);
+  c.kparts = kparts;
+  return prefetch_plan(c, q.g.q.type, threads);
+}
+
+// Whether a one-token K5 (bound in a) runs in two k-parts whose halves the
+// next layer's K1 adds: `want` when that K1 follows in the same pass.
+// (The summing prologue holds the whole row in two float4s per lane: k <= 512 * 4 waves.)
+static bool k5_splits(const Model& m, const GemvArgs& a, uint32_t ntok, bool want) {
+  return want && ntok == 1 && !m.q8 && !a.stream && a.ng >= 2 && m.cfg.embd <= 2048 && !skipped(m, "k5") &&
+         !skipped(m, "k1");
+}
+
+static int pass_layers(const Model& m, bool* head);
+
+// Whether the layer after the current one runs in this pass.
+static bool next_layer_runs(const Model& m) {
+  bool h = true;
+  return m.cur_layer + 1 < pass_layers(m, &h);
+}
+
 static int rec_k1(Model& m, const Layer& L, uint32_t ntok) {
   const llmhip_config& c = m.cfg;
   for (int i = 0; i < L.nqkv; i++) {
@@ -526,6 +564,7 @@ static int rec_k1(Model& m, const Layer& L, uint32_t ntok) {
     a.ctx = m.ctx;
     a.neox = c.rope_neox;
     a.row_base = L.qkv_base[i];
+    if (i == 0) a.pf = warm_for(m, L.o, ntok, 64 * a.waves);
     LLM_TRY(mat_rec(m, "k1", "p1", a, L.qkv_type[i], pro, EPI_QKV, L.qkv[i].g.gguf_bytes(), i == 0));
   }
   m.xsum_ready = m.k5_split;
@@ -535,6 +574,7 @@ static int rec_k1(Model& m, const Layer& L, uint32_t ntok) {
 
 static AttnArgs attn_args(const Model& m, const Layer& L) {
   AttnArgs a;
+  memset(&a, 0, sizeof a);
   a.q = m.q;
   a.kv = L.kv;
   a.pv = m.pv;
@@ -576,7 +616,8 @@ static int rec_k2(Model& m, const Layer& L, uint32_t ntok) {
   if (skipped(m, "k2")) return 0;
   // KV bytes read for the last token of the pass (the decode step's one token)
   uint64_t bytes = 2ull * (m.pos + 1) * m.kvd * 4;
-  const AttnArgs a = attn_args(m, L);
+  AttnArgs a = attn_args(m, L);
+  a.pf = warm_for(m, L.gu[0], ntok, 512);
   if (merge_in_k3(m, L, ntok)) return launch_rec(m, "k2", bytes, [&]() { return attn_launch(a, ntok, m.stream, nullptr, false); });
   if (m.attn_split) m.dispatches++;  // the merge kernel
   if (att_operands(m, ntok)) {
@@ -598,6 +639,10 @@ static int rec_k3(Model& m, const Layer& L, uint32_t ntok) {
   if (m.cur_layer == 0 && !m.embed_in) a.yin = m.xn;  // the residual stream starts at the embedding row
   if (m.xsum_ready) a.yin = m.kpart + 2 * m.cfg.embd;  // x + the previous layer's down halves (K1 summed them)
   m.xsum_ready = false;
+  {
+    const GemvArgs d = base_args(m, L.down, ntok);
+    a.pf = warm_for(m, L.down, ntok, 64 * a.waves, k5_splits(m, d, ntok, next_layer_runs(m)) ? 2 : 1);
+  }
   if (merge_in_k3(m, L, ntok)) {
     a.mpv = m.pv;
     a.mml = m.ml;
@@ -649,9 +694,8 @@ static int rec_k5(Model& m, const Layer& L, uint32_t ntok, bool split = false) {
   a.x = m.act;
   a.ldx = m.cfg.ff;
   a.y = m.x;
-  // (the summing prologue holds the whole row in two float4s per lane: k <= 512 * 4 waves)
-  split = split && ntok == 1 && !m.q8 && !a.stream && a.ng >= 2 && m.cfg.embd <= 2048 && !skipped(m, "k5") &&
-          !skipped(m, "k1");
+  split = k5_splits(m, a, ntok, split);
+  if (next_layer_runs(m)) a.pf = warm_for(m, m.layers[m.cur_layer + 1].qkv[0], ntok, 64 * a.waves);
   if (split) {
     a.kparts = 2;
     a.y = m.kpart;
@@ -1435,6 +1479,7 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
   // as in the decode pass
   auto one = [&](int i) -> int {
     const Layer& ly = m.layers[i % L];
+    m.cur_layer = i % L;  // the launches carry the L2 warm-ups of the pass (Prefetch)
     if (k == "head") {  // the decode head kernel without the sampling kernel, which advances the state
       const QMat& w = m.tied ? m.embd : m.out;
       return gemv_launch(head_args(m, 0, 0), w.g.q.type, PRO_RMS | (m.q8 ? PRO_Q8 : 0), EPI_ARGMAX, m.stream);
@@ -1473,6 +1518,7 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
   if (e0) (void)hipEventDestroy(e0);
   if (e1) (void)hipEventDestroy(e1);
   m.skip = saved;
+  m.cur_layer = -1;
   if (rc) return rc;
   *avg_us = ms * 1000.f / (float)iters;
   if (bytes) *bytes = b;

@@ -12,6 +12,14 @@ namespace llmhip {
 // per-wave indices and loop bounds derived from it live in SGPRs.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
+// state[0] (the first position of the pass) through the scalar cache.  The
+// state is written only by the sampling and advance kernels, never while a
+// kernel that reads it runs, so a constant-memory load is exact; the wait for
+// it is then off the vector-load counter, whose waits are in issue order.
+__device__ __forceinline__ uint32_t state_pos(const uint32_t* state) {
+  return *(const __attribute__((address_space(4))) uint32_t*)state;
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
