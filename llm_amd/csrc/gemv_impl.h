@@ -1771,16 +1771,18 @@ __device__ __forceinline__ void unit_products(const WUnit& w, uint32_t u, int nb
 // miss of its own.
 template <int PRO, int EPI>
 __device__ __forceinline__ void touch_args(GemvArgs& a) {
-  static_assert(offsetof(GemvArgs, qs) < 64 && offsetof(GemvArgs, x) / 64 == 1 && offsetof(GemvArgs, ldy) / 64 == 2 &&
+  static_assert(offsetof(GemvArgs, rows) < 64 && offsetof(GemvArgs, ldx) / 64 == 1 && offsetof(GemvArgs, ldy) / 64 == 2 &&
                     offsetof(GemvArgs, kparts) / 64 == 3 && offsetof(GemvArgs, xout) / 64 == 4 &&
-                    offsetof(GemvArgs, mpv) / 64 == 4 && offsetof(GemvArgs, ff) / 64 == 3 &&
+                    offsetof(GemvArgs, msmax) / 64 == 4 && offsetof(GemvArgs, ff) / 64 == 3 &&
                     offsetof(GemvArgs, up) / 64 == 3,
                 "one field of each argument line");
+  // (integer fields: a pointer that went through the asm would lose its
+  // global address space and be read with flat loads)
   constexpr bool L2 = EPI != EPI_GATEUP, L4 = (PRO & (PRO_MERGE | PRO_XSUM)) != 0;
-  if constexpr (L2 && L4) asm volatile("" : "+s"(a.qs), "+s"(a.x), "+s"(a.ldy), "+s"(a.kparts), "+s"(a.mpv));
-  if constexpr (L2 && !L4) asm volatile("" : "+s"(a.qs), "+s"(a.x), "+s"(a.ldy), "+s"(a.kparts));
-  if constexpr (!L2 && L4) asm volatile("" : "+s"(a.qs), "+s"(a.x), "+s"(a.kparts), "+s"(a.mpv));
-  if constexpr (!L2 && !L4) asm volatile("" : "+s"(a.qs), "+s"(a.x), "+s"(a.kparts));
+  if constexpr (L2 && L4) asm volatile("" : "+s"(a.rows), "+s"(a.ldx), "+s"(a.ldy), "+s"(a.kparts), "+s"(a.msmax));
+  if constexpr (L2 && !L4) asm volatile("" : "+s"(a.rows), "+s"(a.ldx), "+s"(a.ldy), "+s"(a.kparts));
+  if constexpr (!L2 && L4) asm volatile("" : "+s"(a.rows), "+s"(a.ldx), "+s"(a.kparts), "+s"(a.msmax));
+  if constexpr (!L2 && !L4) asm volatile("" : "+s"(a.rows), "+s"(a.ldx), "+s"(a.kparts));
 }
 
 template <uint32_t QT, int NT, int PRO, int EPI, int NU>
@@ -1806,21 +1808,23 @@ __global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(Ge
   float* part = (float*)(lds + nwv * WL::BYTES);
   float* misc = part + nwv * 64 * 2;  // [0, 64): RMS partials; [80, 112): argmax partials
 
-  const uint32_t split = a.split, tpw = nwv / split;
-  const uint32_t lt = wave / split;
+  // split and waves are powers of two and kparts is 1 or 2 (gemv_launch
+  // checks), so the indices below take shifts and masks, not divisions
+  const uint32_t split = a.split, ls = __builtin_ctz(split), tpw = nwv >> ls;
+  const uint32_t lt = wave >> ls;
   // k in parts (one token): workgroup x = (tile group) * kparts + part; part p
   // runs block groups [g0, g1), the last one the tail too, into its own row
-  const uint32_t kp = a.kparts > 1 ? a.kparts : 1, kpart = blockIdx.x % kp, bx = blockIdx.x / kp;
-  const uint32_t g0 = kpart * ng / kp, g1 = (kpart + 1) * ng / kp;
+  const uint32_t lk = a.kparts > 1 ? 1 : 0, kp = 1u << lk, kpart = blockIdx.x & (kp - 1), bx = blockIdx.x >> lk;
+  const uint32_t g0 = (kpart * ng) >> lk, g1 = ((kpart + 1) * ng) >> lk;
   const uint32_t tile = min(bx * tpw + lt, a.tiles - 1);
   const bool has_tile = bx * tpw + lt < a.tiles;
   const bool keep = bx * tpw + lt == 0;  // PRO_MERGE: tile 0's waves also store the merged row
   const int r = lane & 15, q = lane >> 4, slot = lane & 15;
   // this wave's units: groups sp = g0 + sw, sp + split, ... below g1, then the
   // tail (the last part's wave (g1 - g0) % split)
-  const uint32_t sw = wave % split, sp = g0 + sw, gn = g1 - g0;
-  const uint32_t cnt = has_tile && gn > sw ? (gn - sw + split - 1) / split : 0;
-  const bool has_tail = has_tile && a.tail && kpart == kp - 1 && (gn % split) == sw;
+  const uint32_t sw = wave & (split - 1), sp = g0 + sw, gn = g1 - g0;
+  const uint32_t cnt = has_tile && gn > sw ? (gn - sw + split - 1) >> ls : 0;
+  const bool has_tail = has_tile && a.tail && kpart == kp - 1 && (gn & (split - 1)) == sw;
 
   // RMSNorm's sum of squares: the workgroup's waves load the row between
   // them (two float4s per lane and token at once: rows up to 512 * waves floats)
