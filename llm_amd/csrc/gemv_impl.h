@@ -91,10 +91,12 @@ __device__ __forceinline__ void prefetch_run(const Prefetch& p, uint32_t j) {
 
 // ------------------------------------------------------------ row maps
 
+// (hd, the head size of a NEOX map, is a power of two: the model admits 64
+// and 128; shifts instead of divisions)
 __host__ __device__ inline uint32_t pos_of_row(uint32_t lr, uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1,
                                                uint32_t ff) {
   if (map == MAP_NEOX && lr >= seg0 && lr < seg1) {
-    uint32_t local = lr - seg0, h = local / hd, k = local % hd, hp = hd / 2;
+    uint32_t local = lr - seg0, h = local >> __builtin_ctz(hd), k = local & (hd - 1), hp = hd / 2;
     uint32_t side = k >= hp, i = side ? k - hp : k;
     return seg0 + h * hd + 16 * (i / 8) + (i % 8) + 8 * side;
   }
@@ -108,7 +110,7 @@ __host__ __device__ inline uint32_t pos_of_row(uint32_t lr, uint32_t map, uint32
 __host__ __device__ inline uint32_t row_of_pos(uint32_t p, uint32_t map, uint32_t hd, uint32_t seg0, uint32_t seg1,
                                                uint32_t ff) {
   if (map == MAP_NEOX && p >= seg0 && p < seg1) {
-    uint32_t local = p - seg0, h = local / hd, w = local % hd, c = w % 16;
+    uint32_t local = p - seg0, h = local >> __builtin_ctz(hd), w = local & (hd - 1), c = w % 16;
     return seg0 + h * hd + (c / 8) * (hd / 2) + 8 * (w / 16) + (c % 8);
   }
   if (map == MAP_GATEUP) {
@@ -410,8 +412,8 @@ __device__ __forceinline__ EpiIn epi_load(const GemvArgs& a, uint32_t tile, int 
     if (a.bias) e.bias = a.bias[lf];
     if (lf < a.nq + a.nk) {
       const uint32_t hd = a.hd, hp = hd / 2;
-      const uint32_t j = lf < a.nq ? lf : lf - a.nq, w = j % hd;
-      const uint32_t i = a.neox ? w % hp : w / 2;
+      const uint32_t j = lf < a.nq ? lf : lf - a.nq, w = j & (hd - 1);  // hd: 64 or 128
+      const uint32_t i = a.neox ? w & (hp - 1) : w / 2;
       const uint32_t p0 = state_pos(a.state);
       if (okA) {
         const uint64_t o = ((uint64_t)(p0 + tokA) * hp + i) * 2;
@@ -484,7 +486,7 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
         float v = u ? vB : vA, o = u ? oB : oA;
         uint32_t pos = p0 + tok;
         if (lf < a.nq + a.nk) {
-          uint32_t j = lf < a.nq ? lf : lf - a.nq, w = j % hd;
+          uint32_t j = lf < a.nq ? lf : lf - a.nq, w = j & (hd - 1);  // hd: 64 or 128
           bool first = a.neox ? w < hp : (w % 2) == 0;
           const float c = u ? e.cB : e.cA, sn = u ? e.sB : e.sA;
           float x = first ? v : o, z = first ? o : v;
@@ -1506,7 +1508,7 @@ __device__ __forceinline__ void load_items(ItemsOf<NT, PRO>& it, const GemvArgs&
   if constexpr ((PRO & PRO_MERGE) != 0) {
     // one token: the head of elements e0.. (and e0 + 16..), its chunks
     static_assert(NT == 1, "merging prologue: one token");
-    const uint32_t h = e0 / a.hd, d = e0 % a.hd;
+    const uint32_t h = e0 >> __builtin_ctz(a.hd), d = e0 & (a.hd - 1);  // hd: 64 or 128
     const float* ml = a.mml + (uint64_t)h * a.msmax * 2;
     const float* pv = a.mpv + (uint64_t)h * a.msmax * a.hd + d;
 #pragma unroll
@@ -1519,7 +1521,7 @@ __device__ __forceinline__ void load_items(ItemsOf<NT, PRO>& it, const GemvArgs&
       it.oa[c] = *(const f4*)(pv + (uint64_t)cc * a.hd);
       if (NU == 4) it.oc[c] = *(const f4*)(pv + (uint64_t)cc * a.hd + 16);
     }
-    it.P = (state_pos(a.state) + a.mrows) / a.mrows;  // chunks holding positions 0 .. pos
+    it.P = (state_pos(a.state) + a.mrows) >> __builtin_ctz(a.mrows);  // chunks holding positions 0 .. pos (mrows: a power of two)
     it.e0 = e0;
     it.ok = ok;
     return;

@@ -3,6 +3,7 @@
 
 #include "common.h"
 #include "gemv.h"
+#include "wave.h"
 
 namespace llmhip {
 
@@ -19,6 +20,8 @@ struct AttnArgs {
   uint32_t split;  // 0: one chunk (rows <= attn_full_max(hd)); 1: chunks (ATTN_SPLIT_ROWS; one token ATTN_DECODE_ROWS) + merge
   uint32_t kv16;   // the cache holds binary16 values (F16KV)
   float scale;     // f32(1/sqrt(hd)), cpu.go:304
+  // attn_kernel's divisors (heads / kv_heads, ntok * kv_heads, kv_heads), set by attn_launch
+  FastDiv dgq, dni, dkv;
   Prefetch pf;     // one token: an L2 warm-up for a later launch (attn_kernel carries it)
 };
 

@@ -78,16 +78,18 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a_in, uint32_t ntok,
     return;
   }
   // both lines of the arguments it reads in one round of scalar loads (as gemv_kernel's touch_args)
-  static_assert(offsetof(AttnArgs, heads) < 64 && offsetof(AttnArgs, rows) / 64 == 1, "argument lines");
+  static_assert(offsetof(AttnArgs, heads) < 64 && offsetof(AttnArgs, rows) / 64 == 1 &&
+                    offsetof(AttnArgs, dkv) / 64 == 1,
+                "argument lines");
   AttnArgs a = a_in;
   asm volatile("" : "+s"(a.heads), "+s"(a.rows));
   typedef AttnChunk<HD, J, 8, KVH> AC;
   __shared__ AttnLds<HD, 8> sm;
-  const uint32_t GQ = a.heads / a.kv_heads, sb = blockIdx.x / 8;
-  const uint32_t u = 8 * (sb / GQ) + blockIdx.x % 8;
+  const uint32_t GQ = a.dgq.d, sb = blockIdx.x / 8, sq = fdiv(sb, a.dgq);
+  const uint32_t u = 8 * sq + blockIdx.x % 8;
   if (u >= units) return;
-  const uint32_t NI = ntok * a.kv_heads, inst = u % NI, c = u / NI;
-  const uint32_t t = inst / a.kv_heads, g = inst % a.kv_heads, h = g * GQ + sb % GQ;
+  const uint32_t NI = a.dni.d, c = fdiv(u, a.dni), inst = u - c * NI;
+  const uint32_t t = fdiv(inst, a.dkv), g = inst - t * a.kv_heads, h = g * GQ + (sb - sq * GQ);
   const uint32_t tid = threadIdx.x, cl = tid & 15;
   const uint32_t row0 = c * AC::C;
   const float* qp = a.q + (uint64_t)t * a.heads * HD + h * HD + 4 * cl;
@@ -345,7 +347,11 @@ bool attn_ok(uint32_t hd) { return hd == 64 || hd == 128; }
 uint32_t attn_full_max(uint32_t hd) { return hd == 64 ? 256 : 128; }
 
 template <uint32_t HD, uint32_t J, bool SPLIT>
-static void attn_go(const AttnArgs& a, uint32_t ntok, uint32_t units, hipStream_t s, const AttnOps& ops) {
+static void attn_go(const AttnArgs& a0, uint32_t ntok, uint32_t units, hipStream_t s, const AttnOps& ops) {
+  AttnArgs a = a0;
+  a.dgq = fast_div(a.heads / a.kv_heads);
+  a.dni = fast_div(ntok * a.kv_heads);
+  a.dkv = fast_div(a.kv_heads);
   const uint32_t gq = a.heads / a.kv_heads, blocks = 8 * gq * ((units + 7) / 8);
   if (a.pf.wgs && blocks >= XCDS) {  // the warm-up workgroups: a second row (at most as many)
     AttnArgs c = a;

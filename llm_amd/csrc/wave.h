@@ -20,6 +20,21 @@ __device__ __forceinline__ uint32_t state_pos(const uint32_t* state) {
   return *(const __attribute__((address_space(4))) uint32_t*)state;
 }
 
+// n / d by a multiply and a shift, for n < 2^31 and d >= 1 (Granlund and
+// Montgomery's round-up method, "Division by invariant integers using
+// multiplication", 1994): with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1, n / d = (umulhi(n, m) + n) >> l.
+// A runtime division costs a long instruction sequence at a kernel's start.
+struct FastDiv {
+  uint32_t d, mul, sh;
+};
+inline FastDiv fast_div(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) l++;
+  return FastDiv{d, (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1), l};
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) { return (__umulhi(n, f.mul) + n) >> f.sh; }
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
