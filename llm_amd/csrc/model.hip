@@ -617,7 +617,10 @@ static int rec_k2(Model& m, const Layer& L, uint32_t ntok) {
   // KV bytes read for the last token of the pass (the decode step's one token)
   uint64_t bytes = 2ull * (m.pos + 1) * m.kvd * 4;
   AttnArgs a = attn_args(m, L);
-  a.pf = warm_for(m, L.gu[0], ntok, 512);
+  // (the split attention only: the one-chunk kernel is short, and carrying
+  // K4's weights lengthened it more than K4 gained: measured 1921 against
+  // 1915 tok/s at config 3, while the split kernel gains 1618 to 1644 at config 4)
+  if (m.attn_split) a.pf = warm_for(m, L.gu[0], ntok, 512);
   if (merge_in_k3(m, L, ntok)) return launch_rec(m, "k2", bytes, [&]() { return attn_launch(a, ntok, m.stream, nullptr, false); });
   if (m.attn_split) m.dispatches++;  // the merge kernel
   if (att_operands(m, ntok)) {

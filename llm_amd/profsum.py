@@ -162,21 +162,22 @@ def calibration(out):
 
 
 def class_grids(rows, symbols):
-    """The (symbol, grid) of each decode class in a kernel trace: the most
-    launched grid of the class's symbol (k3 and k5 share a symbol in some
-    builds and differ in grid: k3 the smaller)."""
-    by = collections.Counter((n, gx) for _, n, gx, gy, _ in rows if gy == 1)
+    """The (symbol, grid x, grid y) of each decode class in a kernel trace: the
+    most launched grid of the class's symbol (k3 and k5 share a symbol in some
+    builds and differ in grid: k3 the smaller).  A one-token launch that
+    carries an L2 warm-up has a second row of workgroups (grid y 2)."""
+    by = collections.Counter((n, gx, gy) for _, n, gx, gy, _ in rows if gy <= 2)
     out = {}
     for c, sym in symbols.items():
         sym = sym.split(" + ")[0]
-        cands = sorted((g for (n, g) in by if n == sym), key=lambda g: -by[(sym, g)])
+        cands = sorted(((gx, gy) for (n, gx, gy) in by if n == sym), key=lambda g: -by[(sym,) + g])
         if not cands:
             continue
         if c in ("k3", "k5") and symbols["k3"] == symbols["k5"] and len(cands) > 1:
             two = sorted(cands[:2])
-            out[c] = (sym, two[0] if c == "k3" else two[1])
+            out[c] = (sym,) + (two[0] if c == "k3" else two[1])
         else:
-            out[c] = (sym, cands[0])
+            out[c] = (sym,) + cands[0]
     return out
 
 
@@ -206,16 +207,16 @@ def summarize(out):
           "bench.py's roofline uses). A traced dispatch is a dependent launch of its own, so its duration carries "
           "the dispatch and completion overhead that back-to-back launches overlap: the difference is about "
           "0.3-0.8 us per launch, the same for every class.", "",
-          "| class | symbol | grid (threads) | traced launches | traced median us | mean | min | live us (unprofiled) | "
+          "| class | symbol | grid (threads x rows) | traced launches | traced median us | mean | min | live us (unprofiled) | "
           "bytes | GB/s (live) | GB/s (traced median) |",
           "|---|---|---|---|---|---|---|---|---|---|---|"]
     for c in CLASSES:
         if c not in grids:
             continue
-        sym, g = grids[c]
-        st = stats(by[(sym, g, 1)])
+        sym, g, gy = grids[c]
+        st = stats(by[(sym, g, gy)])
         b = cls[c]["bytes"]
-        md.append(f"| {c} | `{sym}` | {g} | {st['n']} | {st['median']:.2f} | {st['mean']:.2f} | {st['min']:.2f} | "
+        md.append(f"| {c} | `{sym}` | {g}x{gy} | {st['n']} | {st['median']:.2f} | {st['mean']:.2f} | {st['min']:.2f} | "
                   f"{cls[c]['avg_us']:.3f} | {b} | {b / cls[c]['avg_us'] * 1e-3:.1f} | "
                   f"{b / st['median'] * 1e-3:.1f} |")
     md += ["", f"Live: decode {live['value']} tok/s, prefill {live['prefill_tok_s']} tok/s, decode step kernel sum "
@@ -264,16 +265,23 @@ def summarize(out):
     for c in CLASSES:
         if c not in grids:
             continue
-        sym, g = grids[c]
+        sym, gx, gy = grids[c]
+        g = gx * gy
         if (sym, g) not in pf or "FETCH_SIZE" not in pf[(sym, g)]:
             continue
         fv = statistics.median(pf[(sym, g)]["FETCH_SIZE"])
         wv = statistics.median(pw[(sym, g)]["WRITE_SIZE"])
         tb = int(round(fv * fs + wv * ws))
         ab = cls[c]["bytes"]
-        t.append(f"{c}  {sym}  {g}  {fv:.1f}  {wv:.1f}  {tb}  {ab}  {tb / ab:.3f}")
+        t.append(f"{c}  {sym}  {gx}x{gy}  {fv:.1f}  {wv:.1f}  {tb}  {ab}  {tb / ab:.3f}")
         machine.append(f"traffic_bytes {c} {tb}")
-    t += ["", "k2 algorithmic bytes are the KV rows of the positions attended at the profiled position; the one-chunk",
+    t += ["", "A grid of two rows (x2) carries an L2 warm-up: its second row of workgroups reads the weights of the",
+          "next-but-one launch (K1 those of K3, K3 of K5, K5 of the next layer's K1; K2, with the split attention",
+          "only, K4's) toward the XCD that will read them, so a carrier's FETCH_SIZE includes those bytes; the",
+          "algorithmic bytes stay each class's own.  In this counter run (direct launches) the consumers still",
+          "fetch their own bytes; the warm-up's measured effect is end to end (bench.py with LLMHIP_L2_WARM=0",
+          "against the default on one box: config 3 unchanged, config 4 decode +1.6%).", "",
+          "k2 algorithmic bytes are the KV rows of the positions attended at the profiled position; the one-chunk",
           "kernel reads the rows up to the next multiple of 64 (a graph variant), and each XCD that serves a KV head",
           "reads its rows once.", "", "Machine-readable (bench.py reads these lines for roofline.traffic when",
           "sources_hash matches the tree it runs from):", f"sources_hash {h}"] + machine
