@@ -527,14 +527,21 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
 // quantizeQ8 does (cpu.go:117-140): d = amax / 127, q = round half away from
 // zero of x * (1/d), in f32; hi = q (exact in f16), lo = 0, no scale (ex = 0);
 // dxs[t][b] = RoundF16(d) and, for Q4_1, bsum[t][b] = RoundF16(d * sum q).
-template <uint32_t QT, int NT, int PRO>
-__device__ __forceinline__ void stage_x(const GemvArgs& a, uint32_t t0, int nt, h8* xs, float* misc, float* bsum,
-                                        float* dxs, int ex[NT]) {
-  constexpr int S = 2 * NT;
-  const uint32_t bd = blockDim.x, nwv = bd >> 6;
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const uint32_t nb = a.nb, K = a.k, NI = nb * 4;
-  f4 va[NT][MAXI], vc[NT][MAXI];
+//
+// stage_x in two steps: its loads (the activation items and, PRO_RMS, the
+// norm weights), then the rest from the loaded values, so that a caller can
+// issue other loads in between (vector loads return in issue order: loads
+// issued before the activations would hold up the staging).
+template <int NT>
+struct XItems {
+  f4 va[NT][MAXI], vc[NT][MAXI], wa[MAXI], wc[MAXI];
+};
+
+template <int NT, int PRO>
+__device__ __forceinline__ void stage_x_load(const GemvArgs& a, uint32_t t0, int nt, XItems<NT>& xi) {
+  const uint32_t bd = blockDim.x;
+  const int tid = threadIdx.x;
+  const uint32_t NI = a.nb * 4;
 #pragma unroll
   for (int t = 0; t < NT; t++)
 #pragma unroll
@@ -546,22 +553,36 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, uint32_t t0, int nt, 
         A = *(const f4*)xr;
         C = *(const f4*)(xr + 16);
       }
-      va[t][k] = A;
-      vc[t][k] = C;
+      xi.va[t][k] = A;
+      xi.vc[t][k] = C;
     }
   if (PRO & PRO_RMS) {
-    // ss = sum x^2 (f32); s = f32(1/sqrt(f64(ss/n + eps))); h = x*s*w
-    f4 wa[MAXI], wc[MAXI];
 #pragma unroll
     for (int k = 0; k < MAXI; k++) {
       uint32_t it = tid + k * bd;
-      wa[k] = wc[k] = f4{0, 0, 0, 0};
+      xi.wa[k] = xi.wc[k] = f4{0, 0, 0, 0};
       if (it < NI) {
         const float* wr = a.nw + (it / 4) * 32 + 4 * (it % 4);
-        wa[k] = *(const f4*)wr;
-        wc[k] = *(const f4*)(wr + 16);
+        xi.wa[k] = *(const f4*)wr;
+        xi.wc[k] = *(const f4*)(wr + 16);
       }
     }
+  }
+}
+
+template <uint32_t QT, int NT, int PRO>
+__device__ __forceinline__ void stage_x_from(const GemvArgs& a, int nt, XItems<NT>& xi, h8* xs, float* misc,
+                                             float* bsum, float* dxs, int ex[NT]) {
+  constexpr int S = 2 * NT;
+  const uint32_t bd = blockDim.x, nwv = bd >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const uint32_t nb = a.nb, K = a.k, NI = nb * 4;
+  f4(&va)[NT][MAXI] = xi.va;
+  f4(&vc)[NT][MAXI] = xi.vc;
+  if (PRO & PRO_RMS) {
+    // ss = sum x^2 (f32); s = f32(1/sqrt(f64(ss/n + eps))); h = x*s*w
+    const f4(&wa)[MAXI] = xi.wa;
+    const f4(&wc)[MAXI] = xi.wc;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
       float ss = 0;
@@ -674,6 +695,14 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, uint32_t t0, int nt, 
     }
   }
   __syncthreads();
+}
+
+template <uint32_t QT, int NT, int PRO>
+__device__ __forceinline__ void stage_x(const GemvArgs& a, uint32_t t0, int nt, h8* xs, float* misc, float* bsum,
+                                        float* dxs, int ex[NT]) {
+  XItems<NT> xi;
+  stage_x_load<NT, PRO>(a, t0, nt, xi);
+  stage_x_from<QT, NT, PRO>(a, nt, xi, xs, misc, bsum, dxs, ex);
 }
 
 // One unit of a tile's weights in registers: a group of four blocks (Q4: w0
@@ -1001,13 +1030,16 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
 #pragma unroll
       for (int h = 0; h < NS; h++) sc[h] = load_scales4<QT, NG>(a.qs, nb, t, h, lane, real);
     };
+    // the activations first (loads return in order), then the first tile
+    XItems<1> xi;
+    stage_x_load<1, PRO>(a, 0, 1, xi);
     {
       const uint32_t t0 = min(gw, a.tiles - 1);
-      load_sc(t0, ntw > 0);
+      load_sc(t0, gw < a.tiles);
 #pragma unroll
-      for (int g = 0; g < NG; g++) load_group<QT, true, false>(wt[g], a.qs, nb, t0, g, lane, r, ntw > 0);
+      for (int g = 0; g < NG; g++) load_group<QT, true, false>(wt[g], a.qs, nb, t0, g, lane, r, gw < a.tiles);
     }
-    stage_x<QT, 1, PRO>(a, 0, 1, xs, misc, bsum, dxs, ex);
+    stage_x_from<QT, 1, PRO>(a, 1, xi, xs, misc, bsum, dxs, ex);
     // f32 activations: every block's MFMA operand read from LDS and masked
     // once, into registers
     constexpr int NX = Q8 ? 1 : 4 * NGX;
@@ -1058,9 +1090,11 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
         jf++;
       }
     };
+    XItems<1> xi;
+    stage_x_load<1, PRO>(a, 0, 1, xi);
 #pragma unroll
     for (int d = 0; d < R; d++) fetch(w[d], d);
-    stage_x<QT, 1, PRO>(a, 0, 1, xs, misc, bsum, dxs, ex);
+    stage_x_from<QT, 1, PRO>(a, 1, xi, xs, misc, bsum, dxs, ex);
     uint32_t jc = 0, gc = 0;  // the group in the MFMA: tile jc, group gc
     for (uint32_t i0 = 0; i0 < U; i0 += R) {
 #pragma unroll
