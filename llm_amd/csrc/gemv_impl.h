@@ -1124,8 +1124,11 @@ constexpr int PMAXI = 4;  // items per thread in prep_kernel: k <= 32 * 4 * 256
 // memory in MFMA operand order for every workgroup of gemm_kernel.  Slots
 // past ntok (up to a whole group of 8) are zero.
 template <int PRO>
-__global__ __launch_bounds__(256) void prep_kernel(GemvArgs a) {
+__global__ __launch_bounds__(256) void prep_kernel(GemvArgs a_in) {
   extern __shared__ __attribute__((aligned(16))) float pl[];
+  // the argument lines it reads in one round (as gemv_kernel's touch_args)
+  GemvArgs a = a_in;
+  asm volatile("" : "+s"(a.rows), "+s"(a.ldx), "+s"(a.msmax), "+s"(a.tg));
   const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const uint32_t nb = a.nb, K = a.k, NI = nb * 4;
   h8* xp = (h8*)a.xp;
@@ -1392,11 +1395,17 @@ __device__ __forceinline__ void gemm_unit(float (&acc)[GT][NG][2], const WUnit (
 }
 
 template <uint32_t QT, int EPI, bool Q8, int GT, int NG>
-__global__ __launch_bounds__(64 * GEMM_MAXW) void gemm_kernel(GemvArgs a) {
+__global__ __launch_bounds__(64 * GEMM_MAXW) void gemm_kernel(GemvArgs a_in) {
   __shared__ float red[GEMM_MAXW][GT * NG * 2][64];
+  // the argument lines it reads in one round (as gemv_kernel's touch_args):
+  // 0-1 the matrix and output, 2 the epilogue's, 3 up / kparts, 4-5 the prepared operands
+  static_assert(offsetof(GemvArgs, xexp) / 64 == 4 && offsetof(GemvArgs, tg) / 64 == 5, "argument lines");
+  GemvArgs a = a_in;
+  asm volatile("" : "+s"(a.rows), "+s"(a.ldx), "+s"(a.ldy), "+s"(a.kparts), "+s"(a.msmax), "+s"(a.tg));
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int r = lane & 15, q = lane >> 4;
-  const uint32_t W = blockDim.x >> 6, nb = a.nb, ng = a.ng;
+  // W: 4 or 8 waves (gemm_shape), so the counts below are shifts
+  const uint32_t W = blockDim.x >> 6, lw = __builtin_ctz(W), nb = a.nb, ng = a.ng;
   const uint32_t g0 = blockIdx.y * NG, tile0 = blockIdx.x * GT;
   bool tv[GT];
   uint32_t tt[GT];
@@ -1412,7 +1421,7 @@ __global__ __launch_bounds__(64 * GEMM_MAXW) void gemm_kernel(GemvArgs a) {
     for (int g = 0; g < NG; g++) acc[u][g][0] = acc[u][g][1] = 0.f;
 
   // groups wave, wave + W, ...: two register sets, A and B, in turn
-  const uint32_t cnt = ng > (uint32_t)wave ? (ng - wave + W - 1) / W : 0;
+  const uint32_t cnt = ng > (uint32_t)wave ? (ng - wave + W - 1) >> lw : 0;
   const uint32_t glast = wave + (cnt ? cnt - 1 : 0) * W;
   WUnit wA[GT], wB[GT];
   XUnit<QT, Q8, NG> xA, xB;
@@ -1436,7 +1445,7 @@ __global__ __launch_bounds__(64 * GEMM_MAXW) void gemm_kernel(GemvArgs a) {
     }
     if (i < cnt) gemm_unit<QT, Q8, GT, NG, false>(acc, wA, xA, 4);
   }
-  if (a.tail && ng % W == (uint32_t)wave) {
+  if (a.tail && (ng & (W - 1)) == (uint32_t)wave) {
     WUnit wt[GT];
     XUnit<QT, Q8, NG> xt;
 #pragma unroll
