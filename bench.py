@@ -40,12 +40,13 @@ def kernel_symbols(attn_full):
     layers, Q8_0 head): gemv_kernel<type, tokens, prologue, epilogue, units
     per staging batch> (K1 after layer 0 adds the previous down projection's
     two k-halves, prologue 65; K5 before the last layer stores those halves,
-    epilogue 0), the one-chunk or split attention, the streaming head <type,
+    epilogue 0, three block groups per wave: four per staging batch), the
+    one-chunk or split attention, the streaming head <type,
     prologue, epilogue, groups per tile>."""
     return {"k1": "gemv_kernel<2u, 1, 65, 2, 2>",
             "k2": "attn_kernel<64u, 8u, false, false, false>" if attn_full else
                   "attn_kernel<64u, 8u, true, false, false>",
-            "k3": "gemv_kernel<2u, 1, 0, 1, 2>", "k4": "gemv_kernel<2u, 1, 1, 3, 2>", "k5": "gemv_kernel<2u, 1, 0, 0, 2>",
+            "k3": "gemv_kernel<2u, 1, 0, 1, 2>", "k4": "gemv_kernel<2u, 1, 1, 3, 2>", "k5": "gemv_kernel<2u, 1, 0, 0, 4>",
             "head": "gemv_stream_kernel<8u, 1, 4, 7>"}
 
 
