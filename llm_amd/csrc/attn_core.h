@@ -100,8 +100,8 @@ struct AttnChunk {
     for (uint32_t v = 0; v < V4; v++)
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        acc[v][k] += __shfl_xor(acc[v][k], 16);
-        acc[v][k] += __shfl_xor(acc[v][k], 32);
+        acc[v][k] += xor16(acc[v][k], lane);
+        acc[v][k] += xor32(acc[v][k], lane);
       }
     if (lane < 16)
 #pragma unroll
@@ -175,8 +175,8 @@ struct AttnChunk {
       for (uint32_t v = 0; v < V4; v++)
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-          acc[v][k] += __shfl_xor(acc[v][k], 16);
-          acc[v][k] += __shfl_xor(acc[v][k], 32);
+          acc[v][k] += xor16(acc[v][k], lane);
+          acc[v][k] += xor32(acc[v][k], lane);
         }
       if (lane < 16)
 #pragma unroll

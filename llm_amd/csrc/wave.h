@@ -62,6 +62,21 @@ __device__ __forceinline__ float row_max16(float x) {
   return x;
 }
 
+// x from lane ^ 16 and lane ^ 32, by gfx950's row swaps (VALU) instead of
+// LDS permutes: v_permlane16_swap(x, x) leaves row r's partner row in the
+// second result for even rows and in the first for odd rows;
+// v_permlane32_swap likewise for the two halves of the wave.
+__device__ __forceinline__ float xor16(float x, int lane) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __uint_as_float(((lane >> 4) & 1) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor32(float x, int lane) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(lane < 32 ? r[1] : r[0]);
+}
+
 __device__ __forceinline__ float lane_value(float x, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
