@@ -63,9 +63,10 @@ enum Epilogue : int {
 // after that launch's `own` (y = 0) touch one dword per 128-byte line of the
 // weight bytes the consumer's workgroups will read, each line from the XCD
 // on which its consumer workgroup will run.  Workgroups go to the 8 XCDs
-// round-robin by launch index, and a line a CU has read stays in its XCD's
-// L2 into later kernels, so the consumer's weight loads hit L2 instead of
-// the memory-side cache or HBM.  No result depends on it.  wgs = 0: none.
+// round-robin by launch index, and a line a CU has read can stay in its
+// XCD's L2 into later kernels, for the consumer's weight loads to find there
+// (or at least in the memory-side cache) rather than in HBM; measured end to
+// end, it pays at long context.  No result depends on it.  wgs = 0: none.
 constexpr uint32_t XCDS = 8;
 struct Prefetch {
   const uint8_t* qs;     // the consumer's tiles

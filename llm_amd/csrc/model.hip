@@ -503,10 +503,10 @@ static GemvArgs base_args(const Model& m, const QMat& q, uint32_t ntok) {
 }
 
 // The L2 warm-up a launch of a one-token pass carries (Prefetch): K1 that of
-// its layer's K3, K2 that of K4, K3 that of K5 and K5 that of the next
-// layer's K1, each launch's idle CUs reading the next-but-one launch's weights
-// into the L2 of the XCD that will read them.  LLMHIP_L2_WARM=0 (read once):
-// none, for comparison.
+// its layer's K3, K2 (with the split attention) that of K4, K3 that of K5 and
+// K5 that of the next layer's K1, each launch's idle CUs reading the
+// next-but-one launch's weights toward the XCD that will read them.
+// LLMHIP_L2_WARM=0 (read once): none, for comparison (results are the same).
 static bool l2_warm() {
   static const bool on = [] {
     const char* v = getenv("LLMHIP_L2_WARM");
