@@ -123,13 +123,16 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a_in, uint32_t ntok,
 // with its own causal bound; outputs (and, EMIT, the O product's operands)
 // as attn_kernel<SPLIT = false> writes them.
 template <uint32_t HD, uint32_t J, bool KVH, bool EMIT, uint32_t QN>
-__global__ __launch_bounds__(512) void attn_multi_kernel(AttnArgs a, uint32_t ntok, uint32_t units, AttnOps ops) {
+__global__ __launch_bounds__(512) void attn_multi_kernel(AttnArgs a_in, uint32_t ntok, uint32_t units, AttnOps ops) {
   typedef AttnChunk<HD, J, 8, KVH> AC;
   __shared__ AttnLds<HD, 8, QN> sm;
-  const uint32_t GQ = a.heads / a.kv_heads, sb = blockIdx.x / 8;
-  const uint32_t u = 8 * (sb / GQ) + blockIdx.x % 8;
+  // both argument lines in one round (as gemv_kernel's touch_args); divisions by multiplies (FastDiv)
+  AttnArgs a = a_in;
+  asm volatile("" : "+s"(a.heads), "+s"(a.rows));
+  const uint32_t GQ = a.dgq.d, sb = blockIdx.x / 8, sq = fdiv(sb, a.dgq);
+  const uint32_t u = 8 * sq + blockIdx.x % 8;
   if (u >= units) return;
-  const uint32_t tp = u / a.kv_heads, g = u % a.kv_heads, h = g * GQ + sb % GQ;
+  const uint32_t tp = fdiv(u, a.dkv), g = u - tp * a.kv_heads, h = g * GQ + (sb - sq * GQ);
   const uint32_t tid = threadIdx.x, cl = tid & 15;
   f4 q[QN][AC::V4];
   uint32_t n[QN];
@@ -169,14 +172,17 @@ __global__ __launch_bounds__(512) void attn_multi_kernel(AttnArgs a, uint32_t nt
 constexpr uint32_t AMMA_KS = 65, AMMA_VS = 80, AMMA_PS = 132;  // LDS row strides (bank-conflict free)
 
 template <bool KVH>
-__global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a, uint32_t ntok, uint32_t nchunks) {
+__global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a_in, uint32_t ntok, FastDiv dch) {
   constexpr uint32_t HD = 64, C = ATTN_SPLIT_ROWS;
   __shared__ float Ks[C * AMMA_KS], Vs[C * AMMA_VS], Ps[4][16 * AMMA_PS];
-  const uint32_t GQ = a.heads / a.kv_heads, nq = ntok * GQ;
-  const uint32_t c = blockIdx.x % nchunks, rest = blockIdx.x / nchunks;
-  const uint32_t g = rest % a.kv_heads, q0 = (rest / a.kv_heads) * 64;
+  // both argument lines in one round (as gemv_kernel's touch_args); divisions by multiplies (FastDiv)
+  AttnArgs a = a_in;
+  asm volatile("" : "+s"(a.heads), "+s"(a.rows));
+  const uint32_t GQ = a.dgq.d, nq = ntok * GQ;
+  const uint32_t rest = fdiv(blockIdx.x, dch), c = blockIdx.x - rest * dch.d;
+  const uint32_t qg = fdiv(rest, a.dkv), g = rest - qg * a.kv_heads, q0 = qg * 64;
   const uint32_t row0 = c * C, pos0 = state_pos(a.state);
-  const uint32_t tlast = (min(q0 + 64, nq) - 1) / GQ;
+  const uint32_t tlast = fdiv(min(q0 + 64, nq) - 1, a.dgq);
   if (q0 >= nq || row0 >= pos0 + tlast + 1) return;  // uniform: no query of the group reaches the chunk
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4, r = lane & 15;
 
@@ -202,7 +208,7 @@ __global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a, uint32_t ntok
   }
 
   // this lane's A rows: query m = r of the wave, dimensions 16 grp .. 16 grp + 15
-  const uint32_t qa = min(q0 + 16 * wave + r, nq - 1), ta = qa / GQ, ha = g * GQ + qa % GQ;
+  const uint32_t qa = min(q0 + 16 * wave + r, nq - 1), ta = fdiv(qa, a.dgq), ha = g * GQ + (qa - ta * GQ);
   f4 aq[4];
   const float* qp = a.q + (uint64_t)ta * a.heads * HD + ha * HD + 16 * grp;
 #pragma unroll
@@ -212,7 +218,7 @@ __global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a, uint32_t ntok
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const uint32_t qd = q0 + 16 * wave + 4 * grp + i;
-    nd[i] = qd < nq ? pos0 + qd / GQ + 1 : 0;
+    nd[i] = qd < nq ? pos0 + fdiv(qd, a.dgq) + 1 : 0;
   }
   __syncthreads();
 
@@ -289,7 +295,7 @@ __global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a, uint32_t ntok
   for (int i = 0; i < 4; i++) {
     const uint32_t qd = q0 + 16 * wave + 4 * grp + i;
     if (qd >= nq || row0 >= nd[i]) continue;
-    const uint32_t t = qd / GQ, h = g * GQ + qd % GQ;
+    const uint32_t t = fdiv(qd, a.dgq), h = g * GQ + (qd - t * GQ);
     const uint64_t th = (uint64_t)t * a.heads + h;
 #pragma unroll
     for (uint32_t dt = 0; dt < HD / 16; dt++) a.pv[(th * a.smax + c) * HD + 16 * dt + r] = O[dt][i];
@@ -388,12 +394,15 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* 
       constexpr uint32_t QN = 2;
       const uint32_t units = (ntok + QN - 1) / QN * a.kv_heads, gq = a.heads / a.kv_heads;
       const dim3 g(8 * gq * ((units + 7) / 8)), b(512);
+      AttnArgs m = a;
+      m.dgq = fast_div(gq);
+      m.dkv = fast_div(a.kv_heads);
       if (a.kv16) {
-        if (ops.xp) hipLaunchKernelGGL((attn_multi_kernel<64, 8, true, true, QN>), g, b, 0, s, a, ntok, units, ops);
-        else hipLaunchKernelGGL((attn_multi_kernel<64, 8, true, false, QN>), g, b, 0, s, a, ntok, units, ops);
+        if (ops.xp) hipLaunchKernelGGL((attn_multi_kernel<64, 8, true, true, QN>), g, b, 0, s, m, ntok, units, ops);
+        else hipLaunchKernelGGL((attn_multi_kernel<64, 8, true, false, QN>), g, b, 0, s, m, ntok, units, ops);
       } else {
-        if (ops.xp) hipLaunchKernelGGL((attn_multi_kernel<64, 8, false, true, QN>), g, b, 0, s, a, ntok, units, ops);
-        else hipLaunchKernelGGL((attn_multi_kernel<64, 8, false, false, QN>), g, b, 0, s, a, ntok, units, ops);
+        if (ops.xp) hipLaunchKernelGGL((attn_multi_kernel<64, 8, false, true, QN>), g, b, 0, s, m, ntok, units, ops);
+        else hipLaunchKernelGGL((attn_multi_kernel<64, 8, false, false, QN>), g, b, 0, s, m, ntok, units, ops);
       }
     } else if (a.hd == 64) attn_go<64, 8, false>(a, ntok, NI, s, ops);
     else attn_go<128, 4, false>(a, ntok, NI, s, ops);
@@ -409,8 +418,12 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* 
   } else if (a.hd == 64) {
     // several tokens: the matrix-core form, 64 queries of a KV head per workgroup
     const uint32_t blocks = chunks * a.kv_heads * ((ntok * (a.heads / a.kv_heads) + 63) / 64);
-    if (a.kv16) hipLaunchKernelGGL((attn_mma_kernel<true>), dim3(blocks), dim3(256), 0, s, a, ntok, chunks);
-    else hipLaunchKernelGGL((attn_mma_kernel<false>), dim3(blocks), dim3(256), 0, s, a, ntok, chunks);
+    AttnArgs b = a;
+    b.dgq = fast_div(a.heads / a.kv_heads);
+    b.dkv = fast_div(a.kv_heads);
+    const FastDiv dch = fast_div(chunks);
+    if (a.kv16) hipLaunchKernelGGL((attn_mma_kernel<true>), dim3(blocks), dim3(256), 0, s, b, ntok, dch);
+    else hipLaunchKernelGGL((attn_mma_kernel<false>), dim3(blocks), dim3(256), 0, s, b, ntok, dch);
   } else {
     attn_go<128, ATTN_SPLIT_ROWS / 32, true>(a, ntok, NI * chunks, s, ops);
   }
