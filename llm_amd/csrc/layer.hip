@@ -381,7 +381,7 @@ static void attn_go(const AttnArgs& a0, uint32_t ntok, uint32_t units, hipStream
 int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* ops_in, bool merge) {
   if (ntok == 0) return 0;
   const AttnOps ops = ops_in ? *ops_in : AttnOps{nullptr, nullptr, nullptr, nullptr, 0};
-  if (!attn_ok(a.hd) || a.rows == 0 || a.rows > a.ctx || a.heads % a.kv_heads)
+  if (!attn_ok(a.hd) || a.rows == 0 || a.rows > a.ctx || a.kv_heads == 0 || a.heads % a.kv_heads)
     return set_error(LLMHIP_ERR_ARG, "llm: attention: head size %u, %u rows of %u not supported", a.hd, a.rows,
                      a.ctx);
   if (a.pf.wgs && (ntok != 1 || ops.xp || a.pf.wgs % XCDS || !a.pf.qs))

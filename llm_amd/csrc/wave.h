@@ -29,6 +29,7 @@ struct FastDiv {
   uint32_t d, mul, sh;
 };
 inline FastDiv fast_div(uint32_t d) {
+  if (d == 0) return FastDiv{0, 0, 0};  // no divisor: callers check their divisors first
   uint32_t l = 0;
   while ((1ull << l) < d) l++;
   return FastDiv{d, (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1), l};
