@@ -89,7 +89,7 @@ struct AttnChunk {
     for (uint32_t j = 0; j < J; j++) {
       const uint32_t p = row0 + slot + S * j;
       if (p < n) {
-        const float e = expf(sj[j] - M);
+        const float e = __expf(sj[j] - M);  // v_exp_f32: a few ulp, inside the parity bounds
         l += e;
 #pragma unroll
         for (uint32_t v = 0; v < V4; v++) acc[v] += e * vr[j][v];
@@ -164,7 +164,7 @@ struct AttnChunk {
       for (uint32_t j = 0; j < J; j++) {
         const uint32_t p = row0 + slot + S * j;
         if (p < n[i]) {
-          const float e = expf(sj[i][j] - M);
+          const float e = __expf(sj[i][j] - M);
           l += e;
 #pragma unroll
           for (uint32_t v = 0; v < V4; v++) acc[v] += e * vr[j][v];

@@ -260,7 +260,7 @@ __global__ __launch_bounds__(256) void attn_mma_kernel(AttnArgs a_in, uint32_t n
 #pragma unroll
     for (uint32_t nt = 0; nt < C / 16; nt++) {
       const bool ok = row0 + 16 * nt + r < nd[i];
-      const float e = ok ? expf(S[nt][i] - m) : 0.f;
+      const float e = ok ? __expf(S[nt][i] - m) : 0.f;
       l += e;
       Ps[wave][(4 * grp + i) * AMMA_PS + 16 * nt + r] = e;
     }
