@@ -1613,7 +1613,7 @@ __device__ __forceinline__ void merge_items(ItemsOf<1, PRO>& it, const GemvArgs&
 #pragma unroll
   for (uint32_t c = 0; c < MC; c++) {
     const bool in = c < it.P;
-    const float w = in ? expf(it.mc[c] - M) : 0.f;
+    const float w = in ? __expf(it.mc[c] - M) : 0.f;
     L += w * (in ? it.lc[c] : 0.f);
 #pragma unroll
     for (int k = 0; k < 4; k++) {

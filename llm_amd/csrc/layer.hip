@@ -333,12 +333,12 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a, AttnOps ops,
     float M2 = M;
 #pragma unroll
     for (uint32_t i = 0; i < B; i++) M2 = fmaxf(M2, c0 + i < P ? mc[i] : -INFINITY);
-    const float r = expf(M - M2);  // 0 on the first batch (M = -inf)
+    const float r = __expf(M - M2);  // 0 on the first batch (M = -inf)
     L *= r;
     o *= r;
 #pragma unroll
     for (uint32_t i = 0; i < B; i++) {
-      const float w = c0 + i < P ? expf(mc[i] - M2) : 0.f;
+      const float w = c0 + i < P ? __expf(mc[i] - M2) : 0.f;
       L += w * lc[i];
       o += w * oc[i];
     }
