@@ -448,13 +448,13 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
       if (okA) {
         uint64_t o = (uint64_t)tokA * a.ldy + lr;
         float gg = a.aux[o];
-        a.y[o] = gg / (1.f + expf(-gg)) * vA;
+        a.y[o] = gg / (1.f + __expf(-gg)) * vA;
         if (a.up) a.up[o] = vA;  // after the gate was read: up may alias aux
       }
       if (okB) {
         uint64_t o = (uint64_t)tokB * a.ldy + lr;
         float gg = a.aux[o];
-        a.y[o] = gg / (1.f + expf(-gg)) * vB;
+        a.y[o] = gg / (1.f + __expf(-gg)) * vB;
         if (a.up) a.up[o] = vB;
       }
     }
@@ -508,8 +508,8 @@ __device__ __forceinline__ void row_epilogue(const GemvArgs& a, uint32_t tile, i
     const uint32_t i = 8 * tile + (r & 7);
     float* dst = r < 8 ? a.y : a.up;
     if (active && i < a.ff && dst) {
-      if (okA) dst[(uint64_t)tokA * a.ff + i] = r < 8 ? vA / (1.f + expf(-vA)) * uA : vA;
-      if (okB) dst[(uint64_t)tokB * a.ff + i] = r < 8 ? vB / (1.f + expf(-vB)) * uB : vB;
+      if (okA) dst[(uint64_t)tokA * a.ff + i] = r < 8 ? vA / (1.f + __expf(-vA)) * uA : vA;
+      if (okB) dst[(uint64_t)tokB * a.ff + i] = r < 8 ? vB / (1.f + __expf(-vB)) * uB : vB;
     }
   }
 }
