@@ -89,6 +89,20 @@ __device__ __forceinline__ void prefetch_run(const Prefetch& p, uint32_t j) {
   asm volatile("" ::"v"(acc));
 }
 
+// f32(1 / sqrt(x)) of a double x (cpu.go:92-95: float32(1/math.Sqrt(...)))
+// without the f64 divide and square-root sequences on the decode kernels'
+// critical path: v_rsq_f64's estimate refined by two Newton steps in f64
+// (each at least doubles its correct bits), then rounded to f32.  x > 0 and
+// finite (the sum of squares plus eps); anything else takes the exact form.
+__device__ __forceinline__ float rms_scale(double x) {
+  if (!(x > 0.0 && x <= 1.7976931348623157e308)) return (float)(1.0 / sqrt(x));
+  double y = __builtin_amdgcn_rsq(x);
+  const double h = 0.5 * x;
+  y = y * (1.5 - h * y * y);
+  y = y * (1.5 - h * y * y);
+  return (float)y;
+}
+
 // ------------------------------------------------------------ row maps
 
 // (hd, the head size of a NEOX map, is a power of two: the model admits 64
@@ -1932,7 +1946,7 @@ __global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(Ge
     for (int t = 0; t < NT; t++) {
       float ss = 0;
       for (uint32_t v = 0; v < nwv; v++) ss += misc[v * NT + t];
-      rs[t] = t < nt ? (float)(1.0 / sqrt((double)(ss / (float)a.k + a.eps))) : 0.f;
+      rs[t] = t < nt ? rms_scale((double)(ss / (float)a.k + a.eps)) : 0.f;
     }
   };
   // LATE (f32 activations): the units are staged as x * w and the products
