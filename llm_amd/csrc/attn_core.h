@@ -36,23 +36,28 @@ struct AttnChunk {
   static constexpr uint32_t V4 = HD / 64, S = 4 * NW, C = S * J;
   f4 kr[J][V4], vr[J][V4];
 
-  // Issue the loads of rows row0 + slot + S*j in [from, lim) of KV head g
-  // (the cache is [2][ctx][kvd]); other rows are left as they are.
+  // Issue the loads of rows row0 + slot + S*j of KV head g (the cache is
+  // [2][ctx][kvd]); a row at or past lim (1 <= lim <= ctx) loads row lim - 1
+  // instead, which reduce masks out with the rest past the causal bound.
+  // The loads are unconditional and all key rows go out before the value
+  // rows: loads complete in issue order, so the scores wait for the keys
+  // only, and the values arrive under the score, max and barrier phase.
   __device__ __forceinline__ void load(const float* kv, uint32_t kvd, uint32_t ctx, uint32_t g, uint32_t row0,
-                                       uint32_t lim, uint32_t from = 0) {
+                                       uint32_t lim) {
     const uint32_t cl = threadIdx.x & 15, slot = threadIdx.x >> 4;
     const uint64_t kb = g * HD + 4 * cl, vb = (uint64_t)ctx * kvd + g * HD + 4 * cl;  // element offsets
+    uint32_t p[J];
 #pragma unroll
-    for (uint32_t j = 0; j < J; j++) {
-      const uint32_t p = row0 + slot + S * j;
-      if (p >= from && p < lim) {
+    for (uint32_t j = 0; j < J; j++) p[j] = min(row0 + slot + S * j, lim - 1);
 #pragma unroll
-        for (uint32_t v = 0; v < V4; v++) {
-          kr[j][v] = kv_load4<KVH>(kv, kb + (uint64_t)p * kvd + 64 * v);
-          vr[j][v] = kv_load4<KVH>(kv, vb + (uint64_t)p * kvd + 64 * v);
-        }
-      }
-    }
+    for (uint32_t j = 0; j < J; j++)
+#pragma unroll
+      for (uint32_t v = 0; v < V4; v++) kr[j][v] = kv_load4<KVH>(kv, kb + (uint64_t)p[j] * kvd + 64 * v);
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++)
+#pragma unroll
+      for (uint32_t v = 0; v < V4; v++) vr[j][v] = kv_load4<KVH>(kv, vb + (uint64_t)p[j] * kvd + 64 * v);
+    __builtin_amdgcn_sched_barrier(0);  // no arithmetic (and no wait) scheduled between the loads
   }
 
   // The rows below n (all of them loaded or set), with q the lane's float4
