@@ -22,7 +22,6 @@ struct AttnArgs {
   float scale;     // f32(1/sqrt(hd)), cpu.go:304
   // attn_kernel's divisors (heads / kv_heads, ntok * kv_heads, kv_heads), set by attn_launch
   FastDiv dgq, dni, dkv;
-  Prefetch pf;     // one token: an L2 warm-up for a later launch (attn_kernel carries it)
 };
 
 // Prefill: att also written as the output projection's prepared operands (per

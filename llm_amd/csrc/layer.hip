@@ -73,10 +73,6 @@ __device__ __forceinline__ void emit_operand(const AttnOps& a, uint32_t t, uint3
 //     bound write nothing.
 template <uint32_t HD, uint32_t J, bool SPLIT, bool KVH, bool EMIT = false>
 __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a_in, uint32_t ntok, uint32_t units, AttnOps ops) {
-  if (blockIdx.y != 0) {  // the L2 warm-up row
-    if (blockIdx.x < a_in.pf.wgs) prefetch_run(a_in.pf, blockIdx.x);
-    return;
-  }
   // both lines of the arguments it reads in one round of scalar loads (as gemv_kernel's touch_args)
   static_assert(offsetof(AttnArgs, heads) < 64 && offsetof(AttnArgs, rows) / 64 == 1 &&
                     offsetof(AttnArgs, dkv) / 64 == 1,
@@ -359,15 +355,6 @@ static void attn_go(const AttnArgs& a0, uint32_t ntok, uint32_t units, hipStream
   a.dni = fast_div(ntok * a.kv_heads);
   a.dkv = fast_div(a.kv_heads);
   const uint32_t gq = a.heads / a.kv_heads, blocks = 8 * gq * ((units + 7) / 8);
-  if (a.pf.wgs && blocks >= XCDS) {  // the warm-up workgroups: a second row (at most as many)
-    AttnArgs c = a;
-    c.pf.own = blocks;
-    c.pf.wgs = std::min(a.pf.wgs, blocks / XCDS * XCDS);
-    const dim3 g(blocks, 2), b(512);
-    if (a.kv16) hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT, true>), g, b, 0, s, c, ntok, units, ops);
-    else hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT, false>), g, b, 0, s, c, ntok, units, ops);
-    return;
-  }
   const dim3 g(blocks), b(512);
   if (!SPLIT && ops.xp) {  // prefill: also the output projection's operands
     if (a.kv16) hipLaunchKernelGGL((attn_kernel<HD, J, false, true, true>), g, b, 0, s, a, ntok, units, ops);
@@ -384,8 +371,6 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* 
   if (!attn_ok(a.hd) || a.rows == 0 || a.rows > a.ctx || a.kv_heads == 0 || a.heads % a.kv_heads)
     return set_error(LLMHIP_ERR_ARG, "llm: attention: head size %u, %u rows of %u not supported", a.hd, a.rows,
                      a.ctx);
-  if (a.pf.wgs && (ntok != 1 || ops.xp || a.pf.wgs % XCDS || !a.pf.qs))
-    return set_error(LLMHIP_ERR_ARG, "llm: attention: an L2 warm-up rides on a one-token launch, in groups of 8");
   const uint32_t NI = ntok * a.kv_heads;
   if (!a.split) {
     if (a.rows > attn_full_max(a.hd)) return set_error(LLMHIP_ERR_ARG, "llm: attention: %u rows in one chunk", a.rows);

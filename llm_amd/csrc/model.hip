@@ -503,9 +503,9 @@ static GemvArgs base_args(const Model& m, const QMat& q, uint32_t ntok) {
 }
 
 // The L2 warm-up a launch of a one-token pass carries (Prefetch): K1 that of
-// its layer's K3, K2 (with the split attention) that of K4, K3 that of K5 and
-// K5 that of the next layer's K1, each launch's idle CUs reading the
-// next-but-one launch's weights toward the XCD that will read them.
+// its layer's K3, K3 that of K5 and K5 that of the next layer's K1, each
+// launch's idle CUs reading the next-but-one launch's weights toward the XCD
+// that will read them.
 // LLMHIP_L2_WARM=0 (read once): none, for comparison (results are the same).
 static bool l2_warm() {
   static const bool on = [] {
@@ -617,10 +617,9 @@ static int rec_k2(Model& m, const Layer& L, uint32_t ntok) {
   // KV bytes read for the last token of the pass (the decode step's one token)
   uint64_t bytes = 2ull * (m.pos + 1) * m.kvd * 4;
   AttnArgs a = attn_args(m, L);
-  // (the split attention only: the one-chunk kernel is short, and carrying
-  // K4's weights lengthened it more than K4 gained: measured 1921 against
-  // 1915 tok/s at config 3, while the split kernel gains 1618 to 1644 at config 4)
-  if (m.attn_split) a.pf = warm_for(m, L.gu[0], ntok, 512);
+  // (it carries no warm-up: K4's weights read by its idle CUs slowed the
+  // split kernel more than K4 gained, config-4 decode 1751 against 1694 tok/s,
+  // and the one-chunk kernel is too short to hide them, 1921 against 1915 at config 3)
   if (merge_in_k3(m, L, ntok)) return launch_rec(m, "k2", bytes, [&]() { return attn_launch(a, ntok, m.stream, nullptr, false); });
   if (m.attn_split) m.dispatches++;  // the merge kernel
   if (att_operands(m, ntok)) {

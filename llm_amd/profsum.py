@@ -276,11 +276,11 @@ def summarize(out):
         t.append(f"{c}  {sym}  {gx}x{gy}  {fv:.1f}  {wv:.1f}  {tb}  {ab}  {tb / ab:.3f}")
         machine.append(f"traffic_bytes {c} {tb}")
     t += ["", "A grid of two rows (x2) carries an L2 warm-up: its second row of workgroups reads the weights of the",
-          "next-but-one launch (K1 those of K3, K3 of K5, K5 of the next layer's K1; K2, with the split attention",
-          "only, K4's) toward the XCD that will read them, so a carrier's FETCH_SIZE includes those bytes; the",
-          "algorithmic bytes stay each class's own.  In this counter run (direct launches) the consumers still",
-          "fetch their own bytes; the warm-up's measured effect is end to end (bench.py with LLMHIP_L2_WARM=0",
-          "against the default on one box: config 3 unchanged, config 4 decode +1.6%).", "",
+          "next-but-one launch (K1 those of K3, K3 of K5, K5 of the next layer's K1) toward the XCD that will read",
+          "them, so a carrier's FETCH_SIZE includes those bytes; the algorithmic bytes stay each class's own.  In",
+          "this counter run (direct launches) the consumers still fetch their own bytes; the warm-up's measured",
+          "effect is end to end (bench.py with LLMHIP_L2_WARM=0 against the default on one box: config 3 unchanged,",
+          "config 4 decode +1.4%).", "",
           "k2 algorithmic bytes are the KV rows of the positions attended at the profiled position; the one-chunk",
           "kernel reads the rows up to the next multiple of 64 (a graph variant), and each XCD that serves a KV head",
           "reads its rows once.", "", "Machine-readable (bench.py reads these lines for roofline.traffic when",
