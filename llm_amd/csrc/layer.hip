@@ -365,6 +365,27 @@ static void attn_go(const AttnArgs& a0, uint32_t ntok, uint32_t units, hipStream
   else hipLaunchKernelGGL((attn_kernel<HD, J, SPLIT, false>), g, b, 0, s, a, ntok, units, ops);
 }
 
+// The one-chunk attention at head size 64 over 32 * J rows: one token as
+// attn_kernel, several two tokens per workgroup (attn_multi_kernel; measured:
+// prefill 53.8k -> 54.8k tok/s, four tokens 53.4k).
+template <uint32_t J>
+static void attn_one_chunk64(const AttnArgs& a, uint32_t ntok, uint32_t NI, hipStream_t s, const AttnOps& ops) {
+  if (ntok == 1) return attn_go<64, J, false>(a, ntok, NI, s, ops);
+  constexpr uint32_t QN = 2;
+  const uint32_t units = (ntok + QN - 1) / QN * a.kv_heads, gq = a.heads / a.kv_heads;
+  const dim3 g(8 * gq * ((units + 7) / 8)), b(512);
+  AttnArgs m = a;
+  m.dgq = fast_div(gq);
+  m.dkv = fast_div(a.kv_heads);
+  if (a.kv16) {
+    if (ops.xp) hipLaunchKernelGGL((attn_multi_kernel<64, J, true, true, QN>), g, b, 0, s, m, ntok, units, ops);
+    else hipLaunchKernelGGL((attn_multi_kernel<64, J, true, false, QN>), g, b, 0, s, m, ntok, units, ops);
+  } else {
+    if (ops.xp) hipLaunchKernelGGL((attn_multi_kernel<64, J, false, true, QN>), g, b, 0, s, m, ntok, units, ops);
+    else hipLaunchKernelGGL((attn_multi_kernel<64, J, false, false, QN>), g, b, 0, s, m, ntok, units, ops);
+  }
+}
+
 int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* ops_in, bool merge) {
   if (ntok == 0) return 0;
   const AttnOps ops = ops_in ? *ops_in : AttnOps{nullptr, nullptr, nullptr, nullptr, 0};
@@ -374,23 +395,17 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* 
   const uint32_t NI = ntok * a.kv_heads;
   if (!a.split) {
     if (a.rows > attn_full_max(a.hd)) return set_error(LLMHIP_ERR_ARG, "llm: attention: %u rows in one chunk", a.rows);
-    if (a.hd == 64 && ntok > 1) {
-      // two tokens per workgroup (measured: prefill 53.8k -> 54.8k tok/s; four: 53.4k)
-      constexpr uint32_t QN = 2;
-      const uint32_t units = (ntok + QN - 1) / QN * a.kv_heads, gq = a.heads / a.kv_heads;
-      const dim3 g(8 * gq * ((units + 7) / 8)), b(512);
-      AttnArgs m = a;
-      m.dgq = fast_div(gq);
-      m.dkv = fast_div(a.kv_heads);
-      if (a.kv16) {
-        if (ops.xp) hipLaunchKernelGGL((attn_multi_kernel<64, 8, true, true, QN>), g, b, 0, s, m, ntok, units, ops);
-        else hipLaunchKernelGGL((attn_multi_kernel<64, 8, true, false, QN>), g, b, 0, s, m, ntok, units, ops);
-      } else {
-        if (ops.xp) hipLaunchKernelGGL((attn_multi_kernel<64, 8, false, true, QN>), g, b, 0, s, m, ntok, units, ops);
-        else hipLaunchKernelGGL((attn_multi_kernel<64, 8, false, false, QN>), g, b, 0, s, m, ntok, units, ops);
-      }
-    } else if (a.hd == 64) attn_go<64, 8, false>(a, ntok, NI, s, ops);
-    else attn_go<128, 4, false>(a, ntok, NI, s, ops);
+    if (a.hd == 64) {
+      // 32 * J rows per workgroup, J the least even count covering a.rows
+      // (a graph variant's multiple of 64), so that few loads repeat the last row
+      const uint32_t J = (a.rows + 63) / 64 * 2;
+      if (J <= 2) attn_one_chunk64<2>(a, ntok, NI, s, ops);
+      else if (J <= 4) attn_one_chunk64<4>(a, ntok, NI, s, ops);
+      else if (J <= 6) attn_one_chunk64<6>(a, ntok, NI, s, ops);
+      else attn_one_chunk64<8>(a, ntok, NI, s, ops);
+    } else {
+      attn_go<128, 4, false>(a, ntok, NI, s, ops);
+    }
     LLM_HIP(hipGetLastError());
     return 0;
   }
