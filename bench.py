@@ -381,8 +381,8 @@ def main():
                          "stream launches, for a profiler: e.g. q4_0:151936x896,q8_0:896x896:64")
     args = ap.parse_args()
     if args.gpus != 1:
-        log("bench.py: this build measures one GPU; the path shards by independent sequences per GPU "
-            "(see DESIGN.md), and no multi-GPU figure is taken")
+        log("bench.py: this build measures one GPU; the path shards by independent sequences, one "
+            "process per GPU, and no multi-GPU figure is taken")
         sys.exit(2)
     from llm_amd import _lib
     if _lib.device_count() < 1:

@@ -3,7 +3,7 @@
 // How examples/generate obtains its GPU in the hip build: device 0 through
 // libllmhip.so, with the device's own limits.  The WebGPU build keeps the
 // batchsink code of main.go:81-96 in device_webgpu.go (//go:build !hip);
-// main.go calls openGPU in their place (INTEGRATION.md shows the edit).
+// main.go calls openGPU in their place (a two-line edit of main.go).
 
 package main
 

@@ -7,7 +7,7 @@
  *
  *  1. llmhip_*  — the device layer.  This is what the Go package's cgo wrapper
  *     binds (its NewGPU keeps parsing the GGUF header and ConfigFrom in Go and
- *     streams raw tensor bytes in).  It replaces the
+ *     streams raw tensor bytes in, go/gpu_hip.go).  It replaces the
  *     webgpu Device / Recorder / Submit / Readback the reference drives.
  *  2. llm_*     — a C++ restatement of the reference's host package for hosts
  *     without Go (tests, benchmarks, the C++ `generate` tool): the GGUF header
