@@ -10,14 +10,9 @@
 #include <cstdio>
 #include <string>
 
-#include "../../include/llmhip.h"
+#include "errors.h"
 
 namespace llmhip {
-
-// Records the thread's last error ("llm: ..."), returns code.
-int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-void clear_error();
-const char* last_error();
 
 #define LLM_HIP(call)                                                                            \
   do {                                                                                           \
@@ -25,12 +20,6 @@ const char* last_error();
     if (e_ != hipSuccess)                                                                        \
       return ::llmhip::set_error(LLMHIP_ERR_DEVICE, "llm: %s failed: %s (%s:%d)", #call,         \
                                  hipGetErrorString(e_), __FILE__, __LINE__);                     \
-  } while (0)
-
-#define LLM_TRY(expr)     \
-  do {                    \
-    int r_ = (expr);      \
-    if (r_ != 0) return r_; \
   } while (0)
 
 // ggml block geometry (gguf/gguf.go:72-92) for the types with kernels.

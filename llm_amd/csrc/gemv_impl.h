@@ -2107,6 +2107,9 @@ static int launch_stream(const GemvArgs& a, hipStream_t s) {
 template <uint32_t QT>
 int gemv_launch_qt(const GemvArgs& a, int pro, int epi, hipStream_t s) {
   if (a.stream && a.ntok == 1) {
+    // the streaming kernel walks whole groups of four blocks only
+    if (a.tail != 0)
+      return set_error(LLMHIP_ERR_ARG, "llm: gemv: the streaming kernel takes no tail blocks (k %u)", a.k);
     switch (pro * 8 + epi) {
       case PRO_PLAIN * 8 + EPI_STORE: return launch_stream<QT, PRO_PLAIN, EPI_STORE>(a, s);
       case PRO_PLAIN * 8 + EPI_ACC: return launch_stream<QT, PRO_PLAIN, EPI_ACC>(a, s);

@@ -527,9 +527,13 @@ static Prefetch warm_for(const Model& m, const QMat& q, uint32_t ntok, uint32_t 
 // Whether a one-token K5 (bound in a) runs in two k-parts whose halves the
 // next layer's K1 adds: `want` when that K1 follows in the same pass.
 // (The summing prologue holds the whole row in two float4s per lane: k <= 512 * 4 waves.)
+// Decode passes only (!embed_in): the halves buffer and the flags that pass
+// them from K5 to K1 to K3 belong to the model, not to a prefill lane, and a
+// prefill's segments of different chunks (a one-token last chunk beside a
+// 64-token one, or every chunk at PrefillBatch 1) are recorded interleaved.
 static bool k5_splits(const Model& m, const GemvArgs& a, uint32_t ntok, bool want) {
-  return want && ntok == 1 && !m.q8 && !a.stream && a.ng >= 2 && m.cfg.embd <= 2048 && !skipped(m, "k5") &&
-         !skipped(m, "k1");
+  return want && ntok == 1 && !m.embed_in && !m.q8 && !a.stream && a.ng >= 2 && m.cfg.embd <= 2048 &&
+         !skipped(m, "k5") && !skipped(m, "k1");
 }
 
 static int pass_layers(const Model& m, bool* head);
@@ -809,6 +813,7 @@ static int record_slot(Model& m, uint32_t ntok, bool head, int s) {
 static int segments(int nl, int G) { return (nl + G) / G; }
 static int record_segment(Model& m, uint32_t ntok, bool head, bool embed_in, int g, int G) {
   m.embed_in = embed_in || ntok != 1;
+  m.k5_split = m.xsum_ready = false;  // an embedding pass never splits its K5 (k5_splits)
   bool h = head;
   const int nl = pass_layers(m, &h);
   for (int s = g * G; s < std::min((g + 1) * G, nl + 1); s++) LLM_TRY(record_slot(m, ntok, head, s));
@@ -825,6 +830,7 @@ static int segment_dep(int g, int G) { return (g * G + G - 2) / G; }
 // embedding row to xn; state advances by ntok.
 static int record_pass(Model& m, uint32_t ntok, bool head, bool embed_in) {
   m.embed_in = embed_in || ntok != 1;
+  m.k5_split = m.xsum_ready = false;  // a pass's last K5 never splits: nothing carries over
   bool h = head;
   const int nl = pass_layers(m, &h);
   for (int s = 0; s <= nl; s++) LLM_TRY(record_slot(m, ntok, head, s));

@@ -1,4 +1,4 @@
-// Host side of the quantised matrices: errors, allocation, staged upload with
+// Host side of the quantised matrices: allocation, staged upload with
 // the repack on the device, dispatch of the typed kernels, and the
 // llmhip_qmat_* / llmhip_device_* entry points.
 #include <algorithm>
@@ -10,22 +10,6 @@
 #include "gemv.h"
 
 namespace llmhip {
-
-static thread_local std::string g_err;
-
-int set_error(int code, const char* fmt, ...) {
-  char buf[1024];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof buf, fmt, ap);
-  va_end(ap);
-  g_err = buf;
-  return code;
-}
-
-void clear_error() { g_err.clear(); }
-
-const char* last_error() { return g_err.c_str(); }
 
 int qmat_place(QMat* m, int device, uint32_t type, uint64_t rows, uint64_t k, uint8_t* mem) {
   QType q;
@@ -193,16 +177,46 @@ using namespace llmhip;
 
 // ------------------------------------------------------------------ C-ABI
 
+// The scratch of llmhip_qmat_gemv_noalloc: the prepared activations of up to
+// 64 tokens of k <= LLMHIP_NOALLOC_MAX_K, one copy per device for the life of
+// the process.  Host code uses the address noalloc_scratch() returns for a
+// device, never the array's name (a host-side stand-in).
+static __device__ __align__(256) uint8_t scratch[xprep_bytes(64, LLMHIP_NOALLOC_MAX_K)];
+
+static std::mutex g_scratch_mu;
+static std::vector<void*> g_scratch_at;  // per device ordinal, from hipGetSymbolAddress
+
+// The array's address on `device`, looked up once per device with that
+// device current (the caller's current device is what it was, afterwards).
+static int noalloc_scratch(int device, void** out) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (device < 0) return set_error(LLMHIP_ERR_ARG, "llm: device %d", device);
+  if ((size_t)device >= g_scratch_at.size()) g_scratch_at.resize((size_t)device + 1, nullptr);
+  if (!g_scratch_at[(size_t)device]) {
+    int cur = 0;
+    LLM_HIP(hipGetDevice(&cur));
+    LLM_HIP(hipSetDevice(device));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    LLM_HIP(hipSetDevice(cur));
+    if (e != hipSuccess || !p)
+      return set_error(LLMHIP_ERR_DEVICE, "llm: no device address for the scratch array: %s", hipGetErrorString(e));
+    g_scratch_at[(size_t)device] = p;
+  }
+  *out = g_scratch_at[(size_t)device];
+  return 0;
+}
+
 struct llmhip_qmat {
   QMat m;
   Stager st;
   hipStream_t stream = nullptr;
   void* xprep = nullptr;  // prepared activations of up to 64 tokens (allocated on first use)
+  void* scratch = nullptr;  // this device's noalloc scratch array (resolved at create)
 };
 
 extern "C" {
 
-const char* llmhip_last_error(void) { return last_error(); }
 
 int llmhip_device_count(int* n) {
   clear_error();
@@ -339,6 +353,7 @@ int llmhip_qmat_create(int ordinal, uint32_t ggml_type, uint64_t rows, uint64_t 
   *out = nullptr;
   llmhip_qmat* q = new llmhip_qmat();
   int rc = qmat_alloc(&q->m, ordinal, ggml_type, rows, k);
+  if (rc == 0) rc = noalloc_scratch(ordinal, &q->scratch);
   if (rc != 0) {
     qmat_release(&q->m);
     delete q;
@@ -401,30 +416,6 @@ static int qmat_launch(llmhip_qmat* q, GemvArgs& a, int epi, hipStream_t s, int 
   return gemm_launch(a, q->m.g.q.type, epi, s);
 }
 
-// The scratch of llmhip_qmat_gemv_noalloc: the prepared activations of up to
-// 64 tokens of k <= LLMHIP_NOALLOC_MAX_K, one copy per device for the life of
-// the process.  Host code uses the address noalloc_scratch() returns for the
-// current device, never the array's name (a host-side stand-in).
-static __device__ __align__(256) uint8_t scratch[xprep_bytes(64, LLMHIP_NOALLOC_MAX_K)];
-
-static std::mutex g_scratch_mu;
-static std::vector<void*> g_scratch_at;  // per device ordinal, from hipGetSymbolAddress
-
-static int noalloc_scratch(int device, void** out) {
-  std::lock_guard<std::mutex> lk(g_scratch_mu);
-  if (device < 0) return set_error(LLMHIP_ERR_ARG, "llm: device %d", device);
-  if ((size_t)device >= g_scratch_at.size()) g_scratch_at.resize((size_t)device + 1, nullptr);
-  if (!g_scratch_at[(size_t)device]) {
-    LLM_HIP(hipSetDevice(device));  // the address is per device: look it up with the device current
-    void* p = nullptr;
-    LLM_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-    if (!p) return set_error(LLMHIP_ERR_DEVICE, "llm: no device address for the scratch array");
-    g_scratch_at[(size_t)device] = p;
-  }
-  *out = g_scratch_at[(size_t)device];
-  return 0;
-}
-
 int llmhip_qmat_gemv(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, int accumulate, void* hip_stream) {
   clear_error();
   GemvArgs a;
@@ -433,6 +424,9 @@ int llmhip_qmat_gemv(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, in
   return qmat_launch(q, a, accumulate ? EPI_ACC : EPI_STORE, (hipStream_t)hip_stream);
 }
 
+// Makes no runtime call but its launches (capturable into a HIP graph): the
+// scratch address was resolved at create, and an upload is complete when
+// llmhip_qmat_upload returns, so no wait for the matrix's own stream either.
 int llmhip_qmat_gemv_noalloc(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, int accumulate,
                              void* hip_stream) {
   clear_error();
@@ -441,10 +435,7 @@ int llmhip_qmat_gemv_noalloc(llmhip_qmat* q, const float* x_dev, float* y_dev, i
                      (unsigned long long)q->m.g.k, (unsigned)LLMHIP_NOALLOC_MAX_K);
   GemvArgs a;
   LLM_TRY(qmat_gemv_args(q, x_dev, y_dev, n, &a));
-  void* xp = nullptr;
-  if (a.ntok >= GEMM_MIN_TOKENS) LLM_TRY(noalloc_scratch(q->m.device, &xp));
-  LLM_TRY(qmat_ready(q));
-  return qmat_launch(q, a, accumulate ? EPI_ACC : EPI_STORE, (hipStream_t)hip_stream, PRO_PLAIN, xp);
+  return qmat_launch(q, a, accumulate ? EPI_ACC : EPI_STORE, (hipStream_t)hip_stream, PRO_PLAIN, q->scratch);
 }
 
 int llmhip_qmat_gemv_q8(llmhip_qmat* q, const float* x_dev, float* y_dev, int n, void* hip_stream) {

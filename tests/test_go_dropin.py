@@ -110,3 +110,69 @@ def test_balanced():
         code = _code(os.path.join(GO, f))
         for a, b in ("()", "{}", "[]"):
             assert code.count(a) == code.count(b), (f, a)
+
+
+# C scalar types of the header and what each may become on the Go side (the
+# conversions gpu_hip.go applies to a field it reads) and in ctypes
+C_TO_GO = {"uint32_t": {"uint32", "uint64", "int", "int64"}, "uint64_t": {"uint64"}, "int64_t": {"int", "int64"},
+           "int32_t": {"int", "int32", "int64"}, "float": {"float32", "float64"}}
+C_TO_CTYPES = {"uint32_t": "c_uint32", "uint64_t": "c_uint64", "int64_t": "c_int64", "int32_t": "c_int32",
+               "float": "c_float"}
+CGO_STRUCTS = ("llmhip_limits", "llmhip_config", "llmhip_stats")
+
+
+def _header_structs():
+    """{struct: [(field, C type)]} of the typedef'd structs in include/llmhip.h, in declaration order."""
+    src = re.sub(r"/\*.*?\*/", " ", open(os.path.join(ROOT, "include", "llmhip.h")).read(), flags=re.S)
+    out = {}
+    for body, name in re.findall(r"typedef struct \w+ \{(.*?)\} (\w+);", src, flags=re.S):
+        fields = []
+        for decl in body.split(";"):
+            m = re.match(r"\s*(u?int(?:32|64)_t|float)\s+(.*)", decl, flags=re.S)
+            if m:
+                fields += [(f.strip(), m.group(1)) for f in m.group(2).split(",")]
+        out[name] = fields
+    return out
+
+
+def test_cgo_struct_fields():
+    """Every field of C.llmhip_limits / llmhip_config / llmhip_stats that
+    gpu_hip.go reads, assigns or sets in a keyed literal exists in
+    include/llmhip.h, with a C type that matches the conversion the Go code
+    applies (gpu.go:28-36,56-60 are the Go types they fill)."""
+    structs = _header_structs()
+    code = _code(os.path.join(GO, "gpu_hip.go"))
+    checked = 0
+    for st in CGO_STRUCTS:
+        fields = dict(structs[st])
+        assert fields, st
+        names = set(re.findall(r"var (\w+) C\." + st + r"\b", code))
+        for var in names:
+            # reads: goType(var.field)
+            for goty, fl in re.findall(r"\b(\w+)\(" + var + r"\.(\w+)\)", code):
+                assert fl in fields, f"gpu_hip.go reads {st}.{fl}, which include/llmhip.h does not declare"
+                assert goty in C_TO_GO[fields[fl]], f"{st}.{fl} is {fields[fl]}, read as {goty}"
+                checked += 1
+            # writes: var.field = C.type(...)
+            for fl, cty in re.findall(r"\b" + var + r"\.(\w+)\s*=\s*C\.(\w+)\(", code):
+                assert fl in fields and fields[fl] == cty, f"{st}.{fl} assigned a C.{cty}, header has {fields.get(fl)}"
+                checked += 1
+        # keyed literals: C.st{field: C.type(...), ...}
+        for body in re.findall(r"C\." + st + r"\{(.*?)\}", code, flags=re.S):
+            keyed = re.findall(r"(\w+):\s*C\.(\w+)\(", body)
+            assert {k for k, _ in keyed} == set(fields), f"the {st} literal sets {sorted(k for k, _ in keyed)}"
+            for fl, cty in keyed:
+                assert fields[fl] == cty, f"{st}.{fl} set from a C.{cty}, header has {fields[fl]}"
+                checked += 1
+    assert checked >= 7 + 14 + 3, checked  # limits read, config literal, stats read
+
+
+def test_ctypes_structs_match_header():
+    """The Python binding's ctypes mirrors of the same structs (llm_amd/_lib.py)
+    hold the header's fields in the header's order with the same widths."""
+    import ctypes
+    from llm_amd import _lib
+    structs = _header_structs()
+    for st, cls in (("llmhip_limits", _lib.Limits), ("llmhip_config", _lib.Config), ("llmhip_stats", _lib.Stats)):
+        want = [(f, getattr(ctypes, C_TO_CTYPES[t])) for f, t in structs[st]]
+        assert [(f, t) for f, t in cls._fields_] == want, st

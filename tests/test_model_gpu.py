@@ -62,6 +62,26 @@ def test_tiny_parity(gpu, name):
     _check(g, cpu, prompt, 40)
 
 
+@pytest.mark.parametrize("prompt_len,batch", [(65, 64), (129, 64), (21, 1), (30, 4)])
+def test_prefill_chunk_edges(gpu, prompt_len, batch):
+    """Prompts whose last prefill chunk is one token (65, 129: a 64-token
+    chunk and a one-token chunk on two lanes of the wavefront), and small
+    PrefillBatch values (every chunk one token on three lanes; chunks of
+    four), on a six-layer model, so that graph segments of three and six
+    layers end between a layer's K1 and its K3: logits and greedy tokens
+    against the oracle's.  A one-token pass of a prefill runs its down
+    projection whole (the two-part form's buffer belongs to decode)."""
+    from llm_amd import llm
+    spec = synth.tiny_qwen(seed=30, layers=6)
+    old = llm.PrefillBatch
+    llm.PrefillBatch = batch
+    try:
+        g, cpu = _open(spec, 256)
+    finally:
+        llm.PrefillBatch = old
+    _check(g, cpu, synth.prompt(31, prompt_len, spec.vocab), 12)
+
+
 @pytest.mark.parametrize("prompt_len,heads,kv_heads,hd", [
     (230, 4, 4, 64), (300, 4, 2, 64), (250, 8, 2, 64), (200, 16, 2, 64), (100, 2, 1, 128), (140, 4, 2, 128)])
 def test_attention_paths(gpu, prompt_len, heads, kv_heads, hd):

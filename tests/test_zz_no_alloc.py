@@ -67,3 +67,70 @@ def test_noalloc_matches_gemv(gpu):
     assert e.value.kind == "ARG" and "8192" in str(e.value)
     for o in (xd, yd, big, m):
         o.close()
+
+
+def _hip():
+    """The HIP runtime libllmhip.so links (already mapped: the same instance)."""
+    from llm_amd import _lib
+    _lib.lib()
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    vp = ctypes.c_void_p
+    for name, args in (("hipStreamCreateWithFlags", [ctypes.POINTER(vp), ctypes.c_uint]),
+                       ("hipStreamBeginCapture", [vp, ctypes.c_int]), ("hipStreamEndCapture", [vp, ctypes.POINTER(vp)]),
+                       ("hipGraphInstantiate", [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t]),
+                       ("hipGraphLaunch", [vp, vp]), ("hipStreamSynchronize", [vp]), ("hipGraphExecDestroy", [vp]),
+                       ("hipGraphDestroy", [vp]), ("hipStreamDestroy", [vp]), ("hipSetDevice", [ctypes.c_int])):
+        getattr(hip, name).argtypes = args
+        getattr(hip, name).restype = ctypes.c_int
+    return hip
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """The allocation-free product captured into a HIP graph (64 tokens: the
+    prep and product pair on the scratch array) on a non-blocking stream,
+    captured from a fresh matrix whose first product is the captured one
+    (nothing is left to allocate or look up at call time), then replayed five
+    times with eager products of another matrix on the same scratch in
+    between; every replay is bit-equal to llmhip_qmat_gemv's result."""
+    from llm_amd import _lib, kernels
+    L, hip = _lib.lib(), _hip()
+    rng = np.random.default_rng(23)
+    rows, k, n = 4864, 896, 64
+    raw = synth.quant_blocks(synth.Q4_0, rows, k, rng)
+    m = kernels.QMat(synth.Q4_0, rows, k, raw)
+    other = kernels.QMat(synth.Q8_0, 896, 4864, synth.quant_blocks(synth.Q8_0, 896, 4864, rng, q8_div=8.0))
+    x = rng.standard_normal((n, k), dtype=np.float32)
+    xd = kernels.DeviceBuffer.from_numpy(x)
+    yd = kernels.DeviceBuffer(n * rows * 4)
+    x2 = kernels.DeviceBuffer.from_numpy(rng.standard_normal((n, 4864), dtype=np.float32))
+    y2 = kernels.DeviceBuffer(n * 896 * 4)
+    s, g, ex = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipSetDevice(0) == 0
+    assert hip.hipStreamCreateWithFlags(ctypes.byref(s), 1) == 0  # hipStreamNonBlocking
+    try:
+        assert hip.hipStreamBeginCapture(s, 1) == 0  # hipStreamCaptureModeThreadLocal
+        rc = L.llmhip_qmat_gemv_noalloc(m._h, xd.ptr, yd.ptr, n, 0, s)
+        assert hip.hipStreamEndCapture(s, ctypes.byref(g)) == 0
+        _lib.check(rc)
+        assert hip.hipGraphInstantiate(ctypes.byref(ex), g, None, None, 0) == 0
+        ref = kernels.DeviceBuffer(n * rows * 4)
+        _lib.check(L.llmhip_qmat_gemv(m._h, xd.ptr, ref.ptr, n, 0, None))
+        kernels.synchronize()
+        want = ref.numpy(np.float32, (n, rows))
+        for rep in range(5):
+            yd.write(np.full((n, rows), np.nan, np.float32))
+            _lib.check(L.llmhip_qmat_gemv_noalloc(other._h, x2.ptr, y2.ptr, n, 0, None))  # the scratch, reused
+            kernels.synchronize()
+            assert hip.hipGraphLaunch(ex, s) == 0 and hip.hipStreamSynchronize(s) == 0
+            got = yd.numpy(np.float32, (n, rows))
+            print(f"replay {rep}: bit-equal {np.array_equal(got.view(np.uint32), want.view(np.uint32))}", flush=True)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), rep
+        ref.close()
+    finally:
+        if ex.value:
+            hip.hipGraphExecDestroy(ex)
+        if g.value:
+            hip.hipGraphDestroy(g)
+        hip.hipStreamDestroy(s)
+        for o in (xd, yd, x2, y2, m, other):
+            o.close()
