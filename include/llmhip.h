@@ -247,6 +247,21 @@ LLMHIP_API int llmhip_model_set_kv_f16(llmhip_model* m, int on);
  * Results match the CPU path with ExactGGML set, not the f32 path.  Call
  * before the first upload. */
 LLMHIP_API int llmhip_model_set_exact_ggml(llmhip_model* m, int on);
+/* The fused decode pass: a decode step's layers in one persistent launch
+ * whose phases (QKV, attention, output projection, gate/up, down) hand their
+ * results to each other through flag-carrying words instead of kernel
+ * boundaries (3 dispatches per token with the head and the sampling kernel,
+ * against five per layer in the reference, fused.go:259-265).  Taken by every
+ * decode step of a model that fits it (finalize decides: one-chunk attention,
+ * embedding <= 1024, feed-forward <= 6144, fused QKV and gate/up groups, f32
+ * activations), else the steps run one launch per kernel; results agree with
+ * the CPU path within the same bounds either way.  on = 0 turns it off, 1 on;
+ * poll_limit > 0 makes a hand-off wait give up after that many polls (0: the
+ * default, about a second), after which the decode call fails with
+ * LLMHIP_ERR_DEVICE and later steps take one launch per kernel.  Returns 1
+ * when decode steps take the fused launch, 0 when not (why, if not null,
+ * receives the reason, cap bytes at most), < 0 on error. */
+LLMHIP_API int llmhip_model_set_fused(llmhip_model* m, int on, uint32_t poll_limit, char* why, uint64_t cap);
 /* Run only the first `layers` layers (no head, no sampling; Layers, gpu.go:143-146). 0 = all. */
 LLMHIP_API int llmhip_model_set_layers(llmhip_model* m, int layers);
 /* Leave kernel classes out of every pass, comma-separated (Skip, gpu.go:769-784):

@@ -98,6 +98,7 @@ SIGNATURES = [
     ("llmhip_model_memory_used", U64, [P]),
     ("llmhip_model_stats", I, [P, ctypes.POINTER(Stats)]),
     ("llmhip_model_config", I, [P, ctypes.POINTER(Config), ctypes.POINTER(I)]),
+    ("llmhip_model_set_fused", I, [P, I, U32, ctypes.c_char_p, U64]),
     ("llmhip_model_set_layers", I, [P, I]),
     ("llmhip_model_set_kv_f16", I, [P, I]),
     ("llmhip_model_set_exact_ggml", I, [P, I]),

@@ -53,10 +53,11 @@ int attn_launch(const AttnArgs& a, uint32_t ntok, hipStream_t s, const AttnOps* 
 // Greedy sampling from the head's per-workgroup partials, the token written
 // to tokens[step + adv] and out[0], the state advanced by adv; with embd and
 // xn also the sampled token's embedding row into xn (the input of the next
-// one-token pass, which then runs no embedding kernel).
+// one-token pass, which then runs no embedding kernel); with epoch, epoch[0]
+// advanced by one (the fused decode pass's flags, pass.h).
 int argmax_launch(const float* pv, const uint32_t* pi, uint32_t n, const float* logits, int32_t* tokens,
                   int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s, const QMat* embd = nullptr,
-                  float* xn = nullptr);
+                  float* xn = nullptr, uint32_t* epoch = nullptr);
 int advance_launch(uint32_t* state, uint32_t n, hipStream_t s);
 // state = (p, p) (a prefill chunk on a lane of its own).
 int set_state_launch(uint32_t* state, uint32_t p, hipStream_t s);

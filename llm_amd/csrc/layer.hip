@@ -457,7 +457,8 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
                                                       int32_t* __restrict__ tokens, int32_t* __restrict__ outb,
                                                       uint32_t* __restrict__ state, uint32_t adv,
                                                       const uint8_t* __restrict__ eq, uint64_t etiles, uint32_t enb,
-                                                      uint32_t eng, uint32_t etail, float* __restrict__ xn) {
+                                                      uint32_t eng, uint32_t etail, float* __restrict__ xn,
+                                                      uint32_t* __restrict__ epoch) {
   __shared__ float sv[16];
   __shared__ uint32_t si[16];
   __shared__ uint32_t tok;
@@ -515,6 +516,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
     state[0] += adv;
     state[1] = step + adv;
     tok = bi;
+    if (epoch) epoch[0] += 1;  // the fused decode pass's flags (pass.h): a new value after every head pass
   }
   if (QT != 0) {
     __syncthreads();
@@ -528,17 +530,18 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
 }
 
 int argmax_launch(const float* pv, const uint32_t* pi, uint32_t n, const float* logits, int32_t* tokens,
-                  int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s, const QMat* e, float* xn) {
+                  int32_t* outb, uint32_t* state, uint32_t adv, hipStream_t s, const QMat* e, float* xn,
+                  uint32_t* epoch) {
   const dim3 g(1), b(1024);
   if (!e || !xn) {
     hipLaunchKernelGGL(argmax_kernel<0>, g, b, 0, s, pv, pi, n, logits, tokens, outb, state, adv, nullptr, 0ull, 0u,
-                       0u, 0u, nullptr);
+                       0u, 0u, nullptr, epoch);
   } else if (e->g.q.type == LLMHIP_Q4_0) {
     hipLaunchKernelGGL(argmax_kernel<LLMHIP_Q4_0>, g, b, 0, s, pv, pi, n, logits, tokens, outb, state, adv, e->qs,
-                       (uint64_t)e->g.tiles, e->g.nb, e->g.ng, e->g.tail, xn);
+                       (uint64_t)e->g.tiles, e->g.nb, e->g.ng, e->g.tail, xn, epoch);
   } else if (e->g.q.type == LLMHIP_Q8_0) {
     hipLaunchKernelGGL(argmax_kernel<LLMHIP_Q8_0>, g, b, 0, s, pv, pi, n, logits, tokens, outb, state, adv, e->qs,
-                       (uint64_t)e->g.tiles, e->g.nb, e->g.ng, e->g.tail, xn);
+                       (uint64_t)e->g.tiles, e->g.nb, e->g.ng, e->g.tail, xn, epoch);
   } else {
     return set_error(LLMHIP_ERR_TYPE, "llm: embedding type %u", e->g.q.type);
   }

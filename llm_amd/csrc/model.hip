@@ -14,6 +14,7 @@
 
 #include "gemv.h"
 #include "layer.h"
+#include "pass.h"
 
 namespace llmhip {
 
@@ -152,6 +153,17 @@ struct Model {
   int lane = 0;
   std::vector<hipEvent_t> seg_done[LANES + 1];
   hipEvent_t lane_ev[LANES] = {};
+  // the fused decode pass (pass.hip): its flag-carrying vectors (one
+  // allocation), control words [epoch, timed-out waits, poll limit, pad], the
+  // layer table on the device and the arguments; pass_ok: the model fits it
+  // (else pass_why), pass_on: decode passes take it (llmhip_model_set_fused)
+  uint64_t* ll = nullptr;
+  uint32_t* pctrl = nullptr;
+  PassLayer* ptab = nullptr;
+  PassArgs pargs{};
+  uint32_t pgrid = 0;
+  bool pass_ok = false, pass_on = true, pass_q8 = false;
+  std::string pass_why = "not finalized";
 };
 
 // Brackets one launch with HIP events on the model's stream when profiling.
@@ -754,7 +766,7 @@ static int rec_head(Model& m, uint32_t xrow, uint32_t adv) {
   const bool emb = !skipped(m, "embed");  // the next one-token pass's input row
   return launch_rec(m, "argmax", 8ull * groups, [&]() {
     return argmax_launch(m.amax_v, m.amax_i, groups, m.logits, m.tokens, m.outb, m.state, adv, m.stream,
-                         emb ? &m.embd : nullptr, emb ? m.xn : nullptr);
+                         emb ? &m.embd : nullptr, emb ? m.xn : nullptr, m.pctrl);
   });
 }
 
@@ -828,9 +840,28 @@ static int segment_dep(int g, int G) { return (g * G + G - 2) / G; }
 // head pass's sampling kernel wrote), the layers, and (head) the logits and
 // the sampled token of the last one, which goes to tokens[step + ntok], its
 // embedding row to xn; state advances by ntok.
+// Whether the one-token pass being recorded runs as the fused decode launch:
+// a decode step (its input row is xn) of a model that fits it, with the
+// one-chunk attention, every layer and kernel class running, f32 activations.
+static bool use_pass(const Model& m, uint32_t ntok, bool head) {
+  bool h = head;
+  return m.pass_ok && m.pass_on && ntok == 1 && !m.embed_in && head && !m.attn_split && !m.q8 && m.skip.empty() &&
+         pass_layers(m, &h) == m.cfg.layers && h;
+}
+
 static int record_pass(Model& m, uint32_t ntok, bool head, bool embed_in) {
   m.embed_in = embed_in || ntok != 1;
   m.k5_split = m.xsum_ready = false;  // a pass's last K5 never splits: nothing carries over
+  if (use_pass(m, ntok, head)) {
+    m.cur_layer = -1;
+    PassArgs a = m.pargs;
+    a.rows = m.attn_rows;
+    uint64_t bytes = 0;
+    for (const Layer& L : m.layers)
+      bytes += L.qkv[0].g.gguf_bytes() + L.o.g.gguf_bytes() + L.gu[0].g.gguf_bytes() + L.down.g.gguf_bytes();
+    LLM_TRY(launch_rec(m, "pass", bytes, [&]() { return pass_launch(a, m.pgrid, m.pass_q8, m.stream); }));
+    return rec_head(m, ntok - 1, ntok);
+  }
   bool h = head;
   const int nl = pass_layers(m, &h);
   for (int s = 0; s <= nl; s++) LLM_TRY(record_slot(m, ntok, head, s));
@@ -1039,6 +1070,91 @@ static int prefill_wavefront(Model& m, uint32_t n) {
   return rc;
 }
 
+static PassMat pass_mat(const QMat& q) {
+  PassMat p;
+  p.qs = q.qs;
+  p.type = q.g.q.type;
+  p.rows = (uint32_t)q.g.rows;
+  p.nb = q.g.nb;
+  p.ng = q.g.ng;
+  p.tail = q.g.tail;
+  p.tiles = (uint32_t)q.g.tiles;
+  p.map = q.map;
+  p.map_hd = q.map_hd;
+  p.map_seg0 = q.map_seg0;
+  p.map_seg1 = q.map_seg1;
+  p.ff = q.ff;
+  return p;
+}
+
+// Whether the model fits the fused decode pass, and its layer table and
+// arguments (at finalize, when every matrix is in place).
+static int pass_setup(Model& m) {
+  const llmhip_config& c = m.cfg;
+  m.pass_ok = false;
+  m.pgrid = pass_grid(m.device, (uint32_t)c.head_dim, m.kv16);
+  std::vector<PassLayer> tab((size_t)c.layers);
+  m.pass_q8 = false;
+  m.pass_why.clear();
+  for (int l = 0; l < c.layers && m.pass_why.empty(); l++) {
+    const Layer& L = m.layers[(size_t)l];
+    if (L.nqkv != 1 || L.ngu != 1) {
+      m.pass_why = "q, k, v or gate, up of different types";
+      break;
+    }
+    PassLayer& p = tab[(size_t)l];
+    p.qkv = pass_mat(L.qkv[0]);
+    p.o = pass_mat(L.o);
+    p.gu = pass_mat(L.gu[0]);
+    p.down = pass_mat(L.down);
+    p.attn_norm = L.attn_norm;
+    p.ffn_norm = L.ffn_norm;
+    p.bias = L.bias;
+    p.kv = L.kv;
+    for (const PassMat* q : {&p.qkv, &p.o, &p.gu, &p.down}) m.pass_q8 = m.pass_q8 || q->type == LLMHIP_Q8_0;
+    if (const char* why = pass_unfit(c, m.kvd, p.qkv, p.o, p.gu, p.down, m.pgrid)) m.pass_why = why;
+  }
+  if (!m.pass_why.empty()) return 0;
+  LLM_HIP(hipMemcpyAsync(m.ptab, tab.data(), tab.size() * sizeof(PassLayer), hipMemcpyHostToDevice, m.stream));
+  LLM_HIP(hipStreamSynchronize(m.stream));
+  PassArgs& a = m.pargs;
+  memset(&a, 0, sizeof a);
+  const uint64_t E = c.embd, F = c.ff;
+  a.layers = m.ptab;
+  a.nlayers = (uint32_t)c.layers;
+  a.xn = m.xn;
+  a.x = m.x;
+  a.q = m.q;
+  a.att = m.att;
+  a.act = m.act;
+  a.up = m.gbuf;
+  a.llx = m.ll;
+  a.llb = m.ll + E;
+  a.llatt = m.ll + 2 * E;
+  a.llq = m.ll + 3 * E;
+  a.llact = m.ll + 4 * E + 2ull * m.kvd;
+  (void)F;
+  a.ctrl = m.pctrl;
+  a.state = m.state;
+  a.cs = m.cs;
+  a.embd = (uint32_t)c.embd;
+  a.ff = (uint32_t)c.ff;
+  a.heads = (uint32_t)c.heads;
+  a.kv_heads = (uint32_t)c.kv_heads;
+  a.hd = (uint32_t)c.head_dim;
+  a.kvd = m.kvd;
+  a.ctx = m.ctx;
+  a.neox = (uint32_t)c.rope_neox;
+  a.kv16 = m.kv16 ? 1 : 0;
+  a.eps = c.eps;
+  a.scale = (float)(1 / std::sqrt((double)c.head_dim));  // cpu.go:304
+  const uint32_t t1 = (uint32_t)(E + 2 * m.kvd + 15) / 16, t3 = (uint32_t)(E + 15) / 16;
+  const uint32_t natt = 8 * (uint32_t)(c.heads / c.kv_heads) * ((uint32_t)(c.kv_heads + 7) / 8);
+  pass_place(&a, m.pgrid, t1, t3, t3, natt);
+  m.pass_ok = true;
+  return 0;
+}
+
 }  // namespace llmhip
 
 using namespace llmhip;
@@ -1096,7 +1212,9 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
       (rc = dalloc_n(*m, &m->tokens, (uint64_t)m->ctx + 1)) || (rc = dalloc_n(*m, &m->outb, 1)) ||
       (rc = dalloc(*m, &m->xprep, xprep_bytes(m->pm, (uint32_t)std::max(c.embd, c.ff)))) ||
       (rc = dalloc_n(*m, &m->cs, (uint64_t)m->ctx * c.head_dim)) || (rc = dalloc_n(*m, &m->h, E)) ||
-      (rc = dalloc_n(*m, &m->xn, E)) || (rc = dalloc_n(*m, &m->kpart, 3 * E)))
+      (rc = dalloc_n(*m, &m->xn, E)) || (rc = dalloc_n(*m, &m->kpart, 3 * E)) ||
+      (rc = dalloc_n(*m, &m->ll, 4 * E + 2ull * m->kvd + F)) || (rc = dalloc_n(*m, &m->pctrl, 4)) ||
+      (rc = dalloc_n(*m, &m->ptab, (uint64_t)c.layers)))
     return fail(rc);
   {  // the prefill lanes: lane 0 is the model's own buffers
     m->lanes[0] = Lane{m->stream, m->x, m->q, m->att, m->act, m->gbuf, m->pv, m->ml, m->xprep, m->state};
@@ -1138,6 +1256,8 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
       hipHostMalloc((void**)&m->bounce, BOUNCE_BYTES, hipHostMallocDefault) != hipSuccess)
     return fail(set_error(LLMHIP_ERR_DEVICE, "llm: hipHostMalloc failed"));
   if ((rc = copy_in(*m, m->cs, cs.data(), cs.size() * 4)) != 0) return fail(rc);
+  const uint32_t ctrl0[4] = {1, 0, 0, 0};  // epoch 1: no word of the zeroed vectors carries a flag of a pass
+  if ((rc = copy_in(*m, m->pctrl, ctrl0, sizeof ctrl0)) != 0) return fail(rc);
   *out = new llmhip_model{m};
   return 0;
 }
@@ -1283,6 +1403,7 @@ int llmhip_model_finalize(llmhip_model* h) {
                        (unsigned long long)kv.second.received, (unsigned long long)kv.second.size);
   LLM_HIP(hipStreamSynchronize(m.stream));
   stager_free(&m.st);  // the load is over: release its pinned and device staging
+  LLM_TRY(pass_setup(m));
   m.stats.submits++;
   m.finalized = true;
   return 0;
@@ -1340,7 +1461,20 @@ int llmhip_model_decode(llmhip_model* h, int cnt, int32_t* out) {
   // four 1508 / 1762, eight 1476 / 1765)
   for (int j = 0; j < cnt; j += 4) LLM_TRY(launch_decode(m, first + (uint32_t)j, (uint32_t)std::min(cnt - j, 4)));
   LLM_HIP(hipMemcpyAsync(m.host, m.tokens + first + 1, (size_t)cnt * 4, hipMemcpyDeviceToHost, m.stream));
+  LLM_HIP(hipMemcpyAsync(m.host + cnt, m.pctrl + 1, 4, hipMemcpyDeviceToHost, m.stream));
   LLM_HIP(hipStreamSynchronize(m.stream));
+  if (m.host[cnt] != 0) {
+    // a fused pass gave up waiting: its results are not to be trusted; later
+    // decode steps take one launch per kernel
+    const uint32_t zero = 0;
+    LLM_TRY(copy_in(m, m.pctrl + 1, &zero, 4));
+    m.pass_ok = false;
+    m.pass_why = "a hand-off wait timed out";
+    destroy_graphs(m);
+    return set_error(LLMHIP_ERR_DEVICE,
+                     "llm: decode: %d waits of the fused pass timed out (later decode steps take one launch per kernel)",
+                     m.host[cnt]);
+  }
   memcpy(out, m.host, (size_t)cnt * 4);
   m.pos += (uint32_t)cnt;
   m.stats.submits++;
@@ -1446,6 +1580,24 @@ int llmhip_model_set_exact_ggml(llmhip_model* h, int on) {
   if (m.q8) m.kv16 = true;  // cpu.go:298: ExactGGML stores K and V in binary16
   destroy_graphs(m);
   return 0;
+}
+
+int llmhip_model_set_fused(llmhip_model* h, int on, uint32_t poll_limit, char* why, uint64_t cap) {
+  clear_error();
+  Model& m = *h->m;
+  LLM_HIP(hipSetDevice(m.device));
+  LLM_HIP(hipStreamSynchronize(m.stream));
+  if (m.pass_on != (on != 0)) destroy_graphs(m);
+  m.pass_on = on != 0;
+  LLM_TRY(copy_in(m, m.pctrl + 2, &poll_limit, 4));
+  const bool taken = m.pass_ok && m.pass_on;
+  if (why && cap) {
+    const std::string w = taken ? "" : !m.pass_on ? "turned off" : m.pass_why;
+    const size_t n = std::min<size_t>(w.size(), cap - 1);
+    memcpy(why, w.data(), n);
+    why[n] = 0;
+  }
+  return taken ? 1 : 0;
 }
 
 int llmhip_model_set_layers(llmhip_model* h, int layers) {

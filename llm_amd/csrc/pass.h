@@ -1,0 +1,68 @@
+// Host-side interface of the fused decode pass (pass.hip): every layer of a
+// one-token pass in one persistent launch.
+#pragma once
+
+#include "common.h"
+#include "gemv.h"
+
+namespace llmhip {
+
+// One layer matrix as the pass reads it (the fields of QMat it needs).
+struct PassMat {
+  const uint8_t* qs;
+  uint32_t type, rows, nb, ng, tail, tiles;
+  uint32_t map, map_hd, map_seg0, map_seg1, ff;
+};
+
+// One layer: the fused [q; k; v] and [gate; up] matrices, the output and
+// down projections, the norm weights, the QKV biases (or null) and the cache.
+struct PassLayer {
+  PassMat qkv, o, gu, down;
+  const float *attn_norm, *ffn_norm, *bias;
+  float* kv;
+};
+
+// The vectors that cross from one phase to the next inside the launch are
+// 64-bit words (f32 bits low, flag high), written and read with agent-scope
+// relaxed atomics, so that a word's value and flag arrive together on any
+// XCD.  A reader polls until every word it needs carries the flag of the
+// current (pass, layer): epoch * layers + layer + 1, where the epoch (ctrl[0])
+// is advanced by the sampling kernel after every head pass, so no flag of an
+// earlier pass matches.  A wait gives up after ctrl[2] polls (0: the default),
+// sets ctrl[1] and stops waiting, so every wave of the launch still ends.
+struct PassArgs {
+  const PassLayer* layers;  // device memory, nlayers entries
+  uint32_t nlayers;
+  const float* xn;                      // layer 0's input row (the sampling kernel wrote it)
+  float *x, *q, *att, *act, *up;        // the last layer's values, stored plainly (the head's input, Peek)
+  uint64_t *llx, *llb, *llq, *llatt, *llact;  // x after a layer, x after attention, [q; k; v] of the position, att, act
+  uint32_t* ctrl;                       // [0] epoch, [1] timed-out waits, [2] poll limit
+  const uint32_t* state;
+  const float* cs;  // RoPE table
+  uint32_t embd, ff, heads, kv_heads, hd, kvd, ctx, neox, kv16;
+  uint32_t rows;  // cache rows the attention reads: a multiple of 64 above the position, <= attn_full_max
+  float eps, scale;
+  // the first workgroup of each phase's work: K1 tiles, attention heads, K3 tiles, K4 (round robin), K5 tiles
+  uint32_t b1, batt, b3, b4, b5;
+};
+
+constexpr uint32_t PASS_WAVES = 8;        // waves per workgroup
+constexpr uint32_t PASS_MAX_EMBD = 1024;  // the phases' staged input row (LDS)
+constexpr uint32_t PASS_K4_TILES = 3;     // gate/up tiles per workgroup, at most
+constexpr uint32_t PASS_K5_UNITS = 6;     // down-projection units (groups of four blocks) per wave, at most
+constexpr uint32_t PASS_SPIN_DEFAULT = 1u << 20;
+
+// Why a model's decode passes cannot take the fused launch (nullptr: they can),
+// for `grid` co-resident workgroups.
+const char* pass_unfit(const llmhip_config& c, uint32_t kvd, const PassMat& qkv, const PassMat& o, const PassMat& gu,
+                       const PassMat& down, uint32_t grid);
+// Workgroups that are all resident at once for the pass kernel of head size
+// hd (0: none; the launch needs every workgroup resident).
+uint32_t pass_grid(int device, uint32_t hd, bool kv16);
+// The work placement of a grid (PassArgs::b*).
+// natt: the attention's workgroup range (8 GQ ceil(kv_heads / 8)).
+void pass_place(PassArgs* a, uint32_t grid, uint32_t t1, uint32_t t3, uint32_t t5, uint32_t natt);
+// q8: some layer matrix is Q8_0.
+int pass_launch(const PassArgs& a, uint32_t grid, bool q8, hipStream_t s);
+
+}  // namespace llmhip

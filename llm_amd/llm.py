@@ -217,6 +217,15 @@ class GPU:
         check(lib().llm_gpu_peek(self._h, name.encode(), out.ctypes.data_as(ctypes.c_void_p), n))
         return out
 
+    def set_fused(self, on=True, poll_limit=0):
+        """Decode steps as the fused launch (llmhip_model_set_fused): returns
+        (taken, reason it is not)."""
+        why = ctypes.create_string_buffer(256)
+        rc = lib().llmhip_model_set_fused(self._m, int(bool(on)), int(poll_limit), why, 256)
+        if rc < 0:
+            check(rc)
+        return rc == 1, why.value.decode()
+
     def bench_kernel(self, kernel, iters):
         """(avg microseconds, algorithmic bytes) of one launch of a decode-step kernel."""
         us, b = ctypes.c_float(), ctypes.c_uint64()
