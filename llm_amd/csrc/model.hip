@@ -1094,6 +1094,7 @@ static int pass_setup(Model& m) {
   m.pass_ok = false;
   m.pgrid = pass_grid(m.device, (uint32_t)c.head_dim, m.kv16);
   std::vector<PassLayer> tab((size_t)c.layers);
+  uint32_t kp = 1;
   m.pass_q8 = false;
   m.pass_why.clear();
   for (int l = 0; l < c.layers && m.pass_why.empty(); l++) {
@@ -1112,7 +1113,7 @@ static int pass_setup(Model& m) {
     p.bias = L.bias;
     p.kv = L.kv;
     for (const PassMat* q : {&p.qkv, &p.o, &p.gu, &p.down}) m.pass_q8 = m.pass_q8 || q->type == LLMHIP_Q8_0;
-    if (const char* why = pass_unfit(c, m.kvd, p.qkv, p.o, p.gu, p.down, m.pgrid)) m.pass_why = why;
+    if (const char* why = pass_unfit(c, m.kvd, p.qkv, p.o, p.gu, p.down, m.pgrid, &kp)) m.pass_why = why;
   }
   if (!m.pass_why.empty()) return 0;
   LLM_HIP(hipMemcpyAsync(m.ptab, tab.data(), tab.size() * sizeof(PassLayer), hipMemcpyHostToDevice, m.stream));
@@ -1128,12 +1129,13 @@ static int pass_setup(Model& m) {
   a.att = m.att;
   a.act = m.act;
   a.up = m.gbuf;
-  a.llx = m.ll;
-  a.llb = m.ll + E;
-  a.llatt = m.ll + 2 * E;
-  a.llq = m.ll + 3 * E;
-  a.llact = m.ll + 4 * E + 2ull * m.kvd;
+  const uint64_t nch = pass_chunks((uint32_t)c.head_dim);
+  a.llq = m.ll;                                        // [E + 2 kvd]
+  a.llo = a.llq + E + 2ull * m.kvd;                    // [chunks][E], then [chunks][heads][2]
+  a.llb = a.llo + nch * E + nch * 2 * c.heads;         // [1 + kp][E]
+  a.llact = a.llb + (1 + kp) * E;                      // [ff]
   (void)F;
+  a.kp = kp;
   a.ctrl = m.pctrl;
   a.state = m.state;
   a.cs = m.cs;
@@ -1149,8 +1151,7 @@ static int pass_setup(Model& m) {
   a.eps = c.eps;
   a.scale = (float)(1 / std::sqrt((double)c.head_dim));  // cpu.go:304
   const uint32_t t1 = (uint32_t)(E + 2 * m.kvd + 15) / 16, t3 = (uint32_t)(E + 15) / 16;
-  const uint32_t natt = 8 * (uint32_t)(c.heads / c.kv_heads) * ((uint32_t)(c.kv_heads + 7) / 8);
-  pass_place(&a, m.pgrid, t1, t3, t3, natt);
+  pass_place(&a, m.pgrid, t1, t3, t3);
   m.pass_ok = true;
   return 0;
 }
@@ -1213,7 +1214,7 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
       (rc = dalloc(*m, &m->xprep, xprep_bytes(m->pm, (uint32_t)std::max(c.embd, c.ff)))) ||
       (rc = dalloc_n(*m, &m->cs, (uint64_t)m->ctx * c.head_dim)) || (rc = dalloc_n(*m, &m->h, E)) ||
       (rc = dalloc_n(*m, &m->xn, E)) || (rc = dalloc_n(*m, &m->kpart, 3 * E)) ||
-      (rc = dalloc_n(*m, &m->ll, 4 * E + 2ull * m->kvd + F)) || (rc = dalloc_n(*m, &m->pctrl, 4)) ||
+      (rc = dalloc_n(*m, &m->ll, pass_words(c, m->kvd))) || (rc = dalloc_n(*m, &m->pctrl, 4)) ||
       (rc = dalloc_n(*m, &m->ptab, (uint64_t)c.layers)))
     return fail(rc);
   {  // the prefill lanes: lane 0 is the model's own buffers

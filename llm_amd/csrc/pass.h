@@ -29,39 +29,56 @@ struct PassLayer {
 // current (pass, layer): epoch * layers + layer + 1, where the epoch (ctrl[0])
 // is advanced by the sampling kernel after every head pass, so no flag of an
 // earlier pass matches.  A wait gives up after ctrl[2] polls (0: the default),
-// sets ctrl[1] and stops waiting, so every wave of the launch still ends.
+// counts itself in ctrl[1] and stops waiting, so every wave of the launch
+// still ends.
 struct PassArgs {
   const PassLayer* layers;  // device memory, nlayers entries
   uint32_t nlayers;
-  const float* xn;                      // layer 0's input row (the sampling kernel wrote it)
-  float *x, *q, *att, *act, *up;        // the last layer's values, stored plainly (the head's input, Peek)
-  uint64_t *llx, *llb, *llq, *llatt, *llact;  // x after a layer, x after attention, [q; k; v] of the position, att, act
-  uint32_t* ctrl;                       // [0] epoch, [1] timed-out waits, [2] poll limit
+  const float* xn;                // layer 0's input row (the sampling kernel wrote it)
+  float *x, *q, *att, *act, *up;  // the last layer's values, stored plainly (the head's input, Peek)
+  uint64_t* llq;    // [E + 2 kvd]: q, and the position's K and V rows (K1)
+  uint64_t* llo;    // [chunks][E] the attention's per-chunk sums of e v, then [chunks][heads][2] each
+                    // chunk's max score and sum of e (K2)
+  uint64_t* llb;    // [1 + kp][E]: x after the attention (K3), then the down projection's k-parts (K5);
+                    // x after the layer is their sum
+  uint64_t* llact;  // [ff]: the SwiGLU activations (K4)
+  uint32_t* ctrl;   // [0] epoch, [1] timed-out waits, [2] poll limit
   const uint32_t* state;
   const float* cs;  // RoPE table
   uint32_t embd, ff, heads, kv_heads, hd, kvd, ctx, neox, kv16;
   uint32_t rows;  // cache rows the attention reads: a multiple of 64 above the position, <= attn_full_max
+  uint32_t kp;    // k-parts of the down projection (1, 2 or 4)
   float eps, scale;
-  // the first workgroup of each phase's work: K1 tiles, attention heads, K3 tiles, K4 (round robin), K5 tiles
+  // the first workgroup of each phase's work: K1 tiles, attention (head, chunk)s, K3 tiles, K4 (round robin),
+  // K5 (tile, part)s
   uint32_t b1, batt, b3, b4, b5;
 };
 
 constexpr uint32_t PASS_WAVES = 8;        // waves per workgroup
-constexpr uint32_t PASS_MAX_EMBD = 1024;  // the phases' staged input row (LDS)
+constexpr uint32_t PASS_MAX_EMBD = 1024;  // the embedding, at most
+constexpr uint32_t PASS_MAX_FF = 6144;    // the feed-forward width, at most (its row is staged in LDS)
 constexpr uint32_t PASS_K4_TILES = 3;     // gate/up tiles per workgroup, at most
-constexpr uint32_t PASS_K5_UNITS = 6;     // down-projection units (groups of four blocks) per wave, at most
+constexpr uint32_t PASS_K5_UNITS = 3;     // down-projection units (groups of four blocks) per wave and part, at most
+constexpr uint32_t PASS_CHUNK_ROWS = 128; // cache rows of an attention chunk (two chunks at head size 64)
 constexpr uint32_t PASS_SPIN_DEFAULT = 1u << 20;
 
+// Attention chunks of a pass at head size hd (the one-chunk range: 256 rows at 64, 128 at 128).
+__host__ __device__ inline uint32_t pass_chunks(uint32_t hd) { return hd == 64 ? 2 : 1; }
+// Flag-carrying words a model's pass needs (PassArgs: llq, llo, llb with the
+// most k-parts, llact).
+inline uint64_t pass_words(const llmhip_config& c, uint32_t kvd) {
+  const uint64_t E = (uint64_t)c.embd, nch = pass_chunks((uint32_t)c.head_dim);
+  return E + 2ull * kvd + nch * (E + 2ull * (uint64_t)c.heads) + 3 * E + (uint64_t)c.ff;
+}
 // Why a model's decode passes cannot take the fused launch (nullptr: they can),
-// for `grid` co-resident workgroups.
+// for `grid` co-resident workgroups; *kp receives the down projection's k-parts.
 const char* pass_unfit(const llmhip_config& c, uint32_t kvd, const PassMat& qkv, const PassMat& o, const PassMat& gu,
-                       const PassMat& down, uint32_t grid);
+                       const PassMat& down, uint32_t grid, uint32_t* kp);
 // Workgroups that are all resident at once for the pass kernel of head size
 // hd (0: none; the launch needs every workgroup resident).
 uint32_t pass_grid(int device, uint32_t hd, bool kv16);
-// The work placement of a grid (PassArgs::b*).
-// natt: the attention's workgroup range (8 GQ ceil(kv_heads / 8)).
-void pass_place(PassArgs* a, uint32_t grid, uint32_t t1, uint32_t t3, uint32_t t5, uint32_t natt);
+// The work placement of a grid (PassArgs::b*); t1, t3, t5: tiles of [q; k; v], W_o and W_down.
+void pass_place(PassArgs* a, uint32_t grid, uint32_t t1, uint32_t t3, uint32_t t5);
 // q8: some layer matrix is Q8_0.
 int pass_launch(const PassArgs& a, uint32_t grid, bool q8, hipStream_t s);
 

@@ -5,27 +5,29 @@
 // Each workgroup has a fixed share of each phase of a layer:
 //   K1  a tile of [q; k; v]: RMSNorm(x) (attn_norm), the product, bias, RoPE,
 //       q out, K and V appended to the cache (kernels_fused.go:47-73);
-//   K2  one query head's attention over the cache rows of the pass
-//       (kernels_fused.go:82-146, one chunk: every position below
-//       attn_full_max);
-//   K3  a tile of W_o att plus the residual (kernels_fused.go:150-170);
+//   K2  one query head over one chunk of 128 cache rows: the chunk's max
+//       score, sum of e and sum of e v (kernels_fused.go:82-146; every
+//       position is below attn_full_max, so there are one or two chunks);
+//   K3  a tile of W_o att plus the residual, att merged from the chunks as
+//       attn_merge_kernel merges them (kernels_fused.go:150-170);
 //   K4  tiles of [gate; up]: RMSNorm (ffn_norm), the product, SwiGLU;
-//   K5  a tile of W_down act plus the residual.
+//   K5  one of kp k-parts of a tile of W_down act; the next layer adds the
+//       parts to the residual, in order.
 // The boundaries between the phases are not kernel boundaries: a phase's
 // result goes out as flag-carrying words (PassArgs) and the next phase's
 // workgroups poll for the words they need, so a hand-off costs a round trip
 // through the memory system instead of a dependent launch.  Every workgroup
-// issues its weight loads for a phase before it waits for the phase's input
-// (K1, K3 and K4 at the layer's start, K5 after K3), and the attention
-// workgroups load the cache rows of earlier positions there too; the row of
-// the current position comes from K1's words.
+// issues a phase's weight loads, and the loads of the inputs its epilogue
+// needs, before it waits for the phase's input; the attention workgroups load
+// the cache rows of earlier positions before waiting for K1's row of the
+// position.
 //
-// The products are those of the decode tile kernel (gemv_impl.h): weights
-// dequantised exactly to f16, activations per unit of 128 elements scaled by
-// a power of two and split into f16 hi + lo, v_mfma_f32_16x16x32_f16, the
-// block scale in f32; RMSNorm's 1/rms applied to the sums at the end.  The
+// The products run on v_mfma_f32_16x16x32_f16 as the decode kernels' do
+// (gemv_impl.h): weights dequantised exactly to f16, the staged row scaled by
+// a power of two and split into f16 hi + lo, the block scale in f32.  The
 // waves of a workgroup split a tile's units (split-K) and add their partial
-// sums through LDS in wave order, so every result is deterministic.
+// sums through LDS in wave order; the k-parts are added in part order: every
+// result is deterministic.
 #include "attn_core.h"
 #include "gemv_impl.h"
 #include "layer.h"
@@ -49,15 +51,16 @@ struct Waiter {
   bool dead;
 };
 
-// Words base[idx[i]] (those with need[i]) polled until each carries `flag`;
-// their f32 values in v (0 where not needed).
-template <int N>
-__device__ __forceinline__ void ll_wait(const uint64_t* base, const uint32_t (&idx)[N], const bool (&need)[N],
-                                        uint32_t flag, float (&v)[N], Waiter& w) {
+// Words at(i) (those with need(i)) polled until each carries `flag`; their
+// f32 values in v (0 where not needed).  Every load is issued before the first
+// wait; a retry follows a short pause.  The addresses and conditions are
+// formed again where used (a thread holds only the words, not N addresses).
+template <int N, class At, class Need>
+__device__ __forceinline__ void ll_wait_f(At at, Need need, uint32_t flag, float (&v)[N], Waiter& w) {
   uint64_t x[N];
   const uint64_t none = (uint64_t)flag << 32;
 #pragma unroll
-  for (int i = 0; i < N; i++) x[i] = need[i] ? ll_load(base + idx[i]) : none;
+  for (int i = 0; i < N; i++) x[i] = need(i) ? ll_load(at(i)) : none;
   uint32_t spins = 0;
   for (;;) {
     bool ok = true;
@@ -69,87 +72,251 @@ __device__ __forceinline__ void ll_wait(const uint64_t* base, const uint32_t (&i
       atomicOr(w.err, 1u);
       break;
     }
+    __builtin_amdgcn_s_sleep(1);
 #pragma unroll
     for (int i = 0; i < N; i++)
-      if ((uint32_t)(x[i] >> 32) != flag) x[i] = ll_load(base + idx[i]);
+      if ((uint32_t)(x[i] >> 32) != flag) x[i] = ll_load(at(i));
   }
 #pragma unroll
   for (int i = 0; i < N; i++) v[i] = __uint_as_float((uint32_t)x[i]);
 }
 
+// ll_wait_f over base[idx[i]] where need[i].
+template <int N>
+__device__ __forceinline__ void ll_wait(const uint64_t* base, const uint32_t (&idx)[N], const bool (&need)[N],
+                                        uint32_t flag, float (&v)[N], Waiter& w) {
+  ll_wait_f<N>([&](int i) { return base + idx[i]; }, [&](int i) { return need[i]; }, flag, v, w);
+}
+
+// The value of a flag-carrying word loaded earlier (x, from p), polled again
+// until it carries `flag` (bounded).
+__device__ __forceinline__ float ll_settle(const uint64_t* p, uint64_t x, uint32_t flag, Waiter& w) {
+  uint32_t spins = 0;
+  while ((uint32_t)(x >> 32) != flag && !w.dead) {
+    if (++spins > w.limit) {
+      w.dead = true;
+      atomicOr(w.err, 1u);
+      break;
+    }
+    x = ll_load(p);
+  }
+  return __uint_as_float((uint32_t)x);
+}
+
+constexpr uint32_t PASS_MAX_ITEMS = PASS_MAX_FF / 8;  // items of 8 elements of the longest staged row
+constexpr uint32_t IPT = (PASS_MAX_ITEMS + 64 * PASS_WAVES - 1) / (64 * PASS_WAVES);  // items per thread
+constexpr uint32_t PASS_MAX_KP = 2;
+constexpr uint32_t WPT_E = PASS_MAX_EMBD / (64 * PASS_WAVES);  // row elements per thread, rows of length E
+constexpr uint32_t WPT_F = PASS_MAX_FF / (64 * PASS_WAVES);    // row elements per thread, the longest row
+
 template <uint32_t HD>
 struct PassLds {
-  float xin[PASS_MAX_EMBD];  // a phase's input row
-  float misc[16];            // the waves' sums of squares
+  float row[PASS_MAX_FF];         // the phase's input row as polled (f32)
+  float nw[PASS_MAX_EMBD];        // RMS phases: the norm weights
+  h8 xs[2 * PASS_MAX_ITEMS];      // the phase's A operands: item it at 2 it (hi) and 2 it + 1 (lo)
+  float bsum[PASS_MAX_ITEMS / 4];  // Q4_1: each block's sum, scaled like the operands
+  float misc[16];                  // the waves' partial sums of squares [0, 8) and maxima [8, 16)
   float part[PASS_K4_TILES][PASS_WAVES][64];  // split-K partials
-  unsigned char wl[PASS_WAVES][WaveLds<1>::BYTES];  // each wave's staged operands
   AttnLds<HD, PASS_WAVES> am;
 };
 
-constexpr uint32_t RPT = PASS_MAX_EMBD / (64 * PASS_WAVES);  // row elements per thread
+// Where a phase's input row comes from (stage_ops).
+enum PassSrc : int {
+  SRC_LL,     // one vector of flag-carrying words
+  SRC_PLAIN,  // plain memory (layer 0's input, which the sampling kernel wrote)
+  SRC_XSUM,   // x = ((xb + p_0) + p_1) + ...: the attention's residual and the down projection's k-parts
+  SRC_MERGE,  // the attention's chunks merged: M = max m_c, w_c = e^(m_c - M), sum w_c o_c / sum w_c l_c
+};
 
-// The phase's input row (n <= PASS_MAX_EMBD floats) into LDS: from
-// flag-carrying words (ll) or plain memory (at layer 0, the row the sampling
-// kernel wrote).  RMS: returns the row's sum of squares (the waves' partial
-// sums added in wave order, the same in every thread).  Ends with a barrier.
-template <bool RMS>
-__device__ __forceinline__ float stage_row(float* xin, float* misc, const uint64_t* ll, const float* plain, uint32_t n,
-                                           uint32_t flag, Waiter& w, uint32_t tid, uint32_t wave) {
-  const uint32_t lane = tid & 63;
-  float v[RPT];
-  if (ll) {
-    uint32_t idx[RPT];
-    bool need[RPT];
+struct StageIn {
+  const uint64_t* ll;  // SRC_LL: the vector; SRC_XSUM: xb, then part p at (1 + p) E; SRC_MERGE: llo
+  const float* plain;  // SRC_PLAIN
+  uint32_t flag, kp, E, heads;
+  uint32_t chunks, nch;  // SRC_MERGE: the chunks holding positions (read), and those of the layout (llo)
+  float* store;        // SRC_MERGE: also store the merged row here (Peek "att"), or null
+};
+
+// Row elements base + tid + 512 k (k < NW; those below base + n) into v,
+// every load issued before the first wait: consecutive threads read
+// consecutive words, so each load instruction of a wave touches four lines
+// (a wave's polls of the row stay few, however many workgroups poll it).
+// SRC_XSUM and SRC_MERGE rows are of length E.
+template <int SRC, uint32_t HD, uint32_t NW>
+__device__ __forceinline__ void load_row(const StageIn& in, uint32_t base, uint32_t n, uint32_t tid, float (&v)[NW],
+                                         Waiter& w) {
+  constexpr uint32_t T = 64 * PASS_WAVES;
+  if constexpr (SRC == SRC_PLAIN) {
 #pragma unroll
-    for (uint32_t k = 0; k < RPT; k++) {
-      idx[k] = tid + 64 * PASS_WAVES * k;
-      need[k] = idx[k] < n;
+    for (uint32_t k = 0; k < NW; k++) v[k] = tid + T * k < n ? in.plain[base + tid + T * k] : 0.f;
+  } else if constexpr (SRC == SRC_LL) {
+    const uint64_t* p = in.ll + base + tid;
+    ll_wait_f<NW>([&](int i) { return p + T * i; }, [&](int i) { return tid + T * i < n; }, in.flag, v, w);
+  } else if constexpr (SRC == SRC_XSUM) {
+    constexpr uint32_t NP = 1 + PASS_MAX_KP;
+    float u[NW * NP];
+    // word i: vector i / NW (xb, then the parts), element tid + T (i % NW)
+    const uint64_t* p = in.ll + tid;
+    ll_wait_f<NW * NP>([&](int i) { return p + (i / NW) * in.E + T * (i % NW); },
+                       [&](int i) { return (uint32_t)(i / NW) <= in.kp && tid + T * (i % NW) < n; }, in.flag, u, w);
+#pragma unroll
+    for (uint32_t k = 0; k < NW; k++) {
+      float x = u[k];
+#pragma unroll
+      for (uint32_t q = 1; q < NP; q++)
+        if (q <= in.kp) x += u[q * NW + k];
+      v[k] = x;
     }
-    ll_wait<RPT>(ll, idx, need, flag, v, w);
-  } else {
+  } else {  // SRC_MERGE
+    constexpr uint32_t MC = 2;  // chunks, at most (pass_chunks)
+    float u[3 * NW * MC];
+    const uint32_t mlb = in.nch * in.E;
+    // words [0, NW MC): chunk i / NW's o at element tid + T (i % NW); then for chunk j / (2 NW) and
+    // element k = (j / 2) % NW, the element's head's m (j even) and l (j odd)
+    ll_wait_f<3 * NW * MC>(
+        [&](int i) {
+          if (i < (int)(NW * MC)) return in.ll + (i / NW) * in.E + tid + T * (i % NW);
+          const uint32_t j = i - NW * MC, c = j / (2 * NW), k = (j / 2) % NW;
+          return in.ll + mlb + 2 * (c * in.heads + (tid + T * k) / HD) + (j % 2);
+        },
+        [&](int i) {
+          const uint32_t c = i < (int)(NW * MC) ? i / NW : (i - NW * MC) / (2 * NW);
+          const uint32_t k = i < (int)(NW * MC) ? i % NW : ((i - NW * MC) / 2) % NW;
+          return c < in.chunks && tid + T * k < n;
+        },
+        in.flag, u, w);
+    // attn_merge_kernel's order (layer.hip): M, then the weights, L and o, then o / L
 #pragma unroll
-    for (uint32_t k = 0; k < RPT; k++) {
-      const uint32_t e = tid + 64 * PASS_WAVES * k;
-      v[k] = e < n ? plain[e] : 0.f;
+    for (uint32_t k = 0; k < NW; k++) {
+      auto mo = [&](uint32_t c, uint32_t which) { return u[NW * MC + 2 * (c * NW + k) + which]; };
+      float M = -INFINITY;
+#pragma unroll
+      for (uint32_t c = 0; c < MC; c++) M = fmaxf(M, c < in.chunks ? mo(c, 0) : -INFINITY);
+      float Ls = 0, o = 0;
+#pragma unroll
+      for (uint32_t c = 0; c < MC; c++) {
+        const bool inc = c < in.chunks;
+        const float wgt = inc ? __expf(mo(c, 0) - M) : 0.f;
+        Ls += wgt * (inc ? mo(c, 1) : 0.f);
+        o += wgt * (inc ? u[c * NW + k] : 0.f);
+      }
+      const bool ok = tid + T * k < n;
+      v[k] = ok ? o / Ls : 0.f;
+      if (in.store && ok) in.store[tid + T * k] = v[k];
     }
   }
-  float ss = 0;
-#pragma unroll
-  for (uint32_t k = 0; k < RPT; k++) {
-    const uint32_t e = tid + 64 * PASS_WAVES * k;
-    if (e < n) {
-      xin[e] = v[k];
-      ss += v[k] * v[k];
-    }
-  }
-  if (RMS) {
-    ss = wave_sum_dpp(ss);
-    if (lane == 0) misc[wave] = ss;
-  }
-  __syncthreads();
-  float tot = 0;
-  if (RMS)
-#pragma unroll
-    for (uint32_t k = 0; k < PASS_WAVES; k++) tot += misc[k];
-  return tot;
 }
 
-// Units of a wave in a phase: u = wave + PASS_WAVES * i (a unit is a group of
-// four blocks, or the tail of nb % 4 blocks: u == ng), for the workgroup's
-// tiles tile[j] (clamped into the matrix; tv[j]: the tile is the
+// The phase's input row (nb blocks of 32 from block nb0 on) staged by the
+// whole workgroup as the A operands of its units, in LDS: item it =
+// (block it / 4, k-group it % 4: elements 4 (it % 4) + 0..3 and
+// 16 + 4 (it % 4) + 0..3 of the block) in MFMA element order, scaled by 2^ex
+// so that the staged values' largest magnitude sits in [2^14, 2^15), and split
+// exactly into f16 hi (xs[2 it]) + lo (xs[2 it + 1]); the blocks' sums (Q4_1:
+// cpu.go:196-198) scaled alike.  RMS: the row is first normed,
+// h = (x s) w with s = f32(1/sqrt(f64(sum x^2 / n + eps))) (cpu.go:90-96);
+// the largest |x w| goes through the same barrier as the sum of squares
+// (max |h| = s max |x w|, s > 0).  The row is polled in element order into
+// LDS (load_row), the norm weights loaded before the wait; the items are then
+// formed from LDS.  Returns ex; two barriers.
+template <int SRC, bool RMS, uint32_t HD>
+__device__ __forceinline__ int stage_ops(PassLds<HD>& L, const StageIn& in, uint32_t nb0, uint32_t nb,
+                                         const float* nw, float eps, Waiter& w, uint32_t tid, uint32_t wave) {
+  constexpr uint32_t T = 64 * PASS_WAVES;
+  constexpr uint32_t NW = (SRC == SRC_LL && !RMS) ? WPT_F : WPT_E;
+  const uint32_t n = nb * 32, NI = nb * 4, lane = tid & 63;
+  float wv[NW];
+  if (RMS)
+#pragma unroll
+    for (uint32_t k = 0; k < NW; k++) wv[k] = tid + T * k < n ? nw[tid + T * k] : 0.f;
+  float v[NW];
+  load_row<SRC, HD, NW>(in, 32 * nb0, n, tid, v, w);
+  float ss = 0, mx = 0;
+#pragma unroll
+  for (uint32_t k = 0; k < NW; k++) {
+    if (tid + T * k < n) {
+      L.row[tid + T * k] = v[k];
+      if (RMS) L.nw[tid + T * k] = wv[k];
+    }
+    ss += v[k] * v[k];
+    mx = fmaxf(mx, RMS ? fabsf(v[k] * wv[k]) : fabsf(v[k]));
+  }
+  if (RMS) ss = wave_sum_dpp(ss);
+  mx = wave_max_dpp(mx);
+  if (lane == 0) {
+    L.misc[wave] = ss;
+    L.misc[8 + wave] = mx;
+  }
+  __syncthreads();
+  float tot = 0, m = 0;
+#pragma unroll
+  for (uint32_t k = 0; k < PASS_WAVES; k++) {
+    tot += L.misc[k];
+    m = fmaxf(m, L.misc[8 + k]);
+  }
+  const float s = RMS ? rms_scale((double)(tot / (float)n + eps)) : 1.f;
+  if (RMS) m *= s;
+  int ex = 0;
+  if (m > 0 && m <= 3.0e38f) {
+    int E;
+    frexpf(m, &E);
+    ex = 15 - E;
+  }
+#pragma unroll
+  for (uint32_t k = 0; k < IPT; k++) {
+    const uint32_t it = tid + T * k;
+    if (k > 0 && NW == WPT_E) break;  // rows of length E: one item per thread
+    const uint32_t e0 = (it / 4) * 32 + 4 * (it % 4);
+    const bool ok = it < NI;
+    f4 a = {0, 0, 0, 0}, c = {0, 0, 0, 0};
+    if (ok) {
+      a = *(const f4*)&L.row[e0];
+      c = *(const f4*)&L.row[e0 + 16];
+      if (RMS) {
+        const f4 wa = *(const f4*)&L.nw[e0], wc = *(const f4*)&L.nw[e0 + 16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          a[i] = __fmul_rn(__fmul_rn(a[i], s), wa[i]);  // cpu.go:96
+          c[i] = __fmul_rn(__fmul_rn(c[i], s), wc[i]);
+        }
+      }
+    }
+    const float vv[8] = {a[0], a[2], c[0], c[2], a[1], a[3], c[1], c[3]};
+    h8 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float sv = ldexpf(vv[i], ex);
+      const _Float16 h = (_Float16)sv;
+      hi[i] = h;
+      lo[i] = (_Float16)(sv - (float)h);
+    }
+    float sx = (a[0] + a[1] + a[2] + a[3]) + (c[0] + c[1] + c[2] + c[3]);
+    sx += __shfl_xor(sx, 1);  // a block's four items: four consecutive lanes
+    sx += __shfl_xor(sx, 2);
+    if (ok) {
+      L.xs[2 * it] = hi;
+      L.xs[2 * it + 1] = lo;
+      if ((it & 3) == 0) L.bsum[it / 4] = ldexpf(sx, ex);
+    }
+  }
+  __syncthreads();
+  return ex;
+}
+
+// Units of a wave in a phase: u = u0 + wave + PASS_WAVES * i < u1 (a unit is a
+// group of four blocks, or the tail of nb % 4 blocks: u == ng), for the
+// workgroup's tiles tile[j] (clamped into the matrix; tv[j]: the tile is the
 // workgroup's).  Absent units read one line of their tile, so the loads need
 // no branch.
 template <uint32_t QT, int MT, int MU>
 __device__ __forceinline__ void units_load(WUnit (&W)[MT][MU], const PassMat& M, const uint32_t (&tile)[MT],
-                                           const bool (&tv)[MT], uint32_t wave, int lane) {
+                                           const bool (&tv)[MT], uint32_t u0, uint32_t u1, uint32_t wave, int lane) {
   const int r = lane & 15;
-  const uint32_t U = M.ng + (M.tail ? 1u : 0u);
 #pragma unroll
   for (int j = 0; j < MT; j++)
 #pragma unroll
     for (int i = 0; i < MU; i++) {
-      const uint32_t u = wave + PASS_WAVES * i;
-      const bool real = tv[j] && u < U;
+      const uint32_t u = u0 + wave + PASS_WAVES * i;
+      const bool real = tv[j] && u < u1;
       if (real && u == M.ng)
         load_unit<QT>(W[j][i], M.qs, M.nb, tile[j], M.ng, M.ng, M.tail, lane, r);
       else
@@ -161,106 +328,62 @@ __device__ __forceinline__ void units_load(WUnit (&W)[MT][MU], const PassMat& M,
 // the second quant word of WUnit is never live).
 template <bool Q8, int MT, int MU>
 __device__ __forceinline__ void units_load_any(WUnit (&W)[MT][MU], const PassMat& M, const uint32_t (&tile)[MT],
-                                               const bool (&tv)[MT], uint32_t wave, int lane) {
-  if (Q8 && M.type == LLMHIP_Q8_0) units_load<LLMHIP_Q8_0, MT, MU>(W, M, tile, tv, wave, lane);
-  else if (M.type == LLMHIP_Q4_1) units_load<LLMHIP_Q4_1, MT, MU>(W, M, tile, tv, wave, lane);
-  else units_load<LLMHIP_Q4_0, MT, MU>(W, M, tile, tv, wave, lane);
+                                               const bool (&tv)[MT], uint32_t u0, uint32_t u1, uint32_t wave,
+                                               int lane) {
+  if (Q8 && M.type == LLMHIP_Q8_0) units_load<LLMHIP_Q8_0, MT, MU>(W, M, tile, tv, u0, u1, wave, lane);
+  else if (M.type == LLMHIP_Q4_1) units_load<LLMHIP_Q4_1, MT, MU>(W, M, tile, tv, u0, u1, wave, lane);
+  else units_load<LLMHIP_Q4_0, MT, MU>(W, M, tile, tv, u0, u1, wave, lane);
 }
 
-// The norm weights of a wave's first batch of items (RMS phases: every unit
-// of the wave in one batch), loaded before the wait for the row.
-struct NormItems {
-  f4 wa, wc;
-};
-__device__ __forceinline__ NormItems norm_load(const PassMat& M, const float* nw, uint32_t wave, int lane) {
-  const uint32_t ub = lane >> 4, b = (lane >> 2) & 3, iq = lane & 3, unit = wave + PASS_WAVES * ub;
-  const bool ok = unit < M.ng || (unit == M.ng && b < M.tail);
-  const uint32_t e0 = ok ? (unit * 4 + b) * 32 + 4 * iq : 0;
-  NormItems n;
-  n.wa = *(const f4*)(nw + e0);
-  n.wc = *(const f4*)(nw + e0 + 16);
-  if (!ok) n.wa = n.wc = f4{0, 0, 0, 0};
-  return n;
-}
-
-// A wave's partial sums for the workgroup's tiles (acc[j]: lanes of q == 0
-// hold row r's sum; see unit_products), its units staged in batches of four
-// from the row in LDS (xin; RMS: times the norm weights, nrm) or, FROM_LL,
-// straight from flag-carrying words.
-template <uint32_t QT, int MT, int MU, bool RMS, bool FROM_LL>
-__device__ __forceinline__ void units_products(const WUnit (&W)[MT][MU], const PassMat& M, const float* xin,
-                                               const NormItems& nrm, const uint64_t* ll, uint32_t flag, Waiter& wt,
-                                               unsigned char* wl, uint32_t wave, int lane, float (&acc)[MT]) {
-  constexpr int PRO = RMS ? PRO_RMS : PRO_PLAIN;
-  h8* ops = (h8*)wl;
-  float* sums = (float*)(wl + WaveLds<1>::OPS);
-  float* dxs = (float*)(wl + WaveLds<1>::OPS + WaveLds<1>::TAB);
-  const uint32_t U = M.ng + (M.tail ? 1u : 0u);
-  const uint32_t nu = U > wave ? (U - 1 - wave) / PASS_WAVES + 1 : 0;
+// A wave's products for the workgroup's tiles from the staged operands (block
+// b of the matrix at staged block b - 4 u0): its units of units_load, W[j][i]
+// of tile j.  acc[j]: lanes of q == 0 hold row r's sum times 2^ex
+// (d (hi + lo) . w per block, + m s_x for Q4_1).
+template <uint32_t QT, int MT, int MU>
+__device__ __forceinline__ void units_mac(const WUnit (&W)[MT][MU], const PassMat& M, const h8* xs, const float* bsum,
+                                          uint32_t u0, uint32_t u1, uint32_t wave, int lane, float (&acc)[MT]) {
+  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
   const int q = lane >> 4, slot = lane & 15;
-  const uint32_t ub = lane >> 4, b = (lane >> 2) & 3, iq = lane & 3;
-  static_assert(!RMS || MU <= 4, "an RMS phase stages its units in one batch");
+  auto block = [&](const WUnit& w, int t, uint32_t b, int j, bool tail) {
+    const u4v X = __builtin_bit_cast(u4v, xs[(b * 4 + q) * 2 + min(slot, 1)]);
+    const h8 Aop = __builtin_bit_cast(h8, X & (slot < 2 ? ~0u : 0u));
+    h8 B;
+    float d, m;
+    if (tail) unit_block<QT, true>(w, j, B, d, m);
+    else unit_block<QT, false>(w, j, B, d, m);
+    const f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aop, B, f4{0, 0, 0, 0}, 0, 0, 0);
+    acc[t] += d * (D[0] + D[1]);
+    if (QT == LLMHIP_Q4_1) acc[t] += m * bsum[b];
+  };
 #pragma unroll
-  for (int i0 = 0; i0 < MU; i0 += 4) {
-    if ((uint32_t)i0 >= nu) break;
-    ItemsOf<1, PRO> it;
-    const uint32_t i = i0 + ub, unit = wave + PASS_WAVES * i;
-    const bool ok = i < nu && (unit < M.ng || b < M.tail);
-    const uint32_t e0 = ok ? (unit * 4 + b) * 32 + 4 * iq : 0;
-    if (FROM_LL) {
-      uint32_t idx[8];
-      bool need[8];
-      float v[8];
+  for (int i = 0; i < MU; i++) {
+    const uint32_t u = u0 + wave + PASS_WAVES * i;
+    if (u >= u1) break;
+    const uint32_t b0 = 4 * (u - u0);  // staged block of the unit's first
+    if (u < M.ng) {
+      // a full group: four blocks, no branch between them (their LDS reads,
+      // dequantisation and MFMAs interleave)
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
-        idx[c] = e0 + c;
-        idx[4 + c] = e0 + 16 + c;
-        need[c] = need[4 + c] = ok;
-      }
-      ll_wait<8>(ll, idx, need, flag, v, wt);
-      it.xa[0] = f4{v[0], v[1], v[2], v[3]};
-      it.xc[0] = f4{v[4], v[5], v[6], v[7]};
+      for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) block(W[t][i], t, b0 + j, j, false);
     } else {
-      const f4 z = {0, 0, 0, 0};
-      const f4 A = *(const f4*)(xin + e0), C = *(const f4*)(xin + e0 + 16);
-      it.xa[0] = ok ? A : z;
-      it.xc[0] = ok ? C : z;
-    }
-    if constexpr (RMS) {
-      it.wa = nrm.wa;
-      it.wc = nrm.wc;
-    }
-    const float rs1[1] = {1.f};
-    int ex[UB][1];
-    stage_items<QT, 1, PRO, 4>(it, rs1, lane, ops, sums, dxs, ex);
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int ii = i0 + u;
-      if (ii >= MU || (uint32_t)ii >= nu) break;
-      const uint32_t un = wave + PASS_WAVES * ii;
-      float dummy = 0;
+      for (int t = 0; t < MT; t++)
 #pragma unroll
-      for (int j = 0; j < MT; j++) {
-        if (un == M.ng)
-          unit_products<QT, 1, false, true>(W[j][ii], u, (int)M.tail, ops, sums, dxs, ex, q, slot, acc[j], dummy);
-        else
-          unit_products<QT, 1, false, false>(W[j][ii], u, 4, ops, sums, dxs, ex, q, slot, acc[j], dummy);
-      }
+        for (int j = 0; j < 3; j++)
+          if (j < (int)M.tail) block(W[t][i], t, b0 + j, j, true);
     }
   }
 }
 
-template <bool Q8, int MT, int MU, bool RMS, bool FROM_LL>
-__device__ __forceinline__ void units_products_any(const WUnit (&W)[MT][MU], const PassMat& M, const float* xin,
-                                                   const NormItems& nrm, const uint64_t* ll, uint32_t flag,
-                                                   Waiter& wt, unsigned char* wl, uint32_t wave, int lane,
-                                                   float (&acc)[MT]) {
-  if (Q8 && M.type == LLMHIP_Q8_0)
-    units_products<LLMHIP_Q8_0, MT, MU, RMS, FROM_LL>(W, M, xin, nrm, ll, flag, wt, wl, wave, lane, acc);
-  else if (M.type == LLMHIP_Q4_1)
-    units_products<LLMHIP_Q4_1, MT, MU, RMS, FROM_LL>(W, M, xin, nrm, ll, flag, wt, wl, wave, lane, acc);
-  else
-    units_products<LLMHIP_Q4_0, MT, MU, RMS, FROM_LL>(W, M, xin, nrm, ll, flag, wt, wl, wave, lane, acc);
+template <bool Q8, int MT, int MU>
+__device__ __forceinline__ void units_mac_any(const WUnit (&W)[MT][MU], const PassMat& M, const h8* xs,
+                                              const float* bsum, uint32_t u0, uint32_t u1, uint32_t wave, int lane,
+                                              float (&acc)[MT]) {
+  if (Q8 && M.type == LLMHIP_Q8_0) units_mac<LLMHIP_Q8_0, MT, MU>(W, M, xs, bsum, u0, u1, wave, lane, acc);
+  else if (M.type == LLMHIP_Q4_1) units_mac<LLMHIP_Q4_1, MT, MU>(W, M, xs, bsum, u0, u1, wave, lane, acc);
+  else units_mac<LLMHIP_Q4_0, MT, MU>(W, M, xs, bsum, u0, u1, wave, lane, acc);
 }
 
 // The waves' partial sums into LDS, a barrier, and for tile j < MT the sum
@@ -278,17 +401,37 @@ __device__ __forceinline__ float split_sum(float (*part)[PASS_WAVES][64], const 
   return v;
 }
 
+typedef const __attribute__((address_space(4))) PassMat CMat;
+// A matrix of the layer table (written by the host before the launch), field
+// by field: scalar loads, which do not wait behind the vector loads in flight.
+__device__ __forceinline__ PassMat cmat(CMat* c) {
+  PassMat m;
+  m.qs = c->qs;
+  m.type = c->type;
+  m.rows = c->rows;
+  m.nb = c->nb;
+  m.ng = c->ng;
+  m.tail = c->tail;
+  m.tiles = c->tiles;
+  m.map = c->map;
+  m.map_hd = c->map_hd;
+  m.map_seg0 = c->map_seg0;
+  m.map_seg1 = c->map_seg1;
+  m.ff = c->ff;
+  return m;
+}
+
 template <uint32_t HD, bool KVH, bool Q8>
 __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
-  constexpr uint32_t V4 = HD / 64, JM = HD == 64 ? 8 : 4, S = 4 * PASS_WAVES;
-  typedef AttnChunk<HD, JM, PASS_WAVES, KVH> AC;
+  constexpr uint32_t V4 = HD / 64, S = 4 * PASS_WAVES, JC = PASS_CHUNK_ROWS / S;
+  typedef AttnChunk<HD, JC, PASS_WAVES, KVH> AC;
   __shared__ PassLds<HD> L;
   const uint32_t wg = blockIdx.x, G = gridDim.x;
   const uint32_t E = a.embd, nq = a.embd, nk = a.kvd, hp = HD / 2;
   const uint32_t pos = state_pos(a.state);
   const uint32_t epoch = *(const __attribute__((address_space(4))) uint32_t*)a.ctrl;
   Waiter wt{a.ctrl + 1, a.ctrl[2] ? a.ctrl[2] : PASS_SPIN_DEFAULT, false};
-  float* xin = L.xin;
+  const uint32_t NCH = pass_chunks(HD), P = pos / PASS_CHUNK_ROWS + 1;  // chunks; those holding rows 0 .. pos
 // The thread's indices, redefined at each phase's start: per-lane offsets
 // formed from them stay inside the phase (hoisted out of the layer loop, every
 // phase's would hold registers through all the others).
@@ -297,67 +440,111 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
   asm volatile("" : "+v"(tid), "+s"(wave));            \
   const uint32_t lane = tid & 63;                      \
   const int r = lane & 15, q = lane >> 4;              \
-  unsigned char* wl = L.wl[wave];                      \
   (void)r;                                             \
-  (void)q;                                             \
-  (void)wl
+  (void)q
 
   // this workgroup's share (the same for every layer)
   const uint32_t T1 = (E + 2 * a.kvd + 15) / 16, T3 = (E + 15) / 16, T5 = (E + 15) / 16;
   const bool has1 = wg >= a.b1 && wg - a.b1 < T1, has3 = wg >= a.b3 && wg - a.b3 < T3,
-             has5 = wg >= a.b5 && wg - a.b5 < T5;
-  const uint32_t t1 = has1 ? wg - a.b1 : 0, t3 = has3 ? wg - a.b3 : 0, t5 = has5 ? wg - a.b5 : 0;
-  const uint32_t GQ = a.heads / a.kv_heads;
+             has5 = wg >= a.b5 && wg - a.b5 < a.kp * T5;
+  const uint32_t t1 = has1 ? wg - a.b1 : 0, t3 = has3 ? wg - a.b3 : 0;
+  const uint32_t t5 = has5 ? (wg - a.b5) % T5 : 0, p5 = has5 ? (wg - a.b5) / T5 : 0;  // K5 tile and part
+  const uint32_t GQ = a.heads / a.kv_heads, natt1 = 8 * GQ * ((a.kv_heads + 7) / 8);
   bool hasA = false;
-  uint32_t hg = 0, hh = 0;  // attention: KV head and query head
-  if (wg >= a.batt) {  // head h = g GQ + s on workgroup batt + 8 (GQ (g / 8) + s) + g % 8 (one XCD per KV head)
-    const uint32_t rel = wg - a.batt, y = rel / 8;
+  uint32_t hg = 0, hh = 0, hc = 0;  // attention: KV head, query head, chunk
+  if (wg >= a.batt && wg - a.batt < NCH * natt1) {
+    // head h = g GQ + s, chunk c on workgroup batt + c natt1 + 8 (GQ (g / 8) + s) + g % 8 (a KV head's
+    // query heads on one XCD)
+    const uint32_t rel0 = wg - a.batt, rel = rel0 % natt1, y = rel / 8;
+    hc = rel0 / natt1;
     hg = (y / GQ) * 8 + rel % 8;
     hh = hg * GQ + y % GQ;
-    hasA = hg < a.kv_heads;
+    hasA = hg < a.kv_heads && hc < P;  // a chunk past the position has nothing to do (K3 reads chunks < P)
   }
   const uint32_t rw4 = (wg + G - a.b4 % G) % G;
+  typedef const __attribute__((address_space(4))) PassLayer CLayer;
 
   for (uint32_t l = 0; l < a.nlayers; l++) {
-    const PassLayer& Y = a.layers[l];
+    CLayer* Y = (CLayer*)a.layers + l;
     const bool last = l + 1 == a.nlayers;
     const uint32_t F = epoch * a.nlayers + l + 1, Fp = F - 1;  // this layer's flag, the previous layer's
     // the flag-word pointers, redefined in every iteration: addresses formed
     // from them stay inside the iteration (hoisted out of the layer loop they
     // would hold registers through every phase)
-    uint64_t *llx = a.llx, *llb = a.llb, *llq = a.llq, *llatt = a.llatt, *llact = a.llact;
-    asm volatile("" : "+s"(llx), "+s"(llb), "+s"(llq), "+s"(llatt), "+s"(llact));
+    uint64_t *llb = a.llb, *llq = a.llq, *llo = a.llo, *llact = a.llact;
+    asm volatile("" : "+s"(llb), "+s"(llq), "+s"(llo), "+s"(llact));
+    // K3's and K4's weights, issued at the layer's start: a workgroup that
+    // has K1 or K2 work first would otherwise start them after it, and they
+    // would arrive inside the phase's wait
+    WUnit w3[1][1], w4[PASS_K4_TILES][1];
+    {
+      PHASE_IDS;
+      if (has3) {
+        const PassMat M = cmat(&Y->o);
+        const uint32_t tt3[1] = {min(t3, M.tiles - 1)};
+        const bool v3[1] = {true};
+        units_load_any<Q8, 1, 1>(w3, M, tt3, v3, 0, M.ng + (M.tail ? 1u : 0u), wave, lane);
+      }
+      const PassMat M = cmat(&Y->gu);
+      if (rw4 < M.tiles) {
+        uint32_t tt4[PASS_K4_TILES];
+        bool v4[PASS_K4_TILES];
+#pragma unroll
+        for (uint32_t j = 0; j < PASS_K4_TILES; j++) {
+          const uint32_t t = rw4 + G * j;
+          v4[j] = t < M.tiles;
+          tt4[j] = v4[j] ? t : 0;
+        }
+        units_load_any<Q8, PASS_K4_TILES, 1>(w4, M, tt4, v4, 0, M.ng + (M.tail ? 1u : 0u), wave, lane);
+      }
+    }
 
     // ---- K1: h = RMSNorm(x) attn_norm; [q; k; v] = W h (+ b); RoPE; K, V appended at pos
     if (has1) {
-      const PassMat& M = Y.qkv;
       PHASE_IDS;
+      const PassMat M = cmat(&Y->qkv);
+      const float* bias_p = Y->bias;
+      float* kvp = Y->kv;
       WUnit w1[1][1];
       const uint32_t tt1[1] = {min(t1, M.tiles - 1)};
       const bool v1[1] = {true};
-      units_load_any<Q8, 1, 1>(w1, M, tt1, v1, wave, lane);
-      const NormItems n1 = norm_load(M, Y.attn_norm, wave, lane);
-      const float ss = stage_row<true>(xin, L.misc, l ? llx : nullptr, a.xn, E, Fp, wt, tid, wave);
+      const uint32_t U = M.ng + (M.tail ? 1u : 0u);
+      units_load_any<Q8, 1, 1>(w1, M, tt1, v1, 0, U, wave, lane);
+      // the epilogue's inputs, ahead of the wait: the lane's bias and RoPE table entries
+      const uint32_t lr = row_of_pos(t1 * 16 + r, M.map, M.map_hd, M.map_seg0, M.map_seg1, M.ff);
+      const bool rv = wave == 0 && q == 0 && lr < M.rows;
+      float bias = 0, c = 0, sn = 0;
+      const uint32_t j = lr < nq ? lr : lr - nq, w = j & (HD - 1);
+      if (rv) {
+        if (bias_p) bias = bias_p[lr];
+        if (lr < nq + nk) {
+          const uint32_t i = a.neox ? w & (hp - 1) : w / 2;
+          const uint64_t co = ((uint64_t)pos * hp + i) * 2;
+          c = a.cs[co];
+          sn = a.cs[co + 1];
+        }
+      }
+      StageIn in{};
+      in.ll = llb;
+      in.plain = a.xn;
+      in.flag = Fp;
+      in.kp = a.kp;
+      in.E = E;
+      const int ex = l ? stage_ops<SRC_XSUM, true>(L, in, 0, M.nb, Y->attn_norm, a.eps, wt, tid, wave)
+                       : stage_ops<SRC_PLAIN, true>(L, in, 0, M.nb, Y->attn_norm, a.eps, wt, tid, wave);
       float acc[1] = {0};
-      units_products_any<Q8, 1, 1, true, false>(w1, M, xin, n1, nullptr, 0, wt, wl, wave, lane, acc);
+      units_mac_any<Q8, 1, 1>(w1, M, L.xs, L.bsum, 0, U, wave, lane, acc);
       float v = split_sum<1>(L.part, acc, wave, lane);
       if (wave == 0) {
-        const float rs = rms_scale((double)(ss / (float)E + a.eps));
-        v *= rs;
-        const uint32_t lr = row_of_pos(t1 * 16 + r, M.map, M.map_hd, M.map_seg0, M.map_seg1, M.ff);
-        const bool rv = q == 0 && lr < M.rows;
-        if (Y.bias && rv) v += Y.bias[lr];
+        v = ldexpf(v, -ex);
+        if (bias_p && rv) v += bias;
         const float o = __shfl_xor(v, a.neox ? 8 : 1);
         if (rv) {
           if (lr < nq + nk) {
-            const uint32_t j = lr < nq ? lr : lr - nq, w = j & (HD - 1);
             const bool first = a.neox ? w < hp : (w % 2) == 0;
-            const uint32_t i = a.neox ? w & (hp - 1) : w / 2;
-            const uint64_t co = ((uint64_t)pos * hp + i) * 2;
-            const float c = a.cs[co], sn = a.cs[co + 1];
-            const float x = first ? v : o, z = first ? o : v;
-            const float res = first ? __fsub_rn(__fmul_rn(x, c), __fmul_rn(z, sn))   // cpu.go:381
-                                    : __fadd_rn(__fmul_rn(x, sn), __fmul_rn(z, c));  // cpu.go:382
+            const float x = first ? v : o, zz = first ? o : v;
+            const float res = first ? __fsub_rn(__fmul_rn(x, c), __fmul_rn(zz, sn))   // cpu.go:381
+                                    : __fadd_rn(__fmul_rn(x, sn), __fmul_rn(zz, c));  // cpu.go:382
             if (lr < nq) {
               ll_store(llq + lr, res, F);
               if (last) a.q[lr] = res;
@@ -366,48 +553,50 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
               float kvv = res;
               if (KVH) {
                 const _Float16 hv = to_f16(res);
-                ((_Float16*)Y.kv)[ci] = hv;
+                ((_Float16*)kvp)[ci] = hv;
                 kvv = (float)hv;
               } else {
-                Y.kv[ci] = res;
+                kvp[ci] = res;
               }
               ll_store(llq + nq + j, kvv, F);
             }
           } else {
-            const uint32_t j = lr - nq - nk;
-            const uint64_t ci = (uint64_t)a.ctx * a.kvd + (uint64_t)pos * a.kvd + j;
+            const uint32_t jv = lr - nq - nk;
+            const uint64_t ci = (uint64_t)a.ctx * a.kvd + (uint64_t)pos * a.kvd + jv;
             float kvv = v;
             if (KVH) {
               const _Float16 hv = to_f16(v);
-              ((_Float16*)Y.kv)[ci] = hv;
+              ((_Float16*)kvp)[ci] = hv;
               kvv = (float)hv;
             } else {
-              Y.kv[ci] = v;
+              kvp[ci] = v;
             }
-            ll_store(llq + nq + nk + j, kvv, F);
+            ll_store(llq + nq + nk + jv, kvv, F);
           }
         }
       }
     }
 
-    // ---- K2: one query head over rows 0 .. pos (cpu.go:300-334): the rows of
-    // earlier positions from the cache, the position's row from K1's words
+    // ---- K2: query head hh over chunk hc's rows (cpu.go:300-334): the rows of
+    // earlier positions from the cache, the position's row from K1's words;
+    // out the chunk's max score M, sum of e L and sum of e v (unnormalised)
     if (hasA) {
       PHASE_IDS;
-      const uint32_t cl = tid & 15, slot = tid >> 4;
+      const uint32_t cl = tid & 15, slot = tid >> 4, row0 = hc * PASS_CHUNK_ROWS;
+      const float* kvp = Y->kv;
       AC rows;
       {
         // 32-bit element offsets (the cache holds 2 ctx kvd < 2^31 elements)
-        const uint32_t lim = max(pos, 1u), Jr = a.rows / S;
+        const uint32_t lim = max(pos, 1u), Jr = min(a.rows - min(a.rows, row0), PASS_CHUNK_ROWS) / S;
         const uint32_t kb = hg * HD + 4 * cl, vb = a.ctx * a.kvd + hg * HD + 4 * cl;
 #pragma unroll
-        for (uint32_t j = 0; j < JM; j++) {
+        for (uint32_t j = 0; j < JC; j++) {
           if (j >= Jr) break;
-          const uint32_t p = min(slot + S * j, lim - 1) * a.kvd;
+          const uint32_t p = min(row0 + slot + S * j, lim - 1) * a.kvd;
 #pragma unroll
           for (uint32_t v = 0; v < V4; v++) {
-            rows.kr[j][v] = kv_load4<KVH>(Y.kv, kb + p + 64 * v);
-            rows.vr[j][v] = kv_load4<KVH>(Y.kv, vb + p + 64 * v);
+            rows.kr[j][v] = kv_load4<KVH>(kvp, kb + p + 64 * v);
+            rows.vr[j][v] = kv_load4<KVH>(kvp, vb + p + 64 * v);
           }
         }
       }
@@ -425,7 +614,8 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
 #pragma unroll
         for (uint32_t k = 0; k < V4; k++) qv[k] = f4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
       }
-      if (slot == pos % S) {  // this thread's rows hold the position's row: K1's words
+      if (pos >= row0 && pos < row0 + PASS_CHUNK_ROWS && slot == (pos - row0) % S) {
+        // this thread's rows hold the position's row: K1's words
         uint32_t idx[8 * V4];
         bool need[8 * V4];
         float v[8 * V4];
@@ -436,9 +626,9 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
           need[k] = need[4 * V4 + k] = true;
         }
         ll_wait<8 * V4>(llq, idx, need, F, v, wt);
-        const uint32_t jp = pos / S;
+        const uint32_t jp = (pos - row0) / S;
 #pragma unroll
-        for (uint32_t j = 0; j < JM; j++)
+        for (uint32_t j = 0; j < JC; j++)
           if (j == jp)
 #pragma unroll
             for (uint32_t k = 0; k < V4; k++) {
@@ -448,74 +638,90 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
             }
       }
       float M_, L_, o;
-      rows.reduce(qv, 0, pos + 1, a.scale, L.am, &M_, &L_, &o);
-      if (tid < HD) {
-        const float att = o / L_;
-        ll_store(llatt + hh * HD + tid, att, F);
-        if (last) a.att[hh * HD + tid] = att;
+      rows.reduce(qv, row0, pos + 1, a.scale, L.am, &M_, &L_, &o);
+      if (tid < HD) ll_store(llo + hc * E + hh * HD + tid, o, F);
+      if (tid == 0) {
+        ll_store(llo + NCH * E + 2 * (hc * a.heads + hh), M_, F);
+        ll_store(llo + NCH * E + 2 * (hc * a.heads + hh) + 1, L_, F);
       }
     }
 
-    // ---- K3: x + W_o att
+    // ---- K3: x + W_o att, att merged from the chunks
     if (has3) {
-      const PassMat& M = Y.o;
       PHASE_IDS;
-      WUnit w3[1][1];
-      const uint32_t tt3[1] = {min(t3, M.tiles - 1)};
-      const bool v3[1] = {true};
-      units_load_any<Q8, 1, 1>(w3, M, tt3, v3, wave, lane);
-      stage_row<false>(xin, L.misc, llatt, nullptr, E, F, wt, tid, wave);
-      float acc[1] = {0};
-      const NormItems none = {};
-      units_products_any<Q8, 1, 1, false, false>(w3, M, xin, none, nullptr, 0, wt, wl, wave, lane, acc);
-      const float v = split_sum<1>(L.part, acc, wave, lane);
-      if (wave == 0) {
-        const uint32_t lr = t3 * 16 + r;
-        const bool rv = q == 0 && lr < M.rows;
-        float res = 0;
+      const PassMat M = cmat(&Y->o);
+      const uint32_t U = M.ng + (M.tail ? 1u : 0u);
+      // the residual row (x before this layer: layer 0's input, or the
+      // previous layer's attention residual plus its down projection's parts),
+      // ahead of the wait
+      const uint32_t lr = t3 * 16 + r;
+      const bool rv = wave == 0 && q == 0 && lr < M.rows;
+      uint64_t r0[1 + PASS_MAX_KP] = {};
+      float resf = 0;
+      if (rv) {
         if (l == 0) {
-          res = rv ? a.xn[lr] : 0.f;
+          resf = a.xn[lr];
         } else {
-          const uint32_t idx[1] = {lr};
-          const bool need[1] = {rv};
-          float x[1];
-          ll_wait<1>(llx, idx, need, Fp, x, wt);
-          res = x[0];
+#pragma unroll
+          for (uint32_t p = 0; p <= PASS_MAX_KP; p++)
+            if (p <= a.kp) r0[p] = ll_load(llb + p * E + lr);
         }
-        if (rv) ll_store(llb + lr, res + v, F);
+      }
+      StageIn in{};
+      in.ll = llo;
+      in.flag = F;
+      in.E = E;
+      in.heads = a.heads;
+      in.chunks = P;
+      in.nch = NCH;
+      in.store = last && t3 == 0 ? a.att : nullptr;
+      const int ex = stage_ops<SRC_MERGE, false>(L, in, 0, M.nb, nullptr, 0.f, wt, tid, wave);
+      float acc[1] = {0};
+      units_mac_any<Q8, 1, 1>(w3, M, L.xs, L.bsum, 0, U, wave, lane, acc);
+      const float v = split_sum<1>(L.part, acc, wave, lane);
+      if (rv) {
+        float res = resf;
+        if (l != 0) {
+          res = ll_settle(llb + lr, r0[0], Fp, wt);
+#pragma unroll
+          for (uint32_t p = 1; p <= PASS_MAX_KP; p++)
+            if (p <= a.kp) res += ll_settle(llb + p * E + lr, r0[p], Fp, wt);
+        }
+        ll_store(llb + lr, res + ldexpf(v, -ex), F);
       }
     }
 
     // ---- K4: h = RMSNorm(x) ffn_norm; act = silu(W_gate h) * (W_up h).
     // K5's weights are issued here too (its workgroups take part in K4).
     WUnit w5[1][PASS_K5_UNITS];
+    uint32_t u50 = 0, u51 = 0;  // K5: this part's units
     {
-      const PassMat& M = Y.gu;
+      const PassMat D = cmat(&Y->down);
+      const uint32_t U5 = D.ng + (D.tail ? 1u : 0u);
+      u50 = p5 * U5 / a.kp;
+      u51 = (p5 + 1) * U5 / a.kp;
+    }
+    {
+      const PassMat M = cmat(&Y->gu);
       if (rw4 < M.tiles) {
         PHASE_IDS;
-        WUnit w4[PASS_K4_TILES][1];
-        uint32_t tt4[PASS_K4_TILES];
-        bool v4[PASS_K4_TILES];
-#pragma unroll
-        for (uint32_t j = 0; j < PASS_K4_TILES; j++) {
-          const uint32_t t = rw4 + G * j;
-          v4[j] = t < M.tiles;
-          tt4[j] = v4[j] ? t : 0;
-        }
-        units_load_any<Q8, PASS_K4_TILES, 1>(w4, M, tt4, v4, wave, lane);
-        const NormItems n4 = norm_load(M, Y.ffn_norm, wave, lane);
+        const uint32_t U = M.ng + (M.tail ? 1u : 0u);
         if (has5) {
-          const uint32_t tt5[1] = {min(t5, Y.down.tiles - 1)};
+          const PassMat D = cmat(&Y->down);
+          const uint32_t tt5[1] = {min(t5, D.tiles - 1)};
           const bool v5[1] = {true};
-          units_load_any<Q8, 1, PASS_K5_UNITS>(w5, Y.down, tt5, v5, wave, lane);
+          units_load_any<Q8, 1, PASS_K5_UNITS>(w5, D, tt5, v5, u50, u51, wave, lane);
         }
-        const float ss = stage_row<true>(xin, L.misc, llb, nullptr, E, F, wt, tid, wave);
+        StageIn in{};
+        in.ll = llb;
+        in.flag = F;
+        const int ex = stage_ops<SRC_LL, true>(L, in, 0, M.nb, Y->ffn_norm, a.eps, wt, tid, wave);
         float acc[PASS_K4_TILES] = {};
-        units_products_any<Q8, PASS_K4_TILES, 1, true, false>(w4, M, xin, n4, nullptr, 0, wt, wl, wave, lane, acc);
+        units_mac_any<Q8, PASS_K4_TILES, 1>(w4, M, L.xs, L.bsum, 0, U, wave, lane, acc);
         float v = split_sum<PASS_K4_TILES>(L.part, acc, wave, lane);
         const uint32_t tile = rw4 + G * wave;
         if (wave < PASS_K4_TILES && tile < M.tiles) {
-          v *= rms_scale((double)(ss / (float)E + a.eps));
+          v = ldexpf(v, -ex);
           // gate row i at lane r < 8, up row i at r + 8 (MAP_GATEUP)
           const float u = __shfl_xor(v, 8);
           const uint32_t i = 8 * tile + (r & 7);
@@ -531,33 +737,48 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
         }
       } else if (has5) {
         PHASE_IDS;
-        const uint32_t tt5[1] = {min(t5, Y.down.tiles - 1)};
+        const PassMat D = cmat(&Y->down);
+        const uint32_t tt5[1] = {min(t5, D.tiles - 1)};
         const bool v5[1] = {true};
-        units_load_any<Q8, 1, PASS_K5_UNITS>(w5, Y.down, tt5, v5, wave, lane);
+        units_load_any<Q8, 1, PASS_K5_UNITS>(w5, D, tt5, v5, u50, u51, wave, lane);
       }
     }
 
-    // ---- K5: x + W_down act
+    // ---- K5: part p5 of W_down act (its k-range of units [u50, u51)); the
+    // next layer (or the last step) adds the parts to the residual
     if (has5) {
-      const PassMat& M = Y.down;
       PHASE_IDS;
-      __syncthreads();  // K4's epilogue has read the partials (K5 stages no row, whose barrier would order it)
+      const PassMat M = cmat(&Y->down);
+      // (stage_ops's barriers also order K4's epilogue reads of the partials
+      // before this phase's writes)
+      StageIn in{};
+      in.ll = llact;
+      in.flag = F;
+      const uint32_t nb0 = 4 * u50, nbp = min(4 * u51, M.nb) - nb0;
+      const int ex = stage_ops<SRC_LL, false>(L, in, nb0, nbp, nullptr, 0.f, wt, tid, wave);
       float acc[1] = {0};
-      const NormItems none = {};
-      units_products_any<Q8, 1, PASS_K5_UNITS, false, true>(w5, M, nullptr, none, llact, F, wt, wl, wave, lane, acc);
+      units_mac_any<Q8, 1, PASS_K5_UNITS>(w5, M, L.xs, L.bsum, u50, u51, wave, lane, acc);
       const float v = split_sum<1>(L.part, acc, wave, lane);
-      if (wave == 0) {
-        const uint32_t lr = t5 * 16 + r;
-        const bool rv = q == 0 && lr < M.rows;
-        const uint32_t idx[1] = {lr};
-        const bool need[1] = {rv};
-        float x[1];
-        ll_wait<1>(llb, idx, need, F, x, wt);
-        if (rv) {
-          if (last) a.x[lr] = x[0] + v;
-          else ll_store(llx + lr, x[0] + v, F);
-        }
-      }
+      const uint32_t lr = t5 * 16 + r;
+      if (wave == 0 && q == 0 && lr < M.rows) ll_store(llb + (1 + p5) * E + lr, ldexpf(v, -ex), F);
+    }
+  }
+
+  // ---- the pass's output row: x = the last layer's residual plus its down
+  // projection's parts (the head's input, Peek("x"))
+  if (wg < T3) {
+    PHASE_IDS;
+    const uint32_t lr = wg * 16 + r, F = epoch * a.nlayers + a.nlayers;
+    if (wave == 0 && q == 0 && lr < E) {
+      uint64_t r0[1 + PASS_MAX_KP] = {};
+#pragma unroll
+      for (uint32_t p = 0; p <= PASS_MAX_KP; p++)
+        if (p <= a.kp) r0[p] = ll_load(a.llb + p * E + lr);
+      float x = ll_settle(a.llb + lr, r0[0], F, wt);
+#pragma unroll
+      for (uint32_t p = 1; p <= PASS_MAX_KP; p++)
+        if (p <= a.kp) x += ll_settle(a.llb + p * E + lr, r0[p], F, wt);
+      a.x[lr] = x;
     }
   }
 }
@@ -567,17 +788,26 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
 // ------------------------------------------------------------------ host
 
 const char* pass_unfit(const llmhip_config& c, uint32_t kvd, const PassMat& qkv, const PassMat& o, const PassMat& gu,
-                       const PassMat& down, uint32_t grid) {
+                       const PassMat& down, uint32_t grid, uint32_t* kp) {
   if (grid == 0) return "no co-resident grid";
   if (c.head_dim != 64 && c.head_dim != 128) return "head size";
   if ((uint32_t)c.embd > PASS_MAX_EMBD) return "embedding above the staged row";
+  if ((uint32_t)c.ff > PASS_MAX_FF) return "feed-forward above the staged row";
   const uint32_t E = (uint32_t)c.embd, GQ = (uint32_t)(c.heads / c.kv_heads);
-  if ((E + 2 * kvd + 15) / 16 > grid || (E + 15) / 16 > grid) return "more tiles than workgroups";
-  if (8 * GQ * ((uint32_t)(c.kv_heads + 7) / 8) > grid) return "more heads than workgroups";
+  const uint32_t T5 = (E + 15) / 16;
+  if ((E + 2 * kvd + 15) / 16 > grid || T5 > grid) return "more tiles than workgroups";
+  if (pass_chunks((uint32_t)c.head_dim) * 8 * GQ * ((uint32_t)(c.kv_heads + 7) / 8) > grid)
+    return "more heads than workgroups";
   auto units = [](const PassMat& m) { return m.ng + (m.tail ? 1u : 0u); };
   if (units(qkv) > PASS_WAVES || units(o) > PASS_WAVES || units(gu) > PASS_WAVES)
     return "more units per tile than waves";
-  if (units(down) > PASS_WAVES * PASS_K5_UNITS) return "down projection too long";
+  *kp = 0;
+  for (uint32_t k : {2u, 1u})  // the most k-parts the grid holds (PASS_MAX_KP)
+    if (k * T5 <= grid && (units(down) + k - 1) / k <= PASS_WAVES * PASS_K5_UNITS && units(down) >= k) {
+      *kp = k;
+      break;
+    }
+  if (*kp == 0) return "down projection too long";
   if (gu.tiles > PASS_K4_TILES * grid) return "gate/up too tall";
   if (gu.map != MAP_GATEUP || o.map != MAP_IDENT || down.map != MAP_IDENT) return "row maps";
   if (qkv.rows != E + 2 * kvd || o.rows != E || down.rows != E || gu.rows != 2 * (uint32_t)c.ff) return "shapes";
@@ -603,18 +833,19 @@ uint32_t pass_grid(int device, uint32_t hd, bool kv16) {
   return 0;
 }
 
-// K1's tiles from workgroup 0, the attention heads after them (from a
-// multiple of 8: a KV head's query heads on one XCD), K3's tiles after those
-// where they fit, K5's at the end (their weights are the largest share a
-// workgroup holds), K4 round robin over the whole grid.  Where the grid is
-// too small for disjoint ranges they overlap (the phases run in turn).
-void pass_place(PassArgs* a, uint32_t grid, uint32_t t1, uint32_t t3, uint32_t t5, uint32_t natt) {
+// K1's tiles from workgroup 0, the attention's (head, chunk)s after them
+// (from a multiple of 8: a KV head's query heads on one XCD), K3's tiles
+// after those where they fit, K5's (tile, part)s at the end, K4 round robin
+// over the whole grid.  Where the grid is too small for disjoint ranges they
+// overlap (the phases run in turn).
+void pass_place(PassArgs* a, uint32_t grid, uint32_t t1, uint32_t t3, uint32_t t5) {
+  const uint32_t natt = pass_chunks(a->hd) * 8 * (a->heads / a->kv_heads) * ((a->kv_heads + 7) / 8);
   a->b1 = 0;
   a->batt = (t1 + 7) / 8 * 8;
   if (a->batt + natt > grid) a->batt = 0;
-  a->b5 = grid - t5;
+  a->b5 = grid - a->kp * t5;
   const uint32_t e = std::max(t1, a->batt + natt);
-  a->b3 = e + t3 <= grid - t5 ? e : 0;
+  a->b3 = e + t3 <= a->b5 ? e : 0;
   a->b4 = 0;
 }
 
