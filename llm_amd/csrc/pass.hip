@@ -81,6 +81,29 @@ __device__ __forceinline__ void ll_wait_f(At at, Need need, uint32_t flag, float
   for (int i = 0; i < N; i++) v[i] = __uint_as_float((uint32_t)x[i]);
 }
 
+// ll_wait_f preceded by a gate: the wave's first lane polls its first word
+// alone until it carries the flag.  A workgroup that reaches a phase long
+// before the phase's input is produced then waits with one load in flight
+// per wave instead of its whole input's, which leaves the memory system to
+// the phases still running.
+template <int N, class At, class Need>
+__device__ __forceinline__ void ll_wait_gated(At at, Need need, uint32_t flag, float (&v)[N], Waiter& w) {
+  const bool g = (threadIdx.x & 63) == 0 && need(0);
+  uint32_t spins = 0;
+  for (;;) {
+    bool ok = true;
+    if (g && !w.dead) ok = (uint32_t)(ll_load(at(0)) >> 32) == flag;
+    if (__all(ok)) break;
+    if (++spins > w.limit) {  // (spins: the same in every lane)
+      if (!w.dead) atomicOr(w.err, 1u);
+      w.dead = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  ll_wait_f<N>(at, need, flag, v, w);
+}
+
 // ll_wait_f over base[idx[i]] where need[i].
 template <int N>
 __device__ __forceinline__ void ll_wait(const uint64_t* base, const uint32_t (&idx)[N], const bool (&need)[N],
@@ -150,13 +173,13 @@ __device__ __forceinline__ void load_row(const StageIn& in, uint32_t base, uint3
     for (uint32_t k = 0; k < NW; k++) v[k] = tid + T * k < n ? in.plain[base + tid + T * k] : 0.f;
   } else if constexpr (SRC == SRC_LL) {
     const uint64_t* p = in.ll + base + tid;
-    ll_wait_f<NW>([&](int i) { return p + T * i; }, [&](int i) { return tid + T * i < n; }, in.flag, v, w);
+    ll_wait_gated<NW>([&](int i) { return p + T * i; }, [&](int i) { return tid + T * i < n; }, in.flag, v, w);
   } else if constexpr (SRC == SRC_XSUM) {
     constexpr uint32_t NP = 1 + PASS_MAX_KP;
     float u[NW * NP];
     // word i: vector i / NW (xb, then the parts), element tid + T (i % NW)
     const uint64_t* p = in.ll + tid;
-    ll_wait_f<NW * NP>([&](int i) { return p + (i / NW) * in.E + T * (i % NW); },
+    ll_wait_gated<NW * NP>([&](int i) { return p + (i / NW) * in.E + T * (i % NW); },
                        [&](int i) { return (uint32_t)(i / NW) <= in.kp && tid + T * (i % NW) < n; }, in.flag, u, w);
 #pragma unroll
     for (uint32_t k = 0; k < NW; k++) {
@@ -172,7 +195,7 @@ __device__ __forceinline__ void load_row(const StageIn& in, uint32_t base, uint3
     const uint32_t mlb = in.nch * in.E;
     // words [0, NW MC): chunk i / NW's o at element tid + T (i % NW); then for chunk j / (2 NW) and
     // element k = (j / 2) % NW, the element's head's m (j even) and l (j odd)
-    ll_wait_f<3 * NW * MC>(
+    ll_wait_gated<3 * NW * MC>(
         [&](int i) {
           if (i < (int)(NW * MC)) return in.ll + (i / NW) * in.E + tid + T * (i % NW);
           const uint32_t j = i - NW * MC, c = j / (2 * NW), k = (j / 2) % NW;
