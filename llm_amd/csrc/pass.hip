@@ -127,7 +127,6 @@ __device__ __forceinline__ float ll_settle(const uint64_t* p, uint64_t x, uint32
 }
 
 constexpr uint32_t PASS_MAX_ITEMS = PASS_MAX_FF / 8;  // items of 8 elements of the longest staged row
-constexpr uint32_t IPT = (PASS_MAX_ITEMS + 64 * PASS_WAVES - 1) / (64 * PASS_WAVES);  // items per thread
 constexpr uint32_t PASS_MAX_KP = 2;
 constexpr uint32_t WPT_E = PASS_MAX_EMBD / (64 * PASS_WAVES);  // row elements per thread, rows of length E
 constexpr uint32_t WPT_F = PASS_MAX_FF / (64 * PASS_WAVES);    // row elements per thread, the longest row
@@ -229,23 +228,27 @@ __device__ __forceinline__ void load_row(const StageIn& in, uint32_t base, uint3
   }
 }
 
-// The phase's input row (nb blocks of 32 from block nb0 on) staged by the
-// whole workgroup as the A operands of its units, in LDS: item it =
-// (block it / 4, k-group it % 4: elements 4 (it % 4) + 0..3 and
-// 16 + 4 (it % 4) + 0..3 of the block) in MFMA element order, scaled by 2^ex
-// so that the staged values' largest magnitude sits in [2^14, 2^15), and split
-// exactly into f16 hi (xs[2 it]) + lo (xs[2 it + 1]); the blocks' sums (Q4_1:
-// cpu.go:196-198) scaled alike.  RMS: the row is first normed,
-// h = (x s) w with s = f32(1/sqrt(f64(sum x^2 / n + eps))) (cpu.go:90-96);
-// the largest |x w| goes through the same barrier as the sum of squares
-// (max |h| = s max |x w|, s > 0).  The row is polled in element order into
-// LDS (load_row), the norm weights loaded before the wait; the items are then
-// formed from LDS.  Returns ex; two barriers.
-template <int SRC, bool RMS, uint32_t HD>
-__device__ __forceinline__ int stage_ops(PassLds<HD>& L, const StageIn& in, uint32_t nb0, uint32_t nb,
-                                         const float* nw, float eps, Waiter& w, uint32_t tid, uint32_t wave) {
+// The phase's input row (nb blocks of 32 from block nb0 on) staged as the A
+// operands of the wave's units (those of units_load: u = u0 + wave + 8 i < u1,
+// i < MU), in LDS: item it = (block it / 4, k-group it % 4: elements
+// 4 (it % 4) + 0..3 and 16 + 4 (it % 4) + 0..3 of the block) in MFMA element
+// order, scaled by 2^ex so that the staged values' largest magnitude sits in
+// [2^14, 2^15), and split exactly into f16 hi (xs[2 it]) + lo (xs[2 it + 1]);
+// the blocks' sums (Q4_1: cpu.go:196-198) scaled alike.  RMS: the row is first
+// normed, h = (x s) w with s = f32(1/sqrt(f64(sum x^2 / n + eps)))
+// (cpu.go:90-96); the largest |x w| goes through the same barrier as the sum
+// of squares (max |h| = s max |x w|, s > 0).  The row is polled in element
+// order into LDS (load_row), the norm weights loaded before the wait; after
+// one barrier each wave forms its own units' items from LDS (no other wave
+// reads them; the next phase overwrites the row only after split_sum's
+// barrier).  Returns ex.
+template <int SRC, bool RMS, int MU, uint32_t HD>
+__device__ __forceinline__ int stage_ops(PassLds<HD>& L, const StageIn& in, uint32_t nb0, uint32_t nb, uint32_t u0,
+                                         uint32_t u1, const float* nw, float eps, Waiter& w, uint32_t tid,
+                                         uint32_t wave) {
   constexpr uint32_t T = 64 * PASS_WAVES;
   constexpr uint32_t NW = (SRC == SRC_LL && !RMS) ? WPT_F : WPT_E;
+  static_assert(16 * MU <= 64, "a wave forms its units' items in one pass");
   const uint32_t n = nb * 32, NI = nb * 4, lane = tid & 63;
   float wv[NW];
   if (RMS)
@@ -284,44 +287,42 @@ __device__ __forceinline__ int stage_ops(PassLds<HD>& L, const StageIn& in, uint
     frexpf(m, &E);
     ex = 15 - E;
   }
+  // lane: item lane % 16 of the wave's unit lane / 16
+  const uint32_t i = lane / 16, u = u0 + wave + PASS_WAVES * i;
+  const uint32_t it = 16 * (u - u0) + (lane & 15);
+  const bool ok = (int)i < MU && u < u1 && it < NI;
+  const uint32_t e0 = (it / 4) * 32 + 4 * (it % 4);
+  f4 a = {0, 0, 0, 0}, c = {0, 0, 0, 0};
+  if (ok) {
+    a = *(const f4*)&L.row[e0];
+    c = *(const f4*)&L.row[e0 + 16];
+    if (RMS) {
+      const f4 wa = *(const f4*)&L.nw[e0], wc = *(const f4*)&L.nw[e0 + 16];
 #pragma unroll
-  for (uint32_t k = 0; k < IPT; k++) {
-    const uint32_t it = tid + T * k;
-    if (k > 0 && NW == WPT_E) break;  // rows of length E: one item per thread
-    const uint32_t e0 = (it / 4) * 32 + 4 * (it % 4);
-    const bool ok = it < NI;
-    f4 a = {0, 0, 0, 0}, c = {0, 0, 0, 0};
-    if (ok) {
-      a = *(const f4*)&L.row[e0];
-      c = *(const f4*)&L.row[e0 + 16];
-      if (RMS) {
-        const f4 wa = *(const f4*)&L.nw[e0], wc = *(const f4*)&L.nw[e0 + 16];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          a[i] = __fmul_rn(__fmul_rn(a[i], s), wa[i]);  // cpu.go:96
-          c[i] = __fmul_rn(__fmul_rn(c[i], s), wc[i]);
-        }
+      for (int k = 0; k < 4; k++) {
+        a[k] = __fmul_rn(__fmul_rn(a[k], s), wa[k]);  // cpu.go:96
+        c[k] = __fmul_rn(__fmul_rn(c[k], s), wc[k]);
       }
     }
-    const float vv[8] = {a[0], a[2], c[0], c[2], a[1], a[3], c[1], c[3]};
-    h8 hi, lo;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float sv = ldexpf(vv[i], ex);
-      const _Float16 h = (_Float16)sv;
-      hi[i] = h;
-      lo[i] = (_Float16)(sv - (float)h);
-    }
-    float sx = (a[0] + a[1] + a[2] + a[3]) + (c[0] + c[1] + c[2] + c[3]);
-    sx += __shfl_xor(sx, 1);  // a block's four items: four consecutive lanes
-    sx += __shfl_xor(sx, 2);
-    if (ok) {
-      L.xs[2 * it] = hi;
-      L.xs[2 * it + 1] = lo;
-      if ((it & 3) == 0) L.bsum[it / 4] = ldexpf(sx, ex);
-    }
   }
-  __syncthreads();
+  const float vv[8] = {a[0], a[2], c[0], c[2], a[1], a[3], c[1], c[3]};
+  h8 hi, lo;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const float sv = ldexpf(vv[k], ex);
+    const _Float16 h = (_Float16)sv;
+    hi[k] = h;
+    lo[k] = (_Float16)(sv - (float)h);
+  }
+  float sx = (a[0] + a[1] + a[2] + a[3]) + (c[0] + c[1] + c[2] + c[3]);
+  sx += __shfl_xor(sx, 1);  // a block's four items: four consecutive lanes
+  sx += __shfl_xor(sx, 2);
+  if (ok) {
+    L.xs[2 * it] = hi;
+    L.xs[2 * it + 1] = lo;
+    if ((it & 3) == 0) L.bsum[it / 4] = ldexpf(sx, ex);
+  }
+  __builtin_amdgcn_wave_barrier();
   return ex;
 }
 
@@ -358,55 +359,89 @@ __device__ __forceinline__ void units_load_any(WUnit (&W)[MT][MU], const PassMat
   else units_load<LLMHIP_Q4_0, MT, MU>(W, M, tile, tv, u0, u1, wave, lane);
 }
 
-// A wave's products for the workgroup's tiles from the staged operands (block
-// b of the matrix at staged block b - 4 u0): its units of units_load, W[j][i]
-// of tile j.  acc[j]: lanes of q == 0 hold row r's sum times 2^ex
-// (d (hi + lo) . w per block, + m s_x for Q4_1).
+// A wave's units dequantised (B operands and block scales; m: Q4_1's block
+// minima), ahead of the wait for the phase's input: after the wait only the
+// MFMAs remain.
+template <int MT, int MU>
+struct UnitsB {
+  h8 B[MT][MU][4];
+  float d[MT][MU][4], m[MT][MU][4];
+};
+
 template <uint32_t QT, int MT, int MU>
-__device__ __forceinline__ void units_mac(const WUnit (&W)[MT][MU], const PassMat& M, const h8* xs, const float* bsum,
-                                          uint32_t u0, uint32_t u1, uint32_t wave, int lane, float (&acc)[MT]) {
-  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
-  const int q = lane >> 4, slot = lane & 15;
-  auto block = [&](const WUnit& w, int t, uint32_t b, int j, bool tail) {
-    const u4v X = __builtin_bit_cast(u4v, xs[(b * 4 + q) * 2 + min(slot, 1)]);
-    const h8 Aop = __builtin_bit_cast(h8, X & (slot < 2 ? ~0u : 0u));
-    h8 B;
-    float d, m;
-    if (tail) unit_block<QT, true>(w, j, B, d, m);
-    else unit_block<QT, false>(w, j, B, d, m);
-    const f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aop, B, f4{0, 0, 0, 0}, 0, 0, 0);
-    acc[t] += d * (D[0] + D[1]);
-    if (QT == LLMHIP_Q4_1) acc[t] += m * bsum[b];
-  };
+__device__ __forceinline__ void units_deq(const WUnit (&W)[MT][MU], const PassMat& M, uint32_t u0, uint32_t wave,
+                                          UnitsB<MT, MU>& ub) {
 #pragma unroll
   for (int i = 0; i < MU; i++) {
     const uint32_t u = u0 + wave + PASS_WAVES * i;
-    if (u >= u1) break;
-    const uint32_t b0 = 4 * (u - u0);  // staged block of the unit's first
-    if (u < M.ng) {
-      // a full group: four blocks, no branch between them (their LDS reads,
-      // dequantisation and MFMAs interleave)
 #pragma unroll
-      for (int t = 0; t < MT; t++)
+    for (int t = 0; t < MT; t++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) block(W[t][i], t, b0 + j, j, false);
-    } else {
-#pragma unroll
-      for (int t = 0; t < MT; t++)
-#pragma unroll
-        for (int j = 0; j < 3; j++)
-          if (j < (int)M.tail) block(W[t][i], t, b0 + j, j, true);
-    }
+      for (int j = 0; j < 4; j++) {
+        ub.B[t][i][j] = h8{};
+        ub.d[t][i][j] = ub.m[t][i][j] = 0.f;
+        if (u < M.ng) unit_block<QT, false>(W[t][i], j, ub.B[t][i][j], ub.d[t][i][j], ub.m[t][i][j]);
+        else if (j < 3) unit_block<QT, true>(W[t][i], j, ub.B[t][i][j], ub.d[t][i][j], ub.m[t][i][j]);
+      }
   }
 }
 
 template <bool Q8, int MT, int MU>
-__device__ __forceinline__ void units_mac_any(const WUnit (&W)[MT][MU], const PassMat& M, const h8* xs,
+__device__ __forceinline__ void units_deq_any(const WUnit (&W)[MT][MU], const PassMat& M, uint32_t u0, uint32_t wave,
+                                              UnitsB<MT, MU>& ub) {
+  if (Q8 && M.type == LLMHIP_Q8_0) units_deq<LLMHIP_Q8_0, MT, MU>(W, M, u0, wave, ub);
+  else if (M.type == LLMHIP_Q4_1) units_deq<LLMHIP_Q4_1, MT, MU>(W, M, u0, wave, ub);
+  else units_deq<LLMHIP_Q4_0, MT, MU>(W, M, u0, wave, ub);
+}
+
+// A wave's products for the workgroup's tiles from the staged operands (block
+// b of the matrix at staged block b - 4 u0): its units of units_load, ub.B[j][i]
+// of tile j.  acc[j]: lanes of q == 0 hold row r's sum times 2^ex
+// (d (hi + lo) . w per block, + m s_x for Q4_1, added block by block).  Every
+// A operand is read before the first MFMA and the MFMAs issue back to back
+// (a block outside the wave's units reads staged block 0 and adds nothing).
+template <uint32_t QT, int MT, int MU>
+__device__ __forceinline__ void units_mac(const UnitsB<MT, MU>& ub, const PassMat& M, const h8* xs,
+                                          const float* bsum, uint32_t u0, uint32_t u1, uint32_t wave, int lane,
+                                          float (&acc)[MT]) {
+  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+  const int q = lane >> 4, slot = lane & 15;
+  const u4v keep = slot < 2 ? ~0u : 0u;
+  h8 A[MU][4];
+  float bs[MU][4];
+  bool on[MU][4];
+#pragma unroll
+  for (int i = 0; i < MU; i++) {
+    const uint32_t u = u0 + wave + PASS_WAVES * i;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      on[i][j] = u < u1 && (u < M.ng || j < (int)M.tail);
+      const uint32_t b = on[i][j] ? 4 * (u - u0) + j : 0;
+      A[i][j] = __builtin_bit_cast(h8, __builtin_bit_cast(u4v, xs[(b * 4 + q) * 2 + min(slot, 1)]) & keep);
+      bs[i][j] = QT == LLMHIP_Q4_1 ? bsum[b] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MU; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+        const f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][j], ub.B[t][i][j], f4{0, 0, 0, 0}, 0, 0, 0);
+        if (on[i][j]) {
+          acc[t] += ub.d[t][i][j] * (D[0] + D[1]);
+          if (QT == LLMHIP_Q4_1) acc[t] += ub.m[t][i][j] * bs[i][j];
+        }
+      }
+}
+
+template <bool Q8, int MT, int MU>
+__device__ __forceinline__ void units_mac_any(const UnitsB<MT, MU>& ub, const PassMat& M, const h8* xs,
                                               const float* bsum, uint32_t u0, uint32_t u1, uint32_t wave, int lane,
                                               float (&acc)[MT]) {
-  if (Q8 && M.type == LLMHIP_Q8_0) units_mac<LLMHIP_Q8_0, MT, MU>(W, M, xs, bsum, u0, u1, wave, lane, acc);
-  else if (M.type == LLMHIP_Q4_1) units_mac<LLMHIP_Q4_1, MT, MU>(W, M, xs, bsum, u0, u1, wave, lane, acc);
-  else units_mac<LLMHIP_Q4_0, MT, MU>(W, M, xs, bsum, u0, u1, wave, lane, acc);
+  if (Q8 && M.type == LLMHIP_Q8_0) units_mac<LLMHIP_Q8_0, MT, MU>(ub, M, xs, bsum, u0, u1, wave, lane, acc);
+  else if (M.type == LLMHIP_Q4_1) units_mac<LLMHIP_Q4_1, MT, MU>(ub, M, xs, bsum, u0, u1, wave, lane, acc);
+  else units_mac<LLMHIP_Q4_0, MT, MU>(ub, M, xs, bsum, u0, u1, wave, lane, acc);
 }
 
 // The waves' partial sums into LDS, a barrier, and for tile j < MT the sum
@@ -553,10 +588,12 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       in.flag = Fp;
       in.kp = a.kp;
       in.E = E;
-      const int ex = l ? stage_ops<SRC_XSUM, true>(L, in, 0, M.nb, Y->attn_norm, a.eps, wt, tid, wave)
-                       : stage_ops<SRC_PLAIN, true>(L, in, 0, M.nb, Y->attn_norm, a.eps, wt, tid, wave);
+      UnitsB<1, 1> ub;
+      units_deq_any<Q8, 1, 1>(w1, M, 0, wave, ub);
+      const int ex = l ? stage_ops<SRC_XSUM, true, 1>(L, in, 0, M.nb, 0, U, Y->attn_norm, a.eps, wt, tid, wave)
+                       : stage_ops<SRC_PLAIN, true, 1>(L, in, 0, M.nb, 0, U, Y->attn_norm, a.eps, wt, tid, wave);
       float acc[1] = {0};
-      units_mac_any<Q8, 1, 1>(w1, M, L.xs, L.bsum, 0, U, wave, lane, acc);
+      units_mac_any<Q8, 1, 1>(ub, M, L.xs, L.bsum, 0, U, wave, lane, acc);
       float v = split_sum<1>(L.part, acc, wave, lane);
       if (wave == 0) {
         v = ldexpf(v, -ex);
@@ -698,9 +735,11 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       in.chunks = P;
       in.nch = NCH;
       in.store = last && t3 == 0 ? a.att : nullptr;
-      const int ex = stage_ops<SRC_MERGE, false>(L, in, 0, M.nb, nullptr, 0.f, wt, tid, wave);
+      UnitsB<1, 1> ub;
+      units_deq_any<Q8, 1, 1>(w3, M, 0, wave, ub);
+      const int ex = stage_ops<SRC_MERGE, false, 1>(L, in, 0, M.nb, 0, U, nullptr, 0.f, wt, tid, wave);
       float acc[1] = {0};
-      units_mac_any<Q8, 1, 1>(w3, M, L.xs, L.bsum, 0, U, wave, lane, acc);
+      units_mac_any<Q8, 1, 1>(ub, M, L.xs, L.bsum, 0, U, wave, lane, acc);
       const float v = split_sum<1>(L.part, acc, wave, lane);
       if (rv) {
         float res = resf;
@@ -738,9 +777,11 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
         StageIn in{};
         in.ll = llb;
         in.flag = F;
-        const int ex = stage_ops<SRC_LL, true>(L, in, 0, M.nb, Y->ffn_norm, a.eps, wt, tid, wave);
+        UnitsB<PASS_K4_TILES, 1> ub;
+        units_deq_any<Q8, PASS_K4_TILES, 1>(w4, M, 0, wave, ub);
+        const int ex = stage_ops<SRC_LL, true, 1>(L, in, 0, M.nb, 0, U, Y->ffn_norm, a.eps, wt, tid, wave);
         float acc[PASS_K4_TILES] = {};
-        units_mac_any<Q8, PASS_K4_TILES, 1>(w4, M, L.xs, L.bsum, 0, U, wave, lane, acc);
+        units_mac_any<Q8, PASS_K4_TILES, 1>(ub, M, L.xs, L.bsum, 0, U, wave, lane, acc);
         float v = split_sum<PASS_K4_TILES>(L.part, acc, wave, lane);
         const uint32_t tile = rw4 + G * wave;
         if (wave < PASS_K4_TILES && tile < M.tiles) {
@@ -772,15 +813,17 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
     if (has5) {
       PHASE_IDS;
       const PassMat M = cmat(&Y->down);
-      // (stage_ops's barriers also order K4's epilogue reads of the partials
+      // (stage_ops's barrier also orders K4's epilogue reads of the partials
       // before this phase's writes)
       StageIn in{};
       in.ll = llact;
       in.flag = F;
       const uint32_t nb0 = 4 * u50, nbp = min(4 * u51, M.nb) - nb0;
-      const int ex = stage_ops<SRC_LL, false>(L, in, nb0, nbp, nullptr, 0.f, wt, tid, wave);
+      UnitsB<1, PASS_K5_UNITS> ub;
+      units_deq_any<Q8, 1, PASS_K5_UNITS>(w5, M, u50, wave, ub);
+      const int ex = stage_ops<SRC_LL, false, PASS_K5_UNITS>(L, in, nb0, nbp, u50, u51, nullptr, 0.f, wt, tid, wave);
       float acc[1] = {0};
-      units_mac_any<Q8, 1, PASS_K5_UNITS>(w5, M, L.xs, L.bsum, u50, u51, wave, lane, acc);
+      units_mac_any<Q8, 1, PASS_K5_UNITS>(ub, M, L.xs, L.bsum, u50, u51, wave, lane, acc);
       const float v = split_sum<1>(L.part, acc, wave, lane);
       const uint32_t lr = t5 * 16 + r;
       if (wave == 0 && q == 0 && lr < M.rows) ll_store(llb + (1 + p5) * E + lr, ldexpf(v, -ex), F);
