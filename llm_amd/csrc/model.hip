@@ -1129,10 +1129,9 @@ static int pass_setup(Model& m) {
   a.att = m.att;
   a.act = m.act;
   a.up = m.gbuf;
-  const uint64_t nch = pass_chunks((uint32_t)c.head_dim);
   a.llq = m.ll;                                        // [E + 2 kvd]
-  a.llo = a.llq + E + 2ull * m.kvd;                    // [chunks][E], then [chunks][heads][2]
-  a.llb = a.llo + nch * E + nch * 2 * c.heads;         // [1 + kp][E]
+  a.llo = a.llq + E + 2ull * m.kvd;                    // [E], [heads][16], then [E]
+  a.llb = a.llo + 2 * E + 16ull * c.heads;             // [1 + kp][E]
   a.llact = a.llb + (1 + kp) * E;                      // [ff]
   (void)F;
   a.kp = kp;

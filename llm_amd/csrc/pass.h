@@ -37,8 +37,8 @@ struct PassArgs {
   const float* xn;                // layer 0's input row (the sampling kernel wrote it)
   float *x, *q, *att, *act, *up;  // the last layer's values, stored plainly (the head's input, Peek)
   uint64_t* llq;    // [E + 2 kvd]: q, and the position's K and V rows (K1)
-  uint64_t* llo;    // [chunks][E] the attention's per-chunk sums of e v, then [chunks][heads][2] each
-                    // chunk's max score and sum of e (K2)
+  uint64_t* llo;    // [E] the first attention chunk's sums of e v, [heads][16] its max scores and sums
+                    // of e (m, l, m, l, ...), then [E] the attention's output (K2)
   uint64_t* llb;    // [1 + kp][E]: x after the attention (K3), then the down projection's k-parts (K5);
                     // x after the layer is their sum
   uint64_t* llact;  // [ff]: the SwiGLU activations (K4)
@@ -67,8 +67,8 @@ __host__ __device__ inline uint32_t pass_chunks(uint32_t hd) { return hd == 64 ?
 // Flag-carrying words a model's pass needs (PassArgs: llq, llo, llb with the
 // most k-parts, llact).
 inline uint64_t pass_words(const llmhip_config& c, uint32_t kvd) {
-  const uint64_t E = (uint64_t)c.embd, nch = pass_chunks((uint32_t)c.head_dim);
-  return E + 2ull * kvd + nch * (E + 2ull * (uint64_t)c.heads) + 3 * E + (uint64_t)c.ff;
+  const uint64_t E = (uint64_t)c.embd;
+  return E + 2ull * kvd + 2 * E + 16ull * (uint64_t)c.heads + 3 * E + (uint64_t)c.ff;
 }
 // Why a model's decode passes cannot take the fused launch (nullptr: they can),
 // for `grid` co-resident workgroups; *kp receives the down projection's k-parts.

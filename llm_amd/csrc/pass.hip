@@ -8,8 +8,9 @@
 //   K2  one query head over one chunk of 128 cache rows: the chunk's max
 //       score, sum of e and sum of e v (kernels_fused.go:82-146; every
 //       position is below attn_full_max, so there are one or two chunks);
-//   K3  a tile of W_o att plus the residual, att merged from the chunks as
-//       attn_merge_kernel merges them (kernels_fused.go:150-170);
+//       the second chunk's workgroup merges the first's sums into its own as
+//       attn_merge_kernel merges chunks and writes the head's output;
+//   K3  a tile of W_o att plus the residual (kernels_fused.go:150-170);
 //   K4  tiles of [gate; up]: RMSNorm (ffn_norm), the product, SwiGLU;
 //   K5  one of kp k-parts of a tile of W_down act; the next layer adds the
 //       parts to the residual, in order.
@@ -147,22 +148,19 @@ enum PassSrc : int {
   SRC_LL,     // one vector of flag-carrying words
   SRC_PLAIN,  // plain memory (layer 0's input, which the sampling kernel wrote)
   SRC_XSUM,   // x = ((xb + p_0) + p_1) + ...: the attention's residual and the down projection's k-parts
-  SRC_MERGE,  // the attention's chunks merged: M = max m_c, w_c = e^(m_c - M), sum w_c o_c / sum w_c l_c
 };
 
 struct StageIn {
-  const uint64_t* ll;  // SRC_LL: the vector; SRC_XSUM: xb, then part p at (1 + p) E; SRC_MERGE: llo
+  const uint64_t* ll;  // SRC_LL: the vector; SRC_XSUM: xb, then part p at (1 + p) E
   const float* plain;  // SRC_PLAIN
-  uint32_t flag, kp, E, heads;
-  uint32_t chunks, nch;  // SRC_MERGE: the chunks holding positions (read), and those of the layout (llo)
-  float* store;        // SRC_MERGE: also store the merged row here (Peek "att"), or null
+  uint32_t flag, kp, E;
 };
 
 // Row elements base + tid + 512 k (k < NW; those below base + n) into v,
 // every load issued before the first wait: consecutive threads read
 // consecutive words, so each load instruction of a wave touches four lines
 // (a wave's polls of the row stay few, however many workgroups poll it).
-// SRC_XSUM and SRC_MERGE rows are of length E.
+// SRC_XSUM rows are of length E.
 template <int SRC, uint32_t HD, uint32_t NW>
 __device__ __forceinline__ void load_row(const StageIn& in, uint32_t base, uint32_t n, uint32_t tid, float (&v)[NW],
                                          Waiter& w) {
@@ -188,43 +186,6 @@ __device__ __forceinline__ void load_row(const StageIn& in, uint32_t base, uint3
         if (q <= in.kp) x += u[q * NW + k];
       v[k] = x;
     }
-  } else {  // SRC_MERGE
-    constexpr uint32_t MC = 2;  // chunks, at most (pass_chunks)
-    float u[3 * NW * MC];
-    const uint32_t mlb = in.nch * in.E;
-    // words [0, NW MC): chunk i / NW's o at element tid + T (i % NW); then for chunk j / (2 NW) and
-    // element k = (j / 2) % NW, the element's head's m (j even) and l (j odd)
-    ll_wait_gated<3 * NW * MC>(
-        [&](int i) {
-          if (i < (int)(NW * MC)) return in.ll + (i / NW) * in.E + tid + T * (i % NW);
-          const uint32_t j = i - NW * MC, c = j / (2 * NW), k = (j / 2) % NW;
-          return in.ll + mlb + 2 * (c * in.heads + (tid + T * k) / HD) + (j % 2);
-        },
-        [&](int i) {
-          const uint32_t c = i < (int)(NW * MC) ? i / NW : (i - NW * MC) / (2 * NW);
-          const uint32_t k = i < (int)(NW * MC) ? i % NW : ((i - NW * MC) / 2) % NW;
-          return c < in.chunks && tid + T * k < n;
-        },
-        in.flag, u, w);
-    // attn_merge_kernel's order (layer.hip): M, then the weights, L and o, then o / L
-#pragma unroll
-    for (uint32_t k = 0; k < NW; k++) {
-      auto mo = [&](uint32_t c, uint32_t which) { return u[NW * MC + 2 * (c * NW + k) + which]; };
-      float M = -INFINITY;
-#pragma unroll
-      for (uint32_t c = 0; c < MC; c++) M = fmaxf(M, c < in.chunks ? mo(c, 0) : -INFINITY);
-      float Ls = 0, o = 0;
-#pragma unroll
-      for (uint32_t c = 0; c < MC; c++) {
-        const bool inc = c < in.chunks;
-        const float wgt = inc ? __expf(mo(c, 0) - M) : 0.f;
-        Ls += wgt * (inc ? mo(c, 1) : 0.f);
-        o += wgt * (inc ? u[c * NW + k] : 0.f);
-      }
-      const bool ok = tid + T * k < n;
-      v[k] = ok ? o / Ls : 0.f;
-      if (in.store && ok) in.store[tid + T * k] = v[k];
-    }
   }
 }
 
@@ -242,12 +203,12 @@ __device__ __forceinline__ void load_row(const StageIn& in, uint32_t base, uint3
 // one barrier each wave forms its own units' items from LDS (no other wave
 // reads them; the next phase overwrites the row only after split_sum's
 // barrier).  Returns ex.
-template <int SRC, bool RMS, int MU, uint32_t HD>
+template <int SRC, bool RMS, int MU, bool LONG = false, uint32_t HD>
 __device__ __forceinline__ int stage_ops(PassLds<HD>& L, const StageIn& in, uint32_t nb0, uint32_t nb, uint32_t u0,
                                          uint32_t u1, const float* nw, float eps, Waiter& w, uint32_t tid,
                                          uint32_t wave) {
   constexpr uint32_t T = 64 * PASS_WAVES;
-  constexpr uint32_t NW = (SRC == SRC_LL && !RMS) ? WPT_F : WPT_E;
+  constexpr uint32_t NW = LONG ? WPT_F : WPT_E;  // LONG: a row longer than E (the feed-forward width)
   static_assert(16 * MU <= 64, "a wave forms its units' items in one pass");
   const uint32_t n = nb * 32, NI = nb * 4, lane = tid & 63;
   float wv[NW];
@@ -699,10 +660,35 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       }
       float M_, L_, o;
       rows.reduce(qv, row0, pos + 1, a.scale, L.am, &M_, &L_, &o);
-      if (tid < HD) ll_store(llo + hc * E + hh * HD + tid, o, F);
-      if (tid == 0) {
-        ll_store(llo + NCH * E + 2 * (hc * a.heads + hh), M_, F);
-        ll_store(llo + NCH * E + 2 * (hc * a.heads + hh) + 1, L_, F);
+      uint64_t* fin = llo + E + 16 * a.heads;  // the attention's output row
+      if (P == 1) {
+        // one chunk: its sums normalised (a one-chunk merge: M = m, weight 1)
+        if (tid < HD) {
+          const float r = o / L_;
+          ll_store(fin + hh * HD + tid, r, F);
+          if (last) a.att[hh * HD + tid] = r;
+        }
+      } else if (hc == 0) {
+        if (tid < HD) ll_store(llo + hh * HD + tid, o, F);
+        // m and l in a whole line of 16 words (m at even words, l at odd):
+        // a store of part of a line has been seen to reach other XCDs later
+        if (tid < 16) ll_store(llo + E + 16 * hh + tid, tid & 1 ? L_ : M_, F);
+      } else if (tid < HD) {
+        // chunk 1 merges chunk 0's sums into its own as attn_merge_kernel
+        // merges chunks (layer.hip): M, then the weights, L and o, then o / L
+        float v[3];  // chunk 0's o, m, l
+        ll_wait_f<3>([&](int i) { return i == 0 ? llo + hh * HD + tid : llo + E + 16 * hh + (i - 1); },
+                     [](int) { return true; }, F, v, wt);
+        const float Mx = fmaxf(fmaxf(-INFINITY, v[1]), M_);
+        const float w0 = __expf(v[1] - Mx), w1 = __expf(M_ - Mx);
+        float Ls = 0, oo = 0;
+        Ls += w0 * v[2];
+        Ls += w1 * L_;
+        oo += w0 * v[0];
+        oo += w1 * o;
+        const float r = oo / Ls;
+        ll_store(fin + hh * HD + tid, r, F);
+        if (last) a.att[hh * HD + tid] = r;
       }
     }
 
@@ -728,16 +714,11 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
         }
       }
       StageIn in{};
-      in.ll = llo;
+      in.ll = llo + E + 16 * a.heads;
       in.flag = F;
-      in.E = E;
-      in.heads = a.heads;
-      in.chunks = P;
-      in.nch = NCH;
-      in.store = last && t3 == 0 ? a.att : nullptr;
       UnitsB<1, 1> ub;
       units_deq_any<Q8, 1, 1>(w3, M, 0, wave, ub);
-      const int ex = stage_ops<SRC_MERGE, false, 1>(L, in, 0, M.nb, 0, U, nullptr, 0.f, wt, tid, wave);
+      const int ex = stage_ops<SRC_LL, false, 1>(L, in, 0, M.nb, 0, U, nullptr, 0.f, wt, tid, wave);
       float acc[1] = {0};
       units_mac_any<Q8, 1, 1>(ub, M, L.xs, L.bsum, 0, U, wave, lane, acc);
       const float v = split_sum<1>(L.part, acc, wave, lane);
@@ -821,7 +802,7 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       const uint32_t nb0 = 4 * u50, nbp = min(4 * u51, M.nb) - nb0;
       UnitsB<1, PASS_K5_UNITS> ub;
       units_deq_any<Q8, 1, PASS_K5_UNITS>(w5, M, u50, wave, ub);
-      const int ex = stage_ops<SRC_LL, false, PASS_K5_UNITS>(L, in, nb0, nbp, u50, u51, nullptr, 0.f, wt, tid, wave);
+      const int ex = stage_ops<SRC_LL, false, PASS_K5_UNITS, true>(L, in, nb0, nbp, u50, u51, nullptr, 0.f, wt, tid, wave);
       float acc[1] = {0};
       units_mac_any<Q8, 1, PASS_K5_UNITS>(ub, M, L.xs, L.bsum, u50, u51, wave, lane, acc);
       const float v = split_sum<1>(L.part, acc, wave, lane);
