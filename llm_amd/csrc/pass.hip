@@ -105,6 +105,13 @@ __device__ __forceinline__ void ll_wait_gated(At at, Need need, uint32_t flag, f
   ll_wait_f<N>(at, need, flag, v, w);
 }
 
+// ll_wait_gated or, where the input is expected soon, ll_wait_f.
+template <int N, class At, class Need>
+__device__ __forceinline__ void ll_wait_row(bool gate, At at, Need need, uint32_t flag, float (&v)[N], Waiter& w) {
+  if (gate) ll_wait_gated<N>(at, need, flag, v, w);
+  else ll_wait_f<N>(at, need, flag, v, w);
+}
+
 // ll_wait_f over base[idx[i]] where need[i].
 template <int N>
 __device__ __forceinline__ void ll_wait(const uint64_t* base, const uint32_t (&idx)[N], const bool (&need)[N],
@@ -154,6 +161,7 @@ struct StageIn {
   const uint64_t* ll;  // SRC_LL: the vector; SRC_XSUM: xb, then part p at (1 + p) E
   const float* plain;  // SRC_PLAIN
   uint32_t flag, kp, E;
+  bool gate;           // wait behind a gate word (ll_wait_gated): the input is expected late
 };
 
 // Row elements base + tid + 512 k (k < NW; those below base + n) into v,
@@ -170,13 +178,13 @@ __device__ __forceinline__ void load_row(const StageIn& in, uint32_t base, uint3
     for (uint32_t k = 0; k < NW; k++) v[k] = tid + T * k < n ? in.plain[base + tid + T * k] : 0.f;
   } else if constexpr (SRC == SRC_LL) {
     const uint64_t* p = in.ll + base + tid;
-    ll_wait_gated<NW>([&](int i) { return p + T * i; }, [&](int i) { return tid + T * i < n; }, in.flag, v, w);
+    ll_wait_row<NW>(in.gate, [&](int i) { return p + T * i; }, [&](int i) { return tid + T * i < n; }, in.flag, v, w);
   } else if constexpr (SRC == SRC_XSUM) {
     constexpr uint32_t NP = 1 + PASS_MAX_KP;
     float u[NW * NP];
     // word i: vector i / NW (xb, then the parts), element tid + T (i % NW)
     const uint64_t* p = in.ll + tid;
-    ll_wait_gated<NW * NP>([&](int i) { return p + (i / NW) * in.E + T * (i % NW); },
+    ll_wait_row<NW * NP>(in.gate, [&](int i) { return p + (i / NW) * in.E + T * (i % NW); },
                        [&](int i) { return (uint32_t)(i / NW) <= in.kp && tid + T * (i % NW) < n; }, in.flag, u, w);
 #pragma unroll
     for (uint32_t k = 0; k < NW; k++) {
@@ -547,6 +555,7 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       in.ll = llb;
       in.plain = a.xn;
       in.flag = Fp;
+      in.gate = true;  // (this workgroup has waited since its K4 work)
       in.kp = a.kp;
       in.E = E;
       UnitsB<1, 1> ub;
@@ -716,6 +725,7 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       StageIn in{};
       in.ll = llo + E + 16 * a.heads;
       in.flag = F;
+      in.gate = true;
       UnitsB<1, 1> ub;
       units_deq_any<Q8, 1, 1>(w3, M, 0, wave, ub);
       const int ex = stage_ops<SRC_LL, false, 1>(L, in, 0, M.nb, 0, U, nullptr, 0.f, wt, tid, wave);
@@ -758,6 +768,7 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
         StageIn in{};
         in.ll = llb;
         in.flag = F;
+        in.gate = !has3;  // K3's workgroups come straight from producing this input
         UnitsB<PASS_K4_TILES, 1> ub;
         units_deq_any<Q8, PASS_K4_TILES, 1>(w4, M, 0, wave, ub);
         const int ex = stage_ops<SRC_LL, true, 1>(L, in, 0, M.nb, 0, U, Y->ffn_norm, a.eps, wt, tid, wave);
@@ -799,6 +810,7 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       StageIn in{};
       in.ll = llact;
       in.flag = F;
+      in.gate = false;  // every K5 workgroup comes straight from its K4 work
       const uint32_t nb0 = 4 * u50, nbp = min(4 * u51, M.nb) - nb0;
       UnitsB<1, PASS_K5_UNITS> ub;
       units_deq_any<Q8, 1, PASS_K5_UNITS>(w5, M, u50, wave, ub);
