@@ -146,7 +146,9 @@ struct PassLds {
   h8 xs[2 * PASS_MAX_ITEMS];      // the phase's A operands: item it at 2 it (hi) and 2 it + 1 (lo)
   float bsum[PASS_MAX_ITEMS / 4];  // Q4_1: each block's sum, scaled like the operands
   float misc[16];                  // the waves' partial sums of squares [0, 8) and maxima [8, 16)
-  float part[PASS_K4_TILES][PASS_WAVES][64];  // split-K partials
+  float part[PASS_K4_TILES][PASS_WAVES][64];  // split-K partials of K1 and K4
+  float part2[1][PASS_WAVES][64];  // those of K3 and K5, which have no barrier before theirs: a wave
+                                   // may write them while another still reads the previous phase's
   AttnLds<HD, PASS_WAVES> am;
 };
 
@@ -197,6 +199,55 @@ __device__ __forceinline__ void load_row(const StageIn& in, uint32_t base, uint3
   }
 }
 
+// The wave's units' items (those of units_load: u = u0 + wave + 8 i < u1,
+// i < MU) from the row in LDS: item it = (block it / 4, k-group it % 4:
+// elements 4 (it % 4) + 0..3 and 16 + 4 (it % 4) + 0..3 of the block) in MFMA
+// element order, RMS: h = (x s) w (cpu.go:96), scaled by 2^ex and split
+// exactly into f16 hi (xs[2 it]) + lo (xs[2 it + 1]); the blocks' sums (Q4_1:
+// cpu.go:196-198) scaled alike.  Only the wave reads them.
+template <bool RMS, int MU, uint32_t HD>
+__device__ __forceinline__ void form_items(PassLds<HD>& L, uint32_t nb, uint32_t u0, uint32_t u1, float s, int ex,
+                                           uint32_t wave, uint32_t lane) {
+  static_assert(16 * MU <= 64, "a wave forms its units' items in one pass");
+  const uint32_t NI = nb * 4;
+  // lane: item lane % 16 of the wave's unit lane / 16
+  const uint32_t i = lane / 16, u = u0 + wave + PASS_WAVES * i;
+  const uint32_t it = 16 * (u - u0) + (lane & 15);
+  const bool ok = (int)i < MU && u < u1 && it < NI;
+  const uint32_t e0 = (it / 4) * 32 + 4 * (it % 4);
+  f4 a = {0, 0, 0, 0}, c = {0, 0, 0, 0};
+  if (ok) {
+    a = *(const f4*)&L.row[e0];
+    c = *(const f4*)&L.row[e0 + 16];
+    if (RMS) {
+      const f4 wa = *(const f4*)&L.nw[e0], wc = *(const f4*)&L.nw[e0 + 16];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        a[k] = __fmul_rn(__fmul_rn(a[k], s), wa[k]);  // cpu.go:96
+        c[k] = __fmul_rn(__fmul_rn(c[k], s), wc[k]);
+      }
+    }
+  }
+  const float vv[8] = {a[0], a[2], c[0], c[2], a[1], a[3], c[1], c[3]};
+  h8 hi, lo;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const float sv = ldexpf(vv[k], ex);
+    const _Float16 h = (_Float16)sv;
+    hi[k] = h;
+    lo[k] = (_Float16)(sv - (float)h);
+  }
+  float sx = (a[0] + a[1] + a[2] + a[3]) + (c[0] + c[1] + c[2] + c[3]);
+  sx += __shfl_xor(sx, 1);  // a block's four items: four consecutive lanes
+  sx += __shfl_xor(sx, 2);
+  if (ok) {
+    L.xs[2 * it] = hi;
+    L.xs[2 * it + 1] = lo;
+    if ((it & 3) == 0) L.bsum[it / 4] = ldexpf(sx, ex);
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
 // The phase's input row (nb blocks of 32 from block nb0 on) staged as the A
 // operands of the wave's units (those of units_load: u = u0 + wave + 8 i < u1,
 // i < MU), in LDS: item it = (block it / 4, k-group it % 4: elements
@@ -217,8 +268,7 @@ __device__ __forceinline__ int stage_ops(PassLds<HD>& L, const StageIn& in, uint
                                          uint32_t wave) {
   constexpr uint32_t T = 64 * PASS_WAVES;
   constexpr uint32_t NW = LONG ? WPT_F : WPT_E;  // LONG: a row longer than E (the feed-forward width)
-  static_assert(16 * MU <= 64, "a wave forms its units' items in one pass");
-  const uint32_t n = nb * 32, NI = nb * 4, lane = tid & 63;
+  const uint32_t n = nb * 32, lane = tid & 63;
   float wv[NW];
   if (RMS)
 #pragma unroll
@@ -256,42 +306,43 @@ __device__ __forceinline__ int stage_ops(PassLds<HD>& L, const StageIn& in, uint
     frexpf(m, &E);
     ex = 15 - E;
   }
-  // lane: item lane % 16 of the wave's unit lane / 16
-  const uint32_t i = lane / 16, u = u0 + wave + PASS_WAVES * i;
-  const uint32_t it = 16 * (u - u0) + (lane & 15);
-  const bool ok = (int)i < MU && u < u1 && it < NI;
-  const uint32_t e0 = (it / 4) * 32 + 4 * (it % 4);
-  f4 a = {0, 0, 0, 0}, c = {0, 0, 0, 0};
-  if (ok) {
-    a = *(const f4*)&L.row[e0];
-    c = *(const f4*)&L.row[e0 + 16];
-    if (RMS) {
-      const f4 wa = *(const f4*)&L.nw[e0], wc = *(const f4*)&L.nw[e0 + 16];
+  form_items<RMS, MU>(L, nb, u0, u1, s, ex, wave, lane);
+  return ex;
+}
+
+// The phase's input row (one vector of flag-carrying words, nb blocks of 32
+// from block nb0 on) staged by each wave for its own units only, with no
+// workgroup barrier: the wave polls its units' elements (unit u: blocks
+// 4 (u - u0) .. 4 (u - u0) + 3 of the row) into its part of the row in LDS
+// and forms their items scaled by its own 2^ex (its largest |x| in
+// [2^14, 2^15)).  A wave whose input is in starts its products while the
+// others still wait; each wave scales its sums back by 2^-ex (exact) before
+// the waves' sums are added.  Returns the wave's ex.
+template <int MU, uint32_t HD>
+__device__ __forceinline__ int stage_wave(PassLds<HD>& L, const StageIn& in, uint32_t nb0, uint32_t nb, uint32_t u0,
+                                          uint32_t u1, Waiter& w, uint32_t wave, uint32_t lane) {
+  const uint32_t n = nb * 32;
+  const uint64_t* p = in.ll + 32 * nb0;
+  // word j: element 128 (u - u0) + 64 (j % 2) + lane of unit u = u0 + wave + 8 (j / 2)
+  auto el = [&](int j) { return 128 * (wave + PASS_WAVES * (j / 2)) + 64 * (j % 2) + lane; };
+  auto need = [&](int j) { return u0 + wave + PASS_WAVES * (j / 2) < u1 && el(j) < n; };
+  float v[2 * MU];
+  ll_wait_row<2 * MU>(in.gate, [&](int j) { return p + el(j); }, need, in.flag, v, w);
+  float mx = 0;
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        a[k] = __fmul_rn(__fmul_rn(a[k], s), wa[k]);  // cpu.go:96
-        c[k] = __fmul_rn(__fmul_rn(c[k], s), wc[k]);
-      }
-    }
+  for (int j = 0; j < 2 * MU; j++) {
+    if (need(j)) L.row[el(j)] = v[j];
+    mx = fmaxf(mx, fabsf(v[j]));
   }
-  const float vv[8] = {a[0], a[2], c[0], c[2], a[1], a[3], c[1], c[3]};
-  h8 hi, lo;
-#pragma unroll
-  for (int k = 0; k < 8; k++) {
-    const float sv = ldexpf(vv[k], ex);
-    const _Float16 h = (_Float16)sv;
-    hi[k] = h;
-    lo[k] = (_Float16)(sv - (float)h);
-  }
-  float sx = (a[0] + a[1] + a[2] + a[3]) + (c[0] + c[1] + c[2] + c[3]);
-  sx += __shfl_xor(sx, 1);  // a block's four items: four consecutive lanes
-  sx += __shfl_xor(sx, 2);
-  if (ok) {
-    L.xs[2 * it] = hi;
-    L.xs[2 * it + 1] = lo;
-    if ((it & 3) == 0) L.bsum[it / 4] = ldexpf(sx, ex);
-  }
+  mx = wave_max_dpp(mx);  // (the same in every lane)
   __builtin_amdgcn_wave_barrier();
+  int ex = 0;
+  if (mx > 0 && mx <= 3.0e38f) {
+    int E;
+    frexpf(mx, &E);
+    ex = 15 - E;
+  }
+  form_items<false, MU>(L, nb, u0, u1, 1.f, ex, wave, lane);
   return ex;
 }
 
@@ -728,10 +779,11 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       in.gate = true;
       UnitsB<1, 1> ub;
       units_deq_any<Q8, 1, 1>(w3, M, 0, wave, ub);
-      const int ex = stage_ops<SRC_LL, false, 1>(L, in, 0, M.nb, 0, U, nullptr, 0.f, wt, tid, wave);
+      const int ex = stage_wave<1>(L, in, 0, M.nb, 0, U, wt, wave, lane);
       float acc[1] = {0};
       units_mac_any<Q8, 1, 1>(ub, M, L.xs, L.bsum, 0, U, wave, lane, acc);
-      const float v = split_sum<1>(L.part, acc, wave, lane);
+      acc[0] = ldexpf(acc[0], -ex);
+      const float v = split_sum<1>(L.part2, acc, wave, lane);
       if (rv) {
         float res = resf;
         if (l != 0) {
@@ -740,7 +792,7 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
           for (uint32_t p = 1; p <= PASS_MAX_KP; p++)
             if (p <= a.kp) res += ll_settle(llb + p * E + lr, r0[p], Fp, wt);
         }
-        ll_store(llb + lr, res + ldexpf(v, -ex), F);
+        ll_store(llb + lr, res + v, F);
       }
     }
 
@@ -805,8 +857,6 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
     if (has5) {
       PHASE_IDS;
       const PassMat M = cmat(&Y->down);
-      // (stage_ops's barrier also orders K4's epilogue reads of the partials
-      // before this phase's writes)
       StageIn in{};
       in.ll = llact;
       in.flag = F;
@@ -814,12 +864,13 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       const uint32_t nb0 = 4 * u50, nbp = min(4 * u51, M.nb) - nb0;
       UnitsB<1, PASS_K5_UNITS> ub;
       units_deq_any<Q8, 1, PASS_K5_UNITS>(w5, M, u50, wave, ub);
-      const int ex = stage_ops<SRC_LL, false, PASS_K5_UNITS, true>(L, in, nb0, nbp, u50, u51, nullptr, 0.f, wt, tid, wave);
+      const int ex = stage_wave<PASS_K5_UNITS>(L, in, nb0, nbp, u50, u51, wt, wave, lane);
       float acc[1] = {0};
       units_mac_any<Q8, 1, PASS_K5_UNITS>(ub, M, L.xs, L.bsum, u50, u51, wave, lane, acc);
-      const float v = split_sum<1>(L.part, acc, wave, lane);
+      acc[0] = ldexpf(acc[0], -ex);
+      const float v = split_sum<1>(L.part2, acc, wave, lane);
       const uint32_t lr = t5 * 16 + r;
-      if (wave == 0 && q == 0 && lr < M.rows) ll_store(llb + (1 + p5) * E + lr, ldexpf(v, -ex), F);
+      if (wave == 0 && q == 0 && lr < M.rows) ll_store(llb + (1 + p5) * E + lr, v, F);
     }
   }
 
