@@ -10,11 +10,15 @@ Generate(prompt, 128) with eos -1; `value` is decode tok/s over the K timed
 rounds (prefill tok/s reported beside it).  Inputs are resident in HBM before
 the timed region (the model is loaded once).
 
-Also measured: per-kernel device times of a decode step (HIP events on the
-model's stream, in the decode loop's cache state) for the roofline of the
-dominant kernel; the isolated GEMV sweep with weights read
-from HBM (rotated copies > 512 MB) and warm; and the CPU oracle (a C
-restatement of the reference's cpu.go) timed on this host's cores.
+Also measured: the device time of each launch of a decode step (the fused
+pass that runs every layer, the head, the sampling kernel: HIP events on the
+model's stream around eager steps) for the roofline of the dominant kernel,
+whose duration comes from the committed kernel trace of these sources when
+there is one; the one-launch-per-phase kernels (prefill, the fallback,
+config 4's decode) back to back; the isolated GEMV sweep
+with weights read from HBM (rotated copies > 512 MB) and warm; and the CPU
+oracle (a C restatement of the reference's cpu.go) timed on this host's
+cores.
 """
 import argparse
 import json
@@ -37,25 +41,29 @@ PMC_SUMMARY = os.path.join(ROOT, "profiles", "pmc_decode_qwen25.txt")
 
 def kernel_symbols(attn_full):
     """Device symbol of each decode kernel class of the config-3 model (Q4_0
-    layers, Q8_0 head): gemv_kernel<type, tokens, prologue, epilogue, units
+    layers, Q8_0 head): the fused pass pass_kernel<head size, binary16 cache,
+    Q8_0 matrices>, the sampling kernel, and for one launch per phase
+    gemv_kernel<type, tokens, prologue, epilogue, units
     per staging batch> (K1 after layer 0 adds the previous down projection's
     two k-halves, prologue 65; K5 before the last layer stores those halves,
     epilogue 0, three block groups per wave: four per staging batch), the
     one-chunk or split attention, the streaming head <type,
     prologue, epilogue, groups per tile>."""
-    return {"k1": "gemv_kernel<2u, 1, 65, 2, 2>",
+    return {"pass": "pass_kernel<64u, false, false>", "argmax": "argmax_kernel",
+            "k1": "gemv_kernel<2u, 1, 65, 2, 2>",
             "k2": "attn_kernel<64u, 8u, false, false, false>" if attn_full else
                   "attn_kernel<64u, 8u, true, false, false>",
             "k3": "gemv_kernel<2u, 1, 0, 1, 2>", "k4": "gemv_kernel<2u, 1, 1, 3, 2>", "k5": "gemv_kernel<2u, 1, 0, 0, 4>",
             "head": "gemv_stream_kernel<8u, 1, 4, 7>"}
 
 
-def pmc_traffic(cls):
-    """HBM bytes per launch of a decode kernel class from the committed
-    rocprofv3 counter summary (lines `traffic_bytes <class> <bytes>`), and
-    whether that summary measured the kernel sources of this tree (its
-    `sources_hash` line against llm_amd.profsum.sources_hash()).  A stale
-    figure is not reported: (None, reason)."""
+def pmc_value(kind, cls):
+    """A figure of a decode kernel class from the committed rocprofv3 summary
+    (lines `traffic_bytes <class> <bytes>`: HBM bytes per launch from the
+    FETCH_SIZE / WRITE_SIZE runs; `duration_us <class> <us>`: the kernel
+    trace's median duration), if that summary measured the kernel sources of
+    this tree (its `sources_hash` line against llm_amd.profsum.sources_hash()).
+    A stale figure is not reported: (None, reason)."""
     from llm_amd import profsum
     want, got, value = profsum.sources_hash(), None, None
     try:
@@ -64,8 +72,8 @@ def pmc_traffic(cls):
                 p = line.split()
                 if len(p) == 2 and p[0] == "sources_hash":
                     got = p[1]
-                if len(p) == 3 and p[0] == "traffic_bytes" and p[1] == cls:
-                    value = int(p[2])
+                if len(p) == 3 and p[0] == kind and p[1] == cls:
+                    value = float(p[2]) if kind == "duration_us" else int(p[2])
     except OSError:
         return None, "no counter summary"
     if got != want:
@@ -119,37 +127,61 @@ def generation(args):
                          "min": min(r.Generated / r.Decode for r in rounds),
                          "max": max(r.Generated / r.Decode for r in rounds)},
     }
-    # per-kernel device times: each decode kernel class launched back to back
-    # across the 24 layers between HIP events on the model's stream
+    # device times of a decode step's launches (the fused pass, the head, the
+    # sampling kernel): HIP events on the model's stream around each launch of
+    # eager decode steps at the positions after the timed rounds
     g.Generate(prompt, 1, -1)
-    per_tok = {"k1": spec.layers, "k2": spec.layers, "k3": spec.layers, "k4": spec.layers, "k5": spec.layers,
-               "head": 1}
-    classes = {}
-    for cls, n in per_tok.items():
-        us, nbytes = g.bench_kernel(cls, 240 if cls != "head" else 50)
-        classes[cls] = {"launches_per_token": n, "avg_us": round(us, 3), "bytes": nbytes,
-                        "us_per_token": round(us * n, 2),
-                        "gbps": round(nbytes / us * 1e-3, 1) if nbytes else None}
-    step_kernel_us = sum(c["us_per_token"] for c in classes.values())
+    agg = {}
+    for _ in range(args.profile_steps):
+        per = {}
+        for c, _layer, b, us in g.profile(2):
+            per.setdefault(c, []).append((b, us))
+        for c, v in per.items():
+            a = agg.setdefault(c, {"n": len(v), "us": [], "bytes": []})
+            a["us"].append(sum(u for _, u in v) / len(v))
+            a["bytes"].append(sum(b for b, _ in v) / len(v))
     syms = kernel_symbols(args.prompt + 1 < 256)
-    for cls in classes:
-        classes[cls]["symbol"] = syms[cls]
-    # the dominant kernel: the class with the most device time per decode token
+    classes = {}
+    for c, a in agg.items():
+        us, nbytes = statistics.mean(a["us"]), int(statistics.mean(a["bytes"]))
+        classes[c] = {"launches_per_token": a["n"], "avg_us": round(us, 3), "bytes": nbytes,
+                      "us_per_token": round(us * a["n"], 2), "gbps": round(nbytes / us * 1e-3, 1) if nbytes else None,
+                      "symbol": syms.get(c)}
+    step_kernel_us = sum(c["us_per_token"] for c in classes.values())
+    # the dominant kernel: the class with the most device time per decode token;
+    # frac from the profiler's duration of that kernel (the committed kernel
+    # trace of this tree's sources), the HIP-event figure beside it
     dom = max(classes, key=lambda k: classes[k]["us_per_token"])
     d = classes[dom]
-    achieved = d["bytes"] / d["avg_us"] * 1e-3
-    traffic, source = pmc_traffic(dom)
-    roofline = {"bound": "hbm", "kernel": dom, "symbol": syms[dom], "achieved": round(achieved, 1),
+    traced_us, tsource = pmc_value("duration_us", dom)
+    traffic, source = pmc_value("traffic_bytes", dom)
+    dur = traced_us if traced_us else d["avg_us"]
+    achieved = d["bytes"] / dur * 1e-3
+    roofline = {"bound": "hbm", "kernel": dom, "symbol": syms.get(dom), "achieved": round(achieved, 1),
                 "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                "traffic": traffic, "traffic_source": source, "bytes_per_launch": d["bytes"], "avg_us": d["avg_us"]}
-    w = [k for k in classes if k != "k2"]
-    gemv_all = sum(classes[k]["bytes"] * classes[k]["launches_per_token"] for k in w) / \
-        sum(classes[k]["us_per_token"] for k in w) * 1e-3
+                "traffic": traffic, "traffic_source": source, "bytes_per_launch": d["bytes"],
+                "duration_us": dur, "duration_source": tsource if traced_us else "HIP events (no current trace)",
+                "event_us": d["avg_us"], "event_achieved": round(d["bytes"] / d["avg_us"] * 1e-3, 1)}
+    if dom == "pass":
+        roofline["note"] = ("one launch runs every layer of the step: its phases hand their results to each other "
+                            "through flag-carrying words, five dependent hand-offs per layer, so the launch is "
+                            "bound by that chain's latency, not by HBM (algorithmic bytes: every layer matrix once "
+                            "and the KV rows attended)")
+    # the kernels of one launch per phase (prefill, the decode fallback, and
+    # the long-context decode, which the fused pass does not take): each class
+    # launched back to back across the 24 layers between HIP events
+    unfused = {}
+    per_tok = {"k1": spec.layers, "k2": spec.layers, "k3": spec.layers, "k4": spec.layers, "k5": spec.layers}
+    for cls, n in per_tok.items():
+        us, nbytes = g.bench_kernel(cls, 240)
+        unfused[cls] = {"launches_per_token": n, "avg_us": round(us, 3), "bytes": nbytes,
+                        "us_per_token": round(us * n, 2), "gbps": round(nbytes / us * 1e-3, 1) if nbytes else None,
+                        "symbol": syms[cls]}
     dispatches = round(sum(r.Dispatches for r in rounds) / max(1, sum(r.Generated for r in rounds)), 1)
     return g, {
         "value": dec, "prefill": pre, "wall": wall, "rounds": per_round, "ms_per_step": wall / args.steps * 1e3,
-        "classes": classes, "step_kernel_us": step_kernel_us, "roofline": roofline,
-        "gemv_aggregate_gbps": gemv_all, "dispatches_per_token": dispatches,
+        "classes": classes, "unfused": unfused, "step_kernel_us": step_kernel_us, "roofline": roofline,
+        "dispatches_per_token": dispatches,
     }
 
 
@@ -218,7 +250,7 @@ def long_context(args):
            "attention_at_end": {"avg_us": round(us, 2), "kv_bytes": nbytes, "gbps": round(nbytes / us * 1e-3, 1),
                                 "note": "the split attention kernel (chunks of 256 rows); their merge runs in the "
                                         "output projection's prologue, so classes_at_end.k3 carries it (k3 merges "
-                                        "nothing at config 3: decode_step.classes.k3)"},
+                                        "nothing at config 3: decode_step.unfused_classes.k3)"},
            "classes_at_end": classes}
     log(f"long context: prefill {res['prefill_tok_s']} tok/s, decode {res['decode_tok_s']} tok/s, "
         f"attention {us:.1f} us for {nbytes} KV bytes")
@@ -371,6 +403,7 @@ def main():
     ap.add_argument("--gen", type=int, default=128)
     ap.add_argument("--ctx", type=int, default=512)
     ap.add_argument("--hbm-bytes", type=int, default=640 << 20, help="rotated copies per sweep shape")
+    ap.add_argument("--profile-steps", type=int, default=12, help="eager decode steps timed per launch")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-long", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -410,8 +443,8 @@ def main():
         "roofline": r["roofline"],
         "prefill_roofline": prefill_roofline(r["prefill"]),
         "decode_step": {"kernel_us": round(r["step_kernel_us"], 2), "wall_us": round(1e6 / r["value"], 2),
-                        "dispatches_per_token": r["dispatches_per_token"],
-                        "gemv_aggregate_gbps": round(r["gemv_aggregate_gbps"], 1), "classes": r["classes"]},
+                        "dispatches_per_token": r["dispatches_per_token"], "classes": r["classes"],
+                        "unfused_classes": r["unfused"]},
     }
     res["load"] = loader(args)
     if not args.no_long:

@@ -856,9 +856,12 @@ static int record_pass(Model& m, uint32_t ntok, bool head, bool embed_in) {
     m.cur_layer = -1;
     PassArgs a = m.pargs;
     a.rows = m.attn_rows;
+    // algorithmic bytes: every layer's matrices and the KV rows of the
+    // positions attended
     uint64_t bytes = 0;
     for (const Layer& L : m.layers)
-      bytes += L.qkv[0].g.gguf_bytes() + L.o.g.gguf_bytes() + L.gu[0].g.gguf_bytes() + L.down.g.gguf_bytes();
+      bytes += L.qkv[0].g.gguf_bytes() + L.o.g.gguf_bytes() + L.gu[0].g.gguf_bytes() + L.down.g.gguf_bytes() +
+               2ull * (m.pos + 1) * m.kvd * (m.kv16 ? 2 : 4);
     LLM_TRY(launch_rec(m, "pass", bytes, [&]() { return pass_launch(a, m.pgrid, m.pass_q8, m.stream); }));
     return rec_head(m, ntok - 1, ntok);
   }

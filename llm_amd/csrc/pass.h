@@ -47,7 +47,7 @@ struct PassArgs {
   const float* cs;  // RoPE table
   uint32_t embd, ff, heads, kv_heads, hd, kvd, ctx, neox, kv16;
   uint32_t rows;  // cache rows the attention reads: a multiple of 64 above the position, <= attn_full_max
-  uint32_t kp;    // k-parts of the down projection (1, 2 or 4)
+  uint32_t kp;    // k-parts of the down projection (1 or 2)
   float eps, scale;
   // the first workgroup of each phase's work: K1 tiles, attention (head, chunk)s, K3 tiles, K4 (round robin),
   // K5 (tile, part)s
@@ -59,6 +59,7 @@ constexpr uint32_t PASS_MAX_EMBD = 1024;  // the embedding, at most
 constexpr uint32_t PASS_MAX_FF = 6144;    // the feed-forward width, at most (its row is staged in LDS)
 constexpr uint32_t PASS_K4_TILES = 3;     // gate/up tiles per workgroup, at most
 constexpr uint32_t PASS_K5_UNITS = 3;     // down-projection units (groups of four blocks) per wave and part, at most
+constexpr uint32_t PASS_MAX_KP = 2;       // k-parts of the down projection, at most
 constexpr uint32_t PASS_CHUNK_ROWS = 128; // cache rows of an attention chunk (two chunks at head size 64)
 constexpr uint32_t PASS_SPIN_DEFAULT = 1u << 20;
 
@@ -68,7 +69,7 @@ __host__ __device__ inline uint32_t pass_chunks(uint32_t hd) { return hd == 64 ?
 // most k-parts, llact).
 inline uint64_t pass_words(const llmhip_config& c, uint32_t kvd) {
   const uint64_t E = (uint64_t)c.embd;
-  return E + 2ull * kvd + 2 * E + 16ull * (uint64_t)c.heads + 3 * E + (uint64_t)c.ff;
+  return E + 2ull * kvd + 2 * E + 16ull * (uint64_t)c.heads + (1 + PASS_MAX_KP) * E + (uint64_t)c.ff;
 }
 // Why a model's decode passes cannot take the fused launch (nullptr: they can),
 // for `grid` co-resident workgroups; *kp receives the down projection's k-parts.

@@ -135,7 +135,6 @@ __device__ __forceinline__ float ll_settle(const uint64_t* p, uint64_t x, uint32
 }
 
 constexpr uint32_t PASS_MAX_ITEMS = PASS_MAX_FF / 8;  // items of 8 elements of the longest staged row
-constexpr uint32_t PASS_MAX_KP = 2;
 constexpr uint32_t WPT_E = PASS_MAX_EMBD / (64 * PASS_WAVES);  // row elements per thread, rows of length E
 constexpr uint32_t WPT_F = PASS_MAX_FF / (64 * PASS_WAVES);    // row elements per thread, the longest row
 
@@ -911,12 +910,16 @@ const char* pass_unfit(const llmhip_config& c, uint32_t kvd, const PassMat& qkv,
   auto units = [](const PassMat& m) { return m.ng + (m.tail ? 1u : 0u); };
   if (units(qkv) > PASS_WAVES || units(o) > PASS_WAVES || units(gu) > PASS_WAVES)
     return "more units per tile than waves";
+  // k-parts: the fewest that leave each wave of a part one unit, else the
+  // most the grid holds (more parts: fewer products per workgroup, more
+  // vectors for the next layer to add)
   *kp = 0;
-  for (uint32_t k : {2u, 1u})  // the most k-parts the grid holds (PASS_MAX_KP)
-    if (k * T5 <= grid && (units(down) + k - 1) / k <= PASS_WAVES * PASS_K5_UNITS && units(down) >= k) {
-      *kp = k;
-      break;
-    }
+  for (uint32_t k = 1; k <= PASS_MAX_KP; k *= 2) {
+    const uint32_t per = (units(down) + k - 1) / k;
+    if (k * T5 > grid || per > PASS_WAVES * PASS_K5_UNITS || units(down) < k) continue;
+    *kp = k;
+    if (per <= PASS_WAVES) break;
+  }
   if (*kp == 0) return "down projection too long";
   if (gu.tiles > PASS_K4_TILES * grid) return "gate/up too tall";
   if (gu.map != MAP_GATEUP || o.map != MAP_IDENT || down.map != MAP_IDENT) return "row maps";

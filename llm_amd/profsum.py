@@ -31,7 +31,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 PROFILES = os.path.join(ROOT, "profiles")
 BENCH = os.path.join(ROOT, "bench.py")
-CLASSES = ["k1", "k2", "k3", "k4", "k5", "head"]
+CLASSES = ["pass", "head", "argmax"]  # a decode step's launches
+UNFUSED = ["k1", "k2", "k3", "k4", "k5"]  # one launch per phase (prefill, fallback, config-4 decode)
 SWEEP = [(576, 576), (1536, 576), (576, 1536), (896, 896), (4864, 896), (896, 4864), (151936, 896)]
 VOCAB = "q4_0:151936x896"
 SQ = ["SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VMEM_RD", "SQ_INSTS_LDS", "SQ_INSTS_SALU",
@@ -189,8 +190,9 @@ def summarize(out):
     by = collections.defaultdict(list)
     for _, n, gx, gy, d in rows:
         by[(n, gx, gy)].append(d)
-    cls = live["decode_step"]["classes"]
-    syms = {c: cls[c]["symbol"] for c in CLASSES}
+    cls = dict(live["decode_step"]["classes"])
+    cls.update(live["decode_step"].get("unfused_classes", {}))
+    syms = {c: cls[c]["symbol"] for c in CLASSES + UNFUSED if c in cls and cls[c].get("symbol")}
     grids = class_grids(rows, syms)
 
     md = ["# Decode and prefill kernels, Qwen2.5-0.5B shape (BASELINE config 3), one MI355X", "",
@@ -201,24 +203,37 @@ def summarize(out):
                        ["python3", BENCH, "--no-sweep", "--no-cpu", "--steps", "2"]),
           "```", "",
           "`LLMHIP_EAGER=1`: passes go to the stream as direct launches instead of hipGraph replays (same kernels, "
-          "arguments and order); rocprofv3's kernel trace of graph replays ended in a host fault. The traced run's "
-          "durations are per dispatch from the profiler's start and end stamps; the live figures are HIP events "
-          "around back-to-back launches of one class over the 24 layers (`llmhip_model_bench_kernel`, the figure "
-          "bench.py's roofline uses). A traced dispatch is a dependent launch of its own, so its duration carries "
-          "the dispatch and completion overhead that back-to-back launches overlap: the difference is about "
-          "0.3-0.8 us per launch, the same for every class.", "",
+          "arguments and order); rocprofv3's kernel trace of graph replays ended in a host fault. Traced durations "
+          "are per dispatch from the profiler's start and end stamps. Live figures (no profiler): a decode step's "
+          "launches between HIP events on the model's stream (`llmhip_model_profile`, eager steps after the timed "
+          "rounds), and for the one-launch-per-phase classes back-to-back launches of one class over the 24 layers "
+          "(`llmhip_model_bench_kernel`).", "",
+          "A decode step (the fused pass: every layer in one launch):", "",
           "| class | symbol | grid (threads x rows) | traced launches | traced median us | mean | min | live us (unprofiled) | "
           "bytes | GB/s (live) | GB/s (traced median) |",
           "|---|---|---|---|---|---|---|---|---|---|---|"]
-    for c in CLASSES:
-        if c not in grids:
-            continue
+    machine_d = []
+
+    def row(c):
         sym, g, gy = grids[c]
         st = stats(by[(sym, g, gy)])
         b = cls[c]["bytes"]
-        md.append(f"| {c} | `{sym}` | {g}x{gy} | {st['n']} | {st['median']:.2f} | {st['mean']:.2f} | {st['min']:.2f} | "
-                  f"{cls[c]['avg_us']:.3f} | {b} | {b / cls[c]['avg_us'] * 1e-3:.1f} | "
-                  f"{b / st['median'] * 1e-3:.1f} |")
+        gl = f"{b / cls[c]['avg_us'] * 1e-3:.1f}" if b else "-"
+        gt = f"{b / st['median'] * 1e-3:.1f}" if b else "-"
+        machine_d.append(f"duration_us {c} {st['median']:.3f}")
+        return (f"| {c} | `{sym}` | {g}x{gy} | {st['n']} | {st['median']:.2f} | {st['mean']:.2f} | {st['min']:.2f} | "
+                f"{cls[c]['avg_us']:.3f} | {b} | {gl} | {gt} |")
+    for c in CLASSES:
+        if c in grids:
+            md.append(row(c))
+    md += ["", "One launch per phase (prefill's kernels, the decode fallback, and config 4's decode, which takes the "
+           "split attention):", "",
+           "| class | symbol | grid (threads x rows) | traced launches | traced median us | mean | min | live us (unprofiled) | "
+           "bytes | GB/s (live) | GB/s (traced median) |",
+           "|---|---|---|---|---|---|---|---|---|---|---|"]
+    for c in UNFUSED:
+        if c in grids:
+            md.append(row(c))
     md += ["", f"Live: decode {live['value']} tok/s, prefill {live['prefill_tok_s']} tok/s, decode step kernel sum "
            f"{live['decode_step']['kernel_us']} us of {live['decode_step']['wall_us']} us per token; traced run: "
            f"decode {traced['value']} tok/s.", "",
@@ -232,7 +247,7 @@ def summarize(out):
             md.append(f"| `{n}` | {gx // gy}x{gy} | {st['n']} | {st['median']:.2f} | {st['mean']:.2f} |")
     lc = live.get("long_context")
     if lc:
-        k3e, k3 = lc["classes_at_end"]["k3"]["avg_us"], live["decode_step"]["classes"]["k3"]["avg_us"]
+        k3e, k3 = lc["classes_at_end"]["k3"]["avg_us"], live["decode_step"]["unfused_classes"]["k3"]["avg_us"]
         md += ["", f"Config 4 (2048-token prompt, 512 tokens, ctx 4096), live: prefill {lc['prefill_tok_s']} tok/s, "
                f"decode {lc['decode_tok_s']} tok/s; at the last position the split attention kernel "
                f"{lc['attention_at_end']['avg_us']} us for {lc['attention_at_end']['kv_bytes']} KV bytes "
@@ -262,7 +277,7 @@ def summarize(out):
           f"WRITE_SIZE x {ws:.1f}.", "",
           "class  symbol  grid  FETCH_SIZE_KiB  WRITE_SIZE_KiB  traffic_bytes  algorithmic_bytes  traffic/algorithmic"]
     machine = []
-    for c in CLASSES:
+    for c in CLASSES + UNFUSED:
         if c not in grids:
             continue
         sym, gx, gy = grids[c]
@@ -273,9 +288,11 @@ def summarize(out):
         wv = statistics.median(pw[(sym, g)]["WRITE_SIZE"])
         tb = int(round(fv * fs + wv * ws))
         ab = cls[c]["bytes"]
-        t.append(f"{c}  {sym}  {gx}x{gy}  {fv:.1f}  {wv:.1f}  {tb}  {ab}  {tb / ab:.3f}")
+        t.append(f"{c}  {sym}  {gx}x{gy}  {fv:.1f}  {wv:.1f}  {tb}  {ab}  " + (f"{tb / ab:.3f}" if ab else "-"))
         machine.append(f"traffic_bytes {c} {tb}")
-    t += ["", "A grid of two rows (x2) carries an L2 warm-up: its second row of workgroups reads the weights of the",
+    t += ["", "The fused pass polls flag-carrying words with coherent loads, which are served beyond the L2: its",
+          "FETCH_SIZE counts those polls beside the weights and KV rows (the algorithmic bytes).", "",
+          "A grid of two rows (x2) carries an L2 warm-up: its second row of workgroups reads the weights of the",
           "next-but-one launch (K1 those of K3, K3 of K5, K5 of the next layer's K1) toward the XCD that will read",
           "them, so a carrier's FETCH_SIZE includes those bytes; the algorithmic bytes stay each class's own.  In",
           "this counter run (direct launches) the consumers still fetch their own bytes; the warm-up's measured",
@@ -284,7 +301,8 @@ def summarize(out):
           "k2 algorithmic bytes are the KV rows of the positions attended at the profiled position; the one-chunk",
           "kernel reads the rows up to the next multiple of 64 (a graph variant), and each XCD that serves a KV head",
           "reads its rows once.", "", "Machine-readable (bench.py reads these lines for roofline.traffic when",
-          "sources_hash matches the tree it runs from):", f"sources_hash {h}"] + machine
+          "sources_hash matches the tree it runs from; duration_us: the kernel trace's median, above):",
+          f"sources_hash {h}"] + machine + machine_d
     write(os.path.join(PROFILES, "pmc_decode_qwen25.txt"), t)
 
     # config-1 sweep: live graph replays beside the traced durations

@@ -1,6 +1,6 @@
 """The measurement plumbing on the CPU: the source fingerprint that ties a
 counter summary under profiles/ to the kernels it measured, and bench.py's
-refusal of a stale traffic figure."""
+refusal of a stale traffic or duration figure."""
 import os
 import sys
 
@@ -15,19 +15,22 @@ def test_sources_hash_stable():
     assert profsum.sources_hash() == h
 
 
-def test_traffic_only_for_matching_sources(tmp_path, monkeypatch):
+def test_figures_only_for_matching_sources(tmp_path, monkeypatch):
     import bench
     from llm_amd import profsum
     good = tmp_path / "good.txt"
-    good.write_text(f"header\nsources_hash {profsum.sources_hash()}\ntraffic_bytes k5 123\n")
+    good.write_text(f"header\nsources_hash {profsum.sources_hash()}\ntraffic_bytes k5 123\nduration_us pass 321.5\n")
     stale = tmp_path / "stale.txt"
-    stale.write_text("sources_hash 000000000000\ntraffic_bytes k5 123\n")
+    stale.write_text("sources_hash 000000000000\ntraffic_bytes k5 123\nduration_us pass 321.5\n")
     monkeypatch.setattr(bench, "PMC_SUMMARY", str(good))
-    assert bench.pmc_traffic("k5")[0] == 123
-    assert bench.pmc_traffic("k4")[0] is None
+    assert bench.pmc_value("traffic_bytes", "k5")[0] == 123
+    assert bench.pmc_value("traffic_bytes", "k4")[0] is None
+    assert bench.pmc_value("duration_us", "pass")[0] == 321.5
+    assert bench.pmc_value("duration_us", "k5")[0] is None
     monkeypatch.setattr(bench, "PMC_SUMMARY", str(stale))
-    value, why = bench.pmc_traffic("k5")
-    assert value is None and "000000000000" in why
+    for kind, cls in (("traffic_bytes", "k5"), ("duration_us", "pass")):
+        value, why = bench.pmc_value(kind, cls)
+        assert value is None and "000000000000" in why
 
 
 def test_committed_summaries_name_their_sources():
