@@ -841,12 +841,13 @@ static int segment_dep(int g, int G) { return (g * G + G - 2) / G; }
 // the sampled token of the last one, which goes to tokens[step + ntok], its
 // embedding row to xn; state advances by ntok.
 // Whether the one-token pass being recorded runs as the fused decode launch:
-// a decode step (its input row is xn) of a model that fits it, with the
-// one-chunk attention, every layer and kernel class running, f32 activations.
+// a decode step (its input row is xn) of a model that fits it, with every
+// layer and kernel class running, f32 activations, and positions past
+// attn_full_max only where the long form holds them.
 static bool use_pass(const Model& m, uint32_t ntok, bool head) {
   bool h = head;
-  return m.pass_ok && m.pass_on && ntok == 1 && !m.embed_in && head && !m.attn_split && !m.q8 && m.skip.empty() &&
-         pass_layers(m, &h) == m.cfg.layers && h;
+  return m.pass_ok && m.pass_on && ntok == 1 && !m.embed_in && head && !m.q8 && m.skip.empty() &&
+         (!m.attn_split || pass_long_fits(m.cfg, m.attn_rows, m.pgrid)) && pass_layers(m, &h) == m.cfg.layers && h;
 }
 
 static int record_pass(Model& m, uint32_t ntok, bool head, bool embed_in) {
@@ -856,13 +857,16 @@ static int record_pass(Model& m, uint32_t ntok, bool head, bool embed_in) {
     m.cur_layer = -1;
     PassArgs a = m.pargs;
     a.rows = m.attn_rows;
+    // the long form's (head, chunk)s at the grid's end
+    const uint32_t pm = (a.rows + PASS_LONG_ROWS - 1) / PASS_LONG_ROWS;
+    a.batl = m.attn_split ? m.pgrid - pm * a.heads : 0;
     // algorithmic bytes: every layer's matrices and the KV rows of the
     // positions attended
     uint64_t bytes = 0;
     for (const Layer& L : m.layers)
       bytes += L.qkv[0].g.gguf_bytes() + L.o.g.gguf_bytes() + L.gu[0].g.gguf_bytes() + L.down.g.gguf_bytes() +
                2ull * (m.pos + 1) * m.kvd * (m.kv16 ? 2 : 4);
-    LLM_TRY(launch_rec(m, "pass", bytes, [&]() { return pass_launch(a, m.pgrid, m.pass_q8, m.stream); }));
+    LLM_TRY(launch_rec(m, "pass", bytes, [&]() { return pass_launch(a, m.pgrid, m.pass_q8, m.attn_split, m.stream); }));
     return rec_head(m, ntok - 1, ntok);
   }
   bool h = head;
@@ -1132,9 +1136,10 @@ static int pass_setup(Model& m) {
   a.att = m.att;
   a.act = m.act;
   a.up = m.gbuf;
+  a.np = pass_partials(c, m.ctx);
   a.llq = m.ll;                                        // [E + 2 kvd]
-  a.llo = a.llq + E + 2ull * m.kvd;                    // [E], [heads][16], then [E]
-  a.llb = a.llo + 2 * E + 16ull * c.heads;             // [1 + kp][E]
+  a.llo = a.llq + E + 2ull * m.kvd;                    // [np][E], [np][heads][16], then [E]
+  a.llb = a.llo + a.np * (E + 16ull * c.heads) + E;    // [1 + kp][E]
   a.llact = a.llb + (1 + kp) * E;                      // [ff]
   (void)F;
   a.kp = kp;
@@ -1216,7 +1221,7 @@ int llmhip_model_create(int ordinal, const llmhip_limits* lim, const llmhip_conf
       (rc = dalloc(*m, &m->xprep, xprep_bytes(m->pm, (uint32_t)std::max(c.embd, c.ff)))) ||
       (rc = dalloc_n(*m, &m->cs, (uint64_t)m->ctx * c.head_dim)) || (rc = dalloc_n(*m, &m->h, E)) ||
       (rc = dalloc_n(*m, &m->xn, E)) || (rc = dalloc_n(*m, &m->kpart, 3 * E)) ||
-      (rc = dalloc_n(*m, &m->ll, pass_words(c, m->kvd))) || (rc = dalloc_n(*m, &m->pctrl, 4)) ||
+      (rc = dalloc_n(*m, &m->ll, pass_words(c, m->kvd, pass_partials(c, m->ctx)))) || (rc = dalloc_n(*m, &m->pctrl, 4)) ||
       (rc = dalloc_n(*m, &m->ptab, (uint64_t)c.layers)))
     return fail(rc);
   {  // the prefill lanes: lane 0 is the model's own buffers

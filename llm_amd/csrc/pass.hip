@@ -149,6 +149,7 @@ struct PassLds {
   float part2[1][PASS_WAVES][64];  // those of K3 and K5, which have no barrier before theirs: a wave
                                    // may write them while another still reads the previous phase's
   AttnLds<HD, PASS_WAVES> am;
+  float mrg[PASS_LONG_CHUNKS][HD + 2];  // the long form's merge: each chunk's o, m and l
 };
 
 // Where a phase's input row comes from (stage_ops).
@@ -498,9 +499,14 @@ __device__ __forceinline__ PassMat cmat(CMat* c) {
   return m;
 }
 
-template <uint32_t HD, bool KVH, bool Q8>
+// LONG: positions past attn_full_max (the split attention's range): chunks
+// of PASS_LONG_ROWS rows, one workgroup per (query head, chunk), the last
+// chunk's workgroup merging the others.
+template <uint32_t HD, bool KVH, bool Q8, bool LONG>
 __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
-  constexpr uint32_t V4 = HD / 64, S = 4 * PASS_WAVES, JC = PASS_CHUNK_ROWS / S;
+  static_assert(!LONG || HD == 64, "the long form holds 256 rows of a 64-wide head per workgroup");
+  constexpr uint32_t RC = LONG ? PASS_LONG_ROWS : PASS_CHUNK_ROWS;  // cache rows of a chunk
+  constexpr uint32_t V4 = HD / 64, S = 4 * PASS_WAVES, JC = RC / S;
   typedef AttnChunk<HD, JC, PASS_WAVES, KVH> AC;
   __shared__ PassLds<HD> L;
   const uint32_t wg = blockIdx.x, G = gridDim.x;
@@ -508,7 +514,7 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
   const uint32_t pos = state_pos(a.state);
   const uint32_t epoch = *(const __attribute__((address_space(4))) uint32_t*)a.ctrl;
   Waiter wt{a.ctrl + 1, a.ctrl[2] ? a.ctrl[2] : PASS_SPIN_DEFAULT, false};
-  const uint32_t NCH = pass_chunks(HD), P = pos / PASS_CHUNK_ROWS + 1;  // chunks; those holding rows 0 .. pos
+  const uint32_t NCH = pass_chunks(HD), P = pos / RC + 1;  // chunks; those holding rows 0 .. pos
 // The thread's indices, redefined at each phase's start: per-lane offsets
 // formed from them stay inside the phase (hoisted out of the layer loop, every
 // phase's would hold registers through all the others).
@@ -529,7 +535,17 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
   const uint32_t GQ = a.heads / a.kv_heads, natt1 = 8 * GQ * ((a.kv_heads + 7) / 8);
   bool hasA = false;
   uint32_t hg = 0, hh = 0, hc = 0;  // attention: KV head, query head, chunk
-  if (wg >= a.batt && wg - a.batt < NCH * natt1) {
+  if (LONG) {
+    // (query head, chunk) on workgroup batl + c heads + h, for the chunks of
+    // the rows this launch may read
+    const uint32_t PM = (a.rows + RC - 1) / RC;
+    if (wg >= a.batl && wg - a.batl < a.heads * PM) {
+      hc = (wg - a.batl) / a.heads;
+      hh = (wg - a.batl) % a.heads;
+      hg = hh / GQ;
+      hasA = hc < P;
+    }
+  } else if (wg >= a.batt && wg - a.batt < NCH * natt1) {
     // head h = g GQ + s, chunk c on workgroup batt + c natt1 + 8 (GQ (g / 8) + s) + g % 8 (a KV head's
     // query heads on one XCD)
     const uint32_t rel0 = wg - a.batt, rel = rel0 % natt1, y = rel / 8;
@@ -662,12 +678,12 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
     // out the chunk's max score M, sum of e L and sum of e v (unnormalised)
     if (hasA) {
       PHASE_IDS;
-      const uint32_t cl = tid & 15, slot = tid >> 4, row0 = hc * PASS_CHUNK_ROWS;
+      const uint32_t cl = tid & 15, slot = tid >> 4, row0 = hc * RC;
       const float* kvp = Y->kv;
       AC rows;
       {
         // 32-bit element offsets (the cache holds 2 ctx kvd < 2^31 elements)
-        const uint32_t lim = max(pos, 1u), Jr = min(a.rows - min(a.rows, row0), PASS_CHUNK_ROWS) / S;
+        const uint32_t lim = max(pos, 1u), Jr = min(a.rows - min(a.rows, row0), RC) / S;
         const uint32_t kb = hg * HD + 4 * cl, vb = a.ctx * a.kvd + hg * HD + 4 * cl;
 #pragma unroll
         for (uint32_t j = 0; j < JC; j++) {
@@ -694,7 +710,7 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
 #pragma unroll
         for (uint32_t k = 0; k < V4; k++) qv[k] = f4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
       }
-      if (pos >= row0 && pos < row0 + PASS_CHUNK_ROWS && slot == (pos - row0) % S) {
+      if (pos >= row0 && pos < row0 + RC && slot == (pos - row0) % S) {
         // this thread's rows hold the position's row: K1's words
         uint32_t idx[8 * V4];
         bool need[8 * V4];
@@ -719,7 +735,11 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       }
       float M_, L_, o;
       rows.reduce(qv, row0, pos + 1, a.scale, L.am, &M_, &L_, &o);
-      uint64_t* fin = llo + E + 16 * a.heads;  // the attention's output row
+      // llo: the partial sums of chunks c < P - 1 (o at c E, m and l in a
+      // whole line of 16 words at np E + 16 (c heads + h), m at even words and
+      // l at odd: a store of part of a line has been seen to reach other XCDs
+      // later), then the output row
+      uint64_t* fin = llo + a.np * (E + 16 * a.heads);
       if (P == 1) {
         // one chunk: its sums normalised (a one-chunk merge: M = m, weight 1)
         if (tid < HD) {
@@ -727,27 +747,68 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
           ll_store(fin + hh * HD + tid, r, F);
           if (last) a.att[hh * HD + tid] = r;
         }
-      } else if (hc == 0) {
-        if (tid < HD) ll_store(llo + hh * HD + tid, o, F);
-        // m and l in a whole line of 16 words (m at even words, l at odd):
-        // a store of part of a line has been seen to reach other XCDs later
-        if (tid < 16) ll_store(llo + E + 16 * hh + tid, tid & 1 ? L_ : M_, F);
-      } else if (tid < HD) {
-        // chunk 1 merges chunk 0's sums into its own as attn_merge_kernel
-        // merges chunks (layer.hip): M, then the weights, L and o, then o / L
-        float v[3];  // chunk 0's o, m, l
-        ll_wait_f<3>([&](int i) { return i == 0 ? llo + hh * HD + tid : llo + E + 16 * hh + (i - 1); },
-                     [](int) { return true; }, F, v, wt);
-        const float Mx = fmaxf(fmaxf(-INFINITY, v[1]), M_);
-        const float w0 = __expf(v[1] - Mx), w1 = __expf(M_ - Mx);
-        float Ls = 0, oo = 0;
-        Ls += w0 * v[2];
-        Ls += w1 * L_;
-        oo += w0 * v[0];
-        oo += w1 * o;
-        const float r = oo / Ls;
-        ll_store(fin + hh * HD + tid, r, F);
-        if (last) a.att[hh * HD + tid] = r;
+      } else if (hc + 1 < P) {
+        if (tid < HD) ll_store(llo + hc * E + hh * HD + tid, o, F);
+        if (tid < 16) ll_store(llo + a.np * E + 16 * (hc * a.heads + hh) + tid, tid & 1 ? L_ : M_, F);
+      } else if (!LONG) {
+        // the second chunk merges the first's sums and its own as
+        // attn_merge_kernel merges chunks (layer.hip): M, then the weights, L
+        // and o, then o / L
+        if (tid < HD) {
+          float v[3];  // chunk 0's o, m, l
+          ll_wait_f<3>([&](int i) { return i == 0 ? llo + hh * HD + tid : llo + a.np * E + 16 * hh + (i - 1); },
+                       [](int) { return true; }, F, v, wt);
+          const float Mx = fmaxf(fmaxf(-INFINITY, v[1]), M_);
+          const float w0 = __expf(v[1] - Mx), w1 = __expf(M_ - Mx);
+          float Ls = 0, oo = 0;
+          Ls += w0 * v[2];
+          Ls += w1 * L_;
+          oo += w0 * v[0];
+          oo += w1 * o;
+          const float r = oo / Ls;
+          ll_store(fin + hh * HD + tid, r, F);
+          if (last) a.att[hh * HD + tid] = r;
+        }
+      } else {
+        // the last chunk merges the others' sums and its own, as above in
+        // chunk order; wave w polls chunks w and w + 8 into LDS
+        const uint32_t lane = tid & 63;
+        float v[6];  // chunk wave + 8 i: o, m, l at 3 i
+        ll_wait_f<6>(
+            [&](int i) {
+              const uint32_t c = wave + PASS_WAVES * (i / 3), k = i % 3;
+              return k == 0 ? llo + c * E + hh * HD + lane : llo + a.np * E + 16 * (c * a.heads + hh) + (k - 1);
+            },
+            [&](int i) { return wave + PASS_WAVES * (i / 3) + 1 < P; }, F, v, wt);
+#pragma unroll
+        for (uint32_t i = 0; i < 2; i++) {
+          const uint32_t c = wave + PASS_WAVES * i;
+          if (c + 1 < P) {
+            L.mrg[c][lane] = v[3 * i];
+            if (lane == 0) {
+              L.mrg[c][HD] = v[3 * i + 1];
+              L.mrg[c][HD + 1] = v[3 * i + 2];
+            }
+          }
+        }
+        __syncthreads();
+        if (tid < HD) {
+          float Mx = -INFINITY;
+          for (uint32_t c = 0; c + 1 < P; c++) Mx = fmaxf(Mx, L.mrg[c][HD]);
+          Mx = fmaxf(Mx, M_);
+          float Ls = 0, oo = 0;
+          for (uint32_t c = 0; c + 1 < P; c++) {
+            const float w = __expf(L.mrg[c][HD] - Mx);
+            Ls += w * L.mrg[c][HD + 1];
+            oo += w * L.mrg[c][tid];
+          }
+          const float w = __expf(M_ - Mx);
+          Ls += w * L_;
+          oo += w * o;
+          const float r = oo / Ls;
+          ll_store(fin + hh * HD + tid, r, F);
+          if (last) a.att[hh * HD + tid] = r;
+        }
       }
     }
 
@@ -773,7 +834,7 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
         }
       }
       StageIn in{};
-      in.ll = llo + E + 16 * a.heads;
+      in.ll = llo + a.np * (E + 16 * a.heads);
       in.flag = F;
       in.gate = true;
       UnitsB<1, 1> ub;
@@ -927,20 +988,26 @@ const char* pass_unfit(const llmhip_config& c, uint32_t kvd, const PassMat& qkv,
   return nullptr;
 }
 
+template <uint32_t HD, bool KVH, bool Q8, bool LONG>
+static int occupancy() {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pass_kernel<HD, KVH, Q8, LONG>, 64 * PASS_WAVES, 0) !=
+      hipSuccess)
+    return 0;
+  return n;
+}
+
 template <uint32_t HD, bool KVH>
 static uint32_t grid_of(int device) {
-  int n = 0, n8 = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pass_kernel<HD, KVH, false>, 64 * PASS_WAVES, 0) !=
-          hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n8, pass_kernel<HD, KVH, true>, 64 * PASS_WAVES, 0) != hipSuccess)
-    return 0;
-  n = std::min(n, n8);
+  // (the forms hold different registers: the least occupancy bounds them all)
+  int n = std::min(occupancy<HD, KVH, false, false>(), occupancy<HD, KVH, true, false>());
+  if (HD == 64) n = std::min({n, occupancy<64, KVH, false, true>(), occupancy<64, KVH, true, true>()});
+  int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
   return n >= 1 && cus > 0 ? (uint32_t)cus : 0;
 }
 
 uint32_t pass_grid(int device, uint32_t hd, bool kv16) {
-  // (the Q8 form holds more registers: its occupancy bounds both)
   if (hd == 64) return kv16 ? grid_of<64, true>(device) : grid_of<64, false>(device);
   if (hd == 128) return kv16 ? grid_of<128, true>(device) : grid_of<128, false>(device);
   return 0;
@@ -962,19 +1029,25 @@ void pass_place(PassArgs* a, uint32_t grid, uint32_t t1, uint32_t t3, uint32_t t
   a->b4 = 0;
 }
 
-template <uint32_t HD, bool KVH>
+template <uint32_t HD, bool KVH, bool LONG>
 static void go(const PassArgs& a, uint32_t grid, bool q8, hipStream_t s) {
-  if (q8) hipLaunchKernelGGL((pass_kernel<HD, KVH, true>), dim3(grid), dim3(64 * PASS_WAVES), 0, s, a);
-  else hipLaunchKernelGGL((pass_kernel<HD, KVH, false>), dim3(grid), dim3(64 * PASS_WAVES), 0, s, a);
+  if (q8) hipLaunchKernelGGL((pass_kernel<HD, KVH, true, LONG>), dim3(grid), dim3(64 * PASS_WAVES), 0, s, a);
+  else hipLaunchKernelGGL((pass_kernel<HD, KVH, false, LONG>), dim3(grid), dim3(64 * PASS_WAVES), 0, s, a);
 }
 
-int pass_launch(const PassArgs& a, uint32_t grid, bool q8, hipStream_t s) {
+int pass_launch(const PassArgs& a, uint32_t grid, bool q8, bool lng, hipStream_t s) {
+  if (lng && a.hd != 64) return set_error(LLMHIP_ERR_ARG, "llm: decode pass: long form at head size %u", a.hd);
   if (a.hd == 64) {
-    if (a.kv16) go<64, true>(a, grid, q8, s);
-    else go<64, false>(a, grid, q8, s);
+    if (lng) {
+      if (a.kv16) go<64, true, true>(a, grid, q8, s);
+      else go<64, false, true>(a, grid, q8, s);
+    } else {
+      if (a.kv16) go<64, true, false>(a, grid, q8, s);
+      else go<64, false, false>(a, grid, q8, s);
+    }
   } else if (a.hd == 128) {
-    if (a.kv16) go<128, true>(a, grid, q8, s);
-    else go<128, false>(a, grid, q8, s);
+    if (a.kv16) go<128, true, false>(a, grid, q8, s);
+    else go<128, false, false>(a, grid, q8, s);
   } else {
     return set_error(LLMHIP_ERR_ARG, "llm: decode pass: head size %u", a.hd);
   }

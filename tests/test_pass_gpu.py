@@ -38,13 +38,20 @@ def test_pass_parity(gpu, name):
     """Decode steps through the fused launch against the oracle, and the
     logits of a decode step against those of the same step taken one launch
     per kernel (the same arithmetic, summed in another order)."""
-    import numpy as np
-    from tests.parity import rel_err
     spec = CASES[name]()
     g, cpu = _open(spec, 256)
     _fused(g)
     prompt = synth.prompt(41, 70, spec.vocab)
     _check(g, cpu, prompt, 60)
+    _fused_vs_plain(g, spec, prompt)
+
+
+def _fused_vs_plain(g, spec, prompt):
+    """The logits after 1 and 8 decode steps through the fused launch against
+    those of the same steps taken one launch per kernel (the same arithmetic,
+    summed in another order), where the tokens agree."""
+    import numpy as np
+    from tests.parity import rel_err
     for steps in (2, 9):
         fused = gpu_generate(g, prompt, steps)
         lf = g.Peek("logits", spec.vocab)
@@ -55,6 +62,20 @@ def test_pass_parity(gpu, name):
         print(f"{steps - 1} decode steps: tokens equal {fused == plain}, logits {rel_err(lf, lp):.2e}", flush=True)
         if fused == plain:
             assert rel_err(lf, lp) <= 1e-5 and np.all(np.isfinite(lf))
+
+
+@pytest.mark.parametrize("start", [300, 1500])
+def test_pass_long_context(gpu, start):
+    """Decode steps past attn_full_max through the long form of the fused
+    launch (256-row chunks, one workgroup per query head and chunk, the last
+    chunk's workgroup merging the others): against the oracle, and against
+    the same steps taken one launch per kernel (the split attention)."""
+    spec = synth.tiny_qwen(seed=24, ctx=2048)
+    g, cpu = _open(spec, 2048)
+    _fused(g)
+    prompt = synth.prompt(43, start, spec.vocab)
+    _check(g, cpu, prompt, 24)
+    _fused_vs_plain(g, spec, prompt)
 
 
 @pytest.mark.parametrize("kv16", [False, True])
