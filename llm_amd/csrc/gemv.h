@@ -58,26 +58,6 @@ enum Epilogue : int {
   EPI_SWIGLU = 5   // y[t*ldy + row] = silu(aux[t*ldy + row]) * v  (up, gate stored apart)
 };
 
-// L2 warm-up for a later one-token launch of the tile kernel (the consumer),
-// carried by an earlier launch: a second row of `wgs` workgroups (y = 1)
-// after that launch's `own` (y = 0) touch one dword per 128-byte line of the
-// weight bytes the consumer's workgroups will read, each line from the XCD
-// on which its consumer workgroup will run.  Workgroups go to the 8 XCDs
-// round-robin by launch index, and a line a CU has read can stay in its
-// XCD's L2 into later kernels, for the consumer's weight loads to find there
-// (or at least in the memory-side cache) rather than in HBM; measured end to
-// end, it pays at long context.  No result depends on it.  wgs = 0: none.
-constexpr uint32_t XCDS = 8;
-struct Prefetch {
-  const uint8_t* qs;     // the consumer's tiles
-  uint32_t wgs, own;     // warm-up workgroups (a multiple of XCDS, <= own); the launch's own (set at launch)
-  uint32_t cgrid;        // consumer workgroups: (tile group) * kparts + part, as gemv_kernel numbers them
-  uint32_t tiles, tpw, kparts, ng;
-  uint32_t tile_bytes;   // bytes per tile
-  uint32_t sbase;        // offset of the scales in a tile (16 nb QB)
-  uint32_t qg, sg;       // quant and scale bytes of a block group (Lay::QG, 64 SB)
-  uint32_t lpt;          // 128-byte lines of one tile a part reads, at most
-};
 
 struct GemvArgs {
   // matrix
@@ -134,7 +114,6 @@ struct GemvArgs {
   float* xdx;      // [tg*8][nb] PRO_Q8: the activation block scales d (binary16 values)
   uint32_t tg;     // token groups of 8
   uint32_t q8;     // the prepared activations are Q8 blocks (PRO_Q8): gemm_kernel's block products
-  Prefetch pf;     // one token, tile kernel: the L2 warm-up this launch carries
 };
 
 // Bytes of the prepared-activation buffers for ntok tokens of k inputs
@@ -165,14 +144,8 @@ int gemm_launch(const GemvArgs& a, uint32_t qtype, int epi, hipStream_t s);
 
 // Bytes of LDS a launch needs, and whether the shape is supported.
 int gemv_launch(const GemvArgs& a, uint32_t qtype, int pro, int epi, hipStream_t s);
-// Workgroups the launch uses along x (EPI_ARGMAX partial count), without any
-// appended prefetch workgroups.
+// Workgroups the launch uses along x (EPI_ARGMAX partial count).
 uint32_t gemv_groups(const GemvArgs& a);
-// The L2 warm-up of a one-token tile-kernel launch `consumer` (its matrix of
-// type qtype bound, kparts set), for a carrier launch of `threads` threads per
-// workgroup: enough workgroups that each thread touches at most `per_thread`
-// lines.  wgs = 0 (nothing) for a streaming-kernel or several-token consumer.
-Prefetch prefetch_plan(const GemvArgs& consumer, uint32_t qtype, uint32_t threads, uint32_t per_thread = 4);
 // Picks the split-K factor (waves per tile) and the waves per workgroup.
 void gemv_pick(uint32_t tiles, uint32_t ng, uint32_t tail, uint32_t nb, uint32_t* split, uint32_t* waves);
 // Picks the streaming form for a one-token launch: workgroups (0: none: fewer than

@@ -52,42 +52,6 @@ __device__ __forceinline__ uint4 ld_stream16(const uint8_t* p) {
   return uint4{v[0], v[1], v[2], v[3]};
 }
 
-// The work of warm-up workgroup j of a launch carrying p (Prefetch, gemv.h):
-// launched as workgroup (j, 1) of a grid of `own` x 2, it runs on XCD
-// c = (own + j) % 8 (workgroups are numbered x-fastest) and, with
-// the other wgs / 8 workgroups of that XCD, touches the lines of the consumer
-// workgroups x = c, c + 8, ...: tile group x / kparts, part x % kparts, whose
-// block groups [g0, g1) (the last part: through the tile's end) are quant
-// bytes [g0 qg, g1 qg) and scale bytes sbase + [g0 sg, g1 sg).  Four loads
-// per thread are in flight at once; the values are only kept alive.
-__device__ __forceinline__ void prefetch_run(const Prefetch& p, uint32_t j) {
-  const uint32_t c = (p.own + j) % XCDS, per = p.wgs / XCDS, k = j / XCDS;
-  const uint32_t nx = p.cgrid > c ? (p.cgrid - c + XCDS - 1) / XCDS : 0;
-  const uint32_t lines = p.tpw * p.lpt, items = nx * lines, step = per * blockDim.x;
-  uint32_t acc = 0;
-  for (uint32_t f0 = k * blockDim.x + threadIdx.x; f0 < items; f0 += 4 * step) {
-    uint32_t v[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const uint32_t f = f0 + u * step;
-      uint64_t off = 0;  // an in-bounds line (the first) where an item has none
-      if (f < items) {
-        const uint32_t x = c + XCDS * (f / lines), l = f % lines;
-        const uint32_t part = x % p.kparts, t = x / p.kparts * p.tpw + l / p.lpt, lt = l % p.lpt;
-        const bool last = part == p.kparts - 1;
-        const uint32_t g0 = part * p.ng / p.kparts, g1 = (part + 1) * p.ng / p.kparts;
-        const uint32_t q0 = g0 * p.qg, q1 = last ? p.sbase : g1 * p.qg;
-        const uint32_t s0 = p.sbase + g0 * p.sg, s1 = last ? p.tile_bytes : p.sbase + g1 * p.sg;
-        const uint32_t nq = (q1 - q0 + 127) / 128;
-        const uint32_t o = lt < nq ? q0 + 128 * lt : s0 + 128 * (lt - nq);
-        if (t < p.tiles && o < (lt < nq ? q1 : s1)) off = (uint64_t)t * p.tile_bytes + (o & ~3u);
-      }
-      v[u] = *(const uint32_t*)(p.qs + off);
-    }
-    acc += v[0] ^ v[1] ^ v[2] ^ v[3];
-  }
-  asm volatile("" ::"v"(acc));
-}
 
 // f32(1 / sqrt(x)) of a double x (cpu.go:92-95: float32(1/math.Sqrt(...)))
 // without the f64 divide and square-root sequences on the decode kernels'
@@ -1846,10 +1810,6 @@ __device__ __forceinline__ void touch_args(GemvArgs& a) {
 
 template <uint32_t QT, int NT, int PRO, int EPI, int NU>
 __global__ __launch_bounds__((PRO & PRO_MERGE) ? 512 : 1024) void gemv_kernel(GemvArgs a_in) {
-  if (NT == 1 && blockIdx.y != 0) {  // the L2 warm-up row (a one-token launch has one row of its own)
-    if (blockIdx.x < a_in.pf.wgs) prefetch_run(a_in.pf, blockIdx.x);
-    return;
-  }
   GemvArgs a = a_in;
   if (NT == 1) touch_args<PRO, EPI>(a);
   typedef WaveLds<NT> WL;
@@ -2126,15 +2086,6 @@ int gemv_launch_qt(const GemvArgs& a, int pro, int epi, hipStream_t s) {
     return set_error(LLMHIP_ERR_ARG, "llm: gemv: %u waves of %d tokens need %u bytes of LDS", a.waves, nt, lds);
   if (epi == EPI_ARGMAX && a.ntok != 1) return set_error(LLMHIP_ERR_ARG, "llm: gemv: argmax epilogue needs one token");
   dim3 grid(gemv_groups(a), (a.ntok + nt - 1) / nt);
-  if (a.pf.wgs) {  // the warm-up workgroups: a second row after the launch's own (at most as many)
-    if (nt != 1 || epi == EPI_ARGMAX || a.pf.wgs % XCDS || !a.pf.qs)
-      return set_error(LLMHIP_ERR_ARG, "llm: gemv: an L2 warm-up rides on a one-token launch, in groups of 8");
-    GemvArgs b = a;
-    b.pf.own = grid.x;
-    b.pf.wgs = std::min(a.pf.wgs, grid.x / XCDS * XCDS);
-    if (b.pf.wgs) grid.y = 2;
-    return launch_nt<QT, 1>(b, pro, epi, grid, lds, s);
-  }
   switch (nt) {
     case 1: return launch_nt<QT, 1>(a, pro, epi, grid, lds, s);
     case 2: return launch_nt<QT, 2>(a, pro, epi, grid, lds, s);

@@ -514,28 +514,6 @@ static GemvArgs base_args(const Model& m, const QMat& q, uint32_t ntok) {
   return a;
 }
 
-// The L2 warm-up a launch of a one-token pass carries (Prefetch): K1 that of
-// its layer's K3, K3 that of K5 and K5 that of the next layer's K1, each
-// launch's idle CUs reading the next-but-one launch's weights toward the XCD
-// that will read them.
-// LLMHIP_L2_WARM=0 (read once): none, for comparison (results are the same).
-static bool l2_warm() {
-  static const bool on = [] {
-    const char* v = getenv("LLMHIP_L2_WARM");
-    return !(v && strcmp(v, "0") == 0);
-  }();
-  return on;
-}
-
-static Prefetch warm_for(const Model& m, const QMat& q, uint32_t ntok, uint32_t threads, uint32_t kparts = 1) {
-  Prefetch p;
-  memset(&p, 0, sizeof p);
-  if (ntok != 1 || !l2_warm()) return p;
-  GemvArgs c = base_args(m, q, 1);
-  c.kparts = kparts;
-  return prefetch_plan(c, q.g.q.type, threads);
-}
-
 // Whether a one-token K5 (bound in a) runs in two k-parts whose halves the
 // next layer's K1 adds: `want` when that K1 follows in the same pass.
 // (The summing prologue holds the whole row in two float4s per lane: k <= 512 * 4 waves.)
@@ -580,7 +558,6 @@ static int rec_k1(Model& m, const Layer& L, uint32_t ntok) {
     a.ctx = m.ctx;
     a.neox = c.rope_neox;
     a.row_base = L.qkv_base[i];
-    if (i == 0) a.pf = warm_for(m, L.o, ntok, 64 * a.waves);
     LLM_TRY(mat_rec(m, "k1", "p1", a, L.qkv_type[i], pro, EPI_QKV, L.qkv[i].g.gguf_bytes(), i == 0));
   }
   m.xsum_ready = m.k5_split;
@@ -633,9 +610,6 @@ static int rec_k2(Model& m, const Layer& L, uint32_t ntok) {
   // KV bytes read for the last token of the pass (the decode step's one token)
   uint64_t bytes = 2ull * (m.pos + 1) * m.kvd * 4;
   AttnArgs a = attn_args(m, L);
-  // (it carries no warm-up: K4's weights read by its idle CUs slowed the
-  // split kernel more than K4 gained, config-4 decode 1751 against 1694 tok/s,
-  // and the one-chunk kernel is too short to hide them, 1921 against 1915 at config 3)
   if (merge_in_k3(m, L, ntok)) return launch_rec(m, "k2", bytes, [&]() { return attn_launch(a, ntok, m.stream, nullptr, false); });
   if (m.attn_split) m.dispatches++;  // the merge kernel
   if (att_operands(m, ntok)) {
@@ -657,10 +631,6 @@ static int rec_k3(Model& m, const Layer& L, uint32_t ntok) {
   if (m.cur_layer == 0 && !m.embed_in) a.yin = m.xn;  // the residual stream starts at the embedding row
   if (m.xsum_ready) a.yin = m.kpart + 2 * m.cfg.embd;  // x + the previous layer's down halves (K1 summed them)
   m.xsum_ready = false;
-  {
-    const GemvArgs d = base_args(m, L.down, ntok);
-    a.pf = warm_for(m, L.down, ntok, 64 * a.waves, k5_splits(m, d, ntok, next_layer_runs(m)) ? 2 : 1);
-  }
   if (merge_in_k3(m, L, ntok)) {
     a.mpv = m.pv;
     a.mml = m.ml;
@@ -713,7 +683,6 @@ static int rec_k5(Model& m, const Layer& L, uint32_t ntok, bool split = false) {
   a.ldx = m.cfg.ff;
   a.y = m.x;
   split = k5_splits(m, a, ntok, split);
-  if (next_layer_runs(m)) a.pf = warm_for(m, m.layers[m.cur_layer + 1].qkv[0], ntok, 64 * a.waves);
   if (split) {
     a.kparts = 2;
     a.y = m.kpart;
@@ -1653,7 +1622,7 @@ int llmhip_model_bench_kernel(llmhip_model* h, const char* kernel, int iters, fl
   // as in the decode pass
   auto one = [&](int i) -> int {
     const Layer& ly = m.layers[i % L];
-    m.cur_layer = i % L;  // the launches carry the L2 warm-ups of the pass (Prefetch)
+    m.cur_layer = i % L;
     if (k == "head") {  // the decode head kernel without the sampling kernel, which advances the state
       const QMat& w = m.tied ? m.embd : m.out;
       return gemv_launch(head_args(m, 0, 0), w.g.q.type, PRO_RMS | (m.q8 ? PRO_Q8 : 0), EPI_ARGMAX, m.stream);

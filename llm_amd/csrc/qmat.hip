@@ -87,32 +87,6 @@ void gemv_pick(uint32_t tiles, uint32_t ng, uint32_t tail, uint32_t nb, uint32_t
   *waves = w;
 }
 
-Prefetch prefetch_plan(const GemvArgs& c, uint32_t qtype, uint32_t threads, uint32_t per_thread) {
-  Prefetch p;
-  memset(&p, 0, sizeof p);
-  if (c.ntok != 1 || c.stream || c.tiles == 0 || threads == 0 || per_thread == 0) return p;
-  const uint32_t qb = qtype == LLMHIP_Q8_0 ? 32 : 16, sb = qtype == LLMHIP_Q4_1 ? 4 : 2;
-  const uint32_t kp = c.kparts > 1 ? c.kparts : 1;
-  p.qs = c.qs;
-  p.cgrid = gemv_groups(c);
-  p.tiles = c.tiles;
-  p.tpw = c.waves / c.split;
-  p.kparts = kp;
-  p.ng = c.ng;
-  p.tile_bytes = 16 * c.nb * (qb + sb);
-  p.sbase = 16 * c.nb * qb;
-  p.qg = 1024 * (qtype == LLMHIP_Q8_0 ? 2 : 1);
-  p.sg = 64 * sb;
-  // the largest part: the last (it has the most groups and the tail)
-  const uint32_t g0 = (kp - 1) * c.ng / kp;
-  p.lpt = (p.sbase - g0 * p.qg + 127) / 128 + (p.tile_bytes - p.sbase - g0 * p.sg + 127) / 128;
-  // the consumer workgroups of the busiest XCD, times their lines
-  const uint64_t items = (uint64_t)((p.cgrid + XCDS - 1) / XCDS) * p.tpw * p.lpt;
-  const uint64_t per = (items + (uint64_t)threads * per_thread - 1) / ((uint64_t)threads * per_thread);
-  p.wgs = (uint32_t)std::min<uint64_t>(per, 64) * XCDS;
-  return p;
-}
-
 uint32_t gemv_groups(const GemvArgs& a) {
   if (a.stream && a.ntok == 1) return a.stream;
   uint32_t tpw = a.waves / a.split;

@@ -165,8 +165,7 @@ def calibration(out):
 def class_grids(rows, symbols):
     """The (symbol, grid x, grid y) of each decode class in a kernel trace: the
     most launched grid of the class's symbol (k3 and k5 share a symbol in some
-    builds and differ in grid: k3 the smaller).  A one-token launch that
-    carries an L2 warm-up has a second row of workgroups (grid y 2)."""
+    builds and differ in grid: k3 the smaller)."""
     by = collections.Counter((n, gx, gy) for _, n, gx, gy, _ in rows if gy <= 2)
     out = {}
     for c, sym in symbols.items():
@@ -292,12 +291,7 @@ def summarize(out):
         machine.append(f"traffic_bytes {c} {tb}")
     t += ["", "The fused pass polls flag-carrying words with coherent loads, which are served beyond the L2: its",
           "FETCH_SIZE counts those polls beside the weights and KV rows (the algorithmic bytes).", "",
-          "A grid of two rows (x2) carries an L2 warm-up: its second row of workgroups reads the weights of the",
-          "next-but-one launch (K1 those of K3, K3 of K5, K5 of the next layer's K1) toward the XCD that will read",
-          "them, so a carrier's FETCH_SIZE includes those bytes; the algorithmic bytes stay each class's own.  In",
-          "this counter run (direct launches) the consumers still fetch their own bytes; the warm-up's measured",
-          "effect is end to end (bench.py with LLMHIP_L2_WARM=0 against the default on one box: config 3 unchanged,",
-          "config 4 decode +1.4%).", "",
+
           "k2 algorithmic bytes are the KV rows of the positions attended at the profiled position; the one-chunk",
           "kernel reads the rows up to the next multiple of 64 (a graph variant), and each XCD that serves a KV head",
           "reads its rows once.", "", "Machine-readable (bench.py reads these lines for roofline.traffic when",
