@@ -42,14 +42,14 @@ PMC_SUMMARY = os.path.join(ROOT, "profiles", "pmc_decode_qwen25.txt")
 def kernel_symbols(attn_full):
     """Device symbol of each decode kernel class of the config-3 model (Q4_0
     layers, Q8_0 head): the fused pass pass_kernel<head size, binary16 cache,
-    Q8_0 matrices>, the sampling kernel, and for one launch per phase
+    Q8_0 matrices, long form>, the sampling kernel, and for one launch per phase
     gemv_kernel<type, tokens, prologue, epilogue, units
     per staging batch> (K1 after layer 0 adds the previous down projection's
     two k-halves, prologue 65; K5 before the last layer stores those halves,
     epilogue 0, three block groups per wave: four per staging batch), the
     one-chunk or split attention, the streaming head <type,
     prologue, epilogue, groups per tile>."""
-    return {"pass": "pass_kernel<64u, false, false>", "argmax": "argmax_kernel",
+    return {"pass": "pass_kernel<64u, false, false, false>", "argmax": "argmax_kernel<2u>",
             "k1": "gemv_kernel<2u, 1, 65, 2, 2>",
             "k2": "attn_kernel<64u, 8u, false, false, false>" if attn_full else
                   "attn_kernel<64u, 8u, true, false, false>",
@@ -185,17 +185,44 @@ def generation(args):
     }
 
 
+MFMA_SUMMARY = os.path.join(ROOT, "profiles", "mfma_util_qwen25.md")
+
+
+def prefill_counter():
+    """The prefill products' MFMA busy fraction from the committed rocprofv3
+    counter summary (rocprofv3's MfmaUtil over every gemm_kernel dispatch),
+    if it measured this tree's sources: (percent or None, source)."""
+    from llm_amd import profsum
+    want, got, value = profsum.sources_hash(), None, None
+    try:
+        with open(MFMA_SUMMARY) as f:
+            for line in f:
+                p = line.split()
+                if len(p) == 2 and p[0] == "sources_hash":
+                    got = p[1]
+                if len(p) == 2 and p[0] == "prefill_gemm_mfma_util":
+                    value = float(p[1])
+    except OSError:
+        return None, "no counter summary"
+    if got != want:
+        return None, f"{os.path.relpath(MFMA_SUMMARY, ROOT)} measured sources {got}, this tree is {want}"
+    return value, f"{os.path.relpath(MFMA_SUMMARY, ROOT)} (sources {got})"
+
+
 def prefill_roofline(tok_s):
     """MFMA utilisation of the prefill chunks: the layers'
     matrix FLOPs (2 per weight per token) at the measured prefill rate, against
-    MI355X's dense f16 MFMA peak."""
+    MI355X's dense f16 MFMA peak, and beside it the counter figure: the MFMA
+    busy fraction of the products while they run."""
     from llm_amd import synth
     s = synth.qwen25(seed=0)
     kvd = s.kv_heads * (s.embd // s.heads)
     per_token = 2 * s.layers * (s.embd * (s.embd + 2 * kvd) + s.embd * s.embd + 3 * s.ff * s.embd)
     achieved = per_token * tok_s * 1e-12
+    busy, source = prefill_counter()
     return {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_MFMA_F16_TFLOPS, 5), "flops_per_token": per_token,
+            "gemm_mfma_busy_pct": busy, "gemm_mfma_busy_source": source,
             "note": "layer matrix FLOPs over the whole prefill time (prep, attention and the head included); the "
                     "products run on v_mfma_f32_16x16x32_f16 with each activation split into two f16 rows, so the "
                     "MFMA units execute twice these FLOPs"}
@@ -238,6 +265,15 @@ def long_context(args):
     prompt = list(synth.prompt(0, 2048, spec.vocab))
     g.Generate(prompt, 512, -1)  # round 0, dropped (as the reference's bench drops it): graphs built
     tm = g.Generate(prompt, 512, -1)
+    # the decode step's launches at the last positions (the fused pass's long form)
+    fused = {}
+    for _ in range(4):
+        for c, _layer, b, u in g.profile(2):
+            f = fused.setdefault(c, {"us": [], "bytes": b})
+            f["us"].append(u)
+    fused = {c: {"avg_us": round(statistics.mean(f["us"]), 3), "bytes": f["bytes"],
+                 "gbps": round(f["bytes"] / statistics.mean(f["us"]) * 1e-3, 1) if f["bytes"] else None}
+             for c, f in fused.items()}
     us, nbytes = g.bench_kernel("k2", 96)
     classes = {}
     for cls in ("k1", "k3", "k4", "k5", "head"):
@@ -247,10 +283,12 @@ def long_context(args):
     res = {"workload": "BASELINE config 4: qwen2.5-0.5b shape, Q4_1 ffn_down on odd layers, Q8_0 head, 2048-token "
                        "prompt, 512 greedy tokens, ctx 4096",
            "prefill_tok_s": round(tm.PromptTokens / tm.Prefill, 1), "decode_tok_s": round(tm.Generated / tm.Decode, 1),
+           "decode_step_at_end": fused,
            "attention_at_end": {"avg_us": round(us, 2), "kv_bytes": nbytes, "gbps": round(nbytes / us * 1e-3, 1),
-                                "note": "the split attention kernel (chunks of 256 rows); their merge runs in the "
-                                        "output projection's prologue, so classes_at_end.k3 carries it (k3 merges "
-                                        "nothing at config 3: decode_step.unfused_classes.k3)"},
+                                "note": "one launch per phase (the fallback): the split attention kernel (chunks of "
+                                        "256 rows); their merge runs in the output projection's prologue, so "
+                                        "classes_at_end.k3 carries it (k3 merges nothing at config 3: "
+                                        "decode_step.unfused_classes.k3)"},
            "classes_at_end": classes}
     log(f"long context: prefill {res['prefill_tok_s']} tok/s, decode {res['decode_tok_s']} tok/s, "
         f"attention {us:.1f} us for {nbytes} KV bytes")

@@ -35,6 +35,9 @@ CLASSES = ["pass", "head", "argmax"]  # a decode step's launches
 UNFUSED = ["k1", "k2", "k3", "k4", "k5"]  # one launch per phase (prefill, fallback, config-4 decode)
 SWEEP = [(576, 576), (1536, 576), (576, 1536), (896, 896), (4864, 896), (896, 4864), (151936, 896)]
 VOCAB = "q4_0:151936x896"
+# MFMA utilisation (rocprofv3's MfmaUtil: SQ_VALU_MFMA_BUSY_CYCLES summed over the SIMDs, over GRBM_GUI_ACTIVE
+# times the SIMDs) and the instruction mix, per dispatch
+MFMA = ["MfmaUtil", "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE"]
 SQ = ["SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VMEM_RD", "SQ_INSTS_LDS", "SQ_INSTS_SALU",
       "SQ_BUSY_CYCLES", "SQ_WAVE_CYCLES"]
 
@@ -68,6 +71,7 @@ def passes(out):
     return [
         ("kt", 600, eager, trace, py + ["--no-sweep", "--no-cpu", "--steps", "2"]),
         ("ktsweep", 600, eager, trace, py + ["--gemv", ",".join(sweep_specs())]),
+        ("psq", 300, eager, ["--pmc"] + MFMA, decode),
         ("pf", 300, eager, ["--pmc", "FETCH_SIZE"], decode),
         ("pw", 300, eager, ["--pmc", "WRITE_SIZE"], decode),
         ("cf", 120, {}, ["--pmc", "FETCH_SIZE"], py + ["--copy-calibration"]),
@@ -86,6 +90,7 @@ def command_text(name, env, opts, prog):
 
 
 def run(out):
+    out = os.path.abspath(out)  # (the passes run from /tmp)
     os.makedirs(out, exist_ok=True)
     with open(os.path.join(out, "sources_hash"), "w") as f:
         f.write(sources_hash() + "\n")
@@ -248,15 +253,18 @@ def summarize(out):
     if lc:
         k3e, k3 = lc["classes_at_end"]["k3"]["avg_us"], live["decode_step"]["unfused_classes"]["k3"]["avg_us"]
         md += ["", f"Config 4 (2048-token prompt, 512 tokens, ctx 4096), live: prefill {lc['prefill_tok_s']} tok/s, "
-               f"decode {lc['decode_tok_s']} tok/s; at the last position the split attention kernel "
+               f"decode {lc['decode_tok_s']} tok/s (the fused pass's long form: "
+               f"{lc.get('decode_step_at_end', {}).get('pass', {}).get('avg_us', '-')} us per launch at the last "
+               f"positions); one launch per phase (the fallback) at the last position: the split attention kernel "
                f"{lc['attention_at_end']['avg_us']} us for {lc['attention_at_end']['kv_bytes']} KV bytes "
                f"({lc['attention_at_end']['gbps']} GB/s); its chunks are merged in the output projection's prologue, "
                f"K3 {k3e} us there against {k3} us at config 3. Traced decode attention kernels and the merging "
-               "K3 (prologue argument 4 + 8 (chunks / 2 - 1)) of the run:", "",
+               "K3 (prologue argument 4 + 8 (chunks / 2 - 1)), and the fused pass's long form, of the run:", "",
                "| symbol | grid | launches | median us | mean |", "|---|---|---|---|---|"]
         for (n, gx, gy), v in sorted(by.items(), key=lambda kv: -sum(kv[1])):
             mk3 = re.match(r"gemv_kernel<\w+, 1, (\d+), 1, 2>", n)
-            if (n.startswith("attn_kernel") and "true, false, false" in n) or (mk3 and int(mk3.group(1)) >= 4):
+            if (n.startswith("attn_kernel") and "true, false, false" in n) or (mk3 and int(mk3.group(1)) >= 4) or \
+                    (n.startswith("pass_kernel") and n.endswith("true>")):
                 st = stats(v)
                 md.append(f"| `{n}` | {gx // gy}x{gy} | {st['n']} | {st['median']:.2f} | {st['mean']:.2f} |")
     write(os.path.join(PROFILES, "decode_kernels_qwen25.md"), md)
@@ -298,6 +306,45 @@ def summarize(out):
           "sources_hash matches the tree it runs from; duration_us: the kernel trace's median, above):",
           f"sources_hash {h}"] + machine + machine_d
     write(os.path.join(PROFILES, "pmc_decode_qwen25.txt"), t)
+
+    # MFMA utilisation of the prefill kernels (and the decode launches)
+    ms = counters(os.path.join(out, "psq", "run_counter_collection.csv"))
+    mu = ["# MFMA utilisation per kernel, Qwen2.5-0.5B shape (BASELINE config 3), one MI355X", "",
+          f"Sources `{h}`. Command (direct launches, one counter pass):", "", "```"]
+    for name, limit, env, opts, prog in passes(out):
+        if name == "psq":
+            mu.append(command_text(name, env, opts, prog))
+    mu += ["```", "",
+           "`MfmaUtil` is rocprofv3's derived counter: SQ_VALU_MFMA_BUSY_CYCLES summed over the SIMDs over "
+           "(GRBM_GUI_ACTIVE x the SIMDs) x 100, for the dispatch alone (counter collection runs one dispatch at a "
+           "time). Medians per dispatch of each kernel and grid (grid = threads); the prefill pair of a 64-token "
+           "chunk is prep_kernel (activation staging) + gemm_kernel; attn_mma_kernel is the chunk's attention.", "",
+           "| kernel | grid | dispatches | MfmaUtil % | SQ_INSTS_MFMA | SQ_INSTS_VALU | MFMA / VALU |",
+           "|---|---|---|---|---|---|---|"]
+    machine_m = []
+    rows_m = []
+    for (k, g), v in ms.items():
+        if not any(x in k for x in ("gemm_kernel", "prep_kernel", "attn_mma", "attn_multi", "pass_kernel",
+                                    "gemv_stream_kernel")):
+            continue
+        if "MfmaUtil" not in v:
+            continue
+        n = len(v["MfmaUtil"])
+        util = statistics.median(v["MfmaUtil"])
+        im = statistics.median(v.get("SQ_INSTS_MFMA", [0]))
+        iv = statistics.median(v.get("SQ_INSTS_VALU", [0]))
+        rows_m.append((k, g, n, util, im, iv))
+    for k, g, n, util, im, iv in sorted(rows_m, key=lambda r: (-r[2], r[0])):
+        mu.append(f"| `{k}` | {g} | {n} | {util:.2f} | {im:.0f} | {iv:.0f} | {im / iv if iv else 0:.3f} |")
+        machine_m.append(f"mfma_util {k.replace(' ', '')}@{g} {util:.3f}")
+    gm = [r for r in rows_m if r[0].startswith("gemm_kernel")]
+    if gm:
+        wsum = sum(r[3] * r[2] for r in gm) / sum(r[2] for r in gm)
+        mu += ["", f"Prefill products (every gemm_kernel dispatch, dispatch-weighted mean): {wsum:.2f}% MFMA busy."]
+        machine_m.append(f"prefill_gemm_mfma_util {wsum:.3f}")
+    mu += ["", "Machine-readable (bench.py reads prefill_gemm_mfma_util when sources_hash matches):",
+           f"sources_hash {h}"] + machine_m
+    write(os.path.join(PROFILES, "mfma_util_qwen25.md"), mu)
 
     # config-1 sweep: live graph replays beside the traced durations
     srows = trace_rows(os.path.join(out, "ktsweep", "run_kernel_trace.csv"))

@@ -34,7 +34,8 @@ def test_figures_only_for_matching_sources(tmp_path, monkeypatch):
 
 
 def test_committed_summaries_name_their_sources():
-    for name in ("decode_kernels_qwen25.md", "pmc_decode_qwen25.txt", "gemv_sweep_config1.md", "gemv_q40_vocab.md"):
+    for name in ("decode_kernels_qwen25.md", "pmc_decode_qwen25.txt", "gemv_sweep_config1.md", "gemv_q40_vocab.md",
+                 "mfma_util_qwen25.md"):
         text = open(os.path.join(ROOT, "profiles", name)).read()
         assert "ources" in text and "rocprofv3" in text, name
 
