@@ -252,9 +252,11 @@ LLMHIP_API int llmhip_model_set_exact_ggml(llmhip_model* m, int on);
  * results to each other through flag-carrying words instead of kernel
  * boundaries (3 dispatches per token with the head and the sampling kernel,
  * against five per layer in the reference, fused.go:259-265).  Taken by every
- * decode step of a model that fits it (finalize decides: one-chunk attention,
+ * decode step of a model that fits it (finalize decides: head size 64 or 128,
  * embedding <= 1024, feed-forward <= 6144, fused QKV and gate/up groups, f32
- * activations), else the steps run one launch per kernel; results agree with
+ * activations; positions past 256 (head size 64) while 16 chunks of 256 rows
+ * of every query head fit the grid, past 128 (head size 128) never), else the
+ * steps run one launch per kernel; results agree with
  * the CPU path within the same bounds either way.  on = 0 turns it off, 1 on;
  * poll_limit > 0 makes a hand-off wait give up after that many polls (0: the
  * default, about a second), after which the decode call fails with
