@@ -872,42 +872,115 @@ __device__ __forceinline__ void group_pre(const WUnit& u, uint32_t g, const h8* 
   }
 }
 
-// group_pre with the four blocks' MFMAs chained through one accumulator:
-// xa[j] holds block j's hi and lo in slots 2j and 2j + 1 (zero elsewhere),
-// so block j's sums land in those slots and lane (r, q) holds blocks 2q and
-// 2q + 1 of row r (q < 2; lanes of q >= 2 hold zeros).  The scales follow:
-// one add and one FMA per pair of blocks instead of per block.  The row's
-// total is split between lanes q = 0 and 1 (added at the tile's end).
+// ---- the streaming kernel's products on the integer matrix cores
+// (v_mfma_i32_16x16x64_i8; f32 activations, k = 896: seven groups per tile).
+// The staged activation x_s = hi + lo (stage_x_from: max |x_s| in
+// [2^14, 2^15)) becomes the integer x_i = round(128 x_s) (|x_i| < 2^22) and
+// three balanced int8 digits, x_i = a 2^16 + b 2^8 + c, b and c in
+// [-128, 127], a in [-65, 65].  The weights enter as int8 (Q8_0 as stored;
+// Q4_0 and Q4_1 nibbles masked out of the lane's words: element 4q + i of a
+// block in the low nibble of byte i of word q, element 16 + 4q + i in its high
+// nibble).  One MFMA takes two blocks of a group: lane (r, q) holds 8 weights
+// of each (16 k-slots), and A row 4j + p holds digit p of block j's
+// activations at block j's slots (zero elsewhere), so after the group's two
+// MFMAs lane (r, q) holds block q's three digit sums of row r, each exact in
+// i32.  Per block: D_p - 8 S_p (Q4_0's offset of 8, with S_p the block's sum
+// of digits p: exact in integers), the digits recombined in f32, times the
+// block's scale d; Q4_1 adds m sum(x).  The products are exact; the roundings
+// are x_i's (2^-23 of the row's largest |x|) and the f32 sums.
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// LDS bytes the integer form adds to the streaming kernel's layout: the
+// digits (per block, digit and k-group: 8 bytes) and the per-block offsets.
+__host__ __device__ constexpr uint32_t i8_lds_bytes(uint32_t nb) { return nb * (3 * 4 * 8 + 16); }
+
+// The digits of the staged items, by the whole workgroup (one thread per
+// item: a block's four items on four consecutive lanes), into dg[(b 3 + p) 4 + q]
+// (8 bytes: the item's elements in the order of the lane's int8 weights) and
+// tb[b] = (8 S_0, 8 S_1, 8 S_2, 0) for Q4_0 (zeros for the other types).  Ends
+// with a barrier.
 template <uint32_t QT>
-__device__ __forceinline__ void group_chain(const WUnit& u, uint32_t g, const h8* xa, const float* bsum,
-                                            const Dq4K& K, int q, float& acc) {
-  h8 B[4];
-  if (QT == LLMHIP_Q8_0) {
-    B[0] = dq8(u.w0.x, u.w0.y);
-    B[1] = dq8(u.w0.z, u.w0.w);
-    B[2] = dq8(u.w1.x, u.w1.y);
-    B[3] = dq8(u.w1.z, u.w1.w);
-  } else {
-    B[0] = dq4k<QT == LLMHIP_Q4_1>(u.w0.x, K);
-    B[1] = dq4k<QT == LLMHIP_Q4_1>(u.w0.y, K);
-    B[2] = dq4k<QT == LLMHIP_Q4_1>(u.w0.z, K);
-    B[3] = dq4k<QT == LLMHIP_Q4_1>(u.w0.w, K);
-  }
-  f4 D = {0, 0, 0, 0};
+__device__ __forceinline__ void stage_digits(const h8* xs, uint32_t nb, uint64_t* dg, i32x4* tb) {
+  const uint32_t NI = nb * 4;
+  for (uint32_t i0 = 0; i0 < NI; i0 += blockDim.x) {
+    const uint32_t it = i0 + threadIdx.x, ic = min(it, NI - 1);
+    const h8 hi = xs[2 * ic], lo = xs[2 * ic + 1];
+    // item order (stage_x_from): e(4q), e(4q+2), e(16+4q), e(16+4q+2), e(4q+1), e(4q+3), e(16+4q+1), e(16+4q+3);
+    // the int8 weights' order: Q4 e(4q..4q+3), e(16+4q..16+4q+3); Q8_0 the repacked bytes
+    // e(4q), e(16+4q), e(4q+2), e(16+4q+2), e(4q+1), e(16+4q+1), e(4q+3), e(16+4q+3)
+    constexpr int O4[8] = {0, 4, 1, 5, 2, 6, 3, 7}, O8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    uint32_t w[3][2] = {{0, 0}, {0, 0}, {0, 0}};
+    int sd[3] = {0, 0, 0};
 #pragma unroll
-  for (int j = 0; j < 4; j++) D = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], B[j], D, 0, 0, 0);
-  const bool hi = (q & 1) != 0;
-  if (QT == LLMHIP_Q4_1) {  // d, m of blocks 2q and 2q + 1
-    const uint32_t s0 = hi ? u.sv.z : u.sv.x, s1 = hi ? u.sv.w : u.sv.y;
-    const uint32_t b0 = 4 * g + 2 * (q & 1);
-    acc = fmaf(f16_hw(s0 & 0xffff), D[0] + D[1], acc);
-    acc = fmaf(f16_hw(s1 & 0xffff), D[2] + D[3], acc);
-    acc = fmaf(f16_hw(s0 >> 16), bsum[b0], acc);
-    acc = fmaf(f16_hw(s1 >> 16), bsum[b0 + 1], acc);
-  } else {  // d of blocks 2q and 2q + 1 in one word
-    const uint32_t sw = hi ? u.sv.y : u.sv.x;
-    acc = fmaf(f16_hw(sw & 0xffff), D[0] + D[1], acc);
-    acc = fmaf(f16_hw(sw >> 16), D[2] + D[3], acc);
+    for (int i = 0; i < 8; i++) {
+      const int e = QT == LLMHIP_Q8_0 ? O8[i] : O4[i];
+      const int v = (int)rintf(((float)hi[e] + (float)lo[e]) * 128.f);
+      const int c = (int)(int8_t)(v & 0xff), t = (v - c) >> 8;
+      const int b = (int)(int8_t)(t & 0xff), a = (t - b) >> 8;
+      const int dgt[3] = {a, b, c};
+#pragma unroll
+      for (int p = 0; p < 3; p++) {
+        w[p][i / 4] |= (uint32_t)(dgt[p] & 0xff) << (8 * (i % 4));
+        sd[p] += dgt[p];
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+      sd[p] += __shfl_xor(sd[p], 1);
+      sd[p] += __shfl_xor(sd[p], 2);
+    }
+    if (it < NI) {
+      const uint32_t blk = it / 4, q = it % 4;
+#pragma unroll
+      for (int p = 0; p < 3; p++) dg[(blk * 3 + p) * 4 + q] = (uint64_t)w[p][0] | (uint64_t)w[p][1] << 32;
+      if (q == 0)
+        tb[blk] = QT == LLMHIP_Q4_0 ? i32x4{8 * sd[0], 8 * sd[1], 8 * sd[2], 0} : i32x4{0, 0, 0, 0};
+    }
+  }
+  __syncthreads();
+}
+
+// Lane (m, kq)'s A operands of group g's two MFMAs: row m = 4 j + p holds
+// digit p (< 3) of block 4 g + j at block j's k-slots (MFMA j / 2, its
+// 8-byte half j % 2), zero elsewhere.
+__device__ __forceinline__ void i8_operands(const uint64_t* dg, uint32_t g, int lane, i32x4 (&xa)[2]) {
+  const uint32_t m = lane & 15, kq = lane >> 4, j = m / 4, p = m % 4;
+  const uint64_t v = dg[((4 * g + j) * 3 + min(p, 2u)) * 4 + kq];
+  const int32_t lo = p < 3 ? (int32_t)(uint32_t)v : 0, hi = p < 3 ? (int32_t)(uint32_t)(v >> 32) : 0;
+#pragma unroll
+  for (uint32_t h = 0; h < 2; h++) {
+    const bool use = j / 2 == h;
+    xa[h] = (j % 2 == 0) ? i32x4{use ? lo : 0, use ? hi : 0, 0, 0} : i32x4{0, 0, use ? lo : 0, use ? hi : 0};
+  }
+}
+
+// One group of a tile on the integer matrix cores: acc (lane (r, q)) +=
+// block 4 g + q's product for row r, times 2^(ex + 7).  T: that block's
+// offsets (tb), bsq: Q4_1's 128 sum(x_s) of the block.
+template <uint32_t QT>
+__device__ __forceinline__ void group_i8(const WUnit& u, const i32x4 (&xa)[2], const i32x4& T, float bsq, int q,
+                                         float& acc) {
+  i32x4 B0, B1;
+  if (QT == LLMHIP_Q8_0) {
+    B0 = __builtin_bit_cast(i32x4, u.w0);
+    B1 = __builtin_bit_cast(i32x4, u.w1);
+  } else {
+    auto lo = [](uint32_t w) { return (int32_t)(w & 0x0F0F0F0Fu); };
+    auto hi = [](uint32_t w) { return (int32_t)((w >> 4) & 0x0F0F0F0Fu); };
+    B0 = i32x4{lo(u.w0.x), hi(u.w0.x), lo(u.w0.y), hi(u.w0.y)};
+    B1 = i32x4{lo(u.w0.z), hi(u.w0.z), lo(u.w0.w), hi(u.w0.w)};
+  }
+  i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[0], B0, i32x4{0, 0, 0, 0}, 0, 0, 0);
+  D = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[1], B1, D, 0, 0, 0);
+  const float t = fmaf((float)(D[0] - T[0]), 65536.f, fmaf((float)(D[1] - T[1]), 256.f, (float)(D[2] - T[2])));
+  if (QT == LLMHIP_Q4_1) {  // (d, m) of block q
+    const uint32_t sw = q == 0 ? u.sv.x : q == 1 ? u.sv.y : q == 2 ? u.sv.z : u.sv.w;
+    acc = fmaf(f16_hw(sw & 0xffff), t, acc);
+    acc = fmaf(f16_hw(sw >> 16), bsq, acc);
+  } else {  // d of blocks 0, 1 in sv.x, of 2, 3 in sv.y
+    const uint32_t sw = q < 2 ? u.sv.x : u.sv.y;
+    acc = fmaf(f16_hw((q & 1) ? sw >> 16 : sw & 0xffff), t, acc);
   }
 }
 
@@ -982,8 +1055,11 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
   // the row epilogue of the wave's tile j (argmax partials in bv / bi)
   auto finish = [&](uint32_t j) {
     const uint32_t tile = gw + j * W;
-    if (NG > 0 && !Q8) acc0 += __shfl_xor(acc0, 16);  // group_chain: lanes q = 0 and 1 hold halves
-    const float v = q == 0 ? ldexpf(acc0, -ex[0]) : 0.f;
+    if (NG > 0 && !Q8) {  // group_i8: lane (r, q) holds block q of every group, times 2^7 more
+      acc0 += __shfl_xor(acc0, 16);
+      acc0 += __shfl_xor(acc0, 32);
+    }
+    const float v = q == 0 ? ldexpf(acc0, -ex[0] - (NG > 0 && !Q8 ? 7 : 0)) : 0.f;
     row_epilogue<EPI>(a, tile, r, true, 0, q == 0, v, 1, false, 0.f);
     if (EPI == EPI_ARGMAX) {
       const uint32_t lr = row_of_pos(tile * 16 + r, a.map, a.map_hd, a.map_seg0, a.map_seg1, a.ff);
@@ -1018,19 +1094,20 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
       for (int g = 0; g < NG; g++) load_group<QT, true, false>(wt[g], a.qs, nb, t0, g, lane, r, gw < a.tiles);
     }
     stage_x_from<QT, 1, PRO>(a, 1, xi, xs, misc, bsum, dxs, ex);
-    // f32 activations: every block's MFMA operand read from LDS and masked
-    // once, into registers
-    constexpr int NX = Q8 ? 1 : 4 * NGX;
-    h8 xa[NX];
-    const Dq4K K = dq4_consts();
-    if (!Q8) {  // block b in slots 2 (b % 4) and 2 (b % 4) + 1 (group_chain)
-      typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    // f32 activations: the integer form's digits staged once per workgroup,
+    // each wave's A operands and per-block offsets in registers
+    constexpr int NX = Q8 ? 1 : NGX;
+    i32x4 xa[NX][2], tq[NX];
+    float bq[NX];
+    if (!Q8) {
+      uint64_t* dg = (uint64_t*)(lds + L.total);
+      i32x4* tb = (i32x4*)(lds + L.total + 96 * nb);
+      stage_digits<QT>(xs, nb, dg, tb);
 #pragma unroll
-      for (int b = 0; b < NX; b++) {
-        const int sl = slot - 2 * (b % 4);
-        const bool in = sl == 0 || sl == 1;
-        const u4v X = __builtin_bit_cast(u4v, xs[(b * 4 + q) * 2 + (in ? sl : 0)]);
-        xa[b] = __builtin_bit_cast(h8, X & (in ? ~0u : 0u));
+      for (int g = 0; g < NX; g++) {
+        i8_operands(dg, g, lane, xa[g]);
+        tq[g] = tb[4 * g + q];
+        bq[g] = QT == LLMHIP_Q4_1 ? 128.f * bsum[4 * g + q] : 0.f;
       }
     }
     for (uint32_t j = 0; j < ntw; j++) {
@@ -1048,7 +1125,7 @@ __global__ __launch_bounds__(512) void gemv_stream_kernel(GemvArgs a) {
         if (Q8)
           group_mfma<QT, 1, Q8>(wt[g], g, xs, bsum, dxs, nb, q, slot, acc0, acc1);
         else
-          group_chain<QT>(wt[g], g, xa + 4 * g, bsum, K, q, acc0);
+          group_i8<QT>(wt[g], xa[g], tq[g], bq[g], q, acc0);
         // the slot's last use before its refill, and the refill issued there:
         // no register copy of a load still in flight (the empty asm keeps the
         // scaled sums from sinking into the epilogue)
@@ -2057,7 +2134,10 @@ static int launch_stream(const GemvArgs& a, hipStream_t s) {
   const Lds L = lds_layout(1, QT, a.nb, a.swaves, (PRO & PRO_Q8) != 0);
   const dim3 g(a.stream), b(64 * a.swaves);
   switch (a.ng) {  // a whole tile in flight per wave where its groups fit the registers
-    case 7: hipLaunchKernelGGL((gemv_stream_kernel<QT, PRO, EPI, 7>), g, b, L.total, s, a); break;
+    case 7:  // (f32 activations: the integer form's digits after the layout)
+      hipLaunchKernelGGL((gemv_stream_kernel<QT, PRO, EPI, 7>), g, b,
+                         L.total + ((PRO & PRO_Q8) ? 0 : i8_lds_bytes(a.nb)), s, a);
+      break;
     default: hipLaunchKernelGGL((gemv_stream_kernel<QT, PRO, EPI, 0>), g, b, L.total, s, a);
   }
   LLM_HIP(hipGetLastError());
