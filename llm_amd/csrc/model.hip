@@ -1109,7 +1109,7 @@ static int pass_setup(Model& m) {
   a.llq = m.ll;                                        // [E + 2 kvd]
   a.llo = a.llq + E + 2ull * m.kvd;                    // [np][E], [np][heads][16], then [E]
   a.llb = a.llo + a.np * (E + 16ull * c.heads) + E;    // [1 + kp][E]
-  a.llact = a.llb + (1 + kp) * E;                      // [ff]
+  a.llact = a.llb + (1 + kp) * E;                      // [pass_act_words(ff)]
   (void)F;
   a.kp = kp;
   a.ctrl = m.pctrl;

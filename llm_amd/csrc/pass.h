@@ -41,7 +41,7 @@ struct PassArgs {
                     // their max scores and sums of e (m, l, m, l, ...), then [E] the attention's output (K2)
   uint64_t* llb;    // [1 + kp][E]: x after the attention (K3), then the down projection's k-parts (K5);
                     // x after the layer is their sum
-  uint64_t* llact;  // [ff]: the SwiGLU activations (K4)
+  uint64_t* llact;  // [pass_act_words(ff)]: the SwiGLU activations (K4), 8 in every 16 words
   uint32_t* ctrl;   // [0] epoch, [1] timed-out waits, [2] poll limit
   const uint32_t* state;
   const float* cs;  // RoPE table
@@ -74,11 +74,15 @@ inline uint32_t pass_partials(const llmhip_config& c, uint32_t ctx) {
   if (c.head_dim != 64 || ctx <= 256) return 1;
   return std::min((ctx + PASS_LONG_ROWS - 1) / PASS_LONG_ROWS, PASS_LONG_CHUNKS) - 1;
 }
+// Words of the activations (PassArgs::llact): each gate/up tile's 8 in a line
+// of 16 words, whose other 8 carry the tile's up rows, so that every store of
+// the phase covers a whole line.
+inline uint64_t pass_act_words(uint64_t ff) { return 16 * ((ff + 7) / 8); }
 // Flag-carrying words a model's pass needs (PassArgs: llq, llo with np
 // chunks' partial sums, llb with the most k-parts, llact).
 inline uint64_t pass_words(const llmhip_config& c, uint32_t kvd, uint32_t np) {
   const uint64_t E = (uint64_t)c.embd;
-  return E + 2ull * kvd + np * (E + 16ull * (uint64_t)c.heads) + E + (1 + PASS_MAX_KP) * E + (uint64_t)c.ff;
+  return E + 2ull * kvd + np * (E + 16ull * (uint64_t)c.heads) + E + (1 + PASS_MAX_KP) * E + pass_act_words((uint64_t)c.ff);
 }
 // Whether a launch whose attention reads `rows` cache rows past
 // attn_full_max fits the long form on `grid` workgroups (head size 64, a

@@ -82,18 +82,19 @@ __device__ __forceinline__ void ll_wait_f(At at, Need need, uint32_t flag, float
   for (int i = 0; i < N; i++) v[i] = __uint_as_float((uint32_t)x[i]);
 }
 
-// ll_wait_f preceded by a gate: the wave's first lane polls its first word
-// alone until it carries the flag.  A workgroup that reaches a phase long
+// ll_wait_f preceded by a gate: the wave's first lane polls its word `gate`
+// alone until it carries the flag (a word of the input's last producers).  A workgroup that reaches a phase long
 // before the phase's input is produced then waits with one load in flight
 // per wave instead of its whole input's, which leaves the memory system to
 // the phases still running.
 template <int N, class At, class Need>
-__device__ __forceinline__ void ll_wait_gated(At at, Need need, uint32_t flag, float (&v)[N], Waiter& w) {
-  const bool g = (threadIdx.x & 63) == 0 && need(0);
+__device__ __forceinline__ void ll_wait_gated(At at, Need need, uint32_t flag, float (&v)[N], Waiter& w,
+                                              int gate = 0) {
+  const bool g = (threadIdx.x & 63) == 0 && need(gate);
   uint32_t spins = 0;
   for (;;) {
     bool ok = true;
-    if (g && !w.dead) ok = (uint32_t)(ll_load(at(0)) >> 32) == flag;
+    if (g && !w.dead) ok = (uint32_t)(ll_load(at(gate)) >> 32) == flag;
     if (__all(ok)) break;
     if (++spins > w.limit) {  // (spins: the same in every lane)
       if (!w.dead) atomicOr(w.err, 1u);
@@ -107,8 +108,9 @@ __device__ __forceinline__ void ll_wait_gated(At at, Need need, uint32_t flag, f
 
 // ll_wait_gated or, where the input is expected soon, ll_wait_f.
 template <int N, class At, class Need>
-__device__ __forceinline__ void ll_wait_row(bool gate, At at, Need need, uint32_t flag, float (&v)[N], Waiter& w) {
-  if (gate) ll_wait_gated<N>(at, need, flag, v, w);
+__device__ __forceinline__ void ll_wait_row(bool gate, At at, Need need, uint32_t flag, float (&v)[N], Waiter& w,
+                                            int gate_word = 0) {
+  if (gate) ll_wait_gated<N>(at, need, flag, v, w, gate_word);
   else ll_wait_f<N>(at, need, flag, v, w);
 }
 
@@ -186,8 +188,10 @@ __device__ __forceinline__ void load_row(const StageIn& in, uint32_t base, uint3
     float u[NW * NP];
     // word i: vector i / NW (xb, then the parts), element tid + T (i % NW)
     const uint64_t* p = in.ll + tid;
+    // (the gate: the wave's word of the last k-part, whose producers finish last)
     ll_wait_row<NW * NP>(in.gate, [&](int i) { return p + (i / NW) * in.E + T * (i % NW); },
-                       [&](int i) { return (uint32_t)(i / NW) <= in.kp && tid + T * (i % NW) < n; }, in.flag, u, w);
+                         [&](int i) { return (uint32_t)(i / NW) <= in.kp && tid + T * (i % NW) < n; }, in.flag, u, w,
+                         (int)(in.kp * NW));
 #pragma unroll
     for (uint32_t k = 0; k < NW; k++) {
       float x = u[k];
@@ -318,16 +322,19 @@ __device__ __forceinline__ int stage_ops(PassLds<HD>& L, const StageIn& in, uint
 // [2^14, 2^15)).  A wave whose input is in starts its products while the
 // others still wait; each wave scales its sums back by 2^-ex (exact) before
 // the waves' sums are added.  Returns the wave's ex.
-template <int MU, uint32_t HD>
+template <int MU, bool ACT, uint32_t HD>
 __device__ __forceinline__ int stage_wave(PassLds<HD>& L, const StageIn& in, uint32_t nb0, uint32_t nb, uint32_t u0,
                                           uint32_t u1, Waiter& w, uint32_t wave, uint32_t lane) {
   const uint32_t n = nb * 32;
-  const uint64_t* p = in.ll + 32 * nb0;
   // word j: element 128 (u - u0) + 64 (j % 2) + lane of unit u = u0 + wave + 8 (j / 2)
   auto el = [&](int j) { return 128 * (wave + PASS_WAVES * (j / 2)) + 64 * (j % 2) + lane; };
   auto need = [&](int j) { return u0 + wave + PASS_WAVES * (j / 2) < u1 && el(j) < n; };
+  auto at = [&](int j) {
+    const uint32_t e = 32 * nb0 + el(j);
+    return in.ll + (ACT ? e + (e & ~7u) : e);  // ACT: 8 of every 16 words
+  };
   float v[2 * MU];
-  ll_wait_row<2 * MU>(in.gate, [&](int j) { return p + el(j); }, need, in.flag, v, w);
+  ll_wait_row<2 * MU>(in.gate, at, need, in.flag, v, w);
   float mx = 0;
 #pragma unroll
   for (int j = 0; j < 2 * MU; j++) {
@@ -839,7 +846,7 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       in.gate = true;
       UnitsB<1, 1> ub;
       units_deq_any<Q8, 1, 1>(w3, M, 0, wave, ub);
-      const int ex = stage_wave<1>(L, in, 0, M.nb, 0, U, wt, wave, lane);
+      const int ex = stage_wave<1, false>(L, in, 0, M.nb, 0, U, wt, wave, lane);
       float acc[1] = {0};
       units_mac_any<Q8, 1, 1>(ub, M, L.xs, L.bsum, 0, U, wave, lane, acc);
       acc[0] = ldexpf(acc[0], -ex);
@@ -893,13 +900,14 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
           // gate row i at lane r < 8, up row i at r + 8 (MAP_GATEUP)
           const float u = __shfl_xor(v, 8);
           const uint32_t i = 8 * tile + (r & 7);
-          if (q == 0 && i < a.ff) {
-            if (r < 8) {
-              const float act = v / (1.f + __expf(-v)) * u;  // cpu.go:345
-              ll_store(llact + i, act, F);
-              if (last) a.act[i] = act;
-            } else if (last) {
-              a.up[i] = v;
+          if (q == 0) {
+            // the tile's 8 activations and, as padding, its 8 up rows: one
+            // whole line of 16 words (pass_act_words)
+            const float act = r < 8 ? v / (1.f + __expf(-v)) * u : v;  // cpu.go:345
+            ll_store(llact + 16 * tile + r, act, F);
+            if (last && i < a.ff) {
+              if (r < 8) a.act[i] = act;
+              else a.up[i] = v;
             }
           }
         }
@@ -918,13 +926,13 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       PHASE_IDS;
       const PassMat M = cmat(&Y->down);
       StageIn in{};
-      in.ll = llact;
+      in.ll = llact;  // (8 of every 16 words: pass_act_words)
       in.flag = F;
       in.gate = false;  // every K5 workgroup comes straight from its K4 work
       const uint32_t nb0 = 4 * u50, nbp = min(4 * u51, M.nb) - nb0;
       UnitsB<1, PASS_K5_UNITS> ub;
       units_deq_any<Q8, 1, PASS_K5_UNITS>(w5, M, u50, wave, ub);
-      const int ex = stage_wave<PASS_K5_UNITS>(L, in, nb0, nbp, u50, u51, wt, wave, lane);
+      const int ex = stage_wave<PASS_K5_UNITS, true>(L, in, nb0, nbp, u50, u51, wt, wave, lane);
       float acc[1] = {0};
       units_mac_any<Q8, 1, PASS_K5_UNITS>(ub, M, L.xs, L.bsum, u50, u51, wave, lane, acc);
       acc[0] = ldexpf(acc[0], -ex);
