@@ -267,7 +267,8 @@ LLMHIP_API int llmhip_model_set_fused(llmhip_model* m, int on, uint32_t poll_lim
 /* Run only the first `layers` layers (no head, no sampling; Layers, gpu.go:143-146). 0 = all. */
 LLMHIP_API int llmhip_model_set_layers(llmhip_model* m, int layers);
 /* Leave kernel classes out of every pass, comma-separated (Skip, gpu.go:769-784):
- * embed, k1, k2, k3, k4, k5, head, argmax, adv, or all.  Output is garbage then. */
+ * embed, k1, k2, k3, k4, k5, head, argmax, adv, or all; a prefill chunk's activation
+ * staging for k1, k3, k4 and k5 also as p1, p3, p4 and p5.  Output is garbage then. */
 LLMHIP_API int llmhip_model_set_skip(llmhip_model* m, const char* classes);
 /* Average device microseconds of one launch of a kernel of the decode step,
  * launched `iters` times back-to-back on the model's stream between hipEvents

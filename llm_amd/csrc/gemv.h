@@ -108,30 +108,39 @@ struct GemvArgs {
   uint32_t msmax, mrows;
   float* matt;
   // prefill (gemm_kernel): activations prepared once per launch by prep_kernel
-  void* xp;        // [tg][nb][64 lanes] 16-byte MFMA operands (hi/lo f16 of 8 tokens)
-  int32_t* xexp;   // [tg*8] power-of-two scale per token
-  float* xbsum;    // [tg*8][nb] scaled block sums (Q4_1); PRO_Q8: the Q8_1 sums s
-  float* xdx;      // [tg*8][nb] PRO_Q8: the activation block scales d (binary16 values)
-  uint32_t tg;     // token groups of 8
+  void* xp;        // [tg][nb][2][64 lanes] 16-byte MFMA operands: group g, block b, part h (0: the f16 hi
+                   // parts, 1: lo), lane l: token 16 g + l % 16, k-group l / 16 of the block
+  int32_t* xexp;   // [tg*16] power-of-two scale per token
+  float* xbsum;    // [tg*16][nb] scaled block sums (Q4_1); PRO_Q8: the Q8_1 sums s
+  float* xdx;      // [tg*16][nb] PRO_Q8: the activation block scales d (binary16 values)
+  uint32_t tg;     // token groups of 16
   uint32_t q8;     // the prepared activations are Q8 blocks (PRO_Q8): gemm_kernel's block products
+  // EPI_GATEUP (gemm_kernel): the activations also as the down projection's
+  // block-scaled operands (op_xp in the layout of xp, op_nb blocks per token;
+  // per token and block op_dx = 2^-e, op_bsum = the block's sum; op_exp = 0),
+  // so that no staging launch runs between the two products (null: not)
+  void* op_xp;
+  float *op_dx, *op_bsum;
+  int32_t* op_exp;
+  uint32_t op_nb;
 };
 
 // Bytes of the prepared-activation buffers for ntok tokens of k inputs
 // (room for xprep_bind's rounding of each part to 256 bytes included).
 constexpr uint64_t xprep_bytes(uint32_t ntok, uint32_t k) {
-  return ((uint64_t)ntok + 7) / 8 * (k / 32) * 64 * 16 + ((uint64_t)ntok + 7) / 8 * 8 * 4 +
-         2 * (((uint64_t)ntok + 7) / 8) * 8 * (k / 32) * 4 + 4 * 256;
+  return ((uint64_t)ntok + 15) / 16 * (k / 32) * 2 * 64 * 16 + ((uint64_t)ntok + 15) / 16 * 16 * 4 +
+         2 * (((uint64_t)ntok + 15) / 16) * 16 * (k / 32) * 4 + 4 * 256;
 }
 // Point a.xp / a.xexp / a.xbsum / a.xdx into one buffer of xprep_bytes.
 inline void xprep_bind(GemvArgs* a, void* buf) {
-  uint64_t tg = (a->ntok + 7) / 8, nb = a->nb;
+  uint64_t tg = (a->ntok + 15) / 16, nb = a->nb;
   char* p = (char*)buf;
   a->xp = p;
-  p += (tg * nb * 64 * 16 + 255) & ~255ull;
+  p += (tg * nb * 2 * 64 * 16 + 255) & ~255ull;
   a->xexp = (int32_t*)p;
-  p += (tg * 8 * 4 + 255) & ~255ull;
+  p += (tg * 16 * 4 + 255) & ~255ull;
   a->xbsum = (float*)p;
-  p += (tg * 8 * nb * 4 + 255) & ~255ull;
+  p += (tg * 16 * nb * 4 + 255) & ~255ull;
   a->xdx = (float*)p;
   a->tg = (uint32_t)tg;
 }

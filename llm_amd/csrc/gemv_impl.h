@@ -1176,23 +1176,25 @@ constexpr int PMAXI = 4;  // items per thread in prep_kernel: k <= 32 * 4 * 256
 
 // One workgroup per token slot: the prologue of the decode kernel for one
 // token (plain, RMSNorm, or the attention merge), written once to global
-// memory in MFMA operand order for every workgroup of gemm_kernel.  Slots
-// past ntok (up to a whole group of 8) are zero.
+// memory in MFMA operand order for every workgroup of gemm_kernel: item it
+// (block it / 4, k-group it % 4) of token t is the operand of lane
+// 16 (it % 4) + t % 16 in group t / 16, its f16 hi parts in the block's first
+// 64 operands, its lo parts in the next 64.  Slots past ntok (up to a whole
+// group of 16) are zero.
 template <int PRO>
 __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a_in) {
-  extern __shared__ __attribute__((aligned(16))) float pl[];
+  __shared__ float red[8];  // [0, 4) wave sums of squares, [4, 8) wave maxima
   // the argument lines it reads in one round (as gemv_kernel's touch_args)
   GemvArgs a = a_in;
   asm volatile("" : "+s"(a.rows), "+s"(a.ldx), "+s"(a.msmax), "+s"(a.tg));
   const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const uint32_t nb = a.nb, K = a.k, NI = nb * 4;
   h8* xp = (h8*)a.xp;
-  const uint32_t tg = t / 8, s2 = 2 * (t % 8);
-  float* red = pl;        // [0, 4) wave sums of squares, [4, 8) wave maxima
+  const uint32_t tg = t / 16, slot = t % 16;
   if (t >= a.ntok) {
     for (uint32_t it = tid; it < NI; it += 256) {
-      xp[((uint64_t)tg * nb + it / 4) * 64 + (it % 4) * 16 + s2] = h8{};
-      xp[((uint64_t)tg * nb + it / 4) * 64 + (it % 4) * 16 + s2 + 1] = h8{};
+      xp[((uint64_t)tg * nb + it / 4) * 128 + (it % 4) * 16 + slot] = h8{};
+      xp[((uint64_t)tg * nb + it / 4) * 128 + 64 + (it % 4) * 16 + slot] = h8{};
     }
     for (uint32_t b = tid; b < nb; b += 256) a.xbsum[(uint64_t)t * nb + b] = a.xdx[(uint64_t)t * nb + b] = 0.f;
     if (tid == 0) a.xexp[t] = 0;
@@ -1272,9 +1274,9 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a_in) {
       qs += __shfl_xor(qs, 1);
       qs += __shfl_xor(qs, 2);
       if (it >= NI) continue;
-      h8* dst = xp + ((uint64_t)tg * nb + it / 4) * 64 + (it % 4) * 16 + s2;
+      h8* dst = xp + ((uint64_t)tg * nb + it / 4) * 128 + (it % 4) * 16 + slot;
       dst[0] = hi;
-      dst[1] = h8{};
+      dst[64] = h8{};
       if ((it & 3) == 0) {
         a.xdx[(uint64_t)t * nb + it / 4] = (float)to_f16(d);
         a.xbsum[(uint64_t)t * nb + it / 4] = (float)to_f16(__fmul_rn(d, (float)qs));
@@ -1317,9 +1319,9 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a_in) {
       hi[i] = h;
       lo[i] = (_Float16)(sv - (float)h);
     }
-    h8* dst = xp + ((uint64_t)tg * nb + it / 4) * 64 + (it % 4) * 16 + s2;
+    h8* dst = xp + ((uint64_t)tg * nb + it / 4) * 128 + (it % 4) * 16 + slot;
     dst[0] = hi;
-    dst[1] = lo;
+    dst[64] = lo;
     float sx = (A[0] + A[1] + A[2] + A[3]) + (C[0] + C[1] + C[2] + C[3]);
     sx += __shfl_xor(sx, 1);
     sx += __shfl_xor(sx, 2);
@@ -1327,51 +1329,53 @@ __global__ __launch_bounds__(256) void prep_kernel(GemvArgs a_in) {
   }
 }
 
-// Prefill matrix product.  A workgroup owns GT 16-row tiles and NG token
-// groups of 8 (grid.y walks the groups); its waves split the block groups of
-// k (split-K).  Each wave pipelines its block groups through two register
-// sets: the weights and activation operands of its next group are in flight
-// while the current one goes through the MFMA.  Every load in that loop is
-// unconditional (indices clamped into the matrix and the prepared
-// activations), so the waits count only what is needed.  A weight word is
-// dequantised once and feeds NG MFMAs per tile, an activation operand GT.
-// The waves' partials meet in LDS; wave w then adds, in wave order, the
-// (tile, token group) pairs w, w + waves, ... and runs their row epilogues.
+// Prefill matrix product.  A workgroup owns GT 16-row tiles and one group of
+// 16 tokens (grid.y walks the groups); its waves split the block groups of k
+// (split-K).  Per block and tile, two MFMAs chained in one accumulator give
+// the 16 tokens' products with the block's 16 rows: A = the tokens' f16 hi
+// parts, then A = their lo parts (v_mfma_f32_16x16x32_f16: lane l holds
+// A[l % 16][8 (l / 16) ..], B[8 (l / 16) ..][l % 16] and D[4 (l / 16) + i][l % 16],
+// i < 4: tokens 4 (l / 16) + i of row l % 16), so each lane scales four
+// token sums by the block's d.  Each wave pipelines its block groups through
+// two register sets: the weights and activation operands of its next group
+// are in flight while the current one goes through the MFMA.  Every load in
+// that loop is unconditional (indices clamped into the matrix and the
+// prepared activations), so the waits count only what is needed.  A weight
+// word is dequantised once and feeds both MFMAs of its tile, an activation
+// operand GT tiles.  The waves' partials meet in LDS; wave w then adds, in
+// wave order, rows w, w + waves, ... (row p: tile p / 2, token pair p % 2 of
+// the lane's four) and runs their row epilogues, having loaded the first
+// one's inputs with its first operands.
 constexpr int GEMM_MAXW = 8;  // waves per workgroup
 
-// The activation side of one block group: 4 blocks x NG token groups of MFMA
-// operands, and per token block scalars where the product needs them (Q8: the
-// activation blocks' d; Q4_1: the block sums that meet m).
-template <uint32_t QT, bool Q8, int NG>
+// The activation side of one block group: 4 blocks x (hi, lo) MFMA operands
+// of the workgroup's 16 tokens, and per block the scalars of the lane's four
+// tokens where the product needs them (Q8: the activation blocks' d; Q4_1:
+// the block sums that meet m).
+template <uint32_t QT, bool Q8>
 struct XUnit {
-  h8 x[4][NG];
-  float xd[Q8 ? 4 : 1][Q8 ? NG : 1][2];
-  float xb[QT == LLMHIP_Q4_1 ? 4 : 1][QT == LLMHIP_Q4_1 ? NG : 1][2];
+  h8 x[4][2];
+  float xd[Q8 ? 4 : 1][Q8 ? 4 : 1];
+  float xb[QT == LLMHIP_Q4_1 ? 4 : 1][QT == LLMHIP_Q4_1 ? 4 : 1];
 };
 
-// Blocks b0 .. b0+3 (clamped to bmax) for the token groups g0 .. g0+NG-1
-// (clamped to the last prepared group).
-template <uint32_t QT, bool Q8, int NG>
-__device__ __forceinline__ void load_xunit(XUnit<QT, Q8, NG>& X, const GemvArgs& a, uint32_t b0, uint32_t bmax,
-                                           uint32_t g0, int lane, int q) {
+// Blocks b0 .. b0+3 (clamped to bmax) of token group g.
+template <uint32_t QT, bool Q8>
+__device__ __forceinline__ void load_xunit(XUnit<QT, Q8>& X, const GemvArgs& a, uint32_t b0, uint32_t bmax,
+                                           uint32_t g, int lane, int q) {
   const h8* xp = (const h8*)a.xp;
-  const uint32_t nb = a.nb, gl = a.tg - 1;
+  const uint32_t nb = a.nb;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const uint32_t b = min(b0 + j, bmax);
+    const h8* xb = xp + ((uint64_t)g * nb + b) * 128 + lane;
+    X.x[j][0] = xb[0];
+    X.x[j][1] = xb[64];
 #pragma unroll
-    for (int g = 0; g < NG; g++) {
-      const uint32_t gg = min(g0 + g, gl);
-      X.x[j][g] = xp[((uint64_t)gg * nb + b) * 64 + lane];
-      const uint64_t iA = (uint64_t)(gg * 8 + 2 * q) * nb + b;
-      if (Q8) {
-        X.xd[j][g][0] = a.xdx[iA];
-        X.xd[j][g][1] = a.xdx[iA + nb];
-      }
-      if (QT == LLMHIP_Q4_1) {
-        X.xb[j][g][0] = a.xbsum[iA];
-        X.xb[j][g][1] = a.xbsum[iA + nb];
-      }
+    for (int i = 0; i < 4; i++) {
+      const uint64_t it = (uint64_t)(g * 16 + 4 * q + i) * nb + b;
+      if (Q8) X.xd[j][i] = a.xdx[it];
+      if (QT == LLMHIP_Q4_1) X.xb[j][i] = a.xbsum[it];
     }
   }
 }
@@ -1412,9 +1416,9 @@ __device__ __forceinline__ void unit_block(const WUnit& u, int j, h8& B, float& 
   }
 }
 
-// The MFMAs of one unit (nblk of its 4 blocks) into acc[tile][group][token of the pair].
-template <uint32_t QT, bool Q8, int GT, int NG, bool TAIL>
-__device__ __forceinline__ void gemm_unit(float (&acc)[GT][NG][2], const WUnit (&w)[GT], const XUnit<QT, Q8, NG>& X,
+// The MFMAs of one unit (nblk of its 4 blocks) into acc[tile][token of the lane's four].
+template <uint32_t QT, bool Q8, int GT, bool TAIL>
+__device__ __forceinline__ void gemm_unit(float (&acc)[GT][4], const WUnit (&w)[GT], const XUnit<QT, Q8>& X,
                                           int nblk) {
 #pragma unroll
   for (int j = 0; j < 4; j++) {
@@ -1424,34 +1428,91 @@ __device__ __forceinline__ void gemm_unit(float (&acc)[GT][NG][2], const WUnit (
 #pragma unroll
     for (int u = 0; u < GT; u++) unit_block<QT, TAIL, true>(w[u], j, B[u], d[u], mm[u]);
 #pragma unroll
-    for (int g = 0; g < NG; g++)
+    for (int u = 0; u < GT; u++) {
+      f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(X.x[j][0], B[u], f4{0, 0, 0, 0}, 0, 0, 0);
+      D = __builtin_amdgcn_mfma_f32_16x16x32_f16(X.x[j][1], B[u], D, 0, 0, 0);
 #pragma unroll
-      for (int u = 0; u < GT; u++) {
-        const f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(X.x[j][g], B[u], f4{0, 0, 0, 0}, 0, 0, 0);
+      for (int i = 0; i < 4; i++) {
         if (Q8) {  // ggml's block product, as in mfma_block
-          float pA = __fmul_rn(__fmul_rn(d[u], X.xd[j][g][0]), D[0] + D[1]);
-          float pB = __fmul_rn(__fmul_rn(d[u], X.xd[j][g][1]), D[2] + D[3]);
-          if (QT == LLMHIP_Q4_1) {
-            pA = __fadd_rn(pA, __fmul_rn(mm[u], X.xb[j][g][0]));
-            pB = __fadd_rn(pB, __fmul_rn(mm[u], X.xb[j][g][1]));
-          }
-          acc[u][g][0] += pA;
-          acc[u][g][1] += pB;
+          float p = __fmul_rn(__fmul_rn(d[u], X.xd[j][i]), D[i]);
+          if (QT == LLMHIP_Q4_1) p = __fadd_rn(p, __fmul_rn(mm[u], X.xb[j][i]));
+          acc[u][i] += p;
         } else {
-          acc[u][g][0] += d[u] * (D[0] + D[1]);
-          acc[u][g][1] += d[u] * (D[2] + D[3]);
-          if (QT == LLMHIP_Q4_1) {
-            acc[u][g][0] += mm[u] * X.xb[j][g][0];
-            acc[u][g][1] += mm[u] * X.xb[j][g][1];
-          }
+          acc[u][i] += d[u] * D[i];
+          if (QT == LLMHIP_Q4_1) acc[u][i] += mm[u] * X.xb[j][i];
         }
       }
+    }
   }
 }
 
-template <uint32_t QT, int EPI, bool Q8, int GT, int NG>
+// The activations of one gate/up epilogue row (tile u of the workgroup, tokens
+// t and t + 1 of its group; gate row i at lane r < 8, up row i at r + 8) into
+// em[token][8 u + i], as EPI_GATEUP forms them.  Every lane calls it.
+__device__ __forceinline__ void emit_act(float (&em)[16][33], uint32_t u, uint32_t t, int r, float vA, float vB) {
+  const float uA = __shfl_xor(vA, 8), uB = __shfl_xor(vB, 8);
+  if (r < 8) {
+    em[t][8 * u + r] = vA / (1.f + __expf(-vA)) * uA;
+    em[t + 1][8 * u + r] = vB / (1.f + __expf(-vB)) * uB;
+  }
+}
+template <int A, int B>
+__device__ __forceinline__ void emit_act(float (&)[A][B], uint32_t, uint32_t, int, float, float) {}
+
+// Block b of the down projection's operands for token group g from em (one
+// wave: lane l forms k-group l / 16 of token l % 16).
+__device__ __forceinline__ void emit_block(const GemvArgs& a, const float (&em)[16][33], uint32_t g, uint32_t b,
+                                           int lane) {
+  const uint32_t t16 = lane & 15, kq = lane >> 4;
+  const uint32_t col[8] = {0, 2, 16, 18, 1, 3, 17, 19};  // {A0, A2, C0, C2, A1, A3, C1, C3}
+  float v[8], mx = 0.f, sm = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    v[i] = em[t16][4 * kq + col[i]];
+    mx = fmaxf(mx, fabsf(v[i]));
+    sm += v[i];
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  sm += __shfl_xor(sm, 16);
+  sm += __shfl_xor(sm, 32);
+  int e = 0;
+  if (mx > 0 && mx <= 3.0e38f) {
+    int E;
+    frexpf(mx, &E);
+    e = 15 - E;
+  }
+  h8 hi, lo;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float sv = ldexpf(v[i], e);
+    const _Float16 hh = (_Float16)sv;
+    hi[i] = hh;
+    lo[i] = (_Float16)(sv - (float)hh);
+  }
+  h8* dst = (h8*)a.op_xp + ((uint64_t)g * a.op_nb + b) * 128 + lane;
+  dst[0] = hi;
+  dst[64] = lo;
+  if (kq == 0) {
+    const uint32_t t = g * 16 + t16;
+    a.op_dx[(uint64_t)t * a.op_nb + b] = ldexpf(1.f, -e);
+    a.op_bsum[(uint64_t)t * a.op_nb + b] = sm;
+    if (b == 0) a.op_exp[t] = 0;
+  }
+}
+
+// EM (EPI_GATEUP, four tiles: the 32 activations of one block of the down
+// projection's input per workgroup): the epilogue rows also put their
+// activations into LDS, and wave 0 then forms the block's operands for the
+// workgroup's 16 tokens (GemvArgs::op_xp) as the attention's emit_operand
+// does: per token the exponent e that puts the block's largest magnitude in
+// [2^14, 2^15), hi = f16(v 2^e), lo = f16(v 2^e - hi), lane t + 16 kq holding
+// k-group kq of token t.
+template <uint32_t QT, int EPI, bool Q8, int GT, bool EM = false>
 __global__ __launch_bounds__(64 * GEMM_MAXW) void gemm_kernel(GemvArgs a_in) {
-  __shared__ float red[GEMM_MAXW][GT * NG * 2][64];
+  static_assert(!EM || (EPI == EPI_GATEUP && GT == 4), "the emitting form is four gate/up tiles");
+  __shared__ float red[GEMM_MAXW][GT * 4][64];
+  __shared__ float em[EM ? 16 : 1][EM ? 33 : 1];
   // the argument lines it reads in one round (as gemv_kernel's touch_args):
   // 0-1 the matrix and output, 2 the epilogue's, 3 up / kparts, 4-5 the prepared operands
   static_assert(offsetof(GemvArgs, xexp) / 64 == 4 && offsetof(GemvArgs, tg) / 64 == 5, "argument lines");
@@ -1461,7 +1522,7 @@ __global__ __launch_bounds__(64 * GEMM_MAXW) void gemm_kernel(GemvArgs a_in) {
   const int r = lane & 15, q = lane >> 4;
   // W: 4 or 8 waves (gemm_shape), so the counts below are shifts
   const uint32_t W = blockDim.x >> 6, lw = __builtin_ctz(W), nb = a.nb, ng = a.ng;
-  const uint32_t g0 = blockIdx.y * NG, tile0 = blockIdx.x * GT;
+  const uint32_t g = blockIdx.y, tile0 = blockIdx.x * GT;
   bool tv[GT];
   uint32_t tt[GT];
 #pragma unroll
@@ -1469,69 +1530,106 @@ __global__ __launch_bounds__(64 * GEMM_MAXW) void gemm_kernel(GemvArgs a_in) {
     tv[u] = tile0 + u < a.tiles;
     tt[u] = tv[u] ? tile0 + u : tile0;
   }
-  float acc[GT][NG][2];
+  float acc[GT][4];
 #pragma unroll
   for (int u = 0; u < GT; u++)
 #pragma unroll
-    for (int g = 0; g < NG; g++) acc[u][g][0] = acc[u][g][1] = 0.f;
+    for (int i = 0; i < 4; i++) acc[u][i] = 0.f;
 
   // groups wave, wave + W, ...: two register sets, A and B, in turn
   const uint32_t cnt = ng > (uint32_t)wave ? (ng - wave + W - 1) >> lw : 0;
   const uint32_t glast = wave + (cnt ? cnt - 1 : 0) * W;
   WUnit wA[GT], wB[GT];
-  XUnit<QT, Q8, NG> xA, xB;
-  auto load = [&](WUnit (&w)[GT], XUnit<QT, Q8, NG>& X, uint32_t gi) {
+  XUnit<QT, Q8> xA, xB;
+  auto load = [&](WUnit (&w)[GT], XUnit<QT, Q8>& X, uint32_t gi) {
 #pragma unroll
     for (int u = 0; u < GT; u++) load_group<QT>(w[u], a.qs, nb, tt[u], gi, lane, r);
-    load_xunit<QT, Q8, NG>(X, a, 4 * gi, 4 * gi + 3, g0, lane, q);
+    load_xunit<QT, Q8>(X, a, 4 * gi, 4 * gi + 3, g, lane, q);
   };
+  // wave w runs the epilogues of rows p = w, w + W, ... < 2 GT, row p being
+  // (tile p / 2, token pair p % 2 of the lane's four); the inputs of its first
+  // (residual, bias, RoPE table, token scales) are loaded with the first
+  // group's operands
+  const bool epw = (uint32_t)wave < (uint32_t)(GT * 2);
+  const uint32_t pu = (uint32_t)wave / 2, ph = (uint32_t)wave % 2;
+  bool ptv = tv[0];
+#pragma unroll
+  for (int u = 1; u < GT; u++) ptv = pu == (uint32_t)u ? tv[u] : ptv;
+  const uint32_t tokA = g * 16 + 4 * q + 2 * ph, tokB = tokA + 1;
+  const bool okA = tokA < a.ntok, okB = tokB < a.ntok;
+  EpiIn ein;
+  int exA = 0, exB = 0;
   if (cnt) {
     // no branch between a load and its use, and scheduling barriers, so the
     // loads of the next group stay ahead of the current group's MFMAs
     load(wA, xA, wave);
+    if (epw) {
+      ein = epi_load<EPI>(a, tile0 + pu, r, ptv, tokA, okA, tokB, okB);
+      exA = okA ? a.xexp[tokA] : 0;
+      exB = okB ? a.xexp[tokB] : 0;
+    }
     uint32_t i = 0;
     for (; i + 1 < cnt; i += 2) {
       load(wB, xB, wave + (i + 1) * W);
       __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
-      gemm_unit<QT, Q8, GT, NG, false>(acc, wA, xA, 4);
+      gemm_unit<QT, Q8, GT, false>(acc, wA, xA, 4);
       load(wA, xA, min(wave + (i + 2) * W, glast));
       __builtin_amdgcn_sched_barrier(0);
-      gemm_unit<QT, Q8, GT, NG, false>(acc, wB, xB, 4);
+      gemm_unit<QT, Q8, GT, false>(acc, wB, xB, 4);
     }
-    if (i < cnt) gemm_unit<QT, Q8, GT, NG, false>(acc, wA, xA, 4);
+    if (i < cnt) gemm_unit<QT, Q8, GT, false>(acc, wA, xA, 4);
+  } else if (epw) {
+    ein = epi_load<EPI>(a, tile0 + pu, r, ptv, tokA, okA, tokB, okB);
+    exA = okA ? a.xexp[tokA] : 0;
+    exB = okB ? a.xexp[tokB] : 0;
   }
   if (a.tail && (ng & (W - 1)) == (uint32_t)wave) {
     WUnit wt[GT];
-    XUnit<QT, Q8, NG> xt;
+    XUnit<QT, Q8> xt;
 #pragma unroll
     for (int u = 0; u < GT; u++) load_unit<QT>(wt[u], a.qs, nb, tt[u], ng, ng, a.tail, lane, r);
-    load_xunit<QT, Q8, NG>(xt, a, 4 * ng, 4 * ng + a.tail - 1, g0, lane, q);
-    gemm_unit<QT, Q8, GT, NG, true>(acc, wt, xt, (int)a.tail);
+    load_xunit<QT, Q8>(xt, a, 4 * ng, 4 * ng + a.tail - 1, g, lane, q);
+    gemm_unit<QT, Q8, GT, true>(acc, wt, xt, (int)a.tail);
   }
 
-  // split-K: every wave's partials into LDS, then pair p = (tile, group) is
-  // added in wave order by wave p % W and goes through the row epilogue
+  // split-K: every wave's partials into LDS, then each epilogue row is added
+  // in wave order by its wave
 #pragma unroll
   for (int u = 0; u < GT; u++)
 #pragma unroll
-    for (int g = 0; g < NG; g++) {
-      red[wave][(u * NG + g) * 2][lane] = acc[u][g][0];
-      red[wave][(u * NG + g) * 2 + 1][lane] = acc[u][g][1];
-    }
+    for (int i = 0; i < 4; i++) red[wave][u * 4 + i][lane] = acc[u][i];
   __syncthreads();
-  for (uint32_t p = wave; p < (uint32_t)(GT * NG); p += W) {
-    const uint32_t u = p / NG, g = p % NG;
-    float s0 = red[0][2 * p][lane], s1 = red[0][2 * p + 1][lane];
+  if (epw) {
+    const uint32_t o = 4 * pu + 2 * ph;
+    float s0 = red[0][o][lane], s1 = red[0][o + 1][lane];
     for (uint32_t w = 1; w < W; w++) {
-      s0 += red[w][2 * p][lane];
-      s1 += red[w][2 * p + 1][lane];
+      s0 += red[w][o][lane];
+      s1 += red[w][o + 1][lane];
     }
-    if (g0 + g >= a.tg) continue;
-    const uint32_t tokA = (g0 + g) * 8 + 2 * q, tokB = tokA + 1;
-    const bool okA = tokA < a.ntok, okB = tokB < a.ntok;
-    const float vA = okA ? ldexpf(s0, -a.xexp[tokA]) : 0.f;
-    const float vB = okB ? ldexpf(s1, -a.xexp[tokB]) : 0.f;
-    row_epilogue<EPI>(a, tile0 + u, r, tv[u], tokA, okA, vA, tokB, okB, vB);
+    const float vA = okA ? ldexpf(s0, -exA) : 0.f;
+    const float vB = okB ? ldexpf(s1, -exB) : 0.f;
+    row_epilogue<EPI>(a, tile0 + pu, r, ptv, tokA, okA, vA, tokB, okB, vB, &ein);
+    if (EM) emit_act(em, pu, 4 * q + 2 * ph, r, vA, vB);
+  }
+  for (uint32_t p = wave + W; p < (uint32_t)(GT * 2); p += W) {  // GT > W / 2
+    const uint32_t u = p / 2, o = 2 * p, tA = g * 16 + 4 * q + 2 * (p % 2), tB = tA + 1;
+    bool v = tv[0];
+#pragma unroll
+    for (int k = 1; k < GT; k++) v = u == (uint32_t)k ? tv[k] : v;
+    float s0 = red[0][o][lane], s1 = red[0][o + 1][lane];
+    for (uint32_t w = 1; w < W; w++) {
+      s0 += red[w][o][lane];
+      s1 += red[w][o + 1][lane];
+    }
+    const bool oA = tA < a.ntok, oB = tB < a.ntok;
+    const float vA = oA ? ldexpf(s0, -a.xexp[tA]) : 0.f;
+    const float vB = oB ? ldexpf(s1, -a.xexp[tB]) : 0.f;
+    row_epilogue<EPI>(a, tile0 + u, r, v, tA, oA, vA, tB, oB, vB);
+    if (EM) emit_act(em, u, 4 * q + 2 * (p % 2), r, vA, vB);
+  }
+  if constexpr (EM) {
+    __syncthreads();
+    if (wave == 0) emit_block(a, em, g, tile0 / 4, lane);
   }
 }
 
@@ -2203,16 +2301,16 @@ int embed_launch_qt(const QMat& m, const int32_t* tokens, const uint32_t* state,
   return 0;
 }
 
-template <uint32_t QT, int EPI, bool Q8, int GT, int NG>
+template <uint32_t QT, int EPI, bool Q8, int GT, bool EM = false>
 static void gemm_go(const GemvArgs& a, uint32_t waves, hipStream_t s) {
-  dim3 grid((a.tiles + GT - 1) / GT, (a.tg + NG - 1) / NG);
-  hipLaunchKernelGGL((gemm_kernel<QT, EPI, Q8, GT, NG>), grid, dim3(64 * waves), 0, s, a);
+  dim3 grid((a.tiles + GT - 1) / GT, a.tg);
+  hipLaunchKernelGGL((gemm_kernel<QT, EPI, Q8, GT, EM>), grid, dim3(64 * waves), 0, s, a);
 }
 
 template <uint32_t QT, int EPI>
 static void gemm_shape(const GemvArgs& a, hipStream_t s) {
-  // Measured on MI355X at 64 tokens (prep + product, Q4_0): two token groups
-  // per workgroup beat four at every layer shape (more workgroups, lower
+  // Measured on MI355X at 64 tokens (prep + product, Q4_0): 16 tokens per
+  // workgroup beat 32 at every layer shape (more workgroups, lower
   // registers: 9728x896 12.6 against 15.2 us, 896x4864 11.8 against 16.6);
   // two tiles per workgroup pay on tall matrices (9728x896: 12.6 against 15.7
   // with one, 14.6 with four); short matrices with many block groups take
@@ -2220,12 +2318,18 @@ static void gemm_shape(const GemvArgs& a, hipStream_t s) {
   const uint32_t units = a.ng + (a.tail ? 1 : 0);
   const bool gt2 = a.tiles >= 256;
   const uint32_t waves = units > 4 && !gt2 ? 8 : 4;
+  if constexpr (EPI == EPI_GATEUP) {
+    if (a.op_xp) {  // the down projection's operands too: four tiles (gemm_launch checked q8 = 0)
+      gemm_go<QT, EPI, false, 4, true>(a, 4, s);
+      return;
+    }
+  }
   if (a.q8) {
-    if (gt2) gemm_go<QT, EPI, true, 2, 2>(a, waves, s);
-    else gemm_go<QT, EPI, true, 1, 2>(a, waves, s);
+    if (gt2) gemm_go<QT, EPI, true, 2>(a, waves, s);
+    else gemm_go<QT, EPI, true, 1>(a, waves, s);
   } else {
-    if (gt2) gemm_go<QT, EPI, false, 2, 2>(a, waves, s);
-    else gemm_go<QT, EPI, false, 1, 2>(a, waves, s);
+    if (gt2) gemm_go<QT, EPI, false, 2>(a, waves, s);
+    else gemm_go<QT, EPI, false, 1>(a, waves, s);
   }
 }
 

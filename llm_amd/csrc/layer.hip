@@ -14,8 +14,8 @@ namespace llmhip {
 // [2^14, 2^15) (0 for an all-zero or non-finite block), hi = f16(v 2^e),
 // lo = f16(v 2^e - hi); item i of the block (elements 4i..4i+3 and
 // 16+4i..16+4i+3) is written by the block's lane 4i as the product's 16-byte
-// operands for token slot t % 8 of group t / 8, in the order
-// {A0, A2, C0, C2, A1, A3, C1, C3} of prep_kernel.
+// operands (hi, then lo 64 operands on) for token t % 16 of group t / 16, in
+// the order {A0, A2, C0, C2, A1, A3, C1, C3} of prep_kernel.
 __device__ __forceinline__ void emit_operand(const AttnOps& a, uint32_t t, uint32_t col, float v) {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   const uint32_t lane = threadIdx.x & 63, j = lane & 31, b = col / 32;
@@ -45,9 +45,9 @@ __device__ __forceinline__ void emit_operand(const AttnOps& a, uint32_t t, uint3
       hi[i] = hh;
       lo[i] = (_Float16)(g[i] - (float)hh);
     }
-    h8* dst = (h8*)a.xp + ((uint64_t)(t / 8) * a.onb + b) * 64 + (j / 4) * 16 + 2 * (t % 8);
+    h8* dst = (h8*)a.xp + ((uint64_t)(t / 16) * a.onb + b) * 128 + (j / 4) * 16 + t % 16;
     dst[0] = hi;
-    dst[1] = lo;
+    dst[64] = lo;
   }
   if (j == 0) {
     a.xdx[(uint64_t)t * a.onb + b] = ldexpf(1.f, -e);

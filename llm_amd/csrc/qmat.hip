@@ -113,7 +113,10 @@ int gemv_launch(const GemvArgs& a, uint32_t qtype, int pro, int epi, hipStream_t
 
 int gemm_launch(const GemvArgs& a, uint32_t qtype, int epi, hipStream_t s) {
   if (a.ntok == 0) return 0;
-  if (a.ntok > a.tg * 8 || a.tg > 8) return set_error(LLMHIP_ERR_ARG, "llm: gemm: %u tokens in %u groups", a.ntok, a.tg);
+  if (a.ntok > a.tg * 16 || a.tg > 4) return set_error(LLMHIP_ERR_ARG, "llm: gemm: %u tokens in %u groups", a.ntok, a.tg);
+  if (a.op_xp && (epi != EPI_GATEUP || a.q8 || a.tiles % 4 || a.op_nb != a.tiles / 4 || !a.op_dx || !a.op_bsum ||
+                  !a.op_exp))
+    return set_error(LLMHIP_ERR_ARG, "llm: gemm: the down operands come from a gate/up product of 32-row blocks");
   switch (qtype) {
     case LLMHIP_Q4_0: return gemm_launch_qt<LLMHIP_Q4_0>(a, epi, s);
     case LLMHIP_Q4_1: return gemm_launch_qt<LLMHIP_Q4_1>(a, epi, s);
