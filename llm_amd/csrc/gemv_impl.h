@@ -2314,10 +2314,13 @@ static void gemm_shape(const GemvArgs& a, hipStream_t s) {
   // registers: 9728x896 12.6 against 15.2 us, 896x4864 11.8 against 16.6);
   // two tiles per workgroup pay on tall matrices (9728x896: 12.6 against 15.7
   // with one, 14.6 with four); short matrices with many block groups take
-  // eight waves, tall ones four.
+  // eight waves, tall ones four.  In the prefill itself (config 3, two
+  // chunks at once): long rows (896x4864) take two tiles and eight waves
+  // (87.4k -> 89.4k tok/s), the [q; k; v] product two tiles and four waves
+  // (-> 90.1k with both); W_o keeps one tile and eight waves.
   const uint32_t units = a.ng + (a.tail ? 1 : 0);
-  const bool gt2 = a.tiles >= 256;
-  const uint32_t waves = units > 4 && !gt2 ? 8 : 4;
+  const bool gt2 = a.tiles >= 256 || units >= 16 || EPI == EPI_QKV;
+  const uint32_t waves = units > 4 && (a.tiles < 256 && EPI != EPI_QKV) ? 8 : 4;
   if constexpr (EPI == EPI_GATEUP) {
     if (a.op_xp) {  // the down projection's operands too: four tiles (gemm_launch checked q8 = 0)
       gemm_go<QT, EPI, false, 4, true>(a, 4, s);
