@@ -812,20 +812,21 @@ static int record_slot(Model& m, uint32_t ntok, bool head, int s) {
   return 0;
 }
 
-// Segments of G slots (layers) of a pass of nl layers, and segment g: slots
-// [g G, (g + 1) G).
-static int segments(int nl, int G) { return (nl + G) / G; }
-static int record_segment(Model& m, uint32_t ntok, bool head, bool embed_in, int g, int G) {
+// A segment of a pass of nl layers: slots [s0, s0 + n) (the pass's slots
+// 0 .. nl).
+static int record_segment(Model& m, uint32_t ntok, bool head, bool embed_in, int s0, int n) {
   m.embed_in = embed_in || ntok != 1;
   m.k5_split = m.xsum_ready = false;  // an embedding pass never splits its K5 (k5_splits)
   bool h = head;
   const int nl = pass_layers(m, &h);
-  for (int s = g * G; s < std::min((g + 1) * G, nl + 1); s++) LLM_TRY(record_slot(m, ntok, head, s));
+  for (int s = s0; s < std::min(s0 + n, nl + 1); s++) LLM_TRY(record_slot(m, ntok, head, s));
   return 0;
 }
-// The segment of the previous chunk that segment g waits for: the one whose
-// slots append the rows of the latest layer whose attention g runs (-1: none).
-static int segment_dep(int g, int G) { return (g * G + G - 2) / G; }
+// A prefill chunk's segments: G slots each from slot `shift` on, the slots
+// before it one segment of their own.  seg_start: the first slot of segment
+// i; seg_of: the segment that holds slot s.
+static int seg_start(int i, int shift, int G) { return shift == 0 ? i * G : i == 0 ? 0 : shift + (i - 1) * G; }
+static int seg_of(int s, int shift, int G) { return shift == 0 ? s / G : s < shift ? 0 : 1 + (s - shift) / G; }
 
 // One pass of ntok tokens at positions state[0] .. state[0]+ntok-1: the
 // embedding (embed_in; else the one token's row is xn, which the previous
@@ -909,7 +910,8 @@ static uint64_t graph_key(const Model& m, uint32_t ntok, bool head, bool embed_i
          ((uint64_t)m.attn_rows << 3) | (embed_in ? 4 : 0) | (m.attn_split ? 2 : 0) | (head ? 1 : 0);
 }
 
-// Capture record_pass (seg -1) or one segment into a graph (once per key).
+// Capture record_pass (seg -1) or the segment of slots [seg, seg + G) into a
+// graph (once per key).
 static int graph_for(Model& m, uint32_t ntok, bool head, bool embed_in, int seg, int G, hipGraphExec_t* out) {
   uint64_t key = graph_key(m, ntok, head, embed_in, seg, G);
   auto it = m.chunk_exec.find(key);
@@ -995,15 +997,17 @@ static int prefill_lanes() {
 // reach 1.55x and 1.84x the throughput of one, four 1.58x): chunk c runs on
 // lane (C-1-c) % L (the last on lane 0, whose buffers Peek and decode use),
 // from its own position (set_state), as graph segments of G layers
-// (record_segment); segment g of chunk c waits for the segment of chunk c-1
-// that appended the cache rows of the latest layer whose attention g runs
-// (segment_dep; the chunks before c-1 ran earlier on its lane or were waited
-// for by c-1).  The chunks of a group of L are enqueued segment by segment in
-// turn, so that each starts one segment behind the one before rather than
-// after the host has enqueued all of it; chunk c's events are set
-// c % (LANES + 1), so that every wait names the record of the chunk right
-// before.  Several chunks' layers then run at once where one chunk's kernels
-// leave the GPU idle.
+// (record_segment); a segment of chunk c waits for the segment of chunk c-1
+// that appended the cache rows of the latest layer whose attention it runs
+// (the chunks before c-1 ran earlier on its lane or were waited for by c-1).
+// The chunks of a group of L are enqueued segment by segment in turn, so that
+// each starts one segment behind the one before rather than after the host
+// has enqueued all of it; chunk c's events are set c % (LANES + 1), so that
+// every wait names the record of the chunk right before.  On two lanes chunk
+// c's segments start c % G slots later than chunk c-1's (seg_start): a
+// segment then waits for the one of c-1 that ends one slot before its own
+// end, so c trails c-1 by G - 1 slots, not G.  Several chunks' layers then
+// run at once where one chunk's kernels leave the GPU idle.
 static int prefill_wavefront(Model& m, uint32_t n) {
   const uint32_t C = (n + m.pm - 1) / m.pm;
   const uint32_t L = std::min<uint32_t>(std::min<uint32_t>(C, 3), (uint32_t)prefill_lanes());
@@ -1021,43 +1025,50 @@ static int prefill_wavefront(Model& m, uint32_t n) {
     m.last_row = *ntok - 1;
   };
   // segments of three layers for a two-chunk prompt, where the second chunk's
-  // lag of one segment weighs most; six for longer ones, where fewer graph
-  // launches weigh more (measured: configs 3 and 4 at one to eight layers).
-  // With three lanes chunk c-2 runs on another stream: its rows are ready for
-  // chunk c because c-1 waited for the same segment of it, which holds them
-  // only when a segment has two or more layers (segment_dep(g) = g).
+  // lag weighs most; six for longer ones, where fewer graph launches weigh
+  // more (measured: configs 3 and 4 at one to eight layers).  With three
+  // lanes chunk c-2 runs on another stream: its rows are ready for chunk c
+  // because c-1 waited for the same segment of it, which holds them only when
+  // a segment has two or more layers and the chunks' segments line up.
   const int G = C <= 2 ? 3 : 6;
   static_assert(LANES <= 3, "the event sets and the G >= 2 argument are for at most three lanes");
+  bool h0 = true;
+  const int nl = pass_layers(m, &h0);
+  auto shift = [&](uint32_t c) { return L == 2 ? (int)(c % (uint32_t)G) : 0; };
   for (uint32_t c0 = 0; c0 < C && rc == 0; c0 += L) {
     const uint32_t cn = std::min(C - c0, L);
-    bool h0 = true;
-    const int ns = segments(pass_layers(m, &h0), G);
-    for (int s = 0; s < ns && rc == 0; s++) {
+    for (int i = 0; rc == 0; i++) {
+      bool any = false;
       for (uint32_t c = c0; c < c0 + cn && rc == 0; c++) {
+        const int s0 = seg_start(i, shift(c), G), s1 = std::min(seg_start(i + 1, shift(c), G), nl + 1);
+        if (s0 > nl) continue;
+        any = true;
         uint32_t a, ntok;
         bool head;
         chunk(c, &a, &ntok, &head);
-        if (s == 0) {
+        if (i == 0) {
           rc = set_state_launch(m.state, a, m.stream);
           m.stats.submits++;
         }
-        const int dep = segment_dep(s, G);
-        if (rc == 0 && c > 0 && dep >= 0 && hipStreamWaitEvent(m.stream, m.seg_done[(c - 1) % S][dep], 0) != hipSuccess)
+        // the latest attention here is layer s1 - 2's, which reads the rows chunk c-1's slot s1 - 2 appends
+        if (rc == 0 && c > 0 && s1 >= 2 &&
+            hipStreamWaitEvent(m.stream, m.seg_done[(c - 1) % S][seg_of(s1 - 2, shift(c - 1), G)], 0) != hipSuccess)
           rc = set_error(LLMHIP_ERR_DEVICE, "llm: prefill: stream wait failed");
         if (rc == 0 && eager_passes()) {
           m.dispatches = 0;
-          rc = record_segment(m, ntok, head, true, s, G);
+          rc = record_segment(m, ntok, head, true, s0, s1 - s0);
           m.stats.dispatches += m.dispatches;
         } else if (rc == 0) {
           hipGraphExec_t ex;
-          rc = graph_for(m, ntok, head, true, s, G, &ex);
+          rc = graph_for(m, ntok, head, true, s0, s1 - s0, &ex);
           if (rc == 0 && hipGraphLaunch(ex, m.stream) != hipSuccess)
             rc = set_error(LLMHIP_ERR_DEVICE, "llm: prefill: graph launch failed");
-          if (rc == 0) m.stats.dispatches += m.graph_nodes[graph_key(m, ntok, head, true, s, G)];
+          if (rc == 0) m.stats.dispatches += m.graph_nodes[graph_key(m, ntok, head, true, s0, s1 - s0)];
         }
-        if (rc == 0 && hipEventRecord(m.seg_done[c % S][s], m.stream) != hipSuccess)
+        if (rc == 0 && hipEventRecord(m.seg_done[c % S][i], m.stream) != hipSuccess)
           rc = set_error(LLMHIP_ERR_DEVICE, "llm: prefill: event record failed");
       }
+      if (!any) break;
     }
   }
   use_lane(m, 0);
