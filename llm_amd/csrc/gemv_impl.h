@@ -898,8 +898,8 @@ __host__ __device__ constexpr uint32_t i8_lds_bytes(uint32_t nb) { return nb * (
 // The digits of the staged items, by the whole workgroup (one thread per
 // item: a block's four items on four consecutive lanes), into dg[(b 3 + p) 4 + q]
 // (8 bytes: the item's elements in the order of the lane's int8 weights) and
-// tb[b] = (8 S_0, 8 S_1, 8 S_2, 0) for Q4_0 (zeros for the other types).  Ends
-// with a barrier.
+// tb[b] = (8 S_0, 8 S_1, 8 S_2, 8 (S_0 2^16 + S_1 2^8 + S_2) modulo 2^32) for
+// Q4_0 (zeros for the other types).  Ends with a barrier.
 template <uint32_t QT>
 __device__ __forceinline__ void stage_digits(const h8* xs, uint32_t nb, uint64_t* dg, i32x4* tb) {
   const uint32_t NI = nb * 4;
@@ -934,8 +934,10 @@ __device__ __forceinline__ void stage_digits(const h8* xs, uint32_t nb, uint64_t
       const uint32_t blk = it / 4, q = it % 4;
 #pragma unroll
       for (int p = 0; p < 3; p++) dg[(blk * 3 + p) * 4 + q] = (uint64_t)w[p][0] | (uint64_t)w[p][1] << 32;
+      // the last word: the three offsets recombined (modulo 2^32), as group_i8 subtracts them
+      const uint32_t tc = ((uint32_t)(8 * sd[0]) << 16) + ((uint32_t)(8 * sd[1]) << 8) + (uint32_t)(8 * sd[2]);
       if (q == 0)
-        tb[blk] = QT == LLMHIP_Q4_0 ? i32x4{8 * sd[0], 8 * sd[1], 8 * sd[2], 0} : i32x4{0, 0, 0, 0};
+        tb[blk] = QT == LLMHIP_Q4_0 ? i32x4{8 * sd[0], 8 * sd[1], 8 * sd[2], (int32_t)tc} : i32x4{0, 0, 0, 0};
     }
   }
   __syncthreads();
@@ -973,7 +975,17 @@ __device__ __forceinline__ void group_i8(const WUnit& u, const i32x4 (&xa)[2], c
   }
   i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[0], B0, i32x4{0, 0, 0, 0}, 0, 0, 0);
   D = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[1], B1, D, 0, 0, 0);
-  const float t = fmaf((float)(D[0] - T[0]), 65536.f, fmaf((float)(D[1] - T[1]), 256.f, (float)(D[2] - T[2])));
+  float t;
+  if (QT == LLMHIP_Q8_0) {
+    t = fmaf((float)(D[0] - T[0]), 65536.f, fmaf((float)(D[1] - T[1]), 256.f, (float)(D[2] - T[2])));
+  } else {
+    // the digits recombined in integers: the block's sum times 128 is below
+    // 32 * 2^22 * 15 < 2^31 in magnitude (Q4_0 with its offset: * 8), so the
+    // sum taken modulo 2^32 is exact, and one conversion rounds it (T[3]: the
+    // offsets recombined the same way)
+    const uint32_t d = (((uint32_t)D[0] << 8) + (uint32_t)D[1]) << 8;
+    t = (float)(int32_t)(d + (uint32_t)D[2] - (uint32_t)T[3]);
+  }
   if (QT == LLMHIP_Q4_1) {  // (d, m) of block q
     const uint32_t sw = q == 0 ? u.sv.x : q == 1 ? u.sv.y : q == 2 ? u.sv.z : u.sv.w;
     acc = fmaf(f16_hw(sw & 0xffff), t, acc);
