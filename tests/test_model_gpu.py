@@ -82,6 +82,37 @@ def test_prefill_chunk_edges(gpu, prompt_len, batch):
     _check(g, cpu, synth.prompt(31, prompt_len, spec.vocab), 12)
 
 
+_TWO_LANES = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+from llm_amd import synth
+from tests.test_model_gpu import _open, _check
+spec = synth.tiny_qwen(seed=30, layers=8)
+g, cpu = _open(spec, 512)
+_check(g, cpu, synth.prompt(32, int(sys.argv[2]), spec.vocab), 8)
+print("two-lane wavefront ok", flush=True)
+"""
+
+
+@pytest.mark.parametrize("prompt_len", [150, 300])
+def test_prefill_two_lanes_staggered(gpu, prompt_len):
+    """The wavefront on two lanes for prompts of three and five chunks
+    (LLMHIP_PREFILL_LANES=2, read once per process, so in a child process):
+    each chunk's segments start c % 6 slots later than the first's, and a
+    segment waits for the previous chunk's segment that holds the slot before
+    its own last (seg_start / seg_of); logits and greedy tokens against the
+    oracle's on an eight-layer model."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, LLMHIP_PREFILL_LANES="2")
+    r = subprocess.run([sys.executable, "-c", _TWO_LANES, root, str(prompt_len)], env=env, cwd=root,
+                       capture_output=True, text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "two-lane wavefront ok" in r.stdout
+
+
 @pytest.mark.parametrize("prompt_len,heads,kv_heads,hd", [
     (230, 4, 4, 64), (300, 4, 2, 64), (250, 8, 2, 64), (200, 16, 2, 64), (100, 2, 1, 128), (140, 4, 2, 128)])
 def test_attention_paths(gpu, prompt_len, heads, kv_heads, hd):
