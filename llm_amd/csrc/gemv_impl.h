@@ -1623,8 +1623,10 @@ __global__ __launch_bounds__(64 * GEMM_MAXW) void gemm_kernel(GemvArgs a_in) {
     row_epilogue<EPI>(a, tile0 + pu, r, ptv, tokA, okA, vA, tokB, okB, vB, &ein);
     if (EM) emit_act(em, pu, 4 * q + 2 * ph, r, vA, vB);
   }
-  for (uint32_t p = wave + W; p < (uint32_t)(GT * 2); p += W) {  // GT > W / 2
-    const uint32_t u = p / 2, o = 2 * p, tA = g * 16 + 4 * q + 2 * (p % 2), tB = tA + 1;
+  // rows past the first wave's (GT > W / 2): W is even, so row p's token pair
+  // is the wave's own, and so are the token scales loaded with the first row
+  for (uint32_t p = wave + W; p < (uint32_t)(GT * 2); p += W) {
+    const uint32_t u = p / 2, o = 2 * p, tA = tokA, tB = tokB;
     bool v = tv[0];
 #pragma unroll
     for (int k = 1; k < GT; k++) v = u == (uint32_t)k ? tv[k] : v;
@@ -1633,11 +1635,10 @@ __global__ __launch_bounds__(64 * GEMM_MAXW) void gemm_kernel(GemvArgs a_in) {
       s0 += red[w][o][lane];
       s1 += red[w][o + 1][lane];
     }
-    const bool oA = tA < a.ntok, oB = tB < a.ntok;
-    const float vA = oA ? ldexpf(s0, -a.xexp[tA]) : 0.f;
-    const float vB = oB ? ldexpf(s1, -a.xexp[tB]) : 0.f;
-    row_epilogue<EPI>(a, tile0 + u, r, v, tA, oA, vA, tB, oB, vB);
-    if (EM) emit_act(em, u, 4 * q + 2 * (p % 2), r, vA, vB);
+    const float vA = okA ? ldexpf(s0, -exA) : 0.f;
+    const float vB = okB ? ldexpf(s1, -exB) : 0.f;
+    row_epilogue<EPI>(a, tile0 + u, r, v, tA, okA, vA, tB, okB, vB);
+    if (EM) emit_act(em, u, 4 * q + 2 * ph, r, vA, vB);
   }
   if constexpr (EM) {
     __syncthreads();
