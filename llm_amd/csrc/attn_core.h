@@ -61,9 +61,12 @@ struct AttnChunk {
   }
 
   // The rows below n (all of them loaded or set), with q the lane's float4
-  // slice of the query: returns the chunk's max M and sum L in every thread,
-  // and o = sum e v[d] for d = tid < HD.  Two barriers; call with the whole
-  // workgroup.
+  // slice of the query: returns the chunk's max M in every thread, and its
+  // sum L and o = sum e v[d] for d = tid < HD.  Each wave weighs its rows by
+  // its own max m_w (e = exp(s - m_w), l_w = sum e, o_w = sum e v); one
+  // barrier shares them, and the output's threads combine them in wave order
+  // with the weights exp(m_w - M), M = max m_w.  Call with the whole
+  // workgroup; at least one row below n.
   __device__ __forceinline__ void reduce(const f4 (&q)[V4], uint32_t row0, uint32_t n, float scale,
                                          AttnLds<HD, NW>& sm, float* M_out, float* L_out, float* o_out) const {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id(), cl = lane & 15, slot = tid >> 4;
@@ -80,12 +83,7 @@ struct AttnChunk {
       sj[j] = p < n ? d * scale : -INFINITY;
       m = fmaxf(m, sj[j]);
     }
-    m = rows_max4(m);
-    if (lane == 0) sm.m[0][wave] = m;
-    __syncthreads();
-    float M = sm.m[0][0];
-#pragma unroll
-    for (uint32_t w = 1; w < NW; w++) M = fmaxf(M, sm.m[0][w]);
+    m = rows_max4(m);  // the wave's max (-inf if none of its rows is below n)
     f4 acc[V4];
 #pragma unroll
     for (uint32_t v = 0; v < V4; v++) acc[v] = f4{0, 0, 0, 0};
@@ -94,7 +92,7 @@ struct AttnChunk {
     for (uint32_t j = 0; j < J; j++) {
       const uint32_t p = row0 + slot + S * j;
       if (p < n) {
-        const float e = __expf(sj[j] - M);  // v_exp_f32: a few ulp, inside the parity bounds
+        const float e = __expf(sj[j] - m);  // v_exp_f32: a few ulp, inside the parity bounds
         l += e;
 #pragma unroll
         for (uint32_t v = 0; v < V4; v++) acc[v] += e * vr[j][v];
@@ -111,16 +109,26 @@ struct AttnChunk {
     if (lane < 16)
 #pragma unroll
       for (uint32_t v = 0; v < V4; v++) sm.o[0][(wave * 16 + cl) * V4 + v] = acc[v];
-    if (lane == 0) sm.l[0][wave] = l;
+    if (lane == 0) {
+      sm.m[0][wave] = m;
+      sm.l[0][wave] = l;
+    }
     __syncthreads();
+    float mw[NW], M = -INFINITY;
+#pragma unroll
+    for (uint32_t w = 0; w < NW; w++) {
+      mw[w] = sm.m[0][w];
+      M = fmaxf(M, mw[w]);
+    }
     *M_out = M;
     float L = 0, o = 0;
     if (tid < HD) {
       const uint32_t fi = tid / 4, ci = fi % 16, vi = fi / 16, k = tid % 4;
 #pragma unroll
       for (uint32_t w = 0; w < NW; w++) {
-        L += sm.l[0][w];
-        o += sm.o[0][(w * 16 + ci) * V4 + vi][k];
+        const float c = mw[w] == -INFINITY ? 0.f : __expf(mw[w] - M);
+        L += c * sm.l[0][w];
+        o += c * sm.o[0][(w * 16 + ci) * V4 + vi][k];
       }
     }
     *L_out = L;
@@ -129,7 +137,8 @@ struct AttnChunk {
 
   // reduce for QN queries of one head over the same rows (several tokens of a
   // prefill chunk): query i has its slice q[i] and its causal bound n[i]; out
-  // per query as reduce's.  The same two barriers for all QN.
+  // per query as reduce's, but with the chunk's max shared first (a barrier)
+  // and every row weighed by it: two barriers for all QN.
   template <uint32_t QN>
   __device__ __forceinline__ void reduce_n(const f4 (&q)[QN][V4], uint32_t row0, const uint32_t (&n)[QN],
                                            float scale, AttnLds<HD, NW, QN>& sm, float (&M_out)[QN],
