@@ -3,15 +3,16 @@
 // records five dispatches per layer, fused.go:259-265).
 //
 // Each workgroup has a fixed share of each phase of a layer:
-//   K1  a tile of [q; k; v]: RMSNorm(x) (attn_norm), the product, bias, RoPE,
-//       q out, K and V appended to the cache (kernels_fused.go:47-73);
+//   K1  a tile of [q; k; v]: RMSNorm(x) (attn_norm, its scale applied to the
+//       product), the product, bias, RoPE, q out, K and V appended to the
+//       cache (kernels_fused.go:47-73);
 //   K2  one query head over one chunk of 128 cache rows: the chunk's max
 //       score, sum of e and sum of e v (kernels_fused.go:82-146; every
 //       position is below attn_full_max, so there are one or two chunks);
 //       the second chunk's workgroup merges the first's sums into its own as
 //       attn_merge_kernel merges chunks and writes the head's output;
 //   K3  a tile of W_o att plus the residual (kernels_fused.go:150-170);
-//   K4  tiles of [gate; up]: RMSNorm (ffn_norm), the product, SwiGLU;
+//   K4  tiles of [gate; up]: RMSNorm (ffn_norm, as K1's), the product, SwiGLU;
 //   K5  one of kp k-parts of a tile of W_down act; the next layer adds the
 //       parts to the residual, in order.
 // The boundaries between the phases are not kernel boundaries: a phase's
@@ -137,8 +138,6 @@ __device__ __forceinline__ float ll_settle(const uint64_t* p, uint64_t x, uint32
 }
 
 constexpr uint32_t PASS_MAX_ITEMS = PASS_MAX_FF / 8;  // items of 8 elements of the longest staged row
-constexpr uint32_t WPT_E = PASS_MAX_EMBD / (64 * PASS_WAVES);  // row elements per thread, rows of length E
-constexpr uint32_t WPT_F = PASS_MAX_FF / (64 * PASS_WAVES);    // row elements per thread, the longest row
 
 template <uint32_t HD>
 struct PassLds {
@@ -146,15 +145,19 @@ struct PassLds {
   float nw[PASS_MAX_EMBD];        // RMS phases: the norm weights
   h8 xs[2 * PASS_MAX_ITEMS];      // the phase's A operands: item it at 2 it (hi) and 2 it + 1 (lo)
   float bsum[PASS_MAX_ITEMS / 4];  // Q4_1: each block's sum, scaled like the operands
-  float misc[16];                  // the waves' partial sums of squares [0, 8) and maxima [8, 16)
-  float part[PASS_K4_TILES][PASS_WAVES][64];  // split-K partials of K1 and K4
-  float part2[1][PASS_WAVES][64];  // those of K3 and K5, which have no barrier before theirs: a wave
-                                   // may write them while another still reads the previous phase's
+  // The RMSNorm phases' partial sums of squares ([0] K1, [1] K4) and split-K
+  // partials, one copy per layer parity: no barrier precedes a phase's
+  // products, so a wave may write a layer's while another still reads those
+  // of the layer before; two layers back, the phase's own barrier has passed.
+  float ss[2][2][PASS_WAVES];
+  float part1[2][1][PASS_WAVES][64];
+  float part4[2][PASS_K4_TILES][PASS_WAVES][64];
+  float part2[1][PASS_WAVES][64];  // K3's and K5's: the phases between them have barriers
   AttnLds<HD, PASS_WAVES> am;
   float mrg[PASS_LONG_CHUNKS][HD + 2];  // the long form's merge: each chunk's o, m and l
 };
 
-// Where a phase's input row comes from (stage_ops).
+// Where an RMSNorm phase's input row comes from (stage_rms_wave).
 enum PassSrc : int {
   SRC_LL,     // one vector of flag-carrying words
   SRC_PLAIN,  // plain memory (layer 0's input, which the sampling kernel wrote)
@@ -167,41 +170,6 @@ struct StageIn {
   uint32_t flag, kp, E;
   bool gate;           // wait behind a gate word (ll_wait_gated): the input is expected late
 };
-
-// Row elements base + tid + 512 k (k < NW; those below base + n) into v,
-// every load issued before the first wait: consecutive threads read
-// consecutive words, so each load instruction of a wave touches four lines
-// (a wave's polls of the row stay few, however many workgroups poll it).
-// SRC_XSUM rows are of length E.
-template <int SRC, uint32_t HD, uint32_t NW>
-__device__ __forceinline__ void load_row(const StageIn& in, uint32_t base, uint32_t n, uint32_t tid, float (&v)[NW],
-                                         Waiter& w) {
-  constexpr uint32_t T = 64 * PASS_WAVES;
-  if constexpr (SRC == SRC_PLAIN) {
-#pragma unroll
-    for (uint32_t k = 0; k < NW; k++) v[k] = tid + T * k < n ? in.plain[base + tid + T * k] : 0.f;
-  } else if constexpr (SRC == SRC_LL) {
-    const uint64_t* p = in.ll + base + tid;
-    ll_wait_row<NW>(in.gate, [&](int i) { return p + T * i; }, [&](int i) { return tid + T * i < n; }, in.flag, v, w);
-  } else if constexpr (SRC == SRC_XSUM) {
-    constexpr uint32_t NP = 1 + PASS_MAX_KP;
-    float u[NW * NP];
-    // word i: vector i / NW (xb, then the parts), element tid + T (i % NW)
-    const uint64_t* p = in.ll + tid;
-    // (the gate: the wave's word of the last k-part, whose producers finish last)
-    ll_wait_row<NW * NP>(in.gate, [&](int i) { return p + (i / NW) * in.E + T * (i % NW); },
-                         [&](int i) { return (uint32_t)(i / NW) <= in.kp && tid + T * (i % NW) < n; }, in.flag, u, w,
-                         (int)(in.kp * NW));
-#pragma unroll
-    for (uint32_t k = 0; k < NW; k++) {
-      float x = u[k];
-#pragma unroll
-      for (uint32_t q = 1; q < NP; q++)
-        if (q <= in.kp) x += u[q * NW + k];
-      v[k] = x;
-    }
-  }
-}
 
 // The wave's units' items (those of units_load: u = u0 + wave + 8 i < u1,
 // i < MU) from the row in LDS: item it = (block it / 4, k-group it % 4:
@@ -252,66 +220,78 @@ __device__ __forceinline__ void form_items(PassLds<HD>& L, uint32_t nb, uint32_t
   __builtin_amdgcn_wave_barrier();
 }
 
-// The phase's input row (nb blocks of 32 from block nb0 on) staged as the A
-// operands of the wave's units (those of units_load: u = u0 + wave + 8 i < u1,
-// i < MU), in LDS: item it = (block it / 4, k-group it % 4: elements
-// 4 (it % 4) + 0..3 and 16 + 4 (it % 4) + 0..3 of the block) in MFMA element
-// order, scaled by 2^ex so that the staged values' largest magnitude sits in
-// [2^14, 2^15), and split exactly into f16 hi (xs[2 it]) + lo (xs[2 it + 1]);
-// the blocks' sums (Q4_1: cpu.go:196-198) scaled alike.  RMS: the row is first
-// normed, h = (x s) w with s = f32(1/sqrt(f64(sum x^2 / n + eps)))
-// (cpu.go:90-96); the largest |x w| goes through the same barrier as the sum
-// of squares (max |h| = s max |x w|, s > 0).  The row is polled in element
-// order into LDS (load_row), the norm weights loaded before the wait; after
-// one barrier each wave forms its own units' items from LDS (no other wave
-// reads them; the next phase overwrites the row only after split_sum's
-// barrier).  Returns ex.
-template <int SRC, bool RMS, int MU, bool LONG = false, uint32_t HD>
-__device__ __forceinline__ int stage_ops(PassLds<HD>& L, const StageIn& in, uint32_t nb0, uint32_t nb, uint32_t u0,
-                                         uint32_t u1, const float* nw, float eps, Waiter& w, uint32_t tid,
-                                         uint32_t wave) {
-  constexpr uint32_t T = 64 * PASS_WAVES;
-  constexpr uint32_t NW = LONG ? WPT_F : WPT_E;  // LONG: a row longer than E (the feed-forward width)
-  const uint32_t n = nb * 32, lane = tid & 63;
-  float wv[NW];
-  if (RMS)
+// An RMSNorm phase's input (K1, K4: a row of nb blocks of 32) staged by each
+// wave for its own units only, with no workgroup barrier, as stage_wave
+// stages K3's and K5's: the wave reads its units' elements (SRC_XSUM: the
+// residual, then the k-parts added in order) and their norm weights (loaded
+// before the wait), puts y = x w into its part of the row in LDS and forms its
+// items from it scaled by its own 2^ex (its largest |y| in [2^14, 2^15)); its
+// partial sum of x^2 goes to ss[wave].  The product is then formed as
+// s (W y), s from the waves' sums (rms_of), for cpu.go:90-96's W ((x s) w).
+// Returns the wave's ex.
+template <int SRC, int MU, uint32_t HD>
+__device__ __forceinline__ int stage_rms_wave(PassLds<HD>& L, const StageIn& in, uint32_t nb, uint32_t u0,
+                                              uint32_t u1, const float* nw, float* ss, Waiter& w, uint32_t wave,
+                                              uint32_t lane) {
+  constexpr int NE = 2 * MU;
+  const uint32_t n = nb * 32;
+  // element j: 128 (u - u0) + 64 (j % 2) + lane of unit u = u0 + wave + 8 (j / 2)
+  auto el = [&](int j) { return 128 * (wave + PASS_WAVES * (j / 2)) + 64 * (j % 2) + lane; };
+  auto need = [&](int j) { return u0 + wave + PASS_WAVES * (j / 2) < u1 && el(j) < n; };
+  float wv[NE], x[NE];
 #pragma unroll
-    for (uint32_t k = 0; k < NW; k++) wv[k] = tid + T * k < n ? nw[tid + T * k] : 0.f;
-  float v[NW];
-  load_row<SRC, HD, NW>(in, 32 * nb0, n, tid, v, w);
-  float ss = 0, mx = 0;
+  for (int j = 0; j < NE; j++) wv[j] = need(j) ? nw[el(j)] : 0.f;
+  if constexpr (SRC == SRC_PLAIN) {
 #pragma unroll
-  for (uint32_t k = 0; k < NW; k++) {
-    if (tid + T * k < n) {
-      L.row[tid + T * k] = v[k];
-      if (RMS) L.nw[tid + T * k] = wv[k];
+    for (int j = 0; j < NE; j++) x[j] = need(j) ? in.plain[el(j)] : 0.f;
+  } else if constexpr (SRC == SRC_LL) {
+    ll_wait_row<NE>(in.gate, [&](int j) { return in.ll + el(j); }, need, in.flag, x, w);
+  } else if constexpr (SRC == SRC_XSUM) {
+    constexpr uint32_t NP = 1 + PASS_MAX_KP;
+    float u[NE * NP];
+    // word i: vector i / NE (xb, then the parts), element i % NE; the gate:
+    // the wave's word of the last k-part, whose producers finish last
+    ll_wait_row<NE * NP>(in.gate, [&](int i) { return in.ll + (i / NE) * in.E + el(i % NE); },
+                         [&](int i) { return (uint32_t)(i / NE) <= in.kp && need(i % NE); }, in.flag, u, w,
+                         (int)(in.kp * NE));
+#pragma unroll
+    for (int k = 0; k < NE; k++) {
+      x[k] = u[k];
+#pragma unroll
+      for (uint32_t q = 1; q < NP; q++)
+        if (q <= in.kp) x[k] += u[q * NE + k];
     }
-    ss += v[k] * v[k];
-    mx = fmaxf(mx, RMS ? fabsf(v[k] * wv[k]) : fabsf(v[k]));
   }
-  if (RMS) ss = wave_sum_dpp(ss);
-  mx = wave_max_dpp(mx);
-  if (lane == 0) {
-    L.misc[wave] = ss;
-    L.misc[8 + wave] = mx;
-  }
-  __syncthreads();
-  float tot = 0, m = 0;
+  float s2 = 0, mx = 0;
 #pragma unroll
-  for (uint32_t k = 0; k < PASS_WAVES; k++) {
-    tot += L.misc[k];
-    m = fmaxf(m, L.misc[8 + k]);
+  for (int j = 0; j < NE; j++) {
+    const float y = __fmul_rn(x[j], wv[j]);
+    if (need(j)) L.row[el(j)] = y;
+    s2 += x[j] * x[j];  // (0 where not needed)
+    mx = fmaxf(mx, fabsf(y));
   }
-  const float s = RMS ? rms_scale((double)(tot / (float)n + eps)) : 1.f;
-  if (RMS) m *= s;
+  s2 = wave_sum_dpp(s2);
+  mx = wave_max_dpp(mx);  // (the same in every lane)
+  if (lane == 0) ss[wave] = s2;
+  __builtin_amdgcn_wave_barrier();
   int ex = 0;
-  if (m > 0 && m <= 3.0e38f) {
+  if (mx > 0 && mx <= 3.0e38f) {
     int E;
-    frexpf(m, &E);
+    frexpf(mx, &E);
     ex = 15 - E;
   }
-  form_items<RMS, MU>(L, nb, u0, u1, s, ex, wave, lane);
+  form_items<false, MU>(L, nb, u0, u1, 1.f, ex, wave, lane);
   return ex;
+}
+
+// The RMS scale s = f32(1/sqrt(f64(sum x^2 / n + eps))) (cpu.go:90-96) from
+// the waves' partial sums (stage_rms_wave), added in wave order; read after
+// a barrier that follows every wave's stage.
+__device__ __forceinline__ float rms_of(const float* ss, uint32_t n, float eps) {
+  float tot = 0;
+#pragma unroll
+  for (uint32_t k = 0; k < PASS_WAVES; k++) tot += ss[k];
+  return rms_scale((double)(tot / (float)n + eps));
 }
 
 // The phase's input row (one vector of flag-carrying words, nb blocks of 32
@@ -633,13 +613,15 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
       in.E = E;
       UnitsB<1, 1> ub;
       units_deq_any<Q8, 1, 1>(w1, M, 0, wave, ub);
-      const int ex = l ? stage_ops<SRC_XSUM, true, 1>(L, in, 0, M.nb, 0, U, Y->attn_norm, a.eps, wt, tid, wave)
-                       : stage_ops<SRC_PLAIN, true, 1>(L, in, 0, M.nb, 0, U, Y->attn_norm, a.eps, wt, tid, wave);
+      float* ss = L.ss[0][l & 1];
+      const int ex = l ? stage_rms_wave<SRC_XSUM, 1>(L, in, M.nb, 0, U, Y->attn_norm, ss, wt, wave, lane)
+                       : stage_rms_wave<SRC_PLAIN, 1>(L, in, M.nb, 0, U, Y->attn_norm, ss, wt, wave, lane);
       float acc[1] = {0};
       units_mac_any<Q8, 1, 1>(ub, M, L.xs, L.bsum, 0, U, wave, lane, acc);
-      float v = split_sum<1>(L.part, acc, wave, lane);
+      acc[0] = ldexpf(acc[0], -ex);
+      float v = split_sum<1>(L.part1[l & 1], acc, wave, lane);
       if (wave == 0) {
-        v = ldexpf(v, -ex);
+        v = __fmul_rn(v, rms_of(ss, M.nb * 32, a.eps));
         if (bias_p && rv) v += bias;
         const float o = __shfl_xor(v, a.neox ? 8 : 1);
         if (rv) {
@@ -890,13 +872,16 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
         in.gate = !has3;  // K3's workgroups come straight from producing this input
         UnitsB<PASS_K4_TILES, 1> ub;
         units_deq_any<Q8, PASS_K4_TILES, 1>(w4, M, 0, wave, ub);
-        const int ex = stage_ops<SRC_LL, true, 1>(L, in, 0, M.nb, 0, U, Y->ffn_norm, a.eps, wt, tid, wave);
+        float* ss = L.ss[1][l & 1];
+        const int ex = stage_rms_wave<SRC_LL, 1>(L, in, M.nb, 0, U, Y->ffn_norm, ss, wt, wave, lane);
         float acc[PASS_K4_TILES] = {};
         units_mac_any<Q8, PASS_K4_TILES, 1>(ub, M, L.xs, L.bsum, 0, U, wave, lane, acc);
-        float v = split_sum<PASS_K4_TILES>(L.part, acc, wave, lane);
+#pragma unroll
+        for (uint32_t t = 0; t < PASS_K4_TILES; t++) acc[t] = ldexpf(acc[t], -ex);
+        float v = split_sum<PASS_K4_TILES>(L.part4[l & 1], acc, wave, lane);
         const uint32_t tile = rw4 + G * wave;
         if (wave < PASS_K4_TILES && tile < M.tiles) {
-          v = ldexpf(v, -ex);
+          v = __fmul_rn(v, rms_of(ss, M.nb * 32, a.eps));
           // gate row i at lane r < 8, up row i at r + 8 (MAP_GATEUP)
           const float u = __shfl_xor(v, 8);
           const uint32_t i = 8 * tile + (r & 7);
