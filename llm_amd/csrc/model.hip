@@ -850,9 +850,6 @@ static int record_pass(Model& m, uint32_t ntok, bool head, bool embed_in) {
     m.cur_layer = -1;
     PassArgs a = m.pargs;
     a.rows = m.attn_rows;
-    // the long form's (head, chunk)s at the grid's end
-    const uint32_t pm = (a.rows + PASS_LONG_ROWS - 1) / PASS_LONG_ROWS;
-    a.batl = m.attn_split ? m.pgrid - pm * a.heads : 0;
     // algorithmic bytes: every layer's matrices and the KV rows of the
     // positions attended
     uint64_t bytes = 0;

@@ -53,7 +53,6 @@ struct PassArgs {
   // the first workgroup of each phase's work: K1 tiles, attention (head, chunk)s, K3 tiles, K4 (round robin),
   // K5 (tile, part)s
   uint32_t b1, batt, b3, b4, b5;
-  uint32_t batl;  // the long form's first attention workgroup (its (head, chunk)s run to the grid's end)
 };
 
 constexpr uint32_t PASS_WAVES = 8;        // waves per workgroup
@@ -86,10 +85,13 @@ inline uint64_t pass_words(const llmhip_config& c, uint32_t kvd, uint32_t np) {
 }
 // Whether a launch whose attention reads `rows` cache rows past
 // attn_full_max fits the long form on `grid` workgroups (head size 64, a
-// workgroup per query head and chunk).
+// workgroup per query head and chunk; the query heads of a (chunk, KV head)
+// pair on one XCD, the pairs dealt to the 8 XCDs in turn, each XCD's units on
+// its workgroups from the grid's end down).
 inline bool pass_long_fits(const llmhip_config& c, uint32_t rows, uint32_t grid) {
   const uint32_t pm = (rows + PASS_LONG_ROWS - 1) / PASS_LONG_ROWS;
-  return c.head_dim == 64 && pm <= PASS_LONG_CHUNKS && (uint64_t)pm * (uint32_t)c.heads <= grid;
+  const uint64_t pairs = (uint64_t)pm * (uint32_t)c.kv_heads, gq = (uint32_t)(c.heads / c.kv_heads);
+  return c.head_dim == 64 && pm <= PASS_LONG_CHUNKS && grid % 8 == 0 && 8 * ((pairs + 7) / 8) * gq <= grid;
 }
 // Why a model's decode passes cannot take the fused launch (nullptr: they can),
 // for `grid` co-resident workgroups; *kp receives the down projection's k-parts.
@@ -100,7 +102,7 @@ const char* pass_unfit(const llmhip_config& c, uint32_t kvd, const PassMat& qkv,
 uint32_t pass_grid(int device, uint32_t hd, bool kv16);
 // The work placement of a grid (PassArgs::b*); t1, t3, t5: tiles of [q; k; v], W_o and W_down.
 void pass_place(PassArgs* a, uint32_t grid, uint32_t t1, uint32_t t3, uint32_t t5);
-// q8: some layer matrix is Q8_0; lng: the long form (a.rows past attn_full_max, a.batl set).
+// q8: some layer matrix is Q8_0; lng: the long form (a.rows past attn_full_max, pass_long_fits).
 int pass_launch(const PassArgs& a, uint32_t grid, bool q8, bool lng, hipStream_t s);
 
 }  // namespace llmhip

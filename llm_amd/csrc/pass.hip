@@ -523,13 +523,18 @@ __global__ __launch_bounds__(512) void pass_kernel(PassArgs a) {
   bool hasA = false;
   uint32_t hg = 0, hh = 0, hc = 0;  // attention: KV head, query head, chunk
   if (LONG) {
-    // (query head, chunk) on workgroup batl + c heads + h, for the chunks of
-    // the rows this launch may read
-    const uint32_t PM = (a.rows + RC - 1) / RC;
-    if (wg >= a.batl && wg - a.batl < a.heads * PM) {
-      hc = (wg - a.batl) / a.heads;
-      hh = (wg - a.batl) % a.heads;
-      hg = hh / GQ;
+    // (query head, chunk)s for the chunks of the rows this launch may read,
+    // grouped by (chunk, KV head) pair p = c kv_heads + g: pair p's GQ query
+    // heads on XCD p % 8 (workgroup w runs on XCD w % 8), so that the pair's
+    // rows are read through one L2; XCD x's units (pairs x, x + 8, ..., GQ
+    // each) on its workgroups from the grid's end down: unit k of XCD x on
+    // workgroup G - 8 (k + 1) + x (G a multiple of 8: pass_long_fits)
+    const uint32_t PM = (a.rows + RC - 1) / RC, x = wg % 8, k = (G + x - wg) / 8 - 1;
+    const uint32_t p = x + 8 * (k / GQ);
+    if (p < PM * a.kv_heads) {
+      hc = p / a.kv_heads;
+      hg = p % a.kv_heads;
+      hh = hg * GQ + k % GQ;
       hasA = hc < P;
     }
   } else if (wg >= a.batt && wg - a.batt < NCH * natt1) {
