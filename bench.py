@@ -489,6 +489,11 @@ def main():
         res["long_context"] = long_context(args)
     if not args.no_sweep:
         res["gemv_sweep"] = sweep(args)
+        # the GEMVs `metric` names (one token, the vocabulary shape), at a glance
+        res["gemv_roofline"] = {
+            f"{e['type']}_{e['rows']}x{e['k']}": {"us": e["hbm_us"], "achieved": e["hbm_gbps"], "peak": PEAK_HBM_GBS,
+                                                  "unit": "GB/s", "frac": e["hbm_frac"]}
+            for e in res["gemv_sweep"] if e["n"] == 1 and e["rows"] == 151936}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(res), flush=True)
