@@ -37,11 +37,16 @@
 
 namespace llmhip {
 
+// The flag-carrying words are device memory: their atomics take the global
+// address space (global_load / global_store with sc1), not the generic one,
+// whose flat instructions also count in the LDS and scalar wait counter.
+typedef __attribute__((address_space(1))) uint64_t gword;
 __device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((const gword*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void ll_store(uint64_t* p, float v, uint32_t flag) {
-  __hip_atomic_store(p, ((uint64_t)flag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((gword*)p, ((uint64_t)flag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // A thread's bounded waits: after `limit` polls of one wait it counts a
