@@ -78,6 +78,27 @@ def test_pass_long_context(gpu, start):
     _fused_vs_plain(g, spec, prompt)
 
 
+def test_pass_long_form_all_chunks(gpu):
+    """The long form at its most chunks (16 of 256 rows: positions past 3584
+    at ctx 4096) with 14 query heads on 2 KV heads, as at the Qwen shape: the
+    query heads of a (chunk, KV head) pair, grouped on one XCD, then take
+    224 workgroups and reach down into those of the [q; k; v] tiles, which run
+    both phases in turn.  Against the oracle and against the same steps one
+    launch per kernel; the dispatch counts show the fused launch ran."""
+    spec = synth.tiny_qwen(seed=25, embd=896, heads=14, kv_heads=2, ff=512, ctx=4096)
+    g, cpu = _open(spec, 4096)
+    _fused(g)
+    prompt = synth.prompt(44, 3900, spec.vocab)
+    fused = g.Generate(list(prompt), 9, -1)
+    g.set_fused(False)
+    plain = g.Generate(list(prompt), 9, -1)
+    _fused(g)
+    print(f"dispatches: fused {fused.Dispatches}, one launch per kernel {plain.Dispatches}", flush=True)
+    assert fused.Dispatches + 8 * 2 * 4 <= plain.Dispatches
+    _check(g, cpu, prompt, 8)
+    _fused_vs_plain(g, spec, prompt)
+
+
 @pytest.mark.parametrize("kv16", [False, True])
 def test_pass_f16_kv(gpu, kv16):
     spec = synth.tiny_qwen(seed=23)
