@@ -88,6 +88,8 @@ __device__ __forceinline__ void ll_wait_f(At at, Need need, uint32_t flag, float
   for (int i = 0; i < N; i++) v[i] = __uint_as_float((uint32_t)x[i]);
 }
 
+constexpr int PASS_GATE_STAGGER = 6;  // s_sleep units (64 cycles) between the gate's two first polls
+
 // ll_wait_f preceded by a gate: the wave's first lane polls its word `gate`
 // alone until it carries the flag (a word of the input's last producers).  A workgroup that reaches a phase long
 // before the phase's input is produced then waits with one load in flight
@@ -96,18 +98,33 @@ __device__ __forceinline__ void ll_wait_f(At at, Need need, uint32_t flag, float
 template <int N, class At, class Need>
 __device__ __forceinline__ void ll_wait_gated(At at, Need need, uint32_t flag, float (&v)[N], Waiter& w,
                                               int gate = 0) {
-  const bool g = (threadIdx.x & 63) == 0 && need(gate);
-  uint32_t spins = 0;
-  for (;;) {
-    bool ok = true;
-    if (g && !w.dead) ok = (uint32_t)(ll_load(at(gate)) >> 32) == flag;
-    if (__all(ok)) break;
-    if (++spins > w.limit) {  // (spins: the same in every lane)
-      if (!w.dead) atomicOr(w.err, 1u);
-      w.dead = true;
-      break;
+  // lane 0's word `gate`, polled by the whole wave at one address (one
+  // request), two polls in flight started PASS_GATE_STAGGER apart: each check
+  // waits for the older one only (loads return in order), so a word that
+  // lands between two polls is seen about half a round trip sooner
+  const uint64_t gp = (uint64_t)at(gate);
+  const uint64_t* p0 = (const uint64_t*)(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(gp >> 32)) << 32) |
+                                         (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)gp));
+  if (__builtin_amdgcn_readfirstlane(need(gate) ? 1 : 0) && !w.dead) {
+    uint64_t x0 = ll_load(p0);
+    __builtin_amdgcn_s_sleep(PASS_GATE_STAGGER);
+    uint64_t x1 = ll_load(p0);
+    uint32_t spins = 0;
+    auto done = [&](uint64_t x) {
+      if (__builtin_amdgcn_readfirstlane((uint32_t)(x >> 32)) == flag) return true;
+      if (++spins > w.limit) {  // (spins: the same in every lane)
+        atomicOr(w.err, 1u);
+        w.dead = true;
+        return true;
+      }
+      return false;
+    };
+    for (;;) {
+      if (done(x0)) break;
+      x0 = ll_load(p0);
+      if (done(x1)) break;
+      x1 = ll_load(p0);
     }
-    __builtin_amdgcn_s_sleep(1);
   }
   ll_wait_f<N>(at, need, flag, v, w);
 }
