@@ -64,12 +64,14 @@ def _fused_vs_plain(g, spec, prompt):
             assert rel_err(lf, lp) <= 1e-5 and np.all(np.isfinite(lf))
 
 
-@pytest.mark.parametrize("start", [300, 1500])
+@pytest.mark.parametrize("start", [250, 300, 1500])
 def test_pass_long_context(gpu, start):
     """Decode steps past attn_full_max through the long form of the fused
     launch (256-row chunks, one workgroup per query head and chunk, the last
     chunk's workgroup merging the others): against the oracle, and against
-    the same steps taken one launch per kernel (the split attention)."""
+    the same steps taken one launch per kernel (the split attention).  From
+    250 the steps cross 256: a submit whose last position is past it runs all
+    its steps in the long form, those below 256 as one chunk."""
     spec = synth.tiny_qwen(seed=24, ctx=2048)
     g, cpu = _open(spec, 2048)
     _fused(g)
