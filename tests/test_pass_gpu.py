@@ -64,16 +64,18 @@ def _fused_vs_plain(g, spec, prompt):
             assert rel_err(lf, lp) <= 1e-5 and np.all(np.isfinite(lf))
 
 
-@pytest.mark.parametrize("start", [250, 300, 1500])
-def test_pass_long_context(gpu, start):
+@pytest.mark.parametrize("start,kv16", [(250, False), (300, False), (505, False), (1500, False), (1500, True)])
+def test_pass_long_context(gpu, start, kv16):
     """Decode steps past attn_full_max through the long form of the fused
     launch (256-row chunks, one workgroup per query head and chunk, the last
     chunk's workgroup merging the others): against the oracle, and against
     the same steps taken one launch per kernel (the split attention).  From
     250 the steps cross 256: a submit whose last position is past it runs all
-    its steps in the long form, those below 256 as one chunk."""
+    its steps in the long form, those below 256 as one chunk; from 505 a
+    submit crosses 512, where the graph variant's rows grow; at 1500 also
+    with the binary16 cache."""
     spec = synth.tiny_qwen(seed=24, ctx=2048)
-    g, cpu = _open(spec, 2048)
+    g, cpu = _open(spec, 2048, f16kv=kv16)
     _fused(g)
     prompt = synth.prompt(43, start, spec.vocab)
     _check(g, cpu, prompt, 24)
